@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Headline benchmark of the MI355X HIP backend for zlm's quantized GEMV path.
+
+A step is one pass of the configs[1] workload -- the Qwen3-8B FFN GEMVs in
+Q8_0 at batch 1: gate 12288x4096, up 12288x4096, down 4096x12288 -- over
+weights already resident in HBM and activations already on the device.  Every
+step reads a different copy of the three weights (>= 512 MiB in rotation), so
+the 256 MiB Infinity Cache cannot serve them and the rate is an HBM rate.
+
+Timing: W warm-up steps, then K steps between two HIP events on the backend's
+stream (the stream every launch goes to).  `value` = algorithmic bytes of a
+step (weights + x + y) / (elapsed / K).  The roofline object reports the
+dominant kernel (the k=4096 Q8_0 GEMV of gate/up), timed the same way on its
+own.  The CPU baseline is the oracle's restatement of zlm's production sweep
+on the same gate weight, on the host cores.
+
+Prints one JSON line.  --gpus N with N > 1 is refused: this backend runs on one
+GPU.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+from zlm_amd import device as zd  # noqa: E402
+from zlm_amd import synth  # noqa: E402
+
+PEAK_GBPS = 8000.0
+MALL_DEFEAT_BYTES = 512 * 1024 * 1024
+METRIC = "quant GEMV HBM GB/s (% of 8 TB/s peak); decode tok/s, Qwen3-8B-shape Q4_0 bs=1"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Gemv:
+    """One GEMV shape with its resident weight copies and device vectors."""
+
+    def __init__(self, dev, name, qt, rows, k, seed, copies=None):
+        self.dev, self.name, self.qt, self.rows, self.k = dev, name, qt, rows, k
+        self.w = synth.weights(qt, rows, k, seed)
+        self.wbytes = self.w.size
+        if copies is None:
+            copies = max(1, math.ceil(MALL_DEFEAT_BYTES / self.wbytes))
+        self.copies = copies
+        self.res = []
+        for _ in range(copies):
+            r = dev.upload_resident(self.w)
+            if r is None:
+                raise RuntimeError(dev.last_error())
+            self.res.append(r)
+        self.x = synth.activation(seed + 1, k)
+        self.x_dev = dev.dev_malloc(k * 4)
+        dev.dev_upload(self.x_dev, self.x)
+        self.y_dev = dev.dev_malloc(rows * 4)
+
+    @property
+    def algo_bytes(self) -> int:
+        return self.wbytes + 4 * self.k + 4 * self.rows
+
+    def desc(self, c):
+        return (self.res[c % self.copies], zd.quant(self.qt), self.rows, self.k, self.x_dev, self.y_dev)
+
+    def free(self):
+        for r in self.res:
+            self.dev.free_resident(r)
+        self.dev.dev_free(self.x_dev)
+        self.dev.dev_free(self.y_dev)
+        self.res = []
+
+
+def time_launches(dev, descs, launches_target, warmup_passes=2):
+    """Average ms per pass over `descs` (a pass = every desc once)."""
+    passes = max(1, launches_target // len(descs))
+    dev.time_gemv_sequence(descs, warmup_passes)
+    ms = dev.time_gemv_sequence(descs, passes)
+    return ms / passes
+
+
+def cpu_baseline(g: Gemv, budget_s: float):
+    import oracle
+
+    threads = min(16, len(os.sched_getaffinity(0)))
+    t1 = oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=threads, reps=1)
+    reps = max(3, min(2000, int(budget_s / max(t1, 1e-6))))
+    best = oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=threads, reps=reps)
+    return {
+        "value": round(g.algo_bytes / best / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"oracle restatement of zlm's production sweep (-O3, x86-64-v3, lanes=8), "
+                  f"{g.name} {g.rows}x{g.k} Q8_0 GEMV, {threads} threads split by rangeOf, "
+                  f"min of {reps} reps ({reps * t1:.1f} s)",
+        "ms_per_gemv": round(best * 1e3, 4),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
+        sys.exit(2)
+
+    dev = zd.Device()
+    if not dev.available():
+        raise SystemExit(f"HIP backend unavailable: {dev.last_error()}")
+    log(f"device: {dev.device_name()}, {dev.cu_count()} CUs")
+
+    # ---- headline: configs[1], Q8_0 Qwen3-8B FFN GEMVs ------------------------------
+    step_w = 2 * synth.weight_bytes(synth.Q8_0, 12288, 4096) + synth.weight_bytes(synth.Q8_0, 4096, 12288)
+    copies = max(1, math.ceil(MALL_DEFEAT_BYTES / step_w))
+    log(f"C1: generating Q8_0 gate/up/down, {copies} resident copies each")
+    gate = Gemv(dev, "gate", synth.Q8_0, 12288, 4096, 0x5A4C4D01, copies)
+    up = Gemv(dev, "up", synth.Q8_0, 12288, 4096, 0x5A4C4D11, copies)
+    down = Gemv(dev, "down", synth.Q8_0, 4096, 12288, 0x5A4C4D21, copies)
+    step_descs = []
+    for c in range(copies):
+        step_descs += [gate.desc(c), up.desc(c), down.desc(c)]
+    step_bytes = gate.algo_bytes + up.algo_bytes + down.algo_bytes
+
+    passes_w = max(1, args.warmup // copies)
+    passes = max(1, args.steps // copies)
+    dev.time_gemv_sequence(step_descs, passes_w)
+    ms_total = dev.time_gemv_sequence(step_descs, passes)
+    steps = passes * copies
+    ms_step = ms_total / steps
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"C1 step: {ms_step * 1e3:.2f} us -> {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak)")
+
+    # dominant kernel: the k=4096 gate/up GEMV, alone, same rotation
+    gu_descs = []
+    for c in range(copies):
+        gu_descs += [gate.desc(c), up.desc(c)]
+    ms_gu = time_launches(dev, gu_descs, 4 * len(gu_descs) * 25) / len(gu_descs)
+    gu_gbps = gate.algo_bytes / (ms_gu * 1e-3) / 1e9
+    ms_dn = time_launches(dev, [down.desc(c) for c in range(copies)], 100 * copies) / copies
+    dn_gbps = down.algo_bytes / (ms_dn * 1e-3) / 1e9
+    log(f"gate/up GEMV {ms_gu * 1e3:.2f} us ({gu_gbps:.1f} GB/s); down GEMV {ms_dn * 1e3:.2f} us ({dn_gbps:.1f} GB/s)")
+
+    extra = {
+        "c1_gate_up_q8_0_12288x4096": {"us": round(ms_gu * 1e3, 3), "GBps": round(gu_gbps, 1)},
+        "c1_down_q8_0_4096x12288": {"us": round(ms_dn * 1e3, 3), "GBps": round(dn_gbps, 1)},
+    }
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        traffic = t.get("zlm_gemv_q8_0_k4096", {}).get("bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(gate, args.cpu_seconds)
+        log(f"CPU: {cpu['value']} GB/s on {cpu['cores']} threads")
+    for g in (gate, up, down):
+        g.free()
+
+    # ---- the other GEMV configs (reported, not the headline) --------------------
+    if not args.quick:
+        others = [
+            ("c0_q4_0_4096x4096", synth.Q4_0, 4096, 4096),
+            ("c3_q4_k_15360x3840", synth.Q4_K, 15360, 3840),
+            ("c3_q4_k_3840x15360", synth.Q4_K, 3840, 15360),
+            ("c3_q6_k_15360x3840", synth.Q6_K, 15360, 3840),
+            ("c3_q6_k_3840x15360", synth.Q6_K, 3840, 15360),
+            ("c3_q6_k_lm_head_262144x3840", synth.Q6_K, 262144, 3840),
+            ("c2_lm_head_q8_0_151936x4096", synth.Q8_0, 151936, 4096),
+        ]
+        for name, qt, rows, k in others:
+            g = Gemv(dev, name, qt, rows, k, 0x5A4C4D40 + rows)
+            descs = [g.desc(c) for c in range(g.copies)]
+            target = max(len(descs), min(400, int(2e9 / g.wbytes)))
+            ms = time_launches(dev, descs, target) / len(descs)
+            gbps = g.algo_bytes / (ms * 1e-3) / 1e9
+            extra[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
+                           "copies": g.copies}
+            log(f"{name}: {ms * 1e3:.2f} us, {gbps:.1f} GB/s ({100 * gbps / PEAK_GBPS:.1f}%)")
+            g.free()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": passes_w * copies,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded splitmix64: f16 scales |N(0,1)|*0.01, int8 quants U[-127,127], x N(0,1))",
+        "config": {
+            "workload": "configs[1]: Q8_0 Qwen3-8B FFN GEMVs at batch 1, gate+up 12288x4096 and down 4096x12288 "
+                        "per step, weights resident in HBM",
+            "weight_copies_rotated": copies,
+            "bytes_per_step": step_bytes,
+        },
+        "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "zlm_gemv_q8_0_k4096 (gate/up 12288x4096)",
+            "achieved": round(gu_gbps, 1),
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gu_gbps / PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": gate.algo_bytes,
+            "avg_launch_us": round(ms_gu * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    dev.deinit()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,221 @@
+/*
+ * zlm_gpu_hip.h -- C ABI of the MI355X (gfx950) HIP co-processor backend for
+ * zlm's quantized GEMV/GEMM path.
+ *
+ * The first block of entry points is the reference's GPU backend contract,
+ * one function per name in `required_ops` (reference
+ * src/gpu/backend/root.zig:299-311), with the semantics of the Vulkan device
+ * it replaces (src/gpu/backend/vulkan/root.zig:22-236):
+ *   - zlm_gpu_init never fails: without a usable GPU it returns a valid, inert
+ *     device whose zlm_gpu_available() is false;
+ *   - nothing is thrown: `false`, ZLM_NULL_HANDLE or NULL means "did not run
+ *     on the device, the caller uses the CPU kernel" (unsupported quant or
+ *     shape, short buffers, allocation or driver failure);
+ *   - results land in host memory: every synchronous op, and
+ *     zlm_gpu_wait_resident for the asynchronous ones, copies `rows` floats
+ *     into `out`;
+ *   - single-threaded: one thread drives a device (the executor's).
+ *
+ * Quant codes: the GGML type code (reference gguf/format.zig:41-77) in bits
+ * 0..7 and the GpuVariant code (reference gpu/kernels/grid.zig:14) in bits
+ * 8..15.  A variant never changes the byte layout, only the kernel.
+ *
+ * Weight bytes are always the raw GGUF blocks (row-major, `rows` rows of
+ * `k / block_elems` blocks).  The device keeps its own layout in HBM.
+ */
+#ifndef ZLM_GPU_HIP_H
+#define ZLM_GPU_HIP_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* In-flight resident dispatches (reference gpu/backend/root.zig:230 RingSize). */
+#define ZLM_RING_SIZE 8
+/* The null async handle (the Zig `?Handle` null). */
+#define ZLM_NULL_HANDLE (-1)
+
+/* GGML type codes (reference gguf/format.zig:41-77). */
+enum {
+    ZLM_GGML_F32 = 0,
+    ZLM_GGML_F16 = 1,
+    ZLM_GGML_Q4_0 = 2,
+    ZLM_GGML_Q4_1 = 3,
+    ZLM_GGML_Q8_0 = 8,
+    ZLM_GGML_Q4_K = 12,
+    ZLM_GGML_Q6_K = 14,
+    ZLM_GGML_BF16 = 30
+};
+
+/* GpuVariant codes (reference gpu/kernels/grid.zig:14). */
+enum {
+    ZLM_VARIANT_PLAIN = 0,
+    ZLM_VARIANT_U4 = 1,
+    ZLM_VARIANT_U8 = 2,
+    ZLM_VARIANT_SUB = 3,
+    ZLM_VARIANT_UN2 = 4,
+    ZLM_VARIANT_UN4 = 5,
+    ZLM_VARIANT_W32 = 6,
+    ZLM_VARIANT_W128 = 7
+};
+
+/* GateUpAct (reference gpu/backend/root.zig:225). */
+enum { ZLM_ACT_SILU = 0, ZLM_ACT_GELU = 1 };
+
+#define ZLM_QUANT(ggml_type, variant) ((uint32_t)(ggml_type) | ((uint32_t)(variant) << 8))
+
+typedef struct zlm_device zlm_device;
+typedef struct zlm_resident zlm_resident;
+
+/* ResidentOp (reference gpu/backend/root.zig:249-254): `out` holds >= rows floats. */
+typedef struct {
+    zlm_resident *res;
+    uint32_t quant;
+    size_t rows;
+    float *out;
+    size_t out_len;
+} zlm_resident_op;
+
+/* Probe (reference gpu/backend/root.zig:260-295).  GB/s over raw weight bytes;
+ * unmeasured fields stay 0; variants are GpuVariant codes. */
+typedef struct {
+    double gemv_gbps;
+    double gemv_streamed_gbps;
+    double matmul_gbps;
+    uint8_t q4_0_variant;
+    uint8_t q4_1_variant;
+    uint8_t q8_0_variant;
+    uint8_t q6_k_variant;
+    uint8_t q4_k_variant;
+    uint8_t f32_variant;
+    uint8_t f16_variant;
+    uint8_t bf16_variant;
+    uint8_t gate_up_variant;
+    uint8_t gate_up_q4_1_variant;
+    uint8_t gate_up_q8_0_variant;
+    double q4_0_u4_gbps;
+    double q4_0_sub_gbps;
+    double q4_0_un2_gbps;
+    double q4_0_un4_gbps;
+    double q4_0_w32_gbps;
+    double q4_0_w128_gbps;
+    double q4_k_gbps;
+    double q4_k_u4_gbps;
+    double gate_up_gbps;
+    double gate_up_u4_gbps;
+} zlm_probe;
+
+/* ---- the backend contract (reference gpu/backend/root.zig:299-311) ---- */
+
+/* Device.init (vulkan/root.zig:28-42): never NULL unless the host is out of memory. */
+zlm_device *zlm_gpu_init(void);
+/* Device.deinit (vulkan/root.zig:44-55); also frees the handle. */
+void zlm_gpu_deinit(zlm_device *dev);
+/* Device.available (vulkan/root.zig:57-59). */
+bool zlm_gpu_available(const zlm_device *dev);
+/* Device.backendName (vulkan/root.zig:61-66): "hip", or "off" when inert. */
+const char *zlm_gpu_backend_name(const zlm_device *dev);
+/* Device.deviceName (vulkan/root.zig:68-71). */
+const char *zlm_gpu_device_name(const zlm_device *dev);
+/* Device.isUma (vulkan/root.zig:73-76). */
+bool zlm_gpu_is_uma(const zlm_device *dev);
+
+/* Device.matVec (vulkan/root.zig:78-87): streamed GEMV, weights staged per call. */
+bool zlm_gpu_mat_vec(zlm_device *dev, uint32_t quant, const void *weight, size_t weight_len, size_t rows,
+                     size_t k, const float *x, size_t x_len, float *out, size_t out_len);
+/* Device.matMulBatch (vulkan/root.zig:89-102): out[t*rows + r], x token-major m*k. */
+bool zlm_gpu_mat_mul_batch(zlm_device *dev, uint32_t quant, const void *weight, size_t weight_len,
+                           size_t rows, size_t k, size_t m, const float *x, size_t x_len, float *out,
+                           size_t out_len);
+/* Device.matMulResident (vulkan/root.zig:104-115). */
+bool zlm_gpu_mat_mul_resident(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
+                              size_t m, const float *x, size_t x_len, float *out, size_t out_len);
+/* Device.matVecResident (vulkan/root.zig:117-125). */
+bool zlm_gpu_mat_vec_resident(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
+                              const float *x, size_t x_len, float *out, size_t out_len);
+/* Device.matVecResidentAsync (vulkan/root.zig:127-136). */
+int32_t zlm_gpu_mat_vec_resident_async(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows,
+                                       size_t k, const float *x, size_t x_len);
+/* Device.matVecResidentBurstAsync (vulkan/root.zig:138-148).  `first` stages x
+ * into the device-owned burst buffer; later members must pass the same x
+ * pointer and length, or they are refused. */
+int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows,
+                                             size_t k, const float *x, size_t x_len, bool first);
+/* Device.matVecGateUpResidentBurstAsync (vulkan/root.zig:150-164). */
+int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device *dev, zlm_resident *res_gate,
+                                                     zlm_resident *res_up, uint32_t quant, size_t rows,
+                                                     size_t k, const float *x, size_t x_len, uint32_t act,
+                                                     uint32_t variant, bool first);
+/* Device.matVecMlpResidentBurstAsync (vulkan/root.zig:166-179). */
+int32_t zlm_gpu_mat_vec_mlp_resident_burst_async(zlm_device *dev, zlm_resident *res_gate, zlm_resident *res_up,
+                                                 zlm_resident *res_down, uint32_t quant, size_t rows, size_t k,
+                                                 size_t ffn, const float *x, size_t x_len, uint32_t act,
+                                                 uint32_t variant, bool first);
+/* Device.matVecMlpPairResidentBurstAsync (vulkan/root.zig:181-194). */
+int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device *dev, zlm_resident *res_gate,
+                                                      zlm_resident *res_up, zlm_resident *res_down,
+                                                      uint32_t gu_quant, uint32_t down_quant, size_t rows,
+                                                      size_t k, size_t ffn, const float *x, size_t x_len,
+                                                      uint32_t act, uint32_t variant, bool first);
+/* Device.waitResident (vulkan/root.zig:196-202). */
+bool zlm_gpu_wait_resident(zlm_device *dev, int32_t handle, float *out, size_t out_len, size_t rows);
+/* Device.matVecResidentBatch (vulkan/root.zig:204-212): <= ZLM_RING_SIZE ops sharing x. */
+bool zlm_gpu_mat_vec_resident_batch(zlm_device *dev, size_t k, const float *x, size_t x_len,
+                                    const zlm_resident_op *ops, size_t n_ops);
+/* Device.uploadResident (vulkan/root.zig:214-224). */
+zlm_resident *zlm_gpu_upload_resident(zlm_device *dev, const void *bytes, size_t len);
+/* Device.freeResident (vulkan/root.zig:226-230). */
+void zlm_gpu_free_resident(zlm_device *dev, zlm_resident *res);
+/* Device.sync (vulkan/root.zig:232-235). */
+void zlm_gpu_sync(zlm_device *dev);
+/* Device.probeGpu (vulkan/root.zig:237-242, generic probe gpu/backend/root.zig:357-498). */
+void zlm_gpu_probe(zlm_device *dev, size_t rows, size_t k, size_t m, zlm_probe *out);
+
+/* Resident.bytes (reference gpu/backend/root.zig:241-244). */
+uint64_t zlm_gpu_resident_bytes(const zlm_resident *res);
+
+/* ---- device-level entry points (no reference counterpart) ----
+ * For callers that keep activations in HBM (the decode-step harness, the
+ * benchmark) and for the bit-exact checks.  All work goes to the device's one
+ * HIP stream, in order. */
+
+/* Human-readable reason of the last failed call on this device ("" if none). */
+const char *zlm_gpu_last_error(const zlm_device *dev);
+/* Number of compute units, 0 when inert. */
+int zlm_gpu_cu_count(const zlm_device *dev);
+void *zlm_gpu_dev_malloc(zlm_device *dev, size_t bytes);
+void zlm_gpu_dev_free(zlm_device *dev, void *ptr);
+bool zlm_gpu_dev_upload(zlm_device *dev, void *dst, const void *src, size_t bytes);
+bool zlm_gpu_dev_download(zlm_device *dev, void *dst, const void *src, size_t bytes);
+/* Enqueue y_dev[0..rows) = W * x_dev on the device stream; no host copies. */
+bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
+                             const float *x_dev, float *y_dev);
+/* Enqueue `iters` GEMVs, rotating over `n_res` residents, between two HIP events
+ * on the device stream; *ms = elapsed GPU milliseconds between the events. */
+bool zlm_gpu_time_mat_vec(zlm_device *dev, zlm_resident *const *res, size_t n_res, uint32_t quant, size_t rows,
+                          size_t k, const float *x_dev, float *y_dev, int iters, double *ms);
+/* One GEMV of a timed sequence (device pointers). */
+typedef struct {
+    zlm_resident *res;
+    uint32_t quant;
+    size_t rows;
+    size_t k;
+    const float *x_dev;
+    float *y_dev;
+} zlm_gemv_desc;
+/* Enqueue descs[0..n) in order, `iters` times, between two HIP events on the
+ * device stream; *ms = elapsed GPU milliseconds between the events. */
+bool zlm_gpu_time_gemv_sequence(zlm_device *dev, const zlm_gemv_desc *descs, size_t n, int iters, double *ms);
+/* Dequantize the first n_elements of a resident from its device layout into host `out`. */
+bool zlm_gpu_dequant_resident(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t n_elements, float *out);
+/* Quantize host x (n floats, n % 32 == 0) to q8 blocks on the device. */
+bool zlm_gpu_quantize_act_q8(zlm_device *dev, const float *x, size_t n, int8_t *qx, float *dx, int32_t *sums);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZLM_GPU_HIP_H */

@@ -1,0 +1,105 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol the
+header declares, and without a GPU the device is inert (the reference's
+`available() == false`, every op refused) -- gpu/root_test.zig:328-336."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+from zlm_amd import device as zd
+from zlm_amd import synth
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "zlm_gpu_hip.h")
+
+# The reference contract's op names (gpu/backend/root.zig:299-311) and the C symbol each maps to.
+REQUIRED_OPS = {
+    "init": "zlm_gpu_init",
+    "deinit": "zlm_gpu_deinit",
+    "available": "zlm_gpu_available",
+    "backendName": "zlm_gpu_backend_name",
+    "deviceName": "zlm_gpu_device_name",
+    "isUma": "zlm_gpu_is_uma",
+    "matVec": "zlm_gpu_mat_vec",
+    "matMulBatch": "zlm_gpu_mat_mul_batch",
+    "matMulResident": "zlm_gpu_mat_mul_resident",
+    "matVecResident": "zlm_gpu_mat_vec_resident",
+    "matVecResidentAsync": "zlm_gpu_mat_vec_resident_async",
+    "matVecResidentBurstAsync": "zlm_gpu_mat_vec_resident_burst_async",
+    "matVecGateUpResidentBurstAsync": "zlm_gpu_mat_vec_gate_up_resident_burst_async",
+    "matVecMlpResidentBurstAsync": "zlm_gpu_mat_vec_mlp_resident_burst_async",
+    "matVecMlpPairResidentBurstAsync": "zlm_gpu_mat_vec_mlp_pair_resident_burst_async",
+    "waitResident": "zlm_gpu_wait_resident",
+    "matVecResidentBatch": "zlm_gpu_mat_vec_resident_batch",
+    "uploadResident": "zlm_gpu_upload_resident",
+    "freeResident": "zlm_gpu_free_resident",
+    "sync": "zlm_gpu_sync",
+    "probeGpu": "zlm_gpu_probe",
+}
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(zlm_gpu_\w+)\s*\(", text)))
+
+
+def test_header_declares_every_required_op():
+    names = declared_functions()
+    for op, sym in REQUIRED_OPS.items():
+        assert sym in names, f"contract op {op} has no C entry point"
+
+
+def test_library_exports_every_declared_symbol():
+    L = zd.lib()
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_code_object_built_for_gfx950():
+    assert os.path.exists(zd.CODE_OBJECT_PATH)
+    blob = open(zd.CODE_OBJECT_PATH, "rb").read()
+    # hipcc --genco writes an offload bundle around the gfx950 ELF
+    assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+
+
+def test_quant_encoding():
+    assert zd.quant(zd.Q4_0) == 2
+    assert zd.quant(zd.Q8_0, zd.U4) == 8 | (1 << 8)
+    assert zd.quant(zd.Q6_K, zd.W128) == 14 | (7 << 8)
+
+
+def test_inert_device_refuses_everything():
+    dev = zd.Device()
+    if dev.available():
+        pytest.skip("a GPU is present; the inert-device contract is checked on GPU-less hosts")
+    assert dev.backend_name() == "off" and dev.device_name() == "off" and not dev.is_uma()
+    rows, k = 8, 64
+    w = synth.weights(synth.Q4_0, rows, k, seed=1)
+    x = synth.activation(1, k)
+    out = np.zeros(rows, np.float32)
+    assert not dev.mat_vec(zd.quant(zd.Q4_0), w, rows, k, x, out)
+    assert not dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, 2, np.zeros(2 * k, np.float32),
+                                 np.zeros(2 * rows, np.float32))
+    assert dev.upload_resident(w) is None
+    fake = zd.Resident(dev, None)
+    assert not dev.mat_vec_resident(fake, zd.quant(zd.Q4_0), rows, k, x, out)
+    assert dev.mat_vec_resident_async(fake, zd.quant(zd.Q4_0), rows, k, x) is None
+    assert dev.mat_vec_resident_burst_async(fake, zd.quant(zd.Q4_0), rows, k, x, True) is None
+    assert dev.mat_vec_gate_up_resident_burst_async(fake, fake, zd.quant(zd.Q4_0), rows, k, x, zd.SILU, 0,
+                                                    True) is None
+    assert not dev.wait_resident(0, out, rows)
+    assert not dev.mat_vec_resident_batch(k, x, [zd.ResidentOp(fake, zd.quant(zd.Q4_0), rows, out)])
+    p = dev.probe_gpu(rows, k, 2)
+    assert p.gemv_gbps == 0 and p.matmul_gbps == 0 and p.q4_0_variant == 0
+    dev.sync()
+    dev.free_resident(fake)
+    dev.deinit()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(zd, "LIB_PATH", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(zd, "_lib", None)
+    with pytest.raises(ImportError):
+        zd.Device()

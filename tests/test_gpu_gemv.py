@@ -1,0 +1,230 @@
+"""GPU parity of the HIP GEMV path against the CPU oracle, through the C ABI.
+
+Bars (from the task's north star and the reference's own GPU tests):
+  * dequantized blocks: bit-exact against the oracle's codecs;
+  * GEMV outputs: relative L2 <= 1e-3 against the oracle's production sweep,
+    and the reference's per-element check |c-g| <= 1e-4 + 1e-4|c| at k=256
+    (5e-3 + 1e-4|c| at k=8192) on its fillWeights-style inputs
+    (reference gpu/root_test.zig:33-50, :52-128);
+  * the activation quantizer: bit-exact (qx, dx, sums).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import assert_close_ref, fill_weights, ref_x, rel_l2
+from zlm_amd import device as zd
+from zlm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K]
+NAMES = {synth.Q4_0: "q4_0", synth.Q8_0: "q8_0", synth.Q4_K: "q4_k", synth.Q6_K: "q6_k"}
+REL_L2 = 1e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
+def test_dequant_bit_exact(dev, qt):
+    rows, k = 48, 512
+    _say(f"dequant {NAMES[qt]} rows={rows} k={k}")
+    w = synth.weights(qt, rows, k, seed=11)
+    res = dev.upload_resident(w)
+    assert res is not None, dev.last_error()
+    got = dev.dequant_resident(res, zd.quant(qt), rows * k)
+    assert got is not None, dev.last_error()
+    want = oracle.dequant(qt, w, rows * k)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    dev.free_resident(res)
+
+
+SHAPES = [(64, 256), (37, 512), (333, 4096), (129, 3840), (64, 8192), (257, 12288), (40, 15360), (16, 32768)]
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("rows,k", SHAPES)
+def test_gemv_matches_oracle(dev, qt, rows, k):
+    if k % synth.BLOCK_ELEMS[qt]:
+        pytest.skip("k not a multiple of the block")
+    _say(f"gemv {NAMES[qt]} rows={rows} k={k}")
+    w = synth.weights(qt, rows, k, seed=rows * 7 + k)
+    x = synth.activation(k + 1, k)
+    want = oracle.matvec(qt, w, k, rows, x)
+    res = dev.upload_resident(w)
+    assert res is not None, dev.last_error()
+    for variant in (zd.PLAIN, zd.U4, zd.UN2):
+        out = np.full(rows, np.nan, np.float32)
+        assert dev.mat_vec_resident(res, zd.quant(qt, variant), rows, k, x, out), dev.last_error()
+        err = rel_l2(out, want)
+        assert err <= REL_L2, f"variant {variant}: rel-L2 {err:.3e}"
+    dev.free_resident(res)
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
+def test_reference_style_parity(dev, qt):
+    """The reference's expectMatVecParity / expectAxisParity inputs and tolerances."""
+    for rows, k, abs_tol in ((64, 256, 1e-4), (64, 8192, 5e-3)):
+        _say(f"reference-style {NAMES[qt]} rows={rows} k={k}")
+        w = fill_weights(qt, rows, k)
+        x = ref_x(k)
+        cpu = oracle.matvec(qt, w, k, rows, x)
+        gpu = np.zeros(rows, np.float32)
+        assert dev.mat_vec(zd.quant(qt), w, rows, k, x, gpu), dev.last_error()
+        assert_close_ref(cpu, gpu, abs_tol=abs_tol)
+        res = dev.upload_resident(w)
+        out = np.zeros(rows, np.float32)
+        assert dev.mat_vec_resident(res, zd.quant(qt), rows, k, x, out)
+        assert_close_ref(cpu, out, abs_tol=abs_tol)
+        h = dev.mat_vec_resident_burst_async(res, zd.quant(qt), rows, k, x, True)
+        assert h is not None, dev.last_error()
+        burst = np.zeros(rows, np.float32)
+        assert dev.wait_resident(h, burst, rows)
+        assert_close_ref(cpu, burst, abs_tol=abs_tol)
+        dev.free_resident(res)
+
+
+def test_async_burst_batch_agree(dev):
+    """Every resident path returns the same bits for the same inputs."""
+    qt, k = synth.Q4_0, 4096
+    shapes = [4096, 1024, 1024]  # q, k, v projections sharing x
+    ws = [synth.weights(qt, r, k, seed=100 + i) for i, r in enumerate(shapes)]
+    x = synth.activation(5, k)
+    ress = [dev.upload_resident(w) for w in ws]
+    ref = []
+    for r, res in zip(shapes, ress):
+        o = np.zeros(r, np.float32)
+        assert dev.mat_vec_resident(res, zd.quant(qt), r, k, x, o)
+        ref.append(o)
+    # plain async
+    hs = [dev.mat_vec_resident_async(res, zd.quant(qt), r, k, x) for r, res in zip(shapes, ress)]
+    assert all(h is not None for h in hs)
+    for h, r, o in zip(hs, shapes, ref):
+        got = np.zeros(r, np.float32)
+        assert dev.wait_resident(h, got, r)
+        np.testing.assert_array_equal(got, o)
+    # burst: first stages x, the rest reuse it
+    hs = [dev.mat_vec_resident_burst_async(res, zd.quant(qt), r, k, x, i == 0)
+          for i, (r, res) in enumerate(zip(shapes, ress))]
+    assert all(h is not None for h in hs)
+    for h, r, o in zip(hs, shapes, ref):
+        got = np.zeros(r, np.float32)
+        assert dev.wait_resident(h, got, r)
+        np.testing.assert_array_equal(got, o)
+    # batch: one x upload, one wait
+    outs = [np.zeros(r, np.float32) for r in shapes]
+    ops = [zd.ResidentOp(res, zd.quant(qt), r, o) for res, r, o in zip(ress, shapes, outs)]
+    assert dev.mat_vec_resident_batch(k, x, ops), dev.last_error()
+    for o, want in zip(outs, ref):
+        np.testing.assert_array_equal(o, want)
+    # oracle agreement of the q projection
+    assert rel_l2(ref[0], oracle.matvec(qt, ws[0], k, shapes[0], x)) <= REL_L2
+    for res in ress:
+        dev.free_resident(res)
+
+
+def test_ring_refuses_ninth_inflight_and_stale_handles(dev):
+    qt, rows, k = synth.Q8_0, 128, 256
+    w = synth.weights(qt, rows, k, seed=3)
+    x = synth.activation(4, k)
+    res = dev.upload_resident(w)
+    hs = [dev.mat_vec_resident_async(res, zd.quant(qt), rows, k, x) for _ in range(zd.RING_SIZE)]
+    assert all(h is not None for h in hs)
+    assert dev.mat_vec_resident_async(res, zd.quant(qt), rows, k, x) is None  # ring full
+    want = oracle.matvec(qt, w, k, rows, x)
+    out = np.zeros(rows, np.float32)
+    for h in hs:
+        assert dev.wait_resident(h, out, rows)
+        assert rel_l2(out, want) <= REL_L2
+    assert not dev.wait_resident(hs[0], out, rows)  # drained handle is stale
+    # after draining, the ring accepts again (more than 8 submits in total)
+    for _ in range(3):
+        h = dev.mat_vec_resident_async(res, zd.quant(qt), rows, k, x)
+        assert h is not None
+        assert dev.wait_resident(h, out, rows)
+    dev.free_resident(res)
+
+
+def test_burst_member_must_share_first_activation(dev):
+    qt, rows, k = synth.Q4_0, 64, 256
+    w = synth.weights(qt, rows, k, seed=8)
+    x = synth.activation(1, k)
+    other = x.copy()
+    res = dev.upload_resident(w)
+    out = np.zeros(rows, np.float32)
+    h = dev.mat_vec_resident_burst_async(res, zd.quant(qt), rows, k, x, True)
+    assert h is not None
+    assert dev.mat_vec_resident_burst_async(res, zd.quant(qt), rows, k, other, False) is None
+    h2 = dev.mat_vec_resident_burst_async(res, zd.quant(qt), rows, k, x, False)
+    assert h2 is not None
+    assert dev.wait_resident(h, out, rows) and dev.wait_resident(h2, out, rows)
+    dev.free_resident(res)
+
+
+def test_rejections_fall_back(dev):
+    """Unsupported quant or shape, short buffers: False, never a crash
+    (reference pipeline.zig:1256-1262)."""
+    rows, k = 16, 256
+    w = synth.weights(synth.Q4_0, rows, k, seed=1)
+    x = synth.activation(1, k)
+    out = np.zeros(rows, np.float32)
+    assert not dev.mat_vec(zd.quant(zd.Q4_1), np.zeros(rows * 8 * 20, np.uint8), rows, k, x, out)
+    assert not dev.mat_vec(zd.quant(zd.F32), np.zeros(rows * k * 4, np.uint8), rows, k, x, out)
+    assert not dev.mat_vec(zd.quant(zd.Q4_0), w, rows, k + 16, np.zeros(k + 16, np.float32), out)  # k % 32
+    assert not dev.mat_vec(zd.quant(zd.Q4_0), w[:-1], rows, k, x, out)  # short weight
+    assert not dev.mat_vec(zd.quant(zd.Q4_0), w, 0, k, x, out)  # rows == 0
+    assert not dev.mat_vec(zd.quant(zd.Q4_0), w, rows, k, x, np.zeros(rows - 1, np.float32))  # short out
+    assert not dev.mat_vec(zd.quant(zd.Q4_0), w, rows, k, x[:-1].copy(), out)  # x length
+    res = dev.upload_resident(w)
+    assert not dev.mat_vec_resident(res, zd.quant(zd.Q4_0), rows + 1, k, x, out)  # resident too short
+    # a resident keeps one layout: a later different quant is refused
+    assert dev.mat_vec_resident(res, zd.quant(zd.Q4_0), rows, k, x, out)
+    assert not dev.mat_vec_resident(res, zd.quant(zd.Q8_0), rows // 2, k, x, out)
+    dev.free_resident(res)
+    # ...and the device is still healthy
+    res = dev.upload_resident(w)
+    assert dev.mat_vec_resident(res, zd.quant(zd.Q4_0), rows, k, x, out)
+    dev.free_resident(res)
+
+
+def test_quantizer_bit_exact(dev):
+    _say("quantize_act_q8")
+    x = synth.activation(21, 4096 * 4)
+    x[:32] = 0.0  # an all-zero block: d = 0, inv = 0
+    x[32:64] = np.float32(127.0) * np.linspace(-1, 1, 32, dtype=np.float32)
+    got = dev.quantize_act_q8(x)
+    assert got is not None, dev.last_error()
+    want = oracle.quantize_act_q8(x)
+    np.testing.assert_array_equal(got[0], want[0])
+    np.testing.assert_array_equal(got[1].view(np.uint32), want[1].view(np.uint32))
+    np.testing.assert_array_equal(got[2], want[2])
+
+
+CONFIG_SHAPES = [
+    ("c0_q4_0", synth.Q4_0, 4096, 4096),
+    ("c1_gate_q8_0", synth.Q8_0, 12288, 4096),
+    ("c1_down_q8_0", synth.Q8_0, 4096, 12288),
+    ("c3_gate_q4_k", synth.Q4_K, 15360, 3840),
+    ("c3_down_q4_k", synth.Q4_K, 3840, 15360),
+    ("c3_gate_q6_k", synth.Q6_K, 15360, 3840),
+    ("c3_down_q6_k", synth.Q6_K, 3840, 15360),
+]
+
+
+@pytest.mark.parametrize("name,qt,rows,k", CONFIG_SHAPES, ids=[c[0] for c in CONFIG_SHAPES])
+def test_benchmark_shapes_match_oracle(dev, name, qt, rows, k):
+    """The full benchmark-config GEMVs against the oracle at their real size."""
+    _say(f"config shape {name}")
+    w = synth.weights(qt, rows, k, seed=0x5A4C4D00 + rows)
+    x = synth.activation(0x5A4C4D09, k)
+    want = oracle.matvec(qt, w, k, rows, x)
+    res = dev.upload_resident(w)
+    out = np.zeros(rows, np.float32)
+    assert dev.mat_vec_resident(res, zd.quant(qt), rows, k, x, out), dev.last_error()
+    assert rel_l2(out, want) <= REL_L2
+    dev.free_resident(res)

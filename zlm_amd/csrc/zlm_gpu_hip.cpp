@@ -1,0 +1,831 @@
+// zlm_gpu_hip.cpp -- host side of the MI355X backend: the C ABI declared in
+// include/zlm_gpu_hip.h over the HIP runtime.
+//
+// The kernels live in a gfx950 code object (zlm_kernels_gfx950.hsaco, next to
+// this library, or $ZLM_HIP_CODE_OBJECT) loaded with hipModuleLoad.  One HIP
+// stream per device carries every copy and launch in order, so a burst's
+// shared activation and a resident's layout conversion are ordered before the
+// kernels that read them without extra synchronisation.
+//
+// Contract behaviour follows the reference Vulkan device
+// (src/gpu/backend/vulkan/root.zig, pipeline.zig); the differences are
+// deliberate hardening of the invariants that device leaves implicit:
+//   * the 8-slot ring refuses a 9th in-flight submit instead of silently
+//     reusing a slot (reference pipeline.zig:1353-1355 wraps unconditionally);
+//     handles carry a generation, so a stale handle is refused by wait;
+//   * a burst member must pass the same x pointer and length as the burst's
+//     first submit (reference pipeline.zig:264-276 only documents it).
+#include "zlm_gpu_hip.h"
+
+#include <dlfcn.h>
+#include <hip/hip_runtime_api.h>
+#include <time.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+namespace {
+
+constexpr int kRing = ZLM_RING_SIZE;
+constexpr uint32_t kNoLayout = 0xffffffffu;
+
+// Supported GEMV quants and their GGUF block geometry.
+struct QuantInfo {
+    uint32_t type;
+    uint32_t block_elems;
+    uint32_t block_bytes;
+    uint32_t payload_bytes;  // bytes per block in the device layout (scale split out)
+    uint32_t scale_offset;   // offset of the f16 scale inside the raw block, or kNoLayout
+    int slot;                // index into the kernel tables
+};
+
+const QuantInfo kQuants[] = {
+    {ZLM_GGML_Q4_0, 32, 18, 16, 0, 0},
+    {ZLM_GGML_Q8_0, 32, 34, 32, 0, 1},
+    {ZLM_GGML_Q4_K, 256, 144, 144, kNoLayout, 2},
+    {ZLM_GGML_Q6_K, 256, 210, 208, 208, 3},
+};
+const char* const kQuantNames[] = {"q4_0", "q8_0", "q4_k", "q6_k"};
+
+const QuantInfo* quant_info(uint32_t quant) {
+    const uint32_t t = quant & 0xffu;
+    for (const QuantInfo& q : kQuants)
+        if (q.type == t) return &q;
+    return nullptr;
+}
+
+uint32_t variant_of(uint32_t quant) { return (quant >> 8) & 0xffu; }
+
+// x capacities of the GEMV instantiations (elements) and their waves per workgroup.
+constexpr int kKcaps[] = {4096, 8192, 16384, 32768};
+constexpr int kKcapWaves[] = {4, 4, 8, 8};
+constexpr int kNumKcap = 4;
+// Row tiles of the GEMV instantiations.
+constexpr int kRts[] = {2, 4, 8};
+constexpr int kNumRt = 3;
+
+// GpuVariant -> row tile.  The reference's variants are Vulkan spec-constant
+// axes (gpu/kernels/grid.zig:41-53); here `u4`/`u8` select the 8-row tile
+// (the reference's u4 is its 8-row group), `un2`/`un4` the 2-row tile, and
+// every other variant the default 4-row tile.
+int rt_index_for_variant(uint32_t v) {
+    switch (v) {
+    case ZLM_VARIANT_U4:
+    case ZLM_VARIANT_U8:
+        return 2;
+    case ZLM_VARIANT_UN2:
+    case ZLM_VARIANT_UN4:
+        return 0;
+    default:
+        return 1;
+    }
+}
+
+struct Slot {
+    hipEvent_t done = nullptr;
+    float* d_y = nullptr;
+    float* h_y = nullptr;
+    size_t y_cap = 0;
+    float* d_x = nullptr;
+    float* h_x = nullptr;
+    size_t x_cap = 0;
+    bool pending = false;
+    uint32_t gen = 0;
+    size_t rows = 0;
+};
+
+}  // namespace
+
+struct zlm_resident {
+    uint64_t bytes = 0;
+    uint8_t* raw = nullptr;        // device copy of the raw blocks, until converted
+    uint8_t* payload = nullptr;    // device layout payload
+    uint16_t* scales = nullptr;    // device layout scales (split quants)
+    uint32_t layout = kNoLayout;   // GGML type of the device layout
+    uint64_t blocks = 0;           // whole blocks in the layout
+    zlm_device* owner = nullptr;
+};
+
+struct zlm_device {
+    bool avail = false;
+    int ordinal = 0;
+    int cus = 0;
+    char name[256] = "off";
+    std::string err;
+
+    hipModule_t mod = nullptr;
+    hipFunction_t gemv[4][kNumKcap][kNumRt] = {};
+    int gemv_grid_cap[4][kNumKcap][kNumRt] = {};
+    hipFunction_t repack = nullptr;
+    hipFunction_t dequant[4] = {};
+    hipFunction_t quantize_q8 = nullptr;
+    hipStream_t stream = nullptr;
+
+    Slot slots[kRing];
+    int next_slot = 0;
+
+    // synchronous-op staging
+    float* d_x = nullptr;
+    float* h_x = nullptr;
+    size_t x_cap = 0;
+    float* d_y = nullptr;
+    float* h_y = nullptr;
+    size_t y_cap = 0;
+    uint8_t* s_raw = nullptr;  // streamed-weight staging (raw blocks)
+    uint64_t s_raw_cap = 0;
+    uint8_t* s_lay = nullptr;  // streamed-weight staging (device layout)
+    uint64_t s_lay_cap = 0;
+
+    // burst-shared activation
+    float* d_bx = nullptr;
+    float* h_bx = nullptr;
+    size_t bx_cap = 0;
+    hipEvent_t bx_copied = nullptr;
+    const float* burst_src = nullptr;
+    size_t burst_len = 0;
+    bool burst_open = false;
+};
+
+namespace {
+
+bool fail(zlm_device* d, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (d) d->err = buf;
+    return false;
+}
+
+bool ok(zlm_device* d, hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    return fail(d, "%s: %s", what, hipGetErrorString(e));
+}
+
+std::string code_object_path() {
+    if (const char* env = getenv("ZLM_HIP_CODE_OBJECT")) return env;
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&zlm_gpu_init), &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t slash = p.rfind('/');
+        std::string dir = (slash == std::string::npos) ? "." : p.substr(0, slash);
+        return dir + "/zlm_kernels_gfx950.hsaco";
+    }
+    return "zlm_kernels_gfx950.hsaco";
+}
+
+bool load_kernels(zlm_device* d) {
+    const std::string path = code_object_path();
+    if (!ok(d, hipModuleLoad(&d->mod, path.c_str()), path.c_str())) return false;
+    char nm[128];
+    for (int q = 0; q < 4; q++) {
+        for (int kc = 0; kc < kNumKcap; kc++) {
+            for (int ri = 0; ri < kNumRt; ri++) {
+                snprintf(nm, sizeof nm, "zlm_gemv_%s_k%d_w%d_r%d", kQuantNames[q], kKcaps[kc], kKcapWaves[kc],
+                         kRts[ri]);
+                if (!ok(d, hipModuleGetFunction(&d->gemv[q][kc][ri], d->mod, nm), nm)) return false;
+                int per_cu = 0;
+                if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, d->gemv[q][kc][ri],
+                                                                       kKcapWaves[kc] * 64, 0) != hipSuccess ||
+                    per_cu < 1)
+                    per_cu = 1;
+                d->gemv_grid_cap[q][kc][ri] = per_cu * d->cus;
+            }
+        }
+        snprintf(nm, sizeof nm, "zlm_dequant_%s", kQuantNames[q]);
+        if (!ok(d, hipModuleGetFunction(&d->dequant[q], d->mod, nm), nm)) return false;
+    }
+    if (!ok(d, hipModuleGetFunction(&d->repack, d->mod, "zlm_repack_split"), "zlm_repack_split")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->quantize_q8, d->mod, "zlm_quantize_q8"), "zlm_quantize_q8")) return false;
+    return true;
+}
+
+// A device buffer and a pinned host buffer of `n` floats sharing one capacity.
+bool ensure_pair(zlm_device* d, float*& dev, float*& host, size_t& cap, size_t n) {
+    if (cap >= n && dev && host) return true;
+    if (dev) hipFree(dev);
+    if (host) hipHostFree(host);
+    dev = nullptr;
+    host = nullptr;
+    cap = 0;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&dev), n * sizeof(float)), "hipMalloc")) return false;
+    if (!ok(d, hipHostMalloc(reinterpret_cast<void**>(&host), n * sizeof(float), hipHostMallocDefault),
+            "hipHostMalloc")) {
+        hipFree(dev);
+        dev = nullptr;
+        return false;
+    }
+    cap = n;
+    return true;
+}
+
+bool ensure_bytes(zlm_device* d, uint8_t*& p, uint64_t& cap, uint64_t n) {
+    if (cap >= n && p) return true;
+    if (p) {
+        hipStreamSynchronize(d->stream);
+        hipFree(p);
+    }
+    p = nullptr;
+    cap = 0;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&p), n ? n : 1), "hipMalloc")) return false;
+    cap = n;
+    return true;
+}
+
+bool launch(zlm_device* d, hipFunction_t f, unsigned grid, unsigned block, void** args, const char* what) {
+    return ok(d, hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, d->stream, args, nullptr), what);
+}
+
+// Bytes of the device layout of `nblk` blocks: payload rounded to 256 B, then scales.
+uint64_t layout_bytes(const QuantInfo* qi, uint64_t nblk) {
+    const uint64_t p = (nblk * qi->payload_bytes + 255) & ~static_cast<uint64_t>(255);
+    return p + nblk * 2 + 256;
+}
+
+// Enqueue the raw -> device-layout conversion of `nblk` blocks into `dst`.
+bool convert_blocks(zlm_device* d, const uint8_t* raw, uint64_t nblk, const QuantInfo* qi, uint8_t* dst,
+                    uint16_t** scales_out) {
+    const uint64_t p = (nblk * qi->payload_bytes + 255) & ~static_cast<uint64_t>(255);
+    uint16_t* scales = reinterpret_cast<uint16_t*>(dst + p);
+    *scales_out = scales;
+    if (nblk == 0) return true;
+    uint32_t bb = qi->block_bytes, so = qi->scale_offset;
+    uint64_t n = nblk;
+    void* args[] = {&raw, &dst, &scales, &n, &bb, &so};
+    return launch(d, d->repack, static_cast<unsigned>((nblk + 255) / 256), 256, args, "repack");
+}
+
+// Convert a resident's raw blocks into the device layout of `qi` (once; the
+// raw copy is released).  A resident keeps one layout for its lifetime.
+bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
+    if (r->layout == qi->type) return true;
+    if (r->layout != kNoLayout) return fail(d, "resident already holds a type-%u layout", r->layout);
+    if (!r->raw) return fail(d, "resident has no raw bytes");
+    const uint64_t nblk = r->bytes / qi->block_bytes;
+    if (qi->scale_offset == kNoLayout) {  // q4_k: the raw blocks are the layout
+        r->payload = r->raw;
+        r->raw = nullptr;
+        r->scales = nullptr;
+    } else {
+        uint8_t* dst = nullptr;
+        if (!ok(d, hipMalloc(reinterpret_cast<void**>(&dst), layout_bytes(qi, nblk)), "hipMalloc layout"))
+            return false;
+        uint16_t* scales = nullptr;
+        if (!convert_blocks(d, r->raw, nblk, qi, dst, &scales)) {
+            hipFree(dst);
+            return false;
+        }
+        hipStreamSynchronize(d->stream);
+        hipFree(r->raw);
+        r->raw = nullptr;
+        r->payload = dst;
+        r->scales = scales;
+    }
+    r->layout = qi->type;
+    r->blocks = nblk;
+    return true;
+}
+
+// Validate a GEMV over resident `r` and pick its kernel.
+bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, hipFunction_t* f,
+                  unsigned* grid, unsigned* block) {
+    if (!d || !d->avail) return fail(d, "device unavailable");
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
+    if (!r) return fail(d, "null resident");
+    if (rows == 0 || k == 0 || k % qi->block_elems != 0) return fail(d, "bad shape rows=%zu k=%zu", rows, k);
+    if (rows > 0xffffffffu) return fail(d, "rows too large");
+    int kc = -1;
+    for (int i = 0; i < kNumKcap; i++)
+        if (static_cast<int>(k) <= kKcaps[i]) {
+            kc = i;
+            break;
+        }
+    if (kc < 0) return fail(d, "k=%zu exceeds the LDS-staged activation capacity", k);
+    const uint64_t nb = k / qi->block_elems;
+    if (r->bytes < rows * nb * qi->block_bytes) return fail(d, "resident too short");
+    if (!ensure_layout(d, r, qi)) return false;
+    if (r->blocks < rows * nb) return fail(d, "resident layout too short");
+    const int ri = rt_index_for_variant(variant_of(quant));
+    *f = d->gemv[qi->slot][kc][ri];
+    const uint64_t tiles = (rows + kRts[ri] - 1) / kRts[ri];
+    const uint64_t wgs = (tiles + kKcapWaves[kc] - 1) / kKcapWaves[kc];
+    *grid = static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->gemv_grid_cap[qi->slot][kc][ri])));
+    *block = static_cast<unsigned>(kKcapWaves[kc] * 64);
+    return true;
+}
+
+bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, const float* x_dev,
+                  float* y_dev) {
+    hipFunction_t f;
+    unsigned grid, block;
+    if (!prepare_gemv(d, r, quant, rows, k, &f, &grid, &block)) return false;
+    const QuantInfo* qi = quant_info(quant);
+    const uint8_t* w = r->payload;
+    const uint16_t* s = r->scales;
+    uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->block_elems);
+    void* args[] = {&w, &s, &x_dev, &y_dev, &rows32, &nb};
+    return launch(d, f, grid, block, args, "gemv");
+}
+
+zlm_resident* new_resident(zlm_device* d, const void* bytes, size_t len) {
+    zlm_resident* r = new (std::nothrow) zlm_resident();
+    if (!r) return nullptr;
+    r->owner = d;
+    r->bytes = len;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&r->raw), len ? len : 1), "hipMalloc resident")) {
+        delete r;
+        return nullptr;
+    }
+    if (len && !ok(d, hipMemcpy(r->raw, bytes, len, hipMemcpyHostToDevice), "upload resident")) {
+        hipFree(r->raw);
+        delete r;
+        return nullptr;
+    }
+    return r;
+}
+
+void release_resident_memory(zlm_resident* r) {
+    if (r->raw) hipFree(r->raw);
+    if (r->payload) hipFree(r->payload);
+    r->raw = nullptr;
+    r->payload = nullptr;
+    r->scales = nullptr;
+    r->layout = kNoLayout;
+    r->blocks = 0;
+}
+
+// Stage host x into the synchronous-op device buffer.
+bool stage_x_sync(zlm_device* d, const float* x, size_t n) {
+    if (!ensure_pair(d, d->d_x, d->h_x, d->x_cap, n)) return false;
+    memcpy(d->h_x, x, n * sizeof(float));
+    return ok(d, hipMemcpyAsync(d->d_x, d->h_x, n * sizeof(float), hipMemcpyHostToDevice, d->stream), "stage x");
+}
+
+bool finish_sync(zlm_device* d, float* out, size_t n) {
+    if (!ok(d, hipMemcpyAsync(d->h_y, d->d_y, n * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y"))
+        return false;
+    if (!ok(d, hipStreamSynchronize(d->stream), "sync")) return false;
+    memcpy(out, d->h_y, n * sizeof(float));
+    return true;
+}
+
+int find_free_slot(zlm_device* d) {
+    for (int i = 0; i < kRing; i++) {
+        const int s = (d->next_slot + i) % kRing;
+        if (!d->slots[s].pending) return s;
+    }
+    return -1;
+}
+
+int32_t make_handle(zlm_device* d, int s) {
+    Slot& sl = d->slots[s];
+    sl.gen = (sl.gen + 1) & 0x0fffffffu;
+    sl.pending = true;
+    d->next_slot = (s + 1) % kRing;
+    return static_cast<int32_t>((sl.gen << 3) | static_cast<uint32_t>(s));
+}
+
+// Launch a resident GEMV reading device x into slot `s`, then queue the read-back.
+bool submit_into_slot(zlm_device* d, int s, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
+                      const float* x_dev) {
+    Slot& sl = d->slots[s];
+    size_t ycap = sl.y_cap;
+    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows)) return false;
+    sl.y_cap = ycap;
+    if (!sl.done && !ok(d, hipEventCreateWithFlags(&sl.done, hipEventDisableTiming), "event")) return false;
+    if (!enqueue_gemv(d, r, quant, rows, k, x_dev, sl.d_y)) return false;
+    if (!ok(d, hipMemcpyAsync(sl.h_y, sl.d_y, rows * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y"))
+        return false;
+    if (!ok(d, hipEventRecord(sl.done, d->stream), "record")) return false;
+    sl.rows = rows;
+    return true;
+}
+
+double now_ns() {
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return static_cast<double>(ts.tv_sec) * 1e9 + static_cast<double>(ts.tv_nsec);
+}
+
+}  // namespace
+
+// ======================= the backend contract =======================
+
+extern "C" zlm_device* zlm_gpu_init(void) {
+    zlm_device* d = new (std::nothrow) zlm_device();
+    if (!d) return nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+        fail(d, "no HIP device");
+        return d;
+    }
+    if (hipSetDevice(0) != hipSuccess) {
+        fail(d, "hipSetDevice failed");
+        return d;
+    }
+    hipDeviceProp_t props;
+    if (hipGetDeviceProperties(&props, 0) != hipSuccess) {
+        fail(d, "hipGetDeviceProperties failed");
+        return d;
+    }
+    if (strncmp(props.gcnArchName, "gfx950", 6) != 0) {
+        fail(d, "device %s is not gfx950", props.gcnArchName);
+        return d;
+    }
+    d->cus = props.multiProcessorCount;
+    snprintf(d->name, sizeof d->name, "%s (%s)", props.name, props.gcnArchName);
+    if (hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess) {
+        fail(d, "hipStreamCreate failed");
+        snprintf(d->name, sizeof d->name, "off");
+        return d;
+    }
+    if (!load_kernels(d)) {
+        std::string why = d->err;
+        if (d->mod) hipModuleUnload(d->mod);
+        d->mod = nullptr;
+        hipStreamDestroy(d->stream);
+        d->stream = nullptr;
+        snprintf(d->name, sizeof d->name, "off");
+        d->err = why;
+        return d;
+    }
+    d->avail = true;
+    d->err.clear();
+    return d;
+}
+
+extern "C" void zlm_gpu_deinit(zlm_device* d) {
+    if (!d) return;
+    if (d->avail) {
+        hipStreamSynchronize(d->stream);
+        for (Slot& s : d->slots) {
+            if (s.done) hipEventDestroy(s.done);
+            if (s.d_y) hipFree(s.d_y);
+            if (s.h_y) hipHostFree(s.h_y);
+            if (s.d_x) hipFree(s.d_x);
+            if (s.h_x) hipHostFree(s.h_x);
+        }
+        if (d->d_x) hipFree(d->d_x);
+        if (d->h_x) hipHostFree(d->h_x);
+        if (d->d_y) hipFree(d->d_y);
+        if (d->h_y) hipHostFree(d->h_y);
+        if (d->d_bx) hipFree(d->d_bx);
+        if (d->h_bx) hipHostFree(d->h_bx);
+        if (d->bx_copied) hipEventDestroy(d->bx_copied);
+        if (d->s_raw) hipFree(d->s_raw);
+        if (d->s_lay) hipFree(d->s_lay);
+        if (d->mod) hipModuleUnload(d->mod);
+        hipStreamDestroy(d->stream);
+    }
+    delete d;
+}
+
+extern "C" bool zlm_gpu_available(const zlm_device* d) { return d && d->avail; }
+
+extern "C" const char* zlm_gpu_backend_name(const zlm_device* d) { return (d && d->avail) ? "hip" : "off"; }
+
+extern "C" const char* zlm_gpu_device_name(const zlm_device* d) { return (d && d->avail) ? d->name : "off"; }
+
+extern "C" bool zlm_gpu_is_uma(const zlm_device*) { return false; }
+
+extern "C" zlm_resident* zlm_gpu_upload_resident(zlm_device* d, const void* bytes, size_t len) {
+    if (!d || !d->avail) return nullptr;
+    if (!bytes && len) return nullptr;
+    return new_resident(d, bytes, len);
+}
+
+extern "C" void zlm_gpu_free_resident(zlm_device* d, zlm_resident* r) {
+    if (!r) return;
+    if (d && d->avail) hipStreamSynchronize(d->stream);
+    release_resident_memory(r);
+    delete r;
+}
+
+extern "C" uint64_t zlm_gpu_resident_bytes(const zlm_resident* r) { return r ? r->bytes : 0; }
+
+extern "C" bool zlm_gpu_mat_vec_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
+                                         const float* x, size_t x_len, float* out, size_t out_len) {
+    if (!d || !d->avail) return false;
+    if (!x || !out || x_len != k || out_len < rows) return fail(d, "bad buffers");
+    hipFunction_t f;
+    unsigned g, b;
+    if (!prepare_gemv(d, r, quant, rows, k, &f, &g, &b)) return false;
+    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, rows)) return false;
+    if (!stage_x_sync(d, x, k)) return false;
+    if (!enqueue_gemv(d, r, quant, rows, k, d->d_x, d->d_y)) return false;
+    return finish_sync(d, out, rows);
+}
+
+extern "C" bool zlm_gpu_mat_vec(zlm_device* d, uint32_t quant, const void* w, size_t w_len, size_t rows, size_t k,
+                                const float* x, size_t x_len, float* out, size_t out_len) {
+    if (!d || !d->avail) return false;
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
+    if (!w || !x || !out || x_len != k || out_len < rows) return fail(d, "bad buffers");
+    if (rows == 0 || k == 0 || k % qi->block_elems != 0) return fail(d, "bad shape");
+    const uint64_t nblk = static_cast<uint64_t>(rows) * (k / qi->block_elems);
+    const uint64_t need = nblk * qi->block_bytes;
+    if (w_len < need) return fail(d, "weight too short");
+    // Stage the raw blocks, convert them into the reusable layout buffer and
+    // run the resident GEMV over a transient view of it.
+    if (!ensure_bytes(d, d->s_raw, d->s_raw_cap, need)) return false;
+    if (!ok(d, hipMemcpyAsync(d->s_raw, w, need, hipMemcpyHostToDevice, d->stream), "stage weights")) return false;
+    zlm_resident view;
+    view.owner = d;
+    view.bytes = need;
+    view.layout = qi->type;
+    view.blocks = nblk;
+    if (qi->scale_offset == kNoLayout) {
+        view.payload = d->s_raw;
+    } else {
+        if (!ensure_bytes(d, d->s_lay, d->s_lay_cap, layout_bytes(qi, nblk))) return false;
+        if (!convert_blocks(d, d->s_raw, nblk, qi, d->s_lay, &view.scales)) return false;
+        view.payload = d->s_lay;
+    }
+    const bool ran = zlm_gpu_mat_vec_resident(d, &view, quant, rows, k, x, x_len, out, out_len);
+    view.payload = nullptr;  // the staging buffers stay owned by the device
+    view.scales = nullptr;
+    return ran;
+}
+
+extern "C" int32_t zlm_gpu_mat_vec_resident_async(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows,
+                                                  size_t k, const float* x, size_t x_len) {
+    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
+    hipFunction_t f;
+    unsigned g, b;
+    if (!prepare_gemv(d, r, quant, rows, k, &f, &g, &b)) return ZLM_NULL_HANDLE;
+    const int s = find_free_slot(d);
+    if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
+    Slot& sl = d->slots[s];
+    size_t xcap = sl.x_cap;
+    if (!ensure_pair(d, sl.d_x, sl.h_x, xcap, k)) return ZLM_NULL_HANDLE;
+    sl.x_cap = xcap;
+    memcpy(sl.h_x, x, k * sizeof(float));
+    if (!ok(d, hipMemcpyAsync(sl.d_x, sl.h_x, k * sizeof(float), hipMemcpyHostToDevice, d->stream), "stage x"))
+        return ZLM_NULL_HANDLE;
+    if (!submit_into_slot(d, s, r, quant, rows, k, sl.d_x)) return ZLM_NULL_HANDLE;
+    return make_handle(d, s);
+}
+
+extern "C" int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device* d, zlm_resident* r, uint32_t quant,
+                                                        size_t rows, size_t k, const float* x, size_t x_len,
+                                                        bool first) {
+    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
+    hipFunction_t f;
+    unsigned g, b;
+    if (!prepare_gemv(d, r, quant, rows, k, &f, &g, &b)) return ZLM_NULL_HANDLE;
+    const int s = find_free_slot(d);
+    if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
+    if (first) {
+        // The previous burst's host->device copy must have consumed the pinned
+        // buffer before it is overwritten.
+        if (d->bx_copied && !ok(d, hipEventSynchronize(d->bx_copied), "burst wait")) return ZLM_NULL_HANDLE;
+        if (!ensure_pair(d, d->d_bx, d->h_bx, d->bx_cap, k)) return ZLM_NULL_HANDLE;
+        if (!d->bx_copied && !ok(d, hipEventCreateWithFlags(&d->bx_copied, hipEventDisableTiming), "event"))
+            return ZLM_NULL_HANDLE;
+        memcpy(d->h_bx, x, k * sizeof(float));
+        if (!ok(d, hipMemcpyAsync(d->d_bx, d->h_bx, k * sizeof(float), hipMemcpyHostToDevice, d->stream),
+                "stage burst x") ||
+            !ok(d, hipEventRecord(d->bx_copied, d->stream), "record")) {
+            d->burst_open = false;
+            return ZLM_NULL_HANDLE;
+        }
+        d->burst_src = x;
+        d->burst_len = k;
+        d->burst_open = true;
+    } else if (!d->burst_open || x != d->burst_src || x_len != d->burst_len) {
+        return fail(d, "burst member does not match the burst's activation"), ZLM_NULL_HANDLE;
+    }
+    if (!submit_into_slot(d, s, r, quant, rows, k, d->d_bx)) return ZLM_NULL_HANDLE;
+    return make_handle(d, s);
+}
+
+extern "C" bool zlm_gpu_wait_resident(zlm_device* d, int32_t h, float* out, size_t out_len, size_t rows) {
+    if (!d || !d->avail || h < 0) return false;
+    const int s = h & (kRing - 1);
+    const uint32_t gen = static_cast<uint32_t>(h) >> 3;
+    Slot& sl = d->slots[s];
+    if (!sl.pending || sl.gen != gen) return fail(d, "stale or unknown handle %d", h);
+    if (!out || out_len < rows || rows > sl.rows) return fail(d, "bad output buffer");
+    if (!ok(d, hipEventSynchronize(sl.done), "wait")) return false;
+    memcpy(out, sl.h_y, rows * sizeof(float));
+    sl.pending = false;
+    return true;
+}
+
+extern "C" bool zlm_gpu_mat_vec_resident_batch(zlm_device* d, size_t k, const float* x, size_t x_len,
+                                               const zlm_resident_op* ops, size_t n) {
+    if (!d || !d->avail) return false;
+    if (!ops || n == 0 || n > kRing || !x || x_len != k) return fail(d, "bad batch");
+    size_t total = 0;
+    for (size_t i = 0; i < n; i++) {
+        hipFunction_t f;
+        unsigned g, b;
+        if (ops[i].rows == 0 || !ops[i].out || ops[i].out_len < ops[i].rows) return fail(d, "bad batch op %zu", i);
+        if (!prepare_gemv(d, ops[i].res, ops[i].quant, ops[i].rows, k, &f, &g, &b)) return false;
+        total += ops[i].rows;
+    }
+    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, total)) return false;
+    if (!stage_x_sync(d, x, k)) return false;
+    size_t off = 0;
+    for (size_t i = 0; i < n; i++) {
+        if (!enqueue_gemv(d, ops[i].res, ops[i].quant, ops[i].rows, k, d->d_x, d->d_y + off)) {
+            hipStreamSynchronize(d->stream);
+            return false;
+        }
+        off += ops[i].rows;
+    }
+    if (!ok(d, hipMemcpyAsync(d->h_y, d->d_y, total * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y") ||
+        !ok(d, hipStreamSynchronize(d->stream), "sync"))
+        return false;
+    off = 0;
+    for (size_t i = 0; i < n; i++) {
+        memcpy(ops[i].out, d->h_y + off, ops[i].rows * sizeof(float));
+        off += ops[i].rows;
+    }
+    return true;
+}
+
+extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void*, size_t, size_t, size_t, size_t,
+                                      const float*, size_t, float*, size_t) {
+    if (!d || !d->avail) return false;
+    return fail(d, "matMulBatch: quant %u has no GEMM kernel yet", quant & 0xffu);
+}
+
+extern "C" bool zlm_gpu_mat_mul_resident(zlm_device* d, zlm_resident*, uint32_t quant, size_t, size_t, size_t,
+                                         const float*, size_t, float*, size_t) {
+    if (!d || !d->avail) return false;
+    return fail(d, "matMulResident: quant %u has no GEMM kernel yet", quant & 0xffu);
+}
+
+extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, zlm_resident*, zlm_resident*,
+                                                                uint32_t, size_t, size_t, const float*, size_t,
+                                                                uint32_t, uint32_t, bool) {
+    if (d && d->avail) fail(d, "fused gate_up not built");
+    return ZLM_NULL_HANDLE;
+}
+
+extern "C" int32_t zlm_gpu_mat_vec_mlp_resident_burst_async(zlm_device* d, zlm_resident*, zlm_resident*,
+                                                            zlm_resident*, uint32_t, size_t, size_t, size_t,
+                                                            const float*, size_t, uint32_t, uint32_t, bool) {
+    if (d && d->avail) fail(d, "fused mlp not built");
+    return ZLM_NULL_HANDLE;
+}
+
+extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, zlm_resident*, zlm_resident*,
+                                                                 zlm_resident*, uint32_t, uint32_t, size_t,
+                                                                 size_t, size_t, const float*, size_t, uint32_t,
+                                                                 uint32_t, bool) {
+    if (d && d->avail) fail(d, "mlp pair not built");
+    return ZLM_NULL_HANDLE;
+}
+
+extern "C" void zlm_gpu_sync(zlm_device* d) {
+    if (d && d->avail) hipStreamSynchronize(d->stream);
+}
+
+extern "C" void zlm_gpu_probe(zlm_device* d, size_t, size_t, size_t, zlm_probe* out) {
+    if (out) memset(out, 0, sizeof *out);
+    (void)d;
+}
+
+// ======================= device-level entry points =======================
+
+extern "C" const char* zlm_gpu_last_error(const zlm_device* d) { return d ? d->err.c_str() : "null device"; }
+
+extern "C" int zlm_gpu_cu_count(const zlm_device* d) { return (d && d->avail) ? d->cus : 0; }
+
+extern "C" void* zlm_gpu_dev_malloc(zlm_device* d, size_t bytes) {
+    if (!d || !d->avail) return nullptr;
+    void* p = nullptr;
+    if (!ok(d, hipMalloc(&p, bytes ? bytes : 1), "hipMalloc")) return nullptr;
+    return p;
+}
+
+extern "C" void zlm_gpu_dev_free(zlm_device* d, void* p) {
+    if (!d || !d->avail || !p) return;
+    hipStreamSynchronize(d->stream);
+    hipFree(p);
+}
+
+extern "C" bool zlm_gpu_dev_upload(zlm_device* d, void* dst, const void* src, size_t n) {
+    if (!d || !d->avail) return false;
+    if (!ok(d, hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, d->stream), "upload")) return false;
+    return ok(d, hipStreamSynchronize(d->stream), "sync");
+}
+
+extern "C" bool zlm_gpu_dev_download(zlm_device* d, void* dst, const void* src, size_t n) {
+    if (!d || !d->avail) return false;
+    if (!ok(d, hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, d->stream), "download")) return false;
+    return ok(d, hipStreamSynchronize(d->stream), "sync");
+}
+
+extern "C" bool zlm_gpu_mat_vec_enqueue(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
+                                        const float* x_dev, float* y_dev) {
+    if (!d || !d->avail) return false;
+    return enqueue_gemv(d, r, quant, rows, k, x_dev, y_dev);
+}
+
+extern "C" bool zlm_gpu_time_mat_vec(zlm_device* d, zlm_resident* const* res, size_t n_res, uint32_t quant,
+                                     size_t rows, size_t k, const float* x_dev, float* y_dev, int iters,
+                                     double* ms) {
+    if (!d || !d->avail || !res || n_res == 0 || iters < 1 || !ms) return false;
+    for (size_t i = 0; i < n_res; i++) {  // converts layouts outside the timed region
+        hipFunction_t f;
+        unsigned g, b;
+        if (!prepare_gemv(d, res[i], quant, rows, k, &f, &g, &b)) return false;
+    }
+    hipEvent_t e0, e1;
+    if (!ok(d, hipEventCreate(&e0), "event") || !ok(d, hipEventCreate(&e1), "event")) return false;
+    bool good = ok(d, hipEventRecord(e0, d->stream), "record");
+    for (int i = 0; good && i < iters; i++) good = enqueue_gemv(d, res[i % n_res], quant, rows, k, x_dev, y_dev);
+    good = good && ok(d, hipEventRecord(e1, d->stream), "record") && ok(d, hipEventSynchronize(e1), "sync");
+    float t = 0.0f;
+    good = good && ok(d, hipEventElapsedTime(&t, e0, e1), "elapsed");
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    *ms = t;
+    return good;
+}
+
+extern "C" bool zlm_gpu_time_gemv_sequence(zlm_device* d, const zlm_gemv_desc* descs, size_t n, int iters,
+                                           double* ms) {
+    if (!d || !d->avail || !descs || n == 0 || iters < 1 || !ms) return false;
+    for (size_t i = 0; i < n; i++) {  // converts layouts outside the timed region
+        hipFunction_t f;
+        unsigned g, b;
+        if (!prepare_gemv(d, descs[i].res, descs[i].quant, descs[i].rows, descs[i].k, &f, &g, &b)) return false;
+    }
+    hipEvent_t e0, e1;
+    if (!ok(d, hipEventCreate(&e0), "event")) return false;
+    if (!ok(d, hipEventCreate(&e1), "event")) {
+        hipEventDestroy(e0);
+        return false;
+    }
+    bool good = ok(d, hipEventRecord(e0, d->stream), "record");
+    for (int it = 0; good && it < iters; it++)
+        for (size_t i = 0; good && i < n; i++)
+            good = enqueue_gemv(d, descs[i].res, descs[i].quant, descs[i].rows, descs[i].k, descs[i].x_dev,
+                                descs[i].y_dev);
+    good = good && ok(d, hipEventRecord(e1, d->stream), "record") && ok(d, hipEventSynchronize(e1), "sync");
+    float t = 0.0f;
+    good = good && ok(d, hipEventElapsedTime(&t, e0, e1), "elapsed");
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    *ms = t;
+    return good;
+}
+
+extern "C" bool zlm_gpu_dequant_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t n, float* out) {
+    if (!d || !d->avail || !r || !out) return false;
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant");
+    if (n % qi->block_elems) return fail(d, "n must be whole blocks");
+    const uint64_t nblk = n / qi->block_elems;
+    if (r->bytes < nblk * qi->block_bytes) return fail(d, "resident too short");
+    if (!ensure_layout(d, r, qi)) return false;
+    float* dev_out = nullptr;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&dev_out), (n ? n : 1) * sizeof(float)), "hipMalloc")) return false;
+    bool good = true;
+    if (nblk) {
+        uint64_t nb = nblk;
+        void* args[] = {&r->payload, &r->scales, &dev_out, &nb};
+        good = launch(d, d->dequant[qi->slot], static_cast<unsigned>((nblk + 255) / 256), 256, args, "dequant");
+    }
+    good = good && ok(d, hipMemcpyAsync(out, dev_out, n * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read") &&
+           ok(d, hipStreamSynchronize(d->stream), "sync");
+    hipFree(dev_out);
+    return good;
+}
+
+extern "C" bool zlm_gpu_quantize_act_q8(zlm_device* d, const float* x, size_t n, int8_t* qx, float* dx,
+                                        int32_t* sums) {
+    if (!d || !d->avail || !x || !qx || !dx || !sums || n % 32) return false;
+    const size_t nblk = n / 32;
+    if (nblk == 0) return true;
+    char* buf = nullptr;
+    const size_t xb = n * 4, qb = (n + 15) & ~size_t(15), db = nblk * 4;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&buf), xb + qb + 2 * db + 64), "hipMalloc")) return false;
+    float* dxx = reinterpret_cast<float*>(buf);
+    int8_t* dq = reinterpret_cast<int8_t*>(buf + xb);
+    float* ddx = reinterpret_cast<float*>(buf + xb + qb);
+    int32_t* ds = reinterpret_cast<int32_t*>(buf + xb + qb + db);
+    uint64_t nb = nblk;
+    void* args[] = {&dxx, &dq, &ddx, &ds, &nb};
+    bool good = ok(d, hipMemcpyAsync(dxx, x, xb, hipMemcpyHostToDevice, d->stream), "upload") &&
+                launch(d, d->quantize_q8, static_cast<unsigned>((nblk + 255) / 256), 256, args, "quantize") &&
+                ok(d, hipMemcpyAsync(qx, dq, n, hipMemcpyDeviceToHost, d->stream), "read qx") &&
+                ok(d, hipMemcpyAsync(dx, ddx, db, hipMemcpyDeviceToHost, d->stream), "read dx") &&
+                ok(d, hipMemcpyAsync(sums, ds, db, hipMemcpyDeviceToHost, d->stream), "read sums") &&
+                ok(d, hipStreamSynchronize(d->stream), "sync");
+    hipFree(buf);
+    return good;
+}

@@ -1,0 +1,394 @@
+"""Python mirror of zlm's GPU ``Device`` over the HIP backend's C ABI.
+
+The method names are the reference contract's ops in snake_case
+(reference ``src/gpu/backend/root.zig:299-311``), with the same argument
+meaning and the same failure convention: an op that did not run on the device
+returns ``False`` (or ``None`` for a handle/resident) and the caller runs the
+CPU kernel.  ``Device()`` never raises for a missing GPU; it is then inert
+(``available() is False``).  A missing *library*, however, is an installation
+error and raises immediately.
+
+Buffers are numpy arrays: weights ``uint8`` (raw GGUF blocks), activations and
+outputs ``float32``, all C-contiguous.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass, field
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(_HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libzlm_gpu_hip.so")
+CODE_OBJECT_PATH = os.path.join(LIB_DIR, "zlm_kernels_gfx950.hsaco")
+
+RING_SIZE = 8
+NULL_HANDLE = -1
+
+# GGML type codes (reference gguf/format.zig:41-77).
+F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 30
+# GpuVariant codes (reference gpu/kernels/grid.zig:14).
+PLAIN, U4, U8, SUB, UN2, UN4, W32, W128 = range(8)
+VARIANT_NAMES = ("plain", "u4", "u8", "sub", "un2", "un4", "w32", "w128")
+# GateUpAct (reference gpu/backend/root.zig:225).
+SILU, GELU = 0, 1
+
+
+def quant(ggml_type: int, variant: int = PLAIN) -> int:
+    """The C ABI's quant code: GGML type in bits 0..7, GpuVariant in 8..15."""
+    return (ggml_type & 0xFF) | ((variant & 0xFF) << 8)
+
+
+class _ResidentOp(ctypes.Structure):
+    _fields_ = [
+        ("res", ctypes.c_void_p),
+        ("quant", ctypes.c_uint32),
+        ("rows", ctypes.c_size_t),
+        ("out", ctypes.c_void_p),
+        ("out_len", ctypes.c_size_t),
+    ]
+
+
+class _GemvDesc(ctypes.Structure):
+    _fields_ = [
+        ("res", ctypes.c_void_p),
+        ("quant", ctypes.c_uint32),
+        ("rows", ctypes.c_size_t),
+        ("k", ctypes.c_size_t),
+        ("x_dev", ctypes.c_void_p),
+        ("y_dev", ctypes.c_void_p),
+    ]
+
+
+class _Probe(ctypes.Structure):
+    _fields_ = [
+        ("gemv_gbps", ctypes.c_double),
+        ("gemv_streamed_gbps", ctypes.c_double),
+        ("matmul_gbps", ctypes.c_double),
+        ("q4_0_variant", ctypes.c_uint8),
+        ("q4_1_variant", ctypes.c_uint8),
+        ("q8_0_variant", ctypes.c_uint8),
+        ("q6_k_variant", ctypes.c_uint8),
+        ("q4_k_variant", ctypes.c_uint8),
+        ("f32_variant", ctypes.c_uint8),
+        ("f16_variant", ctypes.c_uint8),
+        ("bf16_variant", ctypes.c_uint8),
+        ("gate_up_variant", ctypes.c_uint8),
+        ("gate_up_q4_1_variant", ctypes.c_uint8),
+        ("gate_up_q8_0_variant", ctypes.c_uint8),
+        ("q4_0_u4_gbps", ctypes.c_double),
+        ("q4_0_sub_gbps", ctypes.c_double),
+        ("q4_0_un2_gbps", ctypes.c_double),
+        ("q4_0_un4_gbps", ctypes.c_double),
+        ("q4_0_w32_gbps", ctypes.c_double),
+        ("q4_0_w128_gbps", ctypes.c_double),
+        ("q4_k_gbps", ctypes.c_double),
+        ("q4_k_u4_gbps", ctypes.c_double),
+        ("gate_up_gbps", ctypes.c_double),
+        ("gate_up_u4_gbps", ctypes.c_double),
+    ]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded C-ABI library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"HIP backend library missing: {LIB_PATH} (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    P, S, B, U, I32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_bool, ctypes.c_uint32, ctypes.c_int32
+    sig = {
+        "zlm_gpu_init": (P, []),
+        "zlm_gpu_deinit": (None, [P]),
+        "zlm_gpu_available": (B, [P]),
+        "zlm_gpu_backend_name": (ctypes.c_char_p, [P]),
+        "zlm_gpu_device_name": (ctypes.c_char_p, [P]),
+        "zlm_gpu_is_uma": (B, [P]),
+        "zlm_gpu_mat_vec": (B, [P, U, P, S, S, S, P, S, P, S]),
+        "zlm_gpu_mat_mul_batch": (B, [P, U, P, S, S, S, S, P, S, P, S]),
+        "zlm_gpu_mat_mul_resident": (B, [P, P, U, S, S, S, P, S, P, S]),
+        "zlm_gpu_mat_vec_resident": (B, [P, P, U, S, S, P, S, P, S]),
+        "zlm_gpu_mat_vec_resident_async": (I32, [P, P, U, S, S, P, S]),
+        "zlm_gpu_mat_vec_resident_burst_async": (I32, [P, P, U, S, S, P, S, B]),
+        "zlm_gpu_mat_vec_gate_up_resident_burst_async": (I32, [P, P, P, U, S, S, P, S, U, U, B]),
+        "zlm_gpu_mat_vec_mlp_resident_burst_async": (I32, [P, P, P, P, U, S, S, S, P, S, U, U, B]),
+        "zlm_gpu_mat_vec_mlp_pair_resident_burst_async": (I32, [P, P, P, P, U, U, S, S, S, P, S, U, U, B]),
+        "zlm_gpu_wait_resident": (B, [P, I32, P, S, S]),
+        "zlm_gpu_mat_vec_resident_batch": (B, [P, S, P, S, P, S]),
+        "zlm_gpu_upload_resident": (P, [P, P, S]),
+        "zlm_gpu_free_resident": (None, [P, P]),
+        "zlm_gpu_sync": (None, [P]),
+        "zlm_gpu_probe": (None, [P, S, S, S, P]),
+        "zlm_gpu_resident_bytes": (ctypes.c_uint64, [P]),
+        "zlm_gpu_last_error": (ctypes.c_char_p, [P]),
+        "zlm_gpu_cu_count": (ctypes.c_int, [P]),
+        "zlm_gpu_dev_malloc": (P, [P, S]),
+        "zlm_gpu_dev_free": (None, [P, P]),
+        "zlm_gpu_dev_upload": (B, [P, P, P, S]),
+        "zlm_gpu_dev_download": (B, [P, P, P, S]),
+        "zlm_gpu_mat_vec_enqueue": (B, [P, P, U, S, S, P, P]),
+        "zlm_gpu_time_mat_vec": (B, [P, P, S, U, S, S, P, P, ctypes.c_int, P]),
+        "zlm_gpu_time_gemv_sequence": (B, [P, P, S, ctypes.c_int, P]),
+        "zlm_gpu_dequant_resident": (B, [P, P, U, S, P]),
+        "zlm_gpu_quantize_act_q8": (B, [P, P, S, P, P, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _p(a: Optional[np.ndarray]) -> Optional[int]:
+    return None if a is None else a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    a = np.asarray(a)
+    if a.dtype != np.float32 or not a.flags.c_contiguous:
+        raise TypeError("expected a C-contiguous float32 array")
+    return a
+
+
+def _u8(a) -> np.ndarray:
+    a = np.asarray(a)
+    if a.dtype != np.uint8 or not a.flags.c_contiguous:
+        raise TypeError("expected a C-contiguous uint8 array")
+    return a
+
+
+class Resident:
+    """A weight uploaded once into HBM (reference ``Resident``, root.zig:241-244)."""
+
+    def __init__(self, dev: "Device", ptr: int):
+        self._dev = dev
+        self.ptr = ptr
+
+    @property
+    def bytes(self) -> int:
+        return int(lib().zlm_gpu_resident_bytes(self.ptr))
+
+
+@dataclass
+class ResidentOp:
+    """One resident GEMV of a batch (reference ``ResidentOp``, root.zig:249-254)."""
+
+    res: Resident
+    quant: int
+    rows: int
+    out: np.ndarray
+
+
+@dataclass
+class Probe:
+    """Measured co-processor rates (reference ``Probe``, root.zig:260-295)."""
+
+    fields: dict = field(default_factory=dict)
+
+    def __getattr__(self, name):
+        try:
+            return self.fields[name]
+        except KeyError as e:
+            raise AttributeError(name) from e
+
+
+class Device:
+    """The HIP co-processor; inert (``available() is False``) without a gfx950 GPU."""
+
+    def __init__(self) -> None:
+        self._L = lib()
+        self._h = self._L.zlm_gpu_init()
+        if not self._h:
+            raise MemoryError("zlm_gpu_init returned NULL")
+
+    # -- lifecycle / identity -------------------------------------------------
+    def deinit(self) -> None:
+        if self._h:
+            self._L.zlm_gpu_deinit(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.deinit()
+        except Exception:
+            pass
+
+    def available(self) -> bool:
+        return bool(self._h) and bool(self._L.zlm_gpu_available(self._h))
+
+    def backend_name(self) -> str:
+        return self._L.zlm_gpu_backend_name(self._h).decode()
+
+    def device_name(self) -> str:
+        return self._L.zlm_gpu_device_name(self._h).decode()
+
+    def is_uma(self) -> bool:
+        return bool(self._L.zlm_gpu_is_uma(self._h))
+
+    def last_error(self) -> str:
+        return self._L.zlm_gpu_last_error(self._h).decode()
+
+    def cu_count(self) -> int:
+        return int(self._L.zlm_gpu_cu_count(self._h))
+
+    # -- GEMV / GEMM -----------------------------------------------------------
+    def mat_vec(self, quant: int, weight: np.ndarray, rows: int, k: int, x: np.ndarray, out: np.ndarray) -> bool:
+        w, x, out = _u8(weight), _f32(x), _f32(out)
+        return bool(self._L.zlm_gpu_mat_vec(self._h, quant, _p(w), w.size, rows, k, _p(x), x.size, _p(out), out.size))
+
+    def mat_mul_batch(self, quant: int, weight: np.ndarray, rows: int, k: int, m: int, x: np.ndarray,
+                      out: np.ndarray) -> bool:
+        w, x, out = _u8(weight), _f32(x), _f32(out)
+        return bool(self._L.zlm_gpu_mat_mul_batch(self._h, quant, _p(w), w.size, rows, k, m, _p(x), x.size,
+                                                  _p(out), out.size))
+
+    def mat_mul_resident(self, res: Resident, quant: int, rows: int, k: int, m: int, x: np.ndarray,
+                         out: np.ndarray) -> bool:
+        x, out = _f32(x), _f32(out)
+        return bool(self._L.zlm_gpu_mat_mul_resident(self._h, res.ptr, quant, rows, k, m, _p(x), x.size, _p(out),
+                                                     out.size))
+
+    def mat_vec_resident(self, res: Resident, quant: int, rows: int, k: int, x: np.ndarray,
+                         out: np.ndarray) -> bool:
+        x, out = _f32(x), _f32(out)
+        return bool(self._L.zlm_gpu_mat_vec_resident(self._h, res.ptr, quant, rows, k, _p(x), x.size, _p(out),
+                                                     out.size))
+
+    @staticmethod
+    def _handle(h: int) -> Optional[int]:
+        return None if h < 0 else int(h)
+
+    def mat_vec_resident_async(self, res: Resident, quant: int, rows: int, k: int, x: np.ndarray) -> Optional[int]:
+        x = _f32(x)
+        return self._handle(self._L.zlm_gpu_mat_vec_resident_async(self._h, res.ptr, quant, rows, k, _p(x), x.size))
+
+    def mat_vec_resident_burst_async(self, res: Resident, quant: int, rows: int, k: int, x: np.ndarray,
+                                     first: bool) -> Optional[int]:
+        x = _f32(x)
+        return self._handle(self._L.zlm_gpu_mat_vec_resident_burst_async(self._h, res.ptr, quant, rows, k, _p(x),
+                                                                         x.size, first))
+
+    def mat_vec_gate_up_resident_burst_async(self, res_gate: Resident, res_up: Resident, quant: int, rows: int,
+                                             k: int, x: np.ndarray, act: int, variant: int,
+                                             first: bool) -> Optional[int]:
+        x = _f32(x)
+        return self._handle(self._L.zlm_gpu_mat_vec_gate_up_resident_burst_async(
+            self._h, res_gate.ptr, res_up.ptr, quant, rows, k, _p(x), x.size, act, variant, first))
+
+    def mat_vec_mlp_resident_burst_async(self, res_gate: Resident, res_up: Resident, res_down: Resident,
+                                         quant: int, rows: int, k: int, ffn: int, x: np.ndarray, act: int,
+                                         variant: int, first: bool) -> Optional[int]:
+        x = _f32(x)
+        return self._handle(self._L.zlm_gpu_mat_vec_mlp_resident_burst_async(
+            self._h, res_gate.ptr, res_up.ptr, res_down.ptr, quant, rows, k, ffn, _p(x), x.size, act, variant,
+            first))
+
+    def mat_vec_mlp_pair_resident_burst_async(self, res_gate: Resident, res_up: Resident, res_down: Resident,
+                                              gu_quant: int, down_quant: int, rows: int, k: int, ffn: int,
+                                              x: np.ndarray, act: int, variant: int,
+                                              first: bool) -> Optional[int]:
+        x = _f32(x)
+        return self._handle(self._L.zlm_gpu_mat_vec_mlp_pair_resident_burst_async(
+            self._h, res_gate.ptr, res_up.ptr, res_down.ptr, gu_quant, down_quant, rows, k, ffn, _p(x), x.size,
+            act, variant, first))
+
+    def wait_resident(self, h: int, out: np.ndarray, rows: int) -> bool:
+        out = _f32(out)
+        return bool(self._L.zlm_gpu_wait_resident(self._h, h, _p(out), out.size, rows))
+
+    def mat_vec_resident_batch(self, k: int, x: np.ndarray, ops: Sequence[ResidentOp]) -> bool:
+        x = _f32(x)
+        arr = (_ResidentOp * max(1, len(ops)))()
+        for i, op in enumerate(ops):
+            o = _f32(op.out)
+            arr[i] = _ResidentOp(op.res.ptr, op.quant, op.rows, _p(o), o.size)
+        return bool(self._L.zlm_gpu_mat_vec_resident_batch(self._h, k, _p(x), x.size, ctypes.addressof(arr),
+                                                           len(ops)))
+
+    # -- residency -------------------------------------------------------------
+    def upload_resident(self, data: np.ndarray) -> Optional[Resident]:
+        d = _u8(data)
+        ptr = self._L.zlm_gpu_upload_resident(self._h, _p(d), d.size)
+        return Resident(self, ptr) if ptr else None
+
+    def free_resident(self, res: Resident) -> None:
+        if res is not None and res.ptr:
+            self._L.zlm_gpu_free_resident(self._h, res.ptr)
+            res.ptr = None
+
+    def sync(self) -> None:
+        self._L.zlm_gpu_sync(self._h)
+
+    def probe_gpu(self, rows: int, k: int, m: int) -> Probe:
+        p = _Probe()
+        self._L.zlm_gpu_probe(self._h, rows, k, m, ctypes.addressof(p))
+        return Probe({name: getattr(p, name) for name, _ in _Probe._fields_})
+
+    # -- device-level helpers (no reference counterpart) -----------------------
+    def dev_malloc(self, nbytes: int) -> int:
+        p = self._L.zlm_gpu_dev_malloc(self._h, nbytes)
+        if not p:
+            raise MemoryError(self.last_error())
+        return p
+
+    def dev_free(self, ptr: int) -> None:
+        self._L.zlm_gpu_dev_free(self._h, ptr)
+
+    def dev_upload(self, dst: int, src: np.ndarray) -> None:
+        src = np.ascontiguousarray(src)
+        if not self._L.zlm_gpu_dev_upload(self._h, dst, _p(src), src.nbytes):
+            raise RuntimeError(self.last_error())
+
+    def dev_download(self, dst: np.ndarray, src: int) -> None:
+        if not dst.flags.c_contiguous:
+            raise TypeError("destination must be contiguous")
+        if not self._L.zlm_gpu_dev_download(self._h, _p(dst), src, dst.nbytes):
+            raise RuntimeError(self.last_error())
+
+    def mat_vec_enqueue(self, res: Resident, quant: int, rows: int, k: int, x_dev: int, y_dev: int) -> bool:
+        return bool(self._L.zlm_gpu_mat_vec_enqueue(self._h, res.ptr, quant, rows, k, x_dev, y_dev))
+
+    def time_mat_vec(self, residents: Sequence[Resident], quant: int, rows: int, k: int, x_dev: int, y_dev: int,
+                     iters: int) -> float:
+        """GPU milliseconds for `iters` GEMVs rotating over `residents` (HIP events)."""
+        arr = (ctypes.c_void_p * len(residents))(*[r.ptr for r in residents])
+        ms = ctypes.c_double(0.0)
+        if not self._L.zlm_gpu_time_mat_vec(self._h, ctypes.addressof(arr), len(residents), quant, rows, k, x_dev,
+                                            y_dev, iters, ctypes.addressof(ms)):
+            raise RuntimeError(self.last_error())
+        return ms.value
+
+    def time_gemv_sequence(self, descs: Sequence[tuple], iters: int) -> float:
+        """GPU milliseconds for `iters` passes over descs = [(res, quant, rows, k, x_dev, y_dev), ...]."""
+        arr = (_GemvDesc * len(descs))()
+        for i, (res, q, rows, k, xd, yd) in enumerate(descs):
+            arr[i] = _GemvDesc(res.ptr, q, rows, k, xd, yd)
+        ms = ctypes.c_double(0.0)
+        if not self._L.zlm_gpu_time_gemv_sequence(self._h, ctypes.addressof(arr), len(descs), iters,
+                                                  ctypes.addressof(ms)):
+            raise RuntimeError(self.last_error())
+        return ms.value
+
+    def dequant_resident(self, res: Resident, quant: int, n: int) -> Optional[np.ndarray]:
+        out = np.zeros(n, np.float32)
+        if not self._L.zlm_gpu_dequant_resident(self._h, res.ptr, quant, n, _p(out)):
+            return None
+        return out
+
+    def quantize_act_q8(self, x: np.ndarray):
+        x = _f32(x)
+        n = x.size
+        qx = np.zeros(n, np.int8)
+        dx = np.zeros(n // 32, np.float32)
+        sums = np.zeros(n // 32, np.int32)
+        if not self._L.zlm_gpu_quantize_act_q8(self._h, _p(x), n, _p(qx), _p(dx), _p(sums)):
+            return None
+        return qx, dx, sums

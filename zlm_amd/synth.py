@@ -1,0 +1,122 @@
+"""Seeded synthetic GGUF weights and activations for the benchmark configs.
+
+A counter-based splitmix64 stream: value ``i`` of stream ``s`` under seed
+``seed`` is ``mix(base(seed, s) + (i + 1) * GAMMA)``, so any slice of a stream
+can be produced independently (and on the GPU, if ever needed).  Normals are
+Box-Muller over two uniforms.  Each tensor draws its scales, its quant bytes and
+the activation from separate streams.
+
+Distributions follow the benchmark configurations:
+  * Q4_0: per 32-block ``d = f16(|N(0,1)| * 0.02)``, 16 uniform bytes (nibbles
+    uniform on 0..15), value ``(q - 8) * d``.
+  * Q8_0: ``d = f16(|N(0,1)| * 0.01)``, int8 quants uniform on [-127, 127].
+  * Q4_K: ``d``, ``dmin`` = ``f16(|N(0,1)| * 0.02)``; 12 scale bytes and 128
+    quant bytes uniform.
+  * Q6_K: ``ql``, ``qh`` and ``sc`` uniform bytes, ``d = f16(|N(0,1)| * 0.02)``.
+  * activations: fp32 N(0, 1).
+
+The raw byte layout is GGUF's (block formats as in the reference's
+``src/kernels/linear/quant/types.zig:6-53`` and ``gguf/format.zig:135-159``).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+GAMMA = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+_STREAM = np.uint64(0xD1B54A32D192ED03)
+
+# GGML type codes (reference gguf/format.zig:41-77).
+Q4_0, Q4_1, Q8_0, Q4_K, Q6_K = 2, 3, 8, 12, 14
+BLOCK_ELEMS = {Q4_0: 32, Q4_1: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q4_1: 20, Q8_0: 34, Q4_K: 144, Q6_K: 210}
+TYPE_NAMES = {Q4_0: "q4_0", Q4_1: "q4_1", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+
+
+def _mix(z: np.ndarray) -> np.ndarray:
+    z = (z ^ (z >> np.uint64(30))) * _M1
+    z = (z ^ (z >> np.uint64(27))) * _M2
+    return z ^ (z >> np.uint64(31))
+
+
+def _base(seed: int, stream: int) -> np.uint64:
+    s = np.array([seed & 0xFFFFFFFFFFFFFFFF], dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        b = _mix(s + GAMMA)[0] ^ (np.uint64(stream) * _STREAM)
+    return np.uint64(b)
+
+
+def u64(seed: int, stream: int, n: int, offset: int = 0) -> np.ndarray:
+    """``n`` uint64 values of stream ``stream`` starting at counter ``offset``."""
+    with np.errstate(over="ignore"):
+        i = np.arange(offset + 1, offset + n + 1, dtype=np.uint64)
+        return _mix(_base(seed, stream) + i * GAMMA)
+
+
+def random_bytes(seed: int, stream: int, n: int) -> np.ndarray:
+    words = u64(seed, stream, (n + 7) // 8)
+    return words.view(np.uint8)[:n].copy()
+
+
+def uniform01(seed: int, stream: int, n: int) -> np.ndarray:
+    """float64 uniforms on [0, 1)."""
+    return (u64(seed, stream, n) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+def normal(seed: int, stream: int, n: int) -> np.ndarray:
+    """float64 N(0, 1) by Box-Muller over counters (2i, 2i+1)."""
+    w = u64(seed, stream, 2 * n)
+    a = (w[0::2] >> np.uint64(11)).astype(np.float64)
+    b = (w[1::2] >> np.uint64(11)).astype(np.float64)
+    u1 = (a + 1.0) * (1.0 / 9007199254740992.0)  # (0, 1]
+    u2 = b * (1.0 / 9007199254740992.0)
+    return np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+
+
+def activation(seed: int, n: int, stream: int = 9) -> np.ndarray:
+    """fp32 N(0, 1) activation of length ``n``."""
+    return normal(seed, stream, n).astype(np.float32)
+
+
+def _f16_bytes(v: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(-1, 2)
+
+
+def weights(qtype: int, rows: int, k: int, seed: int) -> np.ndarray:
+    """Raw GGUF bytes of a ``rows x k`` weight (row-major blocks), uint8."""
+    be, bb = BLOCK_ELEMS[qtype], BLOCK_BYTES[qtype]
+    if k % be:
+        raise ValueError(f"k={k} is not a multiple of the {TYPE_NAMES[qtype]} block ({be})")
+    nblk = rows * (k // be)
+    out = np.empty((nblk, bb), dtype=np.uint8)
+    if qtype == Q4_0:
+        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
+        out[:, 2:18] = random_bytes(seed, 2, nblk * 16).reshape(nblk, 16)
+    elif qtype == Q8_0:
+        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.01)
+        r = random_bytes(seed, 2, nblk * 64).view(np.uint16).astype(np.uint32)
+        q = ((r * 255) >> 16).astype(np.int32) - 127
+        out[:, 2:34] = q.astype(np.int8).view(np.uint8).reshape(nblk, 32)
+    elif qtype == Q4_1:
+        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
+        out[:, 2:4] = _f16_bytes(-np.abs(normal(seed, 3, nblk)) * 0.1)
+        out[:, 4:20] = random_bytes(seed, 2, nblk * 16).reshape(nblk, 16)
+    elif qtype == Q4_K:
+        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
+        out[:, 2:4] = _f16_bytes(np.abs(normal(seed, 3, nblk)) * 0.02)
+        out[:, 4:144] = random_bytes(seed, 2, nblk * 140).reshape(nblk, 140)
+    elif qtype == Q6_K:
+        out[:, 0:208] = random_bytes(seed, 2, nblk * 208).reshape(nblk, 208)
+        out[:, 208:210] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
+    else:
+        raise ValueError(f"unsupported type {qtype}")
+    return out.reshape(-1)
+
+
+def row_bytes(qtype: int, k: int) -> int:
+    return (k // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
+
+
+def weight_bytes(qtype: int, rows: int, k: int) -> int:
+    return rows * row_bytes(qtype, k)
