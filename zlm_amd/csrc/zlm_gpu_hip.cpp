@@ -26,6 +26,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <string>
 
 namespace {
@@ -60,30 +61,34 @@ const QuantInfo* quant_info(uint32_t quant) {
 
 uint32_t variant_of(uint32_t quant) { return (quant >> 8) & 0xffu; }
 
-// x capacities of the GEMV instantiations (elements) and their waves per workgroup.
-constexpr int kKcaps[] = {4096, 8192, 16384, 32768};
-constexpr int kKcapWaves[] = {4, 4, 8, 8};
-constexpr int kNumKcap = 4;
-// Row tiles of the GEMV instantiations.
-constexpr int kRts[] = {2, 4, 8};
-constexpr int kNumRt = 3;
+// GEMV kernels: 4 waves (256 threads) per workgroup; k up to 32768.
+constexpr int kGemvThreads = 256;
+constexpr size_t kMaxK = 32768;
 
-// GpuVariant -> row tile.  The reference's variants are Vulkan spec-constant
-// axes (gpu/kernels/grid.zig:41-53); here `u4`/`u8` select the 8-row tile
-// (the reference's u4 is its 8-row group), `un2`/`un4` the 2-row tile, and
-// every other variant the default 4-row tile.
-int rt_index_for_variant(uint32_t v) {
+// GpuVariant -> rows per wave tile.  The reference's variants are Vulkan
+// spec-constant axes (gpu/kernels/grid.zig:41-53): `u4`/`u8` (its 8-row group)
+// select the 4-row tile, `un2`/`un4` the 2-row tile, every other variant the
+// default 1-row tile (the fastest measured on gfx950 for the benchmark
+// shapes).  A variant never changes results beyond fp32 summation order.
+int rt_for_variant(uint32_t v) {
     switch (v) {
     case ZLM_VARIANT_U4:
     case ZLM_VARIANT_U8:
-        return 2;
+        return 4;
     case ZLM_VARIANT_UN2:
     case ZLM_VARIANT_UN4:
-        return 0;
+        return 2;
     default:
         return 1;
     }
 }
+
+// A resolved GEMV kernel and its launch bound.
+struct GemvKernel {
+    hipFunction_t fn = nullptr;
+    int rt = 0;
+    int steps = 0;
+};
 
 struct Slot {
     hipEvent_t done = nullptr;
@@ -118,8 +123,7 @@ struct zlm_device {
     std::string err;
 
     hipModule_t mod = nullptr;
-    hipFunction_t gemv[4][kNumKcap][kNumRt] = {};
-    int gemv_grid_cap[4][kNumKcap][kNumRt] = {};
+    std::map<std::string, GemvKernel> gemv;  // by entry-point name; null fn = absent
     hipFunction_t repack = nullptr;
     hipFunction_t dequant[4] = {};
     hipFunction_t quantize_q8 = nullptr;
@@ -184,19 +188,6 @@ bool load_kernels(zlm_device* d) {
     if (!ok(d, hipModuleLoad(&d->mod, path.c_str()), path.c_str())) return false;
     char nm[128];
     for (int q = 0; q < 4; q++) {
-        for (int kc = 0; kc < kNumKcap; kc++) {
-            for (int ri = 0; ri < kNumRt; ri++) {
-                snprintf(nm, sizeof nm, "zlm_gemv_%s_k%d_w%d_r%d", kQuantNames[q], kKcaps[kc], kKcapWaves[kc],
-                         kRts[ri]);
-                if (!ok(d, hipModuleGetFunction(&d->gemv[q][kc][ri], d->mod, nm), nm)) return false;
-                int per_cu = 0;
-                if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, d->gemv[q][kc][ri],
-                                                                       kKcapWaves[kc] * 64, 0) != hipSuccess ||
-                    per_cu < 1)
-                    per_cu = 1;
-                d->gemv_grid_cap[q][kc][ri] = per_cu * d->cus;
-            }
-        }
         snprintf(nm, sizeof nm, "zlm_dequant_%s", kQuantNames[q]);
         if (!ok(d, hipModuleGetFunction(&d->dequant[q], d->mod, nm), nm)) return false;
     }
@@ -291,6 +282,40 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
     return true;
 }
 
+// Look up (and cache) a GEMV entry point by name.
+const GemvKernel* find_gemv(zlm_device* d, const char* name, int rt, int steps) {
+    auto it = d->gemv.find(name);
+    if (it == d->gemv.end()) {
+        GemvKernel g;
+        if (hipModuleGetFunction(&g.fn, d->mod, name) == hipSuccess) {
+            g.rt = rt;
+            g.steps = steps;
+        } else {
+            g.fn = nullptr;
+            hipGetLastError();
+        }
+        it = d->gemv.emplace(name, g).first;
+    }
+    return it->second.fn ? &it->second : nullptr;
+}
+
+// The GEMV kernel for a shape: the instance whose step count equals
+// ceil(chunks per row / 64) with the requested row tile, else with a 1-row
+// tile, else the generic bounded instance.  Chunks per row: k/16 for q8_0,
+// k/32 for q4_0 and the K-quants.
+const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt) {
+    const size_t chunks = (qi->type == ZLM_GGML_Q8_0) ? k / 16 : k / 32;
+    const int steps = static_cast<int>((chunks + 63) / 64);
+    const char* qn = kQuantNames[qi->slot];
+    char nm[96];
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d", qn, rt, steps);
+    if (const GemvKernel* g = find_gemv(d, nm, rt, steps)) return g;
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d", qn, steps);
+    if (const GemvKernel* g = find_gemv(d, nm, 1, steps)) return g;
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_g%d", qn, qi->type == ZLM_GGML_Q8_0 ? 32 : 16);
+    return find_gemv(d, nm, 1, steps);
+}
+
 // Validate a GEMV over resident `r` and pick its kernel.
 bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, hipFunction_t* f,
                   unsigned* grid, unsigned* block) {
@@ -300,23 +325,22 @@ bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     if (!r) return fail(d, "null resident");
     if (rows == 0 || k == 0 || k % qi->block_elems != 0) return fail(d, "bad shape rows=%zu k=%zu", rows, k);
     if (rows > 0xffffffffu) return fail(d, "rows too large");
-    int kc = -1;
-    for (int i = 0; i < kNumKcap; i++)
-        if (static_cast<int>(k) <= kKcaps[i]) {
-            kc = i;
-            break;
-        }
-    if (kc < 0) return fail(d, "k=%zu exceeds the LDS-staged activation capacity", k);
+    if (k > kMaxK) return fail(d, "k=%zu exceeds the LDS-staged activation capacity", k);
     const uint64_t nb = k / qi->block_elems;
     if (r->bytes < rows * nb * qi->block_bytes) return fail(d, "resident too short");
     if (!ensure_layout(d, r, qi)) return false;
     if (r->blocks < rows * nb) return fail(d, "resident layout too short");
-    const int ri = rt_index_for_variant(variant_of(quant));
-    *f = d->gemv[qi->slot][kc][ri];
-    const uint64_t tiles = (rows + kRts[ri] - 1) / kRts[ri];
-    const uint64_t wgs = (tiles + kKcapWaves[kc] - 1) / kKcapWaves[kc];
-    *grid = static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->gemv_grid_cap[qi->slot][kc][ri])));
-    *block = static_cast<unsigned>(kKcapWaves[kc] * 64);
+    const GemvKernel* gk = pick_gemv(d, qi, k, rt_for_variant(variant_of(quant)));
+    if (!gk) return fail(d, "no GEMV kernel for quant %u k=%zu", qi->type, k);
+    *f = gk->fn;
+    const uint64_t tiles = (rows + gk->rt - 1) / gk->rt;
+    const uint64_t wgs = (tiles + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
+    // Measured on gfx950: up to 4 steps per row (k <= 4096 for q8_0, 8192 for
+    // the others) a grid of 4 workgroups per CU is best; wider rows stage a
+    // larger x in LDS and one workgroup per CU looping over tiles is best.
+    const uint64_t cap = static_cast<uint64_t>(d->cus) * (gk->steps > 4 ? 1 : 4);
+    *grid = static_cast<unsigned>(std::min<uint64_t>(wgs, cap));
+    *block = kGemvThreads;
     return true;
 }
 
