@@ -113,6 +113,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="also run the library copy kernel 5x over BYTES (for HBM traffic counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
@@ -123,6 +125,14 @@ def main():
     if not dev.available():
         raise SystemExit(f"HIP backend unavailable: {dev.last_error()}")
     log(f"device: {dev.device_name()}, {dev.cu_count()} CUs")
+    if args.calibrate_copy:
+        nbytes = (args.calibrate_copy // 16) * 16
+        a, b = dev.dev_malloc(nbytes), dev.dev_malloc(nbytes)
+        for _ in range(5):
+            dev.dev_copy(b, a, nbytes)
+        dev.dev_free(a)
+        dev.dev_free(b)
+        log(f"copy calibration: 5 x {nbytes} bytes")
 
     # ---- headline: configs[1], Q8_0 Qwen3-8B FFN GEMVs ------------------------------
     step_w = 2 * synth.weight_bytes(synth.Q8_0, 12288, 4096) + synth.weight_bytes(synth.Q8_0, 4096, 12288)
@@ -165,7 +175,7 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             t = json.load(f)
-        traffic = t.get("zlm_gemv_q8_0_k4096", {}).get("bytes_per_launch")
+        traffic = t.get("zlm_gemv_q8_0_r1_s4", {}).get("bytes_per_launch")
 
     cpu = None
     if not args.no_cpu:
@@ -219,7 +229,7 @@ def main():
         "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "zlm_gemv_q8_0_k4096 (gate/up 12288x4096)",
+            "kernel": "zlm_gemv_q8_0_r1_s4 (gate/up 12288x4096)",
             "achieved": round(gu_gbps, 1),
             "peak": PEAK_GBPS,
             "unit": "GB/s",

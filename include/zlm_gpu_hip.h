@@ -191,6 +191,9 @@ void *zlm_gpu_dev_malloc(zlm_device *dev, size_t bytes);
 void zlm_gpu_dev_free(zlm_device *dev, void *ptr);
 bool zlm_gpu_dev_upload(zlm_device *dev, void *dst, const void *src, size_t bytes);
 bool zlm_gpu_dev_download(zlm_device *dev, void *dst, const void *src, size_t bytes);
+/* Copy `bytes` (a multiple of 16, 16-byte aligned pointers) device to device
+ * with the library's own copy kernel, and wait. */
+bool zlm_gpu_dev_copy(zlm_device *dev, void *dst, const void *src, size_t bytes);
 /* Enqueue y_dev[0..rows) = W * x_dev on the device stream; no host copies. */
 bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
                              const float *x_dev, float *y_dev);

@@ -127,6 +127,7 @@ struct zlm_device {
     hipFunction_t repack = nullptr;
     hipFunction_t dequant[4] = {};
     hipFunction_t quantize_q8 = nullptr;
+    hipFunction_t copy16 = nullptr;
     hipStream_t stream = nullptr;
 
     Slot slots[kRing];
@@ -193,6 +194,7 @@ bool load_kernels(zlm_device* d) {
     }
     if (!ok(d, hipModuleGetFunction(&d->repack, d->mod, "zlm_repack_split"), "zlm_repack_split")) return false;
     if (!ok(d, hipModuleGetFunction(&d->quantize_q8, d->mod, "zlm_quantize_q8"), "zlm_quantize_q8")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->copy16, d->mod, "zlm_copy16"), "zlm_copy16")) return false;
     return true;
 }
 
@@ -750,6 +752,17 @@ extern "C" bool zlm_gpu_dev_download(zlm_device* d, void* dst, const void* src, 
     if (!d || !d->avail) return false;
     if (!ok(d, hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, d->stream), "download")) return false;
     return ok(d, hipStreamSynchronize(d->stream), "sync");
+}
+
+extern "C" bool zlm_gpu_dev_copy(zlm_device* d, void* dst, const void* src, size_t bytes) {
+    if (!d || !d->avail || !dst || !src) return false;
+    if (bytes % 16 || reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(src) % 16)
+        return fail(d, "dev_copy needs 16-byte granules");
+    if (bytes == 0) return true;
+    uint64_t n16 = bytes / 16;
+    const unsigned grid = static_cast<unsigned>(std::min<uint64_t>((n16 + 255) / 256, static_cast<uint64_t>(d->cus) * 8));
+    void* args[] = {const_cast<void**>(&src), &dst, &n16};
+    return launch(d, d->copy16, grid, 256, args, "copy") && ok(d, hipStreamSynchronize(d->stream), "sync");
 }
 
 extern "C" bool zlm_gpu_mat_vec_enqueue(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,

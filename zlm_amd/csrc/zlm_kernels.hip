@@ -769,3 +769,12 @@ extern "C" __global__ void __launch_bounds__(256)
     dx[b] = d;
     sums[b] = s;
 }
+
+// ---- device copy (16-byte granules; the traffic-counter calibration kernel) --
+
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, uint64_t n16) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+        dst[i] = src[i];
+}

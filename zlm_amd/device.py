@@ -133,6 +133,7 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_dev_free": (None, [P, P]),
         "zlm_gpu_dev_upload": (B, [P, P, P, S]),
         "zlm_gpu_dev_download": (B, [P, P, P, S]),
+        "zlm_gpu_dev_copy": (B, [P, P, P, S]),
         "zlm_gpu_mat_vec_enqueue": (B, [P, P, U, S, S, P, P]),
         "zlm_gpu_time_mat_vec": (B, [P, P, S, U, S, S, P, P, ctypes.c_int, P]),
         "zlm_gpu_time_gemv_sequence": (B, [P, P, S, ctypes.c_int, P]),
@@ -351,6 +352,10 @@ class Device:
         if not dst.flags.c_contiguous:
             raise TypeError("destination must be contiguous")
         if not self._L.zlm_gpu_dev_download(self._h, _p(dst), src, dst.nbytes):
+            raise RuntimeError(self.last_error())
+
+    def dev_copy(self, dst: int, src: int, nbytes: int) -> None:
+        if not self._L.zlm_gpu_dev_copy(self._h, dst, src, nbytes):
             raise RuntimeError(self.last_error())
 
     def mat_vec_enqueue(self, res: Resident, quant: int, rows: int, k: int, x_dev: int, y_dev: int) -> bool:
