@@ -197,6 +197,14 @@ bool zlm_gpu_dev_copy(zlm_device *dev, void *dst, const void *src, size_t bytes)
 /* Enqueue y_dev[0..rows) = W * x_dev on the device stream; no host copies. */
 bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
                              const float *x_dev, float *y_dev);
+/* Enqueue the prefill GEMM out_dev[t*rows + r] (x_dev: m x k fp32, token-major):
+ * the q8 activation quantizer, then the int8-MFMA GEMM.  Q4_0 only. */
+bool zlm_gpu_mat_mul_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k, size_t m,
+                             const float *x_dev, float *out_dev);
+/* Enqueue `iters` prefill GEMMs (quantizer + GEMM each), rotating over `n_res`
+ * residents, between two HIP events; *ms = elapsed GPU milliseconds. */
+bool zlm_gpu_time_mat_mul(zlm_device *dev, zlm_resident *const *res, size_t n_res, uint32_t quant, size_t rows,
+                          size_t k, size_t m, const float *x_dev, float *out_dev, int iters, double *ms);
 /* Enqueue `iters` GEMVs, rotating over `n_res` residents, between two HIP events
  * on the device stream; *ms = elapsed GPU milliseconds between the events. */
 bool zlm_gpu_time_mat_vec(zlm_device *dev, zlm_resident *const *res, size_t n_res, uint32_t quant, size_t rows,

@@ -1,0 +1,78 @@
+"""GPU parity of the prefill GEMM (q8 activations, int8 MFMA) through the C ABI.
+
+The oracle is zlm's int path (reference kernels/quantized.zig:49-55 over the
+activation quantizer of matvec/layout.zig:458-476) applied per token:
+relative L2 <= 1e-3 (the block dots are exact integers; only fp32 scaling and
+summation order differ).  Against the fp32 GEMM the reference's own int-vs-fp
+bound applies, |int - fp| <= 0.02 * sum|w*x| (kernels/quantized_test.zig:61).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import rel_l2
+from zlm_amd import device as zd
+from zlm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("rows,k,m", [(64, 256, 4), (100, 512, 37), (64, 1024, 64), (130, 4096, 70), (48, 16384, 3), (70, 4096, 129), (64, 4096, 1)])
+def test_gemm_matches_int_oracle(dev, rows, k, m):
+    _say(f"gemm q4_0 rows={rows} k={k} m={m}")
+    w = synth.weights(synth.Q4_0, rows, k, seed=rows + k + m)
+    x = synth.activation(m + 5, m * k)
+    want = oracle.matmul_int(synth.Q4_0, w, k, rows, m, x)
+    out = np.full(m * rows, np.nan, np.float32)
+    assert dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x, out), dev.last_error()
+    got = out.reshape(m, rows)
+    assert rel_l2(got, want) <= 1e-3
+    res = dev.upload_resident(w)
+    out2 = np.zeros(m * rows, np.float32)
+    assert dev.mat_mul_resident(res, zd.quant(zd.Q4_0), rows, k, m, x, out2), dev.last_error()
+    np.testing.assert_array_equal(out2, out)
+    # the int path stays within the reference's bound of the fp32 GEMM
+    fp = oracle.matmul_rows(synth.Q4_0, w, k, rows, m, x)
+    dq = np.abs(oracle.dequant(synth.Q4_0, w, rows * k).reshape(rows, k).astype(np.float64))
+    mag = np.abs(x.reshape(m, k).astype(np.float64)) @ dq.T
+    assert np.all(np.abs(got - fp) <= 0.02 * mag + 1e-6)
+    dev.free_resident(res)
+
+
+def test_gemm_config4_rows_subset(dev):
+    """configs[4] at full size (12288 x 4096 Q4_0 x 512 tokens); rows checked
+    against the oracle on a slice of the weight (a GEMM row depends only on its
+    own weight row)."""
+    rows, k, m = 12288, 4096, 512
+    _say("gemm config4 full")
+    w = synth.weights(synth.Q4_0, rows, k, seed=0x5A4C4D04)
+    x = synth.activation(0x5A4C4D0D, m * k)
+    res = dev.upload_resident(w)
+    out = np.zeros(m * rows, np.float32)
+    assert dev.mat_mul_resident(res, zd.quant(zd.Q4_0), rows, k, m, x, out), dev.last_error()
+    got = out.reshape(m, rows)
+    rb = synth.row_bytes(synth.Q4_0, k)
+    for r0, r1 in ((0, 256), (6000, 6128), (12160, 12288)):
+        want = oracle.matmul_int(synth.Q4_0, w[r0 * rb:r1 * rb], k, r1 - r0, m, x)
+        assert rel_l2(got[:, r0:r1], want) <= 1e-3, (r0, r1)
+    dev.free_resident(res)
+
+
+def test_gemm_unsupported_quants_fall_back(dev):
+    rows, k, m = 32, 256, 4
+    x = synth.activation(1, m * k)
+    out = np.zeros(m * rows, np.float32)
+    for qt in (synth.Q6_K, synth.Q4_K, synth.Q8_0):
+        w = synth.weights(qt, rows, k, seed=2)
+        assert not dev.mat_mul_batch(zd.quant(qt), w, rows, k, m, x, out)
+    w = synth.weights(synth.Q4_0, rows, k, seed=2)
+    assert not dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x[:-1].copy(), out)  # x length
+    assert not dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x, out[:-1].copy())  # short out
+    assert dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x, out)  # still healthy

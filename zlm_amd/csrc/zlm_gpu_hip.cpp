@@ -112,6 +112,12 @@ struct zlm_resident {
     uint16_t* scales = nullptr;    // device layout scales (split quants)
     uint32_t layout = kNoLayout;   // GGML type of the device layout
     uint64_t blocks = 0;           // whole blocks in the layout
+    // The prefill GEMM's tiled copy of a Q4_0 weight ([rows/32][nb][32][16 B]
+    // + scales [rows/32][nb][32]), built on the first GEMM for a given nb.
+    uint8_t* gemm_payload = nullptr;
+    uint16_t* gemm_scales = nullptr;
+    uint64_t gemm_nb = 0;
+    uint64_t gemm_rt = 0;  // 32-row tiles
     zlm_device* owner = nullptr;
 };
 
@@ -127,7 +133,14 @@ struct zlm_device {
     hipFunction_t repack = nullptr;
     hipFunction_t dequant[4] = {};
     hipFunction_t quantize_q8 = nullptr;
+    hipFunction_t quantize_q8_tiled = nullptr;
+    hipFunction_t tile_q4_0 = nullptr;
     hipFunction_t copy16 = nullptr;
+    hipFunction_t gemm_q4_0 = nullptr;
+
+    // prefill scratch: quantized activations (qx, dx, sums) and staged x/out
+    uint8_t* q_scratch = nullptr;
+    uint64_t q_scratch_cap = 0;
     hipStream_t stream = nullptr;
 
     Slot slots[kRing];
@@ -194,7 +207,11 @@ bool load_kernels(zlm_device* d) {
     }
     if (!ok(d, hipModuleGetFunction(&d->repack, d->mod, "zlm_repack_split"), "zlm_repack_split")) return false;
     if (!ok(d, hipModuleGetFunction(&d->quantize_q8, d->mod, "zlm_quantize_q8"), "zlm_quantize_q8")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->quantize_q8_tiled, d->mod, "zlm_quantize_q8_tiled"), "quantize tiled"))
+        return false;
+    if (!ok(d, hipModuleGetFunction(&d->tile_q4_0, d->mod, "zlm_tile_q4_0"), "zlm_tile_q4_0")) return false;
     if (!ok(d, hipModuleGetFunction(&d->copy16, d->mod, "zlm_copy16"), "zlm_copy16")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->gemm_q4_0, d->mod, "zlm_gemm_q4_0_q8"), "zlm_gemm_q4_0_q8")) return false;
     return true;
 }
 
@@ -379,11 +396,16 @@ zlm_resident* new_resident(zlm_device* d, const void* bytes, size_t len) {
 void release_resident_memory(zlm_resident* r) {
     if (r->raw) hipFree(r->raw);
     if (r->payload) hipFree(r->payload);
+    if (r->gemm_payload) hipFree(r->gemm_payload);
     r->raw = nullptr;
     r->payload = nullptr;
     r->scales = nullptr;
     r->layout = kNoLayout;
     r->blocks = 0;
+    r->gemm_payload = nullptr;
+    r->gemm_scales = nullptr;
+    r->gemm_nb = 0;
+    r->gemm_rt = 0;
 }
 
 // Stage host x into the synchronous-op device buffer.
@@ -437,6 +459,82 @@ double now_ns() {
     timespec ts;
     clock_gettime(CLOCK_MONOTONIC, &ts);
     return static_cast<double>(ts.tv_sec) * 1e9 + static_cast<double>(ts.tv_nsec);
+}
+
+// Build (once per row length) the GEMM's tiled copy of a resident Q4_0 weight
+// from its split layout: payload [rt][nb][32 rows][16 B] and scales
+// [rt][nb][32 rows] over all whole rows the resident holds, rows padded to 32.
+bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, uint64_t nb) {
+    if (r->gemm_payload && r->gemm_nb == nb) return true;
+    if (r->gemm_payload) hipFree(r->gemm_payload);
+    r->gemm_payload = nullptr;
+    r->gemm_scales = nullptr;
+    r->gemm_nb = 0;
+    r->gemm_rt = 0;
+    const uint64_t rows_total = r->blocks / nb;
+    const uint64_t rt = (rows_total + 31) / 32;
+    if (rt == 0 || rt * 32 > 0xffffffffu) return fail(d, "GEMM weight shape out of range");
+    const uint64_t pbytes = rt * nb * 512;
+    const uint64_t sbytes = rt * nb * 32 * 2;
+    uint8_t* p = nullptr;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&p), pbytes + sbytes), "hipMalloc gemm tiles")) return false;
+    uint8_t* payload = r->payload;
+    uint16_t* scales = r->scales;
+    uint8_t* tp = p;
+    uint16_t* ts = reinterpret_cast<uint16_t*>(p + pbytes);
+    uint32_t rows32 = static_cast<uint32_t>(rows_total), nb32 = static_cast<uint32_t>(nb),
+             rt32 = static_cast<uint32_t>(rt);
+    void* args[] = {&payload, &scales, &tp, &ts, &rows32, &nb32, &rt32};
+    const uint64_t n = rt * 32 * nb;
+    if (!launch(d, d->tile_q4_0, static_cast<unsigned>((n + 255) / 256), 256, args, "tile q4_0")) {
+        hipFree(p);
+        return false;
+    }
+    r->gemm_payload = tp;
+    r->gemm_scales = ts;
+    r->gemm_nb = nb;
+    r->gemm_rt = rt;
+    return true;
+}
+
+// Enqueue the prefill GEMM out_dev[t*rows + r] over a resident Q4_0 weight and
+// device activations x_dev (m x k, token-major): quantize x to q8 blocks into
+// the tiled device scratch, then the int8-MFMA GEMM over the tiled weights.
+bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, size_t m,
+                  const float* x_dev, float* out_dev) {
+    if (!d || !d->avail) return fail(d, "device unavailable");
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
+    if (qi->type != ZLM_GGML_Q4_0) return fail(d, "no GEMM kernel for quant %u", qi->type);
+    if (!r || rows == 0 || k == 0 || m == 0 || k % 32) return fail(d, "bad GEMM shape");
+    if (rows > 0x7fffffffu || m > 0x7fffffffu || k / 32 > 0xffffffu) return fail(d, "GEMM shape too large");
+    const uint64_t nb = k / 32;
+    if (r->bytes < rows * nb * qi->block_bytes) return fail(d, "resident too short");
+    if (!ensure_layout(d, r, qi)) return false;
+    if (r->blocks < rows * nb) return fail(d, "resident layout too short");
+    if (!ensure_gemm_tiles(d, r, nb)) return false;
+    if (r->gemm_rt * 32 < rows) return fail(d, "GEMM tiles too short");
+    const uint64_t mt = (static_cast<uint64_t>(m) + 31) / 32;
+    const uint64_t qbytes = mt * 32 * k;  // a multiple of 1024
+    const uint64_t need = qbytes + mt * 32 * nb * 4;
+    if (!ensure_bytes(d, d->q_scratch, d->q_scratch_cap, need)) return false;
+    int8_t* qx = reinterpret_cast<int8_t*>(d->q_scratch);
+    float* dx = reinterpret_cast<float*>(d->q_scratch + qbytes);
+    uint32_t rows32 = static_cast<uint32_t>(rows), m32 = static_cast<uint32_t>(m), nb32 = static_cast<uint32_t>(nb),
+             mt32 = static_cast<uint32_t>(mt);
+    {
+        const uint64_t n = mt * 32 * nb;
+        void* args[] = {const_cast<float**>(&x_dev), &qx, &dx, &m32, &nb32, &mt32};
+        if (!launch(d, d->quantize_q8_tiled, static_cast<unsigned>((n + 255) / 256), 256, args, "quantize tiled"))
+            return false;
+    }
+    const uint8_t* wq = r->gemm_payload;
+    const uint16_t* wd = r->gemm_scales;
+    void* args[] = {&wq, &wd, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
+    return ok(d,
+              hipModuleLaunchKernel(d->gemm_q4_0, static_cast<unsigned>((rows + 63) / 64),
+                                    static_cast<unsigned>((m + 127) / 128), 1, 256, 1, 1, 0, d->stream, args, nullptr),
+              "gemm");
 }
 
 }  // namespace
@@ -505,6 +603,7 @@ extern "C" void zlm_gpu_deinit(zlm_device* d) {
         if (d->h_bx) hipHostFree(d->h_bx);
         if (d->bx_copied) hipEventDestroy(d->bx_copied);
         if (d->s_raw) hipFree(d->s_raw);
+        if (d->q_scratch) hipFree(d->q_scratch);
         if (d->s_lay) hipFree(d->s_lay);
         if (d->mod) hipModuleUnload(d->mod);
         hipStreamDestroy(d->stream);
@@ -680,16 +779,46 @@ extern "C" bool zlm_gpu_mat_vec_resident_batch(zlm_device* d, size_t k, const fl
     return true;
 }
 
-extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void*, size_t, size_t, size_t, size_t,
-                                      const float*, size_t, float*, size_t) {
+extern "C" bool zlm_gpu_mat_mul_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
+                                         size_t m, const float* x, size_t x_len, float* out, size_t out_len) {
     if (!d || !d->avail) return false;
-    return fail(d, "matMulBatch: quant %u has no GEMM kernel yet", quant & 0xffu);
+    if (!x || !out || m == 0 || x_len != m * k || out_len < m * rows) return fail(d, "bad buffers");
+    if (!ensure_pair(d, d->d_x, d->h_x, d->x_cap, m * k)) return false;
+    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, m * rows)) return false;
+    memcpy(d->h_x, x, m * k * sizeof(float));
+    if (!ok(d, hipMemcpyAsync(d->d_x, d->h_x, m * k * sizeof(float), hipMemcpyHostToDevice, d->stream), "stage x"))
+        return false;
+    if (!enqueue_gemm(d, r, quant, rows, k, m, d->d_x, d->d_y)) {
+        hipStreamSynchronize(d->stream);
+        return false;
+    }
+    return finish_sync(d, out, m * rows);
 }
 
-extern "C" bool zlm_gpu_mat_mul_resident(zlm_device* d, zlm_resident*, uint32_t quant, size_t, size_t, size_t,
-                                         const float*, size_t, float*, size_t) {
+extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void* w, size_t w_len, size_t rows,
+                                      size_t k, size_t m, const float* x, size_t x_len, float* out, size_t out_len) {
     if (!d || !d->avail) return false;
-    return fail(d, "matMulResident: quant %u has no GEMM kernel yet", quant & 0xffu);
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
+    if (qi->type != ZLM_GGML_Q4_0) return fail(d, "no GEMM kernel for quant %u", qi->type);
+    if (!w || rows == 0 || k == 0 || k % qi->block_elems) return fail(d, "bad shape");
+    const uint64_t nblk = static_cast<uint64_t>(rows) * (k / qi->block_elems);
+    const uint64_t need = nblk * qi->block_bytes;
+    if (w_len < need) return fail(d, "weight too short");
+    if (!ensure_bytes(d, d->s_raw, d->s_raw_cap, need)) return false;
+    if (!ok(d, hipMemcpyAsync(d->s_raw, w, need, hipMemcpyHostToDevice, d->stream), "stage weights")) return false;
+    zlm_resident view;
+    view.owner = d;
+    view.bytes = need;
+    view.layout = qi->type;
+    view.blocks = nblk;
+    if (!ensure_bytes(d, d->s_lay, d->s_lay_cap, layout_bytes(qi, nblk))) return false;
+    if (!convert_blocks(d, d->s_raw, nblk, qi, d->s_lay, &view.scales)) return false;
+    view.payload = d->s_lay;
+    const bool ran = zlm_gpu_mat_mul_resident(d, &view, quant, rows, k, m, x, x_len, out, out_len);
+    view.payload = nullptr;
+    view.scales = nullptr;
+    return ran;
 }
 
 extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, zlm_resident*, zlm_resident*,
@@ -769,6 +898,35 @@ extern "C" bool zlm_gpu_mat_vec_enqueue(zlm_device* d, zlm_resident* r, uint32_t
                                         const float* x_dev, float* y_dev) {
     if (!d || !d->avail) return false;
     return enqueue_gemv(d, r, quant, rows, k, x_dev, y_dev);
+}
+
+extern "C" bool zlm_gpu_mat_mul_enqueue(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
+                                        size_t m, const float* x_dev, float* out_dev) {
+    if (!d || !d->avail) return false;
+    return enqueue_gemm(d, r, quant, rows, k, m, x_dev, out_dev);
+}
+
+extern "C" bool zlm_gpu_time_mat_mul(zlm_device* d, zlm_resident* const* res, size_t n_res, uint32_t quant,
+                                     size_t rows, size_t k, size_t m, const float* x_dev, float* out_dev, int iters,
+                                     double* ms) {
+    if (!d || !d->avail || !res || n_res == 0 || iters < 1 || !ms) return false;
+    for (size_t i = 0; i < n_res; i++)  // layouts and scratch outside the timed region
+        if (!enqueue_gemm(d, res[i], quant, rows, k, m, x_dev, out_dev)) return false;
+    hipEvent_t e0, e1;
+    if (!ok(d, hipEventCreate(&e0), "event")) return false;
+    if (!ok(d, hipEventCreate(&e1), "event")) {
+        hipEventDestroy(e0);
+        return false;
+    }
+    bool good = ok(d, hipEventRecord(e0, d->stream), "record");
+    for (int i = 0; good && i < iters; i++) good = enqueue_gemm(d, res[i % n_res], quant, rows, k, m, x_dev, out_dev);
+    good = good && ok(d, hipEventRecord(e1, d->stream), "record") && ok(d, hipEventSynchronize(e1), "sync");
+    float t = 0.0f;
+    good = good && ok(d, hipEventElapsedTime(&t, e0, e1), "elapsed");
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    *ms = t;
+    return good;
 }
 
 extern "C" bool zlm_gpu_time_mat_vec(zlm_device* d, zlm_resident* const* res, size_t n_res, uint32_t quant,

@@ -136,6 +136,8 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_dev_copy": (B, [P, P, P, S]),
         "zlm_gpu_mat_vec_enqueue": (B, [P, P, U, S, S, P, P]),
         "zlm_gpu_time_mat_vec": (B, [P, P, S, U, S, S, P, P, ctypes.c_int, P]),
+        "zlm_gpu_mat_mul_enqueue": (B, [P, P, U, S, S, S, P, P]),
+        "zlm_gpu_time_mat_mul": (B, [P, P, S, U, S, S, S, P, P, ctypes.c_int, P]),
         "zlm_gpu_time_gemv_sequence": (B, [P, P, S, ctypes.c_int, P]),
         "zlm_gpu_dequant_resident": (B, [P, P, U, S, P]),
         "zlm_gpu_quantize_act_q8": (B, [P, P, S, P, P, P]),
@@ -368,6 +370,19 @@ class Device:
         ms = ctypes.c_double(0.0)
         if not self._L.zlm_gpu_time_mat_vec(self._h, ctypes.addressof(arr), len(residents), quant, rows, k, x_dev,
                                             y_dev, iters, ctypes.addressof(ms)):
+            raise RuntimeError(self.last_error())
+        return ms.value
+
+    def mat_mul_enqueue(self, res: Resident, quant: int, rows: int, k: int, m: int, x_dev: int, out_dev: int) -> bool:
+        return bool(self._L.zlm_gpu_mat_mul_enqueue(self._h, res.ptr, quant, rows, k, m, x_dev, out_dev))
+
+    def time_mat_mul(self, residents: Sequence[Resident], quant: int, rows: int, k: int, m: int, x_dev: int,
+                     out_dev: int, iters: int) -> float:
+        """GPU milliseconds for `iters` prefill GEMMs (quantizer + GEMM) rotating over `residents`."""
+        arr = (ctypes.c_void_p * len(residents))(*[r.ptr for r in residents])
+        ms = ctypes.c_double(0.0)
+        if not self._L.zlm_gpu_time_mat_mul(self._h, ctypes.addressof(arr), len(residents), quant, rows, k, m, x_dev,
+                                            out_dev, iters, ctypes.addressof(ms)):
             raise RuntimeError(self.last_error())
         return ms.value
 
