@@ -221,6 +221,29 @@ typedef struct {
 /* Enqueue descs[0..n) in order, `iters` times, between two HIP events on the
  * device stream; *ms = elapsed GPU milliseconds between the events. */
 bool zlm_gpu_time_gemv_sequence(zlm_device *dev, const zlm_gemv_desc *descs, size_t n, int iters, double *ms);
+/* GEMV forms of zlm_gemv_op; every form reads x from device memory:
+ *   PLAIN     y = W x
+ *   PAIR      y[r] = act(W x, W_up x)[r]             (the fused gate_up)
+ *   NORM      y = W n,  n = RMSNorm(x, norm_w, eps)  (norm.zig:26-37)
+ *   NORMPAIR  y[r] = act(W n, W_up n)[r]
+ *   RESID     y = res + W x (res may alias y) */
+enum { ZLM_FORM_PLAIN = 0, ZLM_FORM_PAIR = 1, ZLM_FORM_NORM = 2, ZLM_FORM_NORMPAIR = 3, ZLM_FORM_RESID = 4 };
+typedef struct {
+    uint32_t form;
+    uint32_t quant;     /* ZLM_QUANT(type, variant); W and W_up share it */
+    zlm_resident *w;    /* rows x k (the gate for the pair forms) */
+    zlm_resident *w_up; /* pair forms: the up projection, rows x k */
+    size_t rows;
+    size_t k;
+    const float *x;      /* device, k floats */
+    const float *norm_w; /* device, k floats (norm forms) */
+    float eps;           /* norm forms */
+    uint32_t act;        /* pair forms: ZLM_ACT_SILU or ZLM_ACT_GELU */
+    const float *res;    /* device, rows floats (RESID) */
+    float *y;            /* device, rows floats */
+} zlm_gemv_op;
+/* Enqueue one GEMV op on the device stream (no host copies, no wait). */
+bool zlm_gpu_gemv_op_enqueue(zlm_device *dev, const zlm_gemv_op *op);
 /* Dequantize the first n_elements of a resident from its device layout into host `out`. */
 bool zlm_gpu_dequant_resident(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t n_elements, float *out);
 /* Quantize host x (n floats, n % 32 == 0) to q8 blocks on the device. */

@@ -56,12 +56,13 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
 
 
-def test_code_object_built_for_gfx950():
-    assert os.path.exists(zd.CODE_OBJECT_PATH)
-    blob = open(zd.CODE_OBJECT_PATH, "rb").read()
-    # hipcc --genco writes an offload bundle around the gfx950 ELF
-    assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
-    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+def test_code_objects_built_for_gfx950():
+    for path in zd.CODE_OBJECT_PATHS:
+        assert os.path.exists(path), path
+        blob = open(path, "rb").read()
+        # hipcc --genco writes an offload bundle around the gfx950 ELF
+        assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+        assert b"amdgcn-amd-amdhsa--gfx950" in blob
 
 
 def test_quant_encoding():

@@ -1,0 +1,205 @@
+"""GPU parity of the fused GEMV forms through the C ABI.
+
+Contract ops (reference gpu/backend/vulkan/root.zig:150-194):
+  * matVecGateUpResidentBurstAsync: out[r] = act(gate_r . x, up_r . x), against
+    the oracle's fusedGateUpRows restatement (matvec/form/fused.zig:27-86);
+  * matVecMlpResidentBurstAsync / matVecMlpPairResidentBurstAsync: the SwiGLU
+    MLP down . act(gate . x, up . x) (fused.zig:387-413), against the oracle's
+    gate_up followed by its production GEMV.
+Device-level forms used by the decode step: RMSNorm folded into the GEMV
+(norm.zig:26-37, restated here in float64), the residual epilogue and the
+normed gate_up.  Bar: relative L2 <= 1e-3 (the reference GPU tests' shapes
+and activation, gpu/root_test.zig:180-326, use the same kernels).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.helpers import ref_x, rel_l2
+from zlm_amd import device as zd
+from zlm_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K]
+NAMES = {synth.Q4_0: "q4_0", synth.Q8_0: "q8_0", synth.Q4_K: "q4_k", synth.Q6_K: "q6_k"}
+REL_L2 = 1e-3
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _rmsnorm(x, w, eps):
+    """norm.zig:26-37 in float64: x * (1/sqrt(mean(x^2) + eps)) * w."""
+    x64 = x.astype(np.float64)
+    inv = 1.0 / np.sqrt(np.mean(x64 * x64) + eps)
+    return (x64 * inv * w.astype(np.float64)).astype(np.float32)
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("rows,k", [(64, 256), (333, 4096), (130, 3840), (96, 8192), (40, 12288)])
+@pytest.mark.parametrize("act", [zd.SILU, zd.GELU], ids=["silu", "gelu"])
+def test_gate_up_matches_oracle(dev, qt, rows, k, act):
+    if k % synth.BLOCK_ELEMS[qt]:
+        pytest.skip("k not a multiple of the block")
+    _say(f"gate_up {NAMES[qt]} rows={rows} k={k} act={act}")
+    wg = synth.weights(qt, rows, k, seed=rows + k)
+    wu = synth.weights(qt, rows, k, seed=rows + k + 1)
+    x = synth.activation(k + 3, k)
+    want = oracle.gate_up(qt, wg, wu, k, rows, x, act)
+    rg, ru = dev.upload_resident(wg), dev.upload_resident(wu)
+    h = dev.mat_vec_gate_up_resident_burst_async(rg, ru, zd.quant(qt), rows, k, x, act, zd.PLAIN, True)
+    assert h is not None, dev.last_error()
+    out = np.full(rows, np.nan, np.float32)
+    assert dev.wait_resident(h, out, rows), dev.last_error()
+    assert rel_l2(out, want) <= REL_L2
+    dev.free_resident(rg)
+    dev.free_resident(ru)
+
+
+def test_gate_up_reference_shape(dev):
+    """The reference GPU test's gate_up case: 64 rows x k=256 q4_0, x[i] = (i%11)*0.1-0.5."""
+    rows, k = 64, 256
+    wg = synth.weights(synth.Q4_0, rows, k, seed=5)
+    wu = synth.weights(synth.Q4_0, rows, k, seed=6)
+    x = ref_x(k)
+    for act in (zd.SILU, zd.GELU):
+        want = oracle.gate_up(synth.Q4_0, wg, wu, k, rows, x, act)
+        rg, ru = dev.upload_resident(wg), dev.upload_resident(wu)
+        h = dev.mat_vec_gate_up_resident_burst_async(rg, ru, zd.quant(zd.Q4_0), rows, k, x, act, zd.U4, True)
+        out = np.zeros(rows, np.float32)
+        assert h is not None and dev.wait_resident(h, out, rows), dev.last_error()
+        assert np.all(np.abs(out - want) <= 1e-4 + 1e-4 * np.abs(want))
+        dev.free_resident(rg)
+        dev.free_resident(ru)
+
+
+@pytest.mark.parametrize("gq,dq,rows,k,ffn", [
+    (synth.Q4_0, synth.Q4_0, 64, 256, 512),
+    (synth.Q4_0, synth.Q4_0, 4096, 4096, 12288),
+    (synth.Q8_0, synth.Q4_0, 256, 1024, 3072),
+    (synth.Q4_K, synth.Q6_K, 128, 3840, 15360),
+    (synth.Q6_K, synth.Q8_0, 96, 2048, 768),
+])
+def test_mlp_pair_matches_oracle(dev, gq, dq, rows, k, ffn):
+    _say(f"mlp {NAMES[gq]}/{NAMES[dq]} rows={rows} k={k} ffn={ffn}")
+    wg = synth.weights(gq, ffn, k, seed=ffn + 1)
+    wu = synth.weights(gq, ffn, k, seed=ffn + 2)
+    wd = synth.weights(dq, rows, ffn, seed=ffn + 3)
+    x = synth.activation(k + 7, k)
+    mid = oracle.gate_up(gq, wg, wu, k, ffn, x, zd.SILU)
+    want = oracle.matvec(dq, wd, ffn, rows, mid)
+    rg, ru, rd = dev.upload_resident(wg), dev.upload_resident(wu), dev.upload_resident(wd)
+    h = dev.mat_vec_mlp_pair_resident_burst_async(rg, ru, rd, zd.quant(gq), zd.quant(dq), rows, k, ffn, x,
+                                                  zd.SILU, zd.PLAIN, True)
+    assert h is not None, dev.last_error()
+    out = np.full(rows, np.nan, np.float32)
+    assert dev.wait_resident(h, out, rows), dev.last_error()
+    assert rel_l2(out, want) <= REL_L2
+    if gq == dq:
+        h = dev.mat_vec_mlp_resident_burst_async(rg, ru, rd, zd.quant(gq), rows, k, ffn, x, zd.SILU, zd.PLAIN,
+                                                 True)
+        out2 = np.zeros(rows, np.float32)
+        assert h is not None and dev.wait_resident(h, out2, rows), dev.last_error()
+        np.testing.assert_array_equal(out2, out)
+    for r in (rg, ru, rd):
+        dev.free_resident(r)
+
+
+def test_fused_ops_share_the_burst_activation(dev):
+    """A burst: a plain GEMV stages x (first), then gate_up and the MLP reuse it."""
+    rows, k, ffn = 128, 1024, 2048
+    w = synth.weights(synth.Q4_0, rows, k, seed=1)
+    wg = synth.weights(synth.Q4_0, ffn, k, seed=2)
+    wu = synth.weights(synth.Q4_0, ffn, k, seed=3)
+    wd = synth.weights(synth.Q4_0, rows, ffn, seed=4)
+    x = synth.activation(9, k)
+    r, rg, ru, rd = (dev.upload_resident(a) for a in (w, wg, wu, wd))
+    q = zd.quant(zd.Q4_0)
+    h0 = dev.mat_vec_resident_burst_async(r, q, rows, k, x, True)
+    h1 = dev.mat_vec_gate_up_resident_burst_async(rg, ru, q, ffn, k, x, zd.SILU, zd.PLAIN, False)
+    h2 = dev.mat_vec_mlp_resident_burst_async(rg, ru, rd, q, rows, k, ffn, x, zd.SILU, zd.PLAIN, False)
+    assert None not in (h0, h1, h2), dev.last_error()
+    o0, o1, o2 = np.zeros(rows, np.float32), np.zeros(ffn, np.float32), np.zeros(rows, np.float32)
+    assert dev.wait_resident(h2, o2, rows) and dev.wait_resident(h0, o0, rows) and dev.wait_resident(h1, o1, ffn)
+    assert rel_l2(o0, oracle.matvec(synth.Q4_0, w, k, rows, x)) <= REL_L2
+    mid = oracle.gate_up(synth.Q4_0, wg, wu, k, ffn, x, zd.SILU)
+    assert rel_l2(o1, mid) <= REL_L2
+    assert rel_l2(o2, oracle.matvec(synth.Q4_0, wd, ffn, rows, mid)) <= REL_L2
+    # a member with another activation than the burst's is refused
+    other = x.copy()
+    assert dev.mat_vec_gate_up_resident_burst_async(rg, ru, q, ffn, k, other, zd.SILU, zd.PLAIN, False) is None
+    for res in (r, rg, ru, rd):
+        dev.free_resident(res)
+
+
+def test_fused_ops_reject_bad_arguments(dev):
+    rows, k = 32, 256
+    wg = synth.weights(synth.Q4_0, rows, k, seed=1)
+    x = synth.activation(1, k)
+    rg, ru = dev.upload_resident(wg), dev.upload_resident(wg)
+    q = zd.quant(zd.Q4_0)
+    assert dev.mat_vec_gate_up_resident_burst_async(rg, ru, q, rows, k, x, 2, zd.PLAIN, True) is None  # act
+    assert dev.mat_vec_gate_up_resident_burst_async(rg, ru, q, rows + 1, k, x, zd.SILU, zd.PLAIN, True) is None
+    short = dev.upload_resident(wg[: len(wg) // 2].copy())
+    assert dev.mat_vec_mlp_resident_burst_async(rg, ru, short, q, rows, k, k, x, zd.SILU, zd.PLAIN, True) is None
+    h = dev.mat_vec_gate_up_resident_burst_async(rg, ru, q, rows, k, x, zd.SILU, zd.PLAIN, True)
+    out = np.zeros(rows, np.float32)
+    assert h is not None and dev.wait_resident(h, out, rows)  # still healthy
+    for r in (rg, ru, short):
+        dev.free_resident(r)
+
+
+def _dev_vec(dev, a):
+    p = dev.dev_malloc(a.nbytes)
+    dev.dev_upload(p, a)
+    return p
+
+
+@pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("rows,k", [(256, 4096), (100, 3840), (64, 2048)])
+def test_device_forms_match_oracle(dev, qt, rows, k):
+    """norm / resid / normpair forms on device buffers (the decode step's ops)."""
+    if k % synth.BLOCK_ELEMS[qt]:
+        pytest.skip("k not a multiple of the block")
+    _say(f"forms {NAMES[qt]} rows={rows} k={k}")
+    eps = 1e-6
+    w = synth.weights(qt, rows, k, seed=k + 11)
+    wu = synth.weights(qt, rows, k, seed=k + 12)
+    x = synth.activation(k + 13, k) * np.float32(3.0)
+    nw = (1.0 + 0.1 * synth.activation(k + 14, k)).astype(np.float32)
+    res = synth.activation(k + 15, rows)
+    rw, ru = dev.upload_resident(w), dev.upload_resident(wu)
+    xd, nwd, resd, yd = _dev_vec(dev, x), _dev_vec(dev, nw), _dev_vec(dev, res), dev.dev_malloc(rows * 4)
+    q = zd.quant(qt)
+    xn = _rmsnorm(x, nw, eps)
+    cases = [
+        (zd.FORM_NORM, dict(norm_w=nwd, eps=eps), oracle.matvec(qt, w, k, rows, xn)),
+        (zd.FORM_RESID, dict(res=resd), res + oracle.matvec(qt, w, k, rows, x)),
+        (zd.FORM_NORMPAIR, dict(norm_w=nwd, eps=eps, w_up=ru, act=zd.SILU),
+         oracle.gate_up(qt, w, wu, k, rows, xn, zd.SILU)),
+        (zd.FORM_PAIR, dict(w_up=ru, act=zd.GELU), oracle.gate_up(qt, w, wu, k, rows, x, zd.GELU)),
+        (zd.FORM_PLAIN, dict(), oracle.matvec(qt, w, k, rows, x)),
+    ]
+    for form, kw, want in cases:
+        assert dev.gemv_op_enqueue(form, q, rw, rows, k, xd, yd, **kw), dev.last_error()
+        got = np.zeros(rows, np.float32)
+        dev.dev_download(got, yd)
+        assert rel_l2(got, want) <= REL_L2, form
+    # the residual form in place (res aliases y), as the decode step uses it
+    dev.dev_upload(yd, res)
+    assert dev.gemv_op_enqueue(zd.FORM_RESID, q, rw, rows, k, xd, yd, res=yd), dev.last_error()
+    got = np.zeros(rows, np.float32)
+    dev.dev_download(got, yd)
+    assert rel_l2(got, res + oracle.matvec(qt, w, k, rows, x)) <= REL_L2
+    # missing buffers are refused
+    assert not dev.gemv_op_enqueue(zd.FORM_NORM, q, rw, rows, k, xd, yd)
+    assert not dev.gemv_op_enqueue(zd.FORM_PAIR, q, rw, rows, k, xd, yd)
+    for p in (xd, nwd, resd, yd):
+        dev.dev_free(p)
+    dev.free_resident(rw)
+    dev.free_resident(ru)

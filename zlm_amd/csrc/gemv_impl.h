@@ -1,0 +1,713 @@
+// gemv_impl.h -- shared device code of the gfx950 GEMV kernels (included by
+// each zlm_gemv_<quant>.hip instance file and by zlm_kernels.hip).
+//
+// Weight layouts in HBM (produced once by the repack kernels from the raw GGUF
+// blocks of reference src/kernels/linear/quant/types.zig:6-53):
+//   q4_0  payload [rows][nb][16 B nibbles]        + scales [rows][nb] f16
+//   q8_0  payload [rows][nb][32 B int8]           + scales [rows][nb] f16
+//   q6_k  payload [rows][nb][208 B ql|qh|sc]      + scales [rows][nb] f16
+//   q4_k  raw     [rows][nb][144 B]  (already a multiple of 16 B per block)
+// Every payload block is a whole number of 16-byte chunks, so the GEMV
+// streams it with 128-bit loads; a wavefront's 64 lanes read 1 KiB of
+// consecutive payload per load instruction.
+//
+// GEMV scheme (one kernel per quant, templated on the row tile RT, the chunk
+// steps per row STEPS and the x capacity KCAP):
+//   * each wave owns tiles of RT rows (grid-stride over tiles); lane l covers
+//     the row's 16-byte chunks l, l+64, ... (STEPS of them), and the wave
+//     issues all of a tile's loads before computing any, so a tile is one
+//     memory round trip;
+//   * the workgroup stages x (fp32) once into LDS, padded by one float4 per 32
+//     floats so 128-bit LDS reads of neighbouring lanes fall in distinct banks,
+//     plus the fp32 sum of every 16-element run of x.  x's global loads are
+//     issued before the first tile's weight loads and the prologue has no
+//     branches, so the staging barrier waits for x alone;
+//   * the x values a chunk needs are read from LDS once and applied to all RT
+//     rows; the nibble/byte bias (-8 for q4_0, -32 for q6_k) is folded
+//     through the run sums, so the inner loop is extract -> cvt -> fma in fp32;
+//   * the RT per-lane partials are reduced with a transposing butterfly (each
+//     shuffle stage halves the live values), one lane per row writes y.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+constexpr int kWave = 64;
+
+enum QType : int { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
+
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
+}
+
+__device__ __forceinline__ float ub(uint32_t w, int i) { return static_cast<float>((w >> (8 * i)) & 0xffu); }
+__device__ __forceinline__ float sb(uint32_t w, int i) {
+    return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * i)) >> 24);
+}
+
+// LDS position of x element e: one float4 of padding after every 32 floats.
+__device__ __forceinline__ int xpad(int e) { return e + ((e >> 5) << 2); }
+
+// LDS footprint of a staged x of capacity KCAP: the padded values plus one
+// dummy float4 (kDummy) and the run sums plus one dummy slot (index kRuns),
+// the targets of out-of-range threads' stores.
+template <int KCAP>
+struct XTile {
+    static constexpr int kDummy = KCAP + KCAP / 8;
+    static constexpr int kFloats = kDummy + 4;
+    static constexpr int kRuns = KCAP / 16;
+};
+
+// Staging of x[0..k) into LDS (padded) plus the sums of its 16-element runs,
+// in two phases, so a kernel can issue x's global loads first, then its weight
+// loads, and only then wait for x: loads complete in issue order, so x must be
+// requested before the weights or the LDS store would wait for the whole
+// weight tile.  Thread i holds float4 i (+ j*blockDim); the four consecutive
+// lanes that hold one run add their partials with two shuffles.  k is a
+// multiple of 32 and blockDim a multiple of 64, so a run never straddles two
+// waves.  NX = float4s of x per thread.
+template <int NX>
+struct XRegs {
+    float4 v[NX];
+};
+
+// Both phases are branch-free (clamped loads, selects, a dummy LDS slot for
+// out-of-range threads): a branch here would make the compiler wait for every
+// outstanding load, weights included, before the barrier.
+template <int NX>
+__device__ __forceinline__ void xload(const float* __restrict__ x, int k, XRegs<NX>& r) {
+    const int n4 = k >> 2;
+#pragma unroll
+    for (int j = 0; j < NX; j++) {
+        const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+        r.v[j] = reinterpret_cast<const float4*>(x)[min(i, n4 - 1)];
+    }
+}
+
+template <int KCAP, int NX>
+__device__ __forceinline__ void xstore(const XRegs<NX>& r, int k, float* xl, float* xs) {
+    const int n4 = k >> 2;
+#pragma unroll
+    for (int j = 0; j < NX; j++) {
+        const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+        const bool valid = i < n4;
+        float4 v = r.v[j];
+        v.x = valid ? v.x : 0.0f;
+        v.y = valid ? v.y : 0.0f;
+        v.z = valid ? v.z : 0.0f;
+        v.w = valid ? v.w : 0.0f;
+        *reinterpret_cast<float4*>(xl + (valid ? xpad(i << 2) : XTile<KCAP>::kDummy)) = v;
+        float s = (v.x + v.y) + (v.z + v.w);
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        xs[(valid && (i & 3) == 0) ? (i >> 2) : XTile<KCAP>::kRuns] = s;
+    }
+    __syncthreads();
+}
+
+// xstore with RMSNorm folded in (reference kernels/transformer/norm.zig:26-37:
+// out = x * (1/sqrt(mean(x^2) + eps)) * w).  LDS receives x*w; the scalar
+// 1/sqrt(mean(x^2)+eps) is returned and applied to the row sums, so the norm
+// costs no pass of its own.  Every workgroup reduces the same per-wave partials
+// in the same order, so all of them use the same scale.  `red` holds one float
+// per wave.
+template <int KCAP, int NX, int WAVES>
+__device__ __forceinline__ float xstore_norm(const XRegs<NX>& r, const XRegs<NX>& g, int k, float eps, float* xl,
+                                             float* xs, float* red) {
+    const int n4 = k >> 2;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NX; j++) {
+        const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+        const bool valid = i < n4;
+        float4 v = r.v[j];
+        v.x = valid ? v.x : 0.0f;
+        v.y = valid ? v.y : 0.0f;
+        v.z = valid ? v.z : 0.0f;
+        v.w = valid ? v.w : 0.0f;
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+        v.x *= g.v[j].x;
+        v.y *= g.v[j].y;
+        v.z *= g.v[j].z;
+        v.w *= g.v[j].w;
+        *reinterpret_cast<float4*>(xl + (valid ? xpad(i << 2) : XTile<KCAP>::kDummy)) = v;
+        float s = (v.x + v.y) + (v.z + v.w);
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        xs[(valid && (i & 3) == 0) ? (i >> 2) : XTile<KCAP>::kRuns] = s;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < WAVES; w++) tot += red[w];
+    return 1.0f / sqrtf(tot / static_cast<float>(k) + eps);
+}
+
+__device__ __forceinline__ float4 lds4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
+// ---- per-quant fragments --------------------------------------------------
+// A fragment is what one lane loads for one 16-byte chunk position `c` of RT
+// rows; `load_frag` only issues global loads, `compute_frag` only touches
+// registers and LDS, so the main loop can keep the next fragment's loads in
+// flight while it computes the current one.
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) {
+    if constexpr (NT) {
+        const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+        return make_uint4(t.x, t.y, t.z, t.w);
+    } else {
+        return *reinterpret_cast<const uint4*>(p);
+    }
+}
+
+template <bool NT>
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) {
+    if constexpr (NT) {
+        const v2u t = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+        return make_uint2(t.x, t.y);
+    } else {
+        return *reinterpret_cast<const uint2*>(p);
+    }
+}
+
+template <bool NT>
+__device__ __forceinline__ uint32_t ld2(const uint16_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+template <int QT, int RT>
+struct Frag;
+
+template <int RT>
+struct Frag<Q4_0, RT> {
+    uint4 q[RT];
+    uint32_t d[RT];
+};
+template <int RT>
+struct Frag<Q8_0, RT> {
+    uint4 q[RT];
+    uint32_t d[RT];
+};
+template <int RT>
+struct Frag<Q4_K, RT> {
+    uint4 hd[RT];
+    uint4 q[RT];
+};
+template <int RT>
+struct Frag<Q6_K, RT> {
+    uint4 ql[RT];
+    uint4 qh[RT];
+    uint2 sc[RT];
+    uint32_t d[RT];
+};
+
+// q4_0: chunk c = block c (16 nibble bytes).  q8_0: chunk c = half block c
+// (16 int8; block c/2 holds the scale).  q4_k / q6_k: 8 chunks per 256-element
+// super-block (c>>3), see the compute steps.
+// The rows a wave tile covers: for each of its RT fragment rows, the matrix
+// (payload and scales) and the row index.  A plain tile is RT consecutive rows
+// of one matrix; a pair tile (fused gate_up) is RT/2 rows of the gate matrix
+// followed by the same RT/2 rows of the up matrix.
+template <int RT>
+struct TileRows {
+    const uint8_t* w[RT];
+    const uint16_t* d[RT];
+    uint32_t r[RT];
+};
+
+template <int QT, int RT, bool NT>
+__device__ __forceinline__ void load_frag(Frag<QT, RT>& f, const TileRows<RT>& tr, uint32_t nb, int c) {
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const uint8_t* __restrict__ w = tr.w[r];
+        const uint16_t* __restrict__ dsc = tr.d[r];
+        const size_t row = tr.r[r];
+        if constexpr (QT == Q4_0) {
+            const size_t bi = row * nb + c;
+            f.q[r] = ld16<NT>(w + bi * 16);
+            f.d[r] = ld2<NT>(dsc + bi);
+        } else if constexpr (QT == Q8_0) {
+            f.q[r] = ld16<NT>(w + (row * (2 * nb) + c) * 16);
+            f.d[r] = ld2<NT>(dsc + row * nb + (c >> 1));
+        } else if constexpr (QT == Q4_K) {
+            const uint8_t* blk = w + (row * nb + (c >> 3)) * 144;
+            f.hd[r] = ld16<false>(blk);
+            f.q[r] = ld16<NT>(blk + 16 + 16 * (c & 7));
+        } else {
+            const int p = c & 7, n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
+            const size_t bi = row * nb + (c >> 3);
+            const uint8_t* blk = w + bi * 208;
+            f.ql[r] = ld16<NT>(blk + 64 * n + 32 * ws + 16 * h);
+            f.qh[r] = ld16<false>(blk + 128 + 32 * n + 16 * h);
+            f.sc[r] = ld8<false>(blk + 192 + 8 * n);
+            f.d[r] = ld2<false>(dsc + bi);
+        }
+    }
+}
+
+// Byte j of a q4_0 block holds element j (low nibble) and j+16 (high);
+// value (nib-8)*d, and Sum (nib-8)*x = Sum nib*x - 8*Sum x.
+template <int RT>
+__device__ __forceinline__ void compute_q4_0(const Frag<Q4_0, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    const float* xb = xl + xpad(c << 5);
+    const float xsum = xs[2 * c] + xs[2 * c + 1];
+    float s[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) s[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = lds4(xb + 4 * i);
+        const float4 xh = lds4(xb + 16 + 4 * i);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint32_t wv = (&f.q[r].x)[i];
+            const uint32_t lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
+            s[r] = fmaf(ub(lo, 0), xa.x, s[r]);
+            s[r] = fmaf(ub(lo, 1), xa.y, s[r]);
+            s[r] = fmaf(ub(lo, 2), xa.z, s[r]);
+            s[r] = fmaf(ub(lo, 3), xa.w, s[r]);
+            s[r] = fmaf(ub(hi, 0), xh.x, s[r]);
+            s[r] = fmaf(ub(hi, 1), xh.y, s[r]);
+            s[r] = fmaf(ub(hi, 2), xh.z, s[r]);
+            s[r] = fmaf(ub(hi, 3), xh.w, s[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, fmaf(-8.0f, xsum, s[r]), acc[r]);
+}
+
+template <int RT>
+__device__ __forceinline__ void compute_q8_0(const Frag<Q8_0, RT>& f, const float* xl, const float*, int c,
+                                             bool valid, float* acc) {
+    const float* xb = xl + xpad(c << 4);
+    float s[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) s[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = lds4(xb + 4 * i);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint32_t wv = (&f.q[r].x)[i];
+            s[r] = fmaf(sb(wv, 0), xa.x, s[r]);
+            s[r] = fmaf(sb(wv, 1), xa.y, s[r]);
+            s[r] = fmaf(sb(wv, 2), xa.z, s[r]);
+            s[r] = fmaf(sb(wv, 3), xa.w, s[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, s[r], acc[r]);
+}
+
+// getScaleMinK4 (reference quant/k_quants.zig:24-32) on the 12 packed bytes
+// held as three dwords; j in 0..7, any lane-varying j.
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, float& sc, float& mn) {
+    const int t = (j & 3) * 8;
+    const uint32_t b0 = (s0 >> t) & 0xffu, b1 = (s1 >> t) & 0xffu, b2 = (s2 >> t) & 0xffu;
+    uint32_t d, m;
+    if (j < 4) {
+        d = b0 & 63u;
+        m = b1 & 63u;
+    } else {
+        d = (b2 & 15u) | ((b0 >> 6) << 4);
+        m = (b2 >> 4) | ((b1 >> 6) << 4);
+    }
+    sc = static_cast<float>(d);
+    mn = static_cast<float>(m);
+}
+
+// q4_k piece p = c&7 of super-block c>>3 (16 qs bytes of group g = p/2): low
+// nibbles are elements 64g + 16(p%2) + j (scale 2g), high nibbles +32 (scale
+// 2g+1); value d*sc*nib - dmin*mn.
+template <int RT>
+__device__ __forceinline__ void compute_q4_k(const Frag<Q4_K, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    const int sbk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
+    const int elo = 256 * sbk + 64 * g + 16 * h, ehi = elo + 32;
+    const float* xa_p = xl + xpad(elo);
+    const float* xb_p = xl + xpad(ehi);
+    const float xs_lo = xs[elo >> 4], xs_hi = xs[ehi >> 4];
+    float slo[RT], shi[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) slo[r] = shi[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = lds4(xa_p + 4 * i);
+        const float4 xb = lds4(xb_p + 4 * i);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint32_t wv = (&f.q[r].x)[i];
+            const uint32_t lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
+            slo[r] = fmaf(ub(lo, 0), xa.x, slo[r]);
+            slo[r] = fmaf(ub(lo, 1), xa.y, slo[r]);
+            slo[r] = fmaf(ub(lo, 2), xa.z, slo[r]);
+            slo[r] = fmaf(ub(lo, 3), xa.w, slo[r]);
+            shi[r] = fmaf(ub(hi, 0), xb.x, shi[r]);
+            shi[r] = fmaf(ub(hi, 1), xb.y, shi[r]);
+            shi[r] = fmaf(ub(hi, 2), xb.z, shi[r]);
+            shi[r] = fmaf(ub(hi, 3), xb.w, shi[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const uint32_t dd = valid ? f.hd[r].x : 0u;
+        const float d = h2f(dd), dmin = h2f(dd >> 16);
+        float sc1, mn1, sc2, mn2;
+        scale_min_k4(2 * g, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc1, mn1);
+        scale_min_k4(2 * g + 1, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc2, mn2);
+        float t = (d * sc1) * slo[r];
+        t = fmaf(d * sc2, shi[r], t);
+        t = fmaf(-(dmin * mn1), xs_lo, t);
+        t = fmaf(-(dmin * mn2), xs_hi, t);
+        acc[r] += t;
+    }
+}
+
+// q6_k part p = c&7 of super-block c>>3: half n = p/4, 16-run h, ql half ws;
+// low nibbles + qh bits 2ws are elements 128n + 32ws + 16h + j, high nibbles +
+// qh bits 4+2ws are those +64.  value d*sc*(q-32); Sum (q-32)*x = Sum q*x - 32*Sum x.
+template <int RT>
+__device__ __forceinline__ void compute_q6_k(const Frag<Q6_K, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    const int sbk = c >> 3, p = c & 7, n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
+    const int ea = 256 * sbk + 128 * n + 32 * ws + 16 * h, eb = ea + 64;
+    const float* xa_p = xl + xpad(ea);
+    const float* xb_p = xl + xpad(eb);
+    const float xs_a = xs[ea >> 4], xs_b = xs[eb >> 4];
+    const int sh_lo = 2 * ws, sh_hi = 4 + 2 * ws, sci = 8 * (h + 2 * ws);
+    float sa[RT], sbv[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) sa[r] = sbv[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = lds4(xa_p + 4 * i);
+        const float4 xb = lds4(xb_p + 4 * i);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
+            const uint32_t lo = (lw & 0x0F0F0F0Fu) | (((hw >> sh_lo) & 0x03030303u) << 4);
+            const uint32_t hi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> sh_hi) & 0x03030303u) << 4);
+            sa[r] = fmaf(ub(lo, 0), xa.x, sa[r]);
+            sa[r] = fmaf(ub(lo, 1), xa.y, sa[r]);
+            sa[r] = fmaf(ub(lo, 2), xa.z, sa[r]);
+            sa[r] = fmaf(ub(lo, 3), xa.w, sa[r]);
+            sbv[r] = fmaf(ub(hi, 0), xb.x, sbv[r]);
+            sbv[r] = fmaf(ub(hi, 1), xb.y, sbv[r]);
+            sbv[r] = fmaf(ub(hi, 2), xb.z, sbv[r]);
+            sbv[r] = fmaf(ub(hi, 3), xb.w, sbv[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const float d = valid ? h2f(f.d[r]) : 0.0f;
+        const float sc_a = static_cast<float>(static_cast<int32_t>(f.sc[r].x << (24 - sci)) >> 24);
+        const float sc_b = static_cast<float>(static_cast<int32_t>(f.sc[r].y << (24 - sci)) >> 24);
+        float t = (d * sc_a) * fmaf(-32.0f, xs_a, sa[r]);
+        t = fmaf(d * sc_b, fmaf(-32.0f, xs_b, sbv[r]), t);
+        acc[r] += t;
+    }
+}
+
+template <int QT, int RT>
+__device__ __forceinline__ void compute_frag(const Frag<QT, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    if constexpr (QT == Q4_0) compute_q4_0<RT>(f, xl, xs, c, valid, acc);
+    if constexpr (QT == Q8_0) compute_q8_0<RT>(f, xl, xs, c, valid, acc);
+    if constexpr (QT == Q4_K) compute_q4_k<RT>(f, xl, xs, c, valid, acc);
+    if constexpr (QT == Q6_K) compute_q6_k<RT>(f, xl, xs, c, valid, acc);
+}
+
+// Prologue / epilogue forms of the GEMV (template parameters PRO and EPI).
+//   PRO_PLAIN  x staged as is
+//   PRO_NORM   RMSNorm(x, xw, eps) folded in (xstore_norm)
+//   EPI_PLAIN  y[r] = row sum
+//   EPI_RESID  y[r] = res[r] + row sum (res may alias y: one lane reads and
+//              writes each row)
+//   EPI_PAIR   fused gate_up: y[r] = act(gate row r . x, up row r . x)
+enum : int { PRO_PLAIN = 0, PRO_NORM = 1 };
+enum : int { EPI_PLAIN = 0, EPI_RESID = 1, EPI_PAIR = 2 };
+
+// Kernel arguments of every GEMV form, passed by value.
+struct GemvArgs {
+    const uint8_t* w0;   // payload (the gate matrix for EPI_PAIR)
+    const uint16_t* d0;  // split f16 scales (unused for q4_k)
+    const uint8_t* w1;   // EPI_PAIR: the up matrix
+    const uint16_t* d1;
+    const float* x;
+    const float* xw;     // PRO_NORM: the norm weight, k floats
+    float* y;
+    const float* res;    // EPI_RESID
+    uint32_t rows;       // output rows
+    uint32_t nb;         // blocks per row
+    float eps;           // PRO_NORM
+    uint32_t act;        // EPI_PAIR: 0 silu, 1 gelu_tanh (reference GateUpAct)
+};
+
+// ActivationKind.apply (reference kernels/transformer/activation.zig:8-13).
+__device__ __forceinline__ float gate_act(uint32_t act, float g, float u) {
+    if (act == 1u) {
+        const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+        return (0.5f * g * (1.0f + tanhf(inner))) * u;
+    }
+    return (g / (1.0f + expf(-g))) * u;
+}
+
+template <int RT, bool PAIR>
+__device__ __forceinline__ TileRows<RT> tile_rows(const GemvArgs& a, uint32_t t) {
+    constexpr int RP = PAIR ? RT / 2 : RT;
+    TileRows<RT> tr;
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const bool second = PAIR && r >= RP;
+        tr.w[r] = second ? a.w1 : a.w0;
+        tr.d[r] = second ? a.d1 : a.d0;
+        tr.r[r] = min(t * RP + static_cast<uint32_t>(r % RP), a.rows - 1);
+    }
+    return tr;
+}
+
+// Reduce RT per-lane partials over the wavefront and store the tile's rows.
+// Stage s exchanges across lane bit (5-s) and keeps half of the live values,
+// so RT values cost RT-1 + (6-log2 RT) shuffles instead of 6*RT.  Afterwards
+// fragment row i's sum sits in lanes [i*64/RT, (i+1)*64/RT); for a pair tile
+// the up row of gate row i is row i + RT/2, i.e. 32 lanes up.
+template <int RT, int EPI>
+__device__ __forceinline__ void reduce_store(float* v, const GemvArgs& a, uint32_t t, float scale, int lane) {
+    constexpr int LOG = (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
+#pragma unroll
+    for (int st = 0; st < LOG; st++) {
+        const int half = (RT >> st) >> 1;
+        const int bit = 32 >> st;
+        const bool upper = (lane & bit) != 0;
+#pragma unroll
+        for (int i = 0; i < half; i++) {
+            const float keep = upper ? v[half + i] : v[i];
+            const float send = upper ? v[i] : v[half + i];
+            v[i] = keep + __shfl_xor(send, bit, kWave);
+        }
+    }
+    float s = v[0];
+#pragma unroll
+    for (int off = 32 >> LOG; off >= 1; off >>= 1) s += __shfl_xor(s, off, kWave);
+    s *= scale;
+    const uint32_t fr = static_cast<uint32_t>(lane >> (6 - LOG));  // fragment row of this lane
+    const bool leader = (lane & ((64 >> LOG) - 1)) == 0;
+    if constexpr (EPI == EPI_PAIR) {
+        static_assert(RT >= 2, "a pair tile holds a gate and an up row");
+        const float u = __shfl_xor(s, 32, kWave);
+        const uint32_t row = t * (RT / 2) + fr;
+        if (leader && fr < static_cast<uint32_t>(RT / 2) && row < a.rows) a.y[row] = gate_act(a.act, s, u);
+    } else {
+        const uint32_t row = t * RT + fr;
+        if (leader && row < a.rows) {
+            if constexpr (EPI == EPI_RESID) a.y[row] = a.res[row] + s;
+            else a.y[row] = s;
+        }
+    }
+}
+
+template <int QT>
+__device__ __forceinline__ int chunks_per_row(uint32_t nb) {
+    return (QT == Q4_0) ? static_cast<int>(nb) : (QT == Q8_0) ? static_cast<int>(2 * nb) : static_cast<int>(8 * nb);
+}
+
+template <int QT>
+__device__ __forceinline__ int elems_per_block() {
+    return (QT == Q4_0 || QT == Q8_0) ? 32 : 256;
+}
+
+// Issue the loads of chunk group `cb` (chunks cb + lane + 64*s, s < STEPS) of
+// a row tile.  Rows past the end are clamped to the last row (tile_rows) and
+// chunk positions past the row's end to its last chunk, so the loads are
+// branch-free; compute_group gives those a zero scale.  With EXACT the caller
+// guarantees STEPS == ceil(C/64) (one group); otherwise steps that start past
+// the row's end are skipped by a wave-uniform test.
+template <int QT, int RT, int STEPS, bool EXACT, bool NT>
+__device__ __forceinline__ void load_group(Frag<QT, RT> (&f)[STEPS], const TileRows<RT>& tr, uint32_t nb, int C,
+                                           int cb, int lane) {
+#pragma unroll
+    for (int s = 0; s < STEPS; s++)
+        if (EXACT || cb + s * kWave < C) load_frag<QT, RT, NT>(f[s], tr, nb, min(cb + lane + s * kWave, C - 1));
+}
+
+template <int QT, int RT, int STEPS, bool EXACT>
+__device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], const float* xl, const float* xs,
+                                              int C, int cb, int lane, float* acc) {
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+        const int c = cb + lane + s * kWave;
+        if (EXACT || cb + s * kWave < C) compute_frag<QT, RT>(f[s], xl, xs, min(c, C - 1), c < C, acc);
+    }
+}
+
+// One GEMV: y[r] = sum_k w[r,k] * x[k] for r < rows, k = nb * block_elems,
+// in the prologue/epilogue form PRO/EPI.  A wave owns row tiles
+// blockIdx*WAVES + wid + j*gridDim*WAVES.  For each tile it issues the loads
+// of every chunk step (64 consecutive 16-byte chunks per row per step) before
+// it computes any of them, so a tile costs one memory round trip (the generic
+// form, !EXACT, walks the row in groups of STEPS steps, one round trip per
+// group).  The first tile is peeled and kept branch-free: x's loads (and the
+// norm weight's), then the tile's loads, then x's LDS store and the barrier,
+// so the barrier waits for x only and step s computes as soon as its own loads
+// land.  Occupancy (several waves per SIMD) overlaps one wave's compute with
+// others' loads.
+template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT, int PRO, int EPI>
+__device__ __forceinline__ void gemv(const GemvArgs& a) {
+    __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
+    __shared__ float xs[XTile<KCAP>::kRuns + 1];
+    __shared__ float red[WAVES];
+    constexpr bool PAIR = EPI == EPI_PAIR;
+    constexpr int RP = PAIR ? RT / 2 : RT;  // output rows per tile
+    constexpr int NX = (KCAP / 4 + WAVES * kWave - 1) / (WAVES * kWave);
+    constexpr int GROUP = STEPS * kWave;    // chunks per group
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wid = threadIdx.x / kWave;
+    const int C = chunks_per_row<QT>(a.nb);
+    const uint32_t ntiles = (a.rows + RP - 1) / RP;
+    const uint32_t tstride = gridDim.x * WAVES;
+    uint32_t tile = blockIdx.x * WAVES + wid;
+
+    const int k = static_cast<int>(a.nb) * elems_per_block<QT>();
+    XRegs<NX> xr, gr;
+    xload(a.x, k, xr);
+    if constexpr (PRO == PRO_NORM) xload(a.xw, k, gr);
+    Frag<QT, RT> f[STEPS];
+    TileRows<RT> tr = tile_rows<RT, PAIR>(a, min(tile, ntiles - 1));
+    load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, 0, lane);
+    float scale = 1.0f;
+    if constexpr (PRO == PRO_NORM) scale = xstore_norm<KCAP, NX, WAVES>(xr, gr, k, a.eps, xl, xs, red);
+    else xstore<KCAP>(xr, k, xl, xs);
+
+    float acc[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+    compute_group<QT, RT, STEPS, EXACT>(f, xl, xs, C, 0, lane, acc);
+    if constexpr (!EXACT) {
+        for (int cb = GROUP; cb < C; cb += GROUP) {
+            load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
+            compute_group<QT, RT, STEPS, EXACT>(f, xl, xs, C, cb, lane, acc);
+        }
+    }
+    if (tile < ntiles) reduce_store<RT, EPI>(acc, a, tile, scale, lane);
+    for (tile += tstride; tile < ntiles; tile += tstride) {
+        tr = tile_rows<RT, PAIR>(a, tile);
+#pragma unroll
+        for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+        for (int cb = 0; cb < (EXACT ? 1 : C); cb += GROUP) {
+            load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
+            compute_group<QT, RT, STEPS, EXACT>(f, xl, xs, C, cb, lane, acc);
+        }
+        reduce_store<RT, EPI>(acc, a, tile, scale, lane);
+    }
+}
+}  // namespace
+
+// ---- GEMV entry points ---------------------------------------------------
+// zlm_gemv_<quant>_r<RT>_s<STEPS>: STEPS == ceil(chunks per row / 64) exactly
+// (q4_0 and the K-quants have k/32 chunks per row, q8_0 k/16), x capacity the
+// smallest of 4096/8192/16384/32768 that holds STEPS steps.
+// zlm_gemv_<quant>_r1_g: the generic form for any other k up to 32768 (walks
+// the row in groups of 4 steps, 8 for q8_0).
+// Every instance runs 4 waves (256 threads) per workgroup.
+
+#define ZLM_GEMV(NAME, QT, KCAP, RT, STEPS, EXACT)                                                        \
+    extern "C" __global__ void __launch_bounds__(256)                                                    \
+        NAME(const uint8_t* __restrict__ w, const uint16_t* __restrict__ dsc, const float* __restrict__ x, \
+             float* __restrict__ y, uint32_t rows, uint32_t nb) {                                        \
+        GemvArgs a = {w, dsc, w, dsc, x, x, y, y, rows, nb, 0.0f, 0u};                                  \
+        gemv<QT, KCAP, 4, RT, STEPS, EXACT, true, PRO_PLAIN, EPI_PLAIN>(a);                             \
+    }
+
+// The fused forms take one GemvArgs: zlm_gemv_<quant>_<form>_s<STEPS> (exact
+// steps) and zlm_gemv_<quant>_<form>_g<STEPS> (generic), form one of
+//   pair      gate_up: act(gate.x) * (up.x), one gate and one up row per tile
+//   norm      RMSNorm(x) then the GEMV
+//   normpair  RMSNorm(x) then gate_up
+//   resid     y = res + W.x
+#define ZLM_GEMVX(NAME, QT, KCAP, RT, STEPS, EXACT, PRO, EPI)                        \
+    extern "C" __global__ void __launch_bounds__(256) NAME(GemvArgs a) {            \
+        gemv<QT, KCAP, 4, RT, STEPS, EXACT, true, PRO, EPI>(a);                     \
+    }
+#define ZLM_GEMVX_FORMS(QN, QT, KCAP, STEPS, EXACT, SFX)                                           \
+    ZLM_GEMVX(zlm_gemv_##QN##_pair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_PLAIN, EPI_PAIR)           \
+    ZLM_GEMVX(zlm_gemv_##QN##_norm_##SFX, QT, KCAP, 1, STEPS, EXACT, PRO_NORM, EPI_PLAIN)           \
+    ZLM_GEMVX(zlm_gemv_##QN##_normpair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_NORM, EPI_PAIR)        \
+    ZLM_GEMVX(zlm_gemv_##QN##_resid_##SFX, QT, KCAP, 1, STEPS, EXACT, PRO_PLAIN, EPI_RESID)
+
+// q4_0 / q4_k / q6_k: KCAP = 2048 * STEPS rounded up to a tier.
+#define ZLM_GEMV_Q4(QN, QT)                                         \
+    ZLM_GEMV_Q4_COMMON(QN, QT)                                      \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s6, QT, 16384, 2, 6, true)
+
+// The K-quants keep RT 1 from 6 steps up (their fragments are larger).
+#define ZLM_GEMV_Q4_COMMON(QN, QT)                                  \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s1, QT, 4096, 1, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s1, QT, 4096, 2, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s1, QT, 4096, 4, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s2, QT, 4096, 1, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s2, QT, 4096, 2, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s2, QT, 4096, 4, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s3, QT, 8192, 1, 3, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s3, QT, 8192, 2, 3, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s3, QT, 8192, 4, 3, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s4, QT, 8192, 1, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s4, QT, 8192, 2, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s4, QT, 8192, 4, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s6, QT, 16384, 1, 6, true)          \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s8, QT, 16384, 1, 8, true)          \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_g, QT, 32768, 1, 4, false)
+
+// q8_0: KCAP = 1024 * STEPS rounded up to a tier.
+#define ZLM_GEMV_Q8(QN, QT)                                         \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s1, QT, 4096, 1, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s1, QT, 4096, 2, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s1, QT, 4096, 4, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s2, QT, 4096, 1, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s2, QT, 4096, 2, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s2, QT, 4096, 4, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s3, QT, 4096, 1, 3, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s3, QT, 4096, 2, 3, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s3, QT, 4096, 4, 3, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s4, QT, 4096, 1, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s4, QT, 4096, 2, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s4, QT, 4096, 4, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s6, QT, 8192, 1, 6, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s6, QT, 8192, 2, 6, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s8, QT, 8192, 1, 8, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s8, QT, 8192, 2, 8, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s12, QT, 16384, 1, 12, true)        \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s12, QT, 16384, 2, 12, true)        \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s15, QT, 16384, 1, 15, true)        \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s16, QT, 16384, 1, 16, true)        \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_g, QT, 32768, 1, 8, false)
+
+// Fused forms: q4_0 / q4_k / q6_k at 1-4 steps (k <= 8192; q4_0 also at 6
+// steps, k = 12288, where the K-quants' larger fragments would spill), q8_0
+// at 2-4, 6, 8 and 12 steps, plus the generic forms.
+#define ZLM_GEMVX_Q4(QN, QT)                          \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 1, true, s1)        \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 2, true, s2)        \
+    ZLM_GEMVX_FORMS(QN, QT, 8192, 3, true, s3)        \
+    ZLM_GEMVX_FORMS(QN, QT, 8192, 4, true, s4)        \
+    ZLM_GEMVX_FORMS(QN, QT, 32768, 4, false, g)
+#define ZLM_GEMVX_Q8(QN, QT)                          \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 2, true, s2)        \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 3, true, s3)        \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 4, true, s4)        \
+    ZLM_GEMVX_FORMS(QN, QT, 8192, 6, true, s6)        \
+    ZLM_GEMVX_FORMS(QN, QT, 8192, 8, true, s8)        \
+    ZLM_GEMVX_FORMS(QN, QT, 16384, 12, true, s12)     \
+    ZLM_GEMVX_FORMS(QN, QT, 32768, 8, false, g)

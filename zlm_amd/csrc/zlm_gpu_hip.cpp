@@ -1,8 +1,10 @@
 // zlm_gpu_hip.cpp -- host side of the MI355X backend: the C ABI declared in
 // include/zlm_gpu_hip.h over the HIP runtime.
 //
-// The kernels live in a gfx950 code object (zlm_kernels_gfx950.hsaco, next to
-// this library, or $ZLM_HIP_CODE_OBJECT) loaded with hipModuleLoad.  One HIP
+// The kernels live in gfx950 code objects next to this library, loaded with
+// hipModuleLoad: zlm_kernels_gfx950.hsaco (layout, dequant, quantizer, GEMM,
+// decode glue; $ZLM_HIP_CODE_OBJECT overrides its path) and one
+// zlm_gemv_<quant>_gfx950.hsaco per quant with that quant's GEMV forms.  One HIP
 // stream per device carries every copy and launch in order, so a burst's
 // shared activation and a resident's layout conversion are ordered before the
 // kernels that read them without extra synchronisation.
@@ -83,7 +85,7 @@ int rt_for_variant(uint32_t v) {
     }
 }
 
-// A resolved GEMV kernel and its launch bound.
+// A resolved GEMV kernel: rows per tile and exact steps (0 = generic).
 struct GemvKernel {
     hipFunction_t fn = nullptr;
     int rt = 0;
@@ -128,7 +130,8 @@ struct zlm_device {
     char name[256] = "off";
     std::string err;
 
-    hipModule_t mod = nullptr;
+    hipModule_t mod = nullptr;          // zlm_kernels_gfx950.hsaco
+    hipModule_t gemv_mod[4] = {};       // zlm_gemv_<quant>_gfx950.hsaco, by QuantInfo::slot
     std::map<std::string, GemvKernel> gemv;  // by entry-point name; null fn = absent
     hipFunction_t repack = nullptr;
     hipFunction_t dequant[4] = {};
@@ -158,6 +161,11 @@ struct zlm_device {
     uint8_t* s_lay = nullptr;  // streamed-weight staging (device layout)
     uint64_t s_lay_cap = 0;
 
+    // the fused MLP's ffn_mid (device side; the host half is unused)
+    float* d_mid = nullptr;
+    float* h_mid = nullptr;
+    size_t mid_cap = 0;
+
     // burst-shared activation
     float* d_bx = nullptr;
     float* h_bx = nullptr;
@@ -185,22 +193,37 @@ bool ok(zlm_device* d, hipError_t e, const char* what) {
     return fail(d, "%s: %s", what, hipGetErrorString(e));
 }
 
-std::string code_object_path() {
-    if (const char* env = getenv("ZLM_HIP_CODE_OBJECT")) return env;
+// Directory of this library (the code objects sit beside it).
+std::string library_dir() {
     Dl_info info;
     if (dladdr(reinterpret_cast<void*>(&zlm_gpu_init), &info) && info.dli_fname) {
         std::string p(info.dli_fname);
         size_t slash = p.rfind('/');
-        std::string dir = (slash == std::string::npos) ? "." : p.substr(0, slash);
-        return dir + "/zlm_kernels_gfx950.hsaco";
+        return (slash == std::string::npos) ? "." : p.substr(0, slash);
     }
-    return "zlm_kernels_gfx950.hsaco";
+    return ".";
+}
+
+void unload_modules(zlm_device* d) {
+    if (d->mod) hipModuleUnload(d->mod);
+    d->mod = nullptr;
+    for (hipModule_t& m : d->gemv_mod) {
+        if (m) hipModuleUnload(m);
+        m = nullptr;
+    }
+    d->gemv.clear();
 }
 
 bool load_kernels(zlm_device* d) {
-    const std::string path = code_object_path();
+    const std::string dir = library_dir();
+    const char* env = getenv("ZLM_HIP_CODE_OBJECT");
+    const std::string path = env ? std::string(env) : dir + "/zlm_kernels_gfx950.hsaco";
     if (!ok(d, hipModuleLoad(&d->mod, path.c_str()), path.c_str())) return false;
     char nm[128];
+    for (int q = 0; q < 4; q++) {
+        const std::string gp = dir + "/zlm_gemv_" + kQuantNames[q] + "_gfx950.hsaco";
+        if (!ok(d, hipModuleLoad(&d->gemv_mod[q], gp.c_str()), gp.c_str())) return false;
+    }
     for (int q = 0; q < 4; q++) {
         snprintf(nm, sizeof nm, "zlm_dequant_%s", kQuantNames[q]);
         if (!ok(d, hipModuleGetFunction(&d->dequant[q], d->mod, nm), nm)) return false;
@@ -301,12 +324,12 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
     return true;
 }
 
-// Look up (and cache) a GEMV entry point by name.
-const GemvKernel* find_gemv(zlm_device* d, const char* name, int rt, int steps) {
+// Look up (and cache) a GEMV entry point by name in its quant's code object.
+const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps) {
     auto it = d->gemv.find(name);
     if (it == d->gemv.end()) {
         GemvKernel g;
-        if (hipModuleGetFunction(&g.fn, d->mod, name) == hipSuccess) {
+        if (hipModuleGetFunction(&g.fn, d->gemv_mod[slot], name) == hipSuccess) {
             g.rt = rt;
             g.steps = steps;
         } else {
@@ -328,19 +351,16 @@ const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
     snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d", qn, rt, steps);
-    if (const GemvKernel* g = find_gemv(d, nm, rt, steps)) return g;
+    if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d", qn, steps);
-    if (const GemvKernel* g = find_gemv(d, nm, 1, steps)) return g;
-    snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_g%d", qn, qi->type == ZLM_GGML_Q8_0 ? 32 : 16);
-    return find_gemv(d, nm, 1, steps);
+    if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps)) return g;
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_g", qn);
+    return find_gemv(d, qi->slot, nm, 1, 0);
 }
 
-// Validate a GEMV over resident `r` and pick its kernel.
-bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, hipFunction_t* f,
-                  unsigned* grid, unsigned* block) {
-    if (!d || !d->avail) return fail(d, "device unavailable");
-    const QuantInfo* qi = quant_info(quant);
-    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
+// Validate resident `r` as a rows x k weight of quant `qi` and make sure its
+// device layout exists.
+bool check_resident(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t rows, size_t k) {
     if (!r) return fail(d, "null resident");
     if (rows == 0 || k == 0 || k % qi->block_elems != 0) return fail(d, "bad shape rows=%zu k=%zu", rows, k);
     if (rows > 0xffffffffu) return fail(d, "rows too large");
@@ -349,16 +369,31 @@ bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     if (r->bytes < rows * nb * qi->block_bytes) return fail(d, "resident too short");
     if (!ensure_layout(d, r, qi)) return false;
     if (r->blocks < rows * nb) return fail(d, "resident layout too short");
+    return true;
+}
+
+// Grid of a GEMV launch: one wave per tile up to a per-CU cap.  Measured on
+// gfx950: up to 4 steps per row (k <= 4096 for q8_0, 8192 for the others) a
+// grid of 4 workgroups per CU is best; wider rows stage a larger x in LDS and
+// one workgroup per CU looping over tiles is best.  steps 0 = the generic
+// instance (32768-float x capacity, one workgroup per CU).
+unsigned gemv_grid(const zlm_device* d, uint64_t tiles, int steps) {
+    const uint64_t wgs = (tiles + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
+    const uint64_t cap = static_cast<uint64_t>(d->cus) * ((steps == 0 || steps > 4) ? 1 : 4);
+    return static_cast<unsigned>(std::min<uint64_t>(wgs, cap));
+}
+
+// Validate a GEMV over resident `r` and pick its kernel.
+bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, hipFunction_t* f,
+                  unsigned* grid, unsigned* block) {
+    if (!d || !d->avail) return fail(d, "device unavailable");
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
+    if (!check_resident(d, r, qi, rows, k)) return false;
     const GemvKernel* gk = pick_gemv(d, qi, k, rt_for_variant(variant_of(quant)));
     if (!gk) return fail(d, "no GEMV kernel for quant %u k=%zu", qi->type, k);
     *f = gk->fn;
-    const uint64_t tiles = (rows + gk->rt - 1) / gk->rt;
-    const uint64_t wgs = (tiles + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
-    // Measured on gfx950: up to 4 steps per row (k <= 4096 for q8_0, 8192 for
-    // the others) a grid of 4 workgroups per CU is best; wider rows stage a
-    // larger x in LDS and one workgroup per CU looping over tiles is best.
-    const uint64_t cap = static_cast<uint64_t>(d->cus) * (gk->steps > 4 ? 1 : 4);
-    *grid = static_cast<unsigned>(std::min<uint64_t>(wgs, cap));
+    *grid = gemv_grid(d, (rows + gk->rt - 1) / gk->rt, gk->steps);
     *block = kGemvThreads;
     return true;
 }
@@ -374,6 +409,81 @@ bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->block_elems);
     void* args[] = {&w, &s, &x_dev, &y_dev, &rows32, &nb};
     return launch(d, f, grid, block, args, "gemv");
+}
+
+// ---- fused GEMV forms (prologue/epilogue variants of the same kernel) ----
+
+const char* const kFormNames[] = {"plain", "pair", "norm", "normpair", "resid"};
+
+bool form_is_pair(uint32_t form) { return form == ZLM_FORM_PAIR || form == ZLM_FORM_NORMPAIR; }
+bool form_is_norm(uint32_t form) { return form == ZLM_FORM_NORM || form == ZLM_FORM_NORMPAIR; }
+
+// Kernel-argument block of the fused forms; the same layout as GemvArgs in
+// gemv_impl.h (passed by value as the kernel's only argument).
+struct GemvArgsHost {
+    const uint8_t* w0;
+    const uint16_t* d0;
+    const uint8_t* w1;
+    const uint16_t* d1;
+    const float* x;
+    const float* xw;
+    float* y;
+    const float* res;
+    uint32_t rows;
+    uint32_t nb;
+    float eps;
+    uint32_t act;
+};
+static_assert(sizeof(GemvArgsHost) == 80, "GemvArgs layout");
+
+// The fused-form kernel for a shape: the exact-steps instance, else the
+// generic one.
+const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form) {
+    const size_t chunks = (qi->type == ZLM_GGML_Q8_0) ? k / 16 : k / 32;
+    const int steps = static_cast<int>((chunks + 63) / 64);
+    const int rt = form_is_pair(form) ? 2 : 1;
+    const char* qn = kQuantNames[qi->slot];
+    char nm[96];
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d", qn, kFormNames[form], steps);
+    if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_g", qn, kFormNames[form]);
+    return find_gemv(d, qi->slot, nm, rt, 0);
+}
+
+// Enqueue one GEMV op on device buffers: validate the residents, pick the
+// kernel of the op's form and launch it on the device stream.
+bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
+    if (!d || !d->avail) return fail(d, "device unavailable");
+    if (op.form > ZLM_FORM_RESID) return fail(d, "unknown GEMV form %u", op.form);
+    if (op.form == ZLM_FORM_PLAIN) {
+        if (!op.x || !op.y) return fail(d, "null buffer");
+        return enqueue_gemv(d, op.w, op.quant, op.rows, op.k, op.x, op.y);
+    }
+    const QuantInfo* qi = quant_info(op.quant);
+    if (!qi) return fail(d, "unsupported quant %u", op.quant & 0xffu);
+    const bool pair = form_is_pair(op.form);
+    if (!op.x || !op.y || (form_is_norm(op.form) && !op.norm_w) || (op.form == ZLM_FORM_RESID && !op.res))
+        return fail(d, "null buffer");
+    if (pair && op.act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", op.act);
+    if (!check_resident(d, op.w, qi, op.rows, op.k)) return false;
+    if (pair && !check_resident(d, op.w_up, qi, op.rows, op.k)) return false;
+    const GemvKernel* gk = pick_gemvx(d, qi, op.k, op.form);
+    if (!gk) return fail(d, "no %s GEMV kernel for quant %u k=%zu", kFormNames[op.form], qi->type, op.k);
+    GemvArgsHost a;
+    a.w0 = op.w->payload;
+    a.d0 = op.w->scales;
+    a.w1 = pair ? op.w_up->payload : op.w->payload;
+    a.d1 = pair ? op.w_up->scales : op.w->scales;
+    a.x = op.x;
+    a.xw = form_is_norm(op.form) ? op.norm_w : op.x;
+    a.y = op.y;
+    a.res = op.form == ZLM_FORM_RESID ? op.res : op.y;
+    a.rows = static_cast<uint32_t>(op.rows);
+    a.nb = static_cast<uint32_t>(op.k / qi->block_elems);
+    a.eps = op.eps;
+    a.act = op.act;
+    void* args[] = {&a};
+    return launch(d, gk->fn, gemv_grid(d, op.rows, gk->steps), kGemvThreads, args, kFormNames[op.form]);
 }
 
 zlm_resident* new_resident(zlm_device* d, const void* bytes, size_t len) {
@@ -571,8 +681,7 @@ extern "C" zlm_device* zlm_gpu_init(void) {
     }
     if (!load_kernels(d)) {
         std::string why = d->err;
-        if (d->mod) hipModuleUnload(d->mod);
-        d->mod = nullptr;
+        unload_modules(d);
         hipStreamDestroy(d->stream);
         d->stream = nullptr;
         snprintf(d->name, sizeof d->name, "off");
@@ -599,13 +708,15 @@ extern "C" void zlm_gpu_deinit(zlm_device* d) {
         if (d->h_x) hipHostFree(d->h_x);
         if (d->d_y) hipFree(d->d_y);
         if (d->h_y) hipHostFree(d->h_y);
+        if (d->d_mid) hipFree(d->d_mid);
+        if (d->h_mid) hipHostFree(d->h_mid);
         if (d->d_bx) hipFree(d->d_bx);
         if (d->h_bx) hipHostFree(d->h_bx);
         if (d->bx_copied) hipEventDestroy(d->bx_copied);
         if (d->s_raw) hipFree(d->s_raw);
         if (d->q_scratch) hipFree(d->q_scratch);
         if (d->s_lay) hipFree(d->s_lay);
-        if (d->mod) hipModuleUnload(d->mod);
+        unload_modules(d);
         hipStreamDestroy(d->stream);
     }
     delete d;
@@ -699,6 +810,77 @@ extern "C" int32_t zlm_gpu_mat_vec_resident_async(zlm_device* d, zlm_resident* r
     return make_handle(d, s);
 }
 
+namespace {
+
+// The burst-shared activation (reference pipeline.zig:1422-1484): `first`
+// stages x into the device-owned buffer, later members must pass the same x
+// pointer and length and reuse it.  Returns the device copy, or null.
+const float* stage_burst(zlm_device* d, const float* x, size_t x_len, bool first) {
+    if (first) {
+        // The previous burst's host->device copy must have consumed the pinned
+        // buffer before it is overwritten.
+        if (d->bx_copied && !ok(d, hipEventSynchronize(d->bx_copied), "burst wait")) return nullptr;
+        if (!ensure_pair(d, d->d_bx, d->h_bx, d->bx_cap, x_len)) return nullptr;
+        if (!d->bx_copied && !ok(d, hipEventCreateWithFlags(&d->bx_copied, hipEventDisableTiming), "event"))
+            return nullptr;
+        memcpy(d->h_bx, x, x_len * sizeof(float));
+        if (!ok(d, hipMemcpyAsync(d->d_bx, d->h_bx, x_len * sizeof(float), hipMemcpyHostToDevice, d->stream),
+                "stage burst x") ||
+            !ok(d, hipEventRecord(d->bx_copied, d->stream), "record")) {
+            d->burst_open = false;
+            return nullptr;
+        }
+        d->burst_src = x;
+        d->burst_len = x_len;
+        d->burst_open = true;
+    } else if (!d->burst_open || x != d->burst_src || x_len != d->burst_len) {
+        fail(d, "burst member does not match the burst's activation");
+        return nullptr;
+    }
+    return d->d_bx;
+}
+
+// Make slot `s` ready to receive `rows` floats.
+bool prepare_slot(zlm_device* d, int s, size_t rows) {
+    Slot& sl = d->slots[s];
+    size_t ycap = sl.y_cap;
+    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows)) return false;
+    sl.y_cap = ycap;
+    if (!sl.done && !ok(d, hipEventCreateWithFlags(&sl.done, hipEventDisableTiming), "event")) return false;
+    return true;
+}
+
+// Queue slot `s`'s read-back of `rows` floats and its completion event.
+bool finish_slot(zlm_device* d, int s, size_t rows) {
+    Slot& sl = d->slots[s];
+    if (!ok(d, hipMemcpyAsync(sl.h_y, sl.d_y, rows * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y"))
+        return false;
+    if (!ok(d, hipEventRecord(sl.done, d->stream), "record")) return false;
+    sl.rows = rows;
+    return true;
+}
+
+// The fused MLP behind both MLP contract ops: gate_up (pair form) into the
+// device-side ffn_mid, then the down GEMV into slot `s`.
+bool enqueue_mlp(zlm_device* d, int s, zlm_resident* rg, zlm_resident* ru, zlm_resident* rd, uint32_t gu_quant,
+                 uint32_t down_quant, size_t rows, size_t k, size_t ffn, const float* x_dev, uint32_t act) {
+    if (!ensure_pair(d, d->d_mid, d->h_mid, d->mid_cap, ffn)) return false;
+    zlm_gemv_op gu = {};
+    gu.form = ZLM_FORM_PAIR;
+    gu.quant = gu_quant;
+    gu.w = rg;
+    gu.w_up = ru;
+    gu.rows = ffn;
+    gu.k = k;
+    gu.x = x_dev;
+    gu.act = act;
+    gu.y = d->d_mid;
+    if (!enqueue_op(d, gu)) return false;
+    return enqueue_gemv(d, rd, down_quant, rows, ffn, d->d_mid, d->slots[s].d_y);
+}
+
+}  // namespace
+
 extern "C" int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device* d, zlm_resident* r, uint32_t quant,
                                                         size_t rows, size_t k, const float* x, size_t x_len,
                                                         bool first) {
@@ -709,27 +891,9 @@ extern "C" int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device* d, zlm_resid
     if (!prepare_gemv(d, r, quant, rows, k, &f, &g, &b)) return ZLM_NULL_HANDLE;
     const int s = find_free_slot(d);
     if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
-    if (first) {
-        // The previous burst's host->device copy must have consumed the pinned
-        // buffer before it is overwritten.
-        if (d->bx_copied && !ok(d, hipEventSynchronize(d->bx_copied), "burst wait")) return ZLM_NULL_HANDLE;
-        if (!ensure_pair(d, d->d_bx, d->h_bx, d->bx_cap, k)) return ZLM_NULL_HANDLE;
-        if (!d->bx_copied && !ok(d, hipEventCreateWithFlags(&d->bx_copied, hipEventDisableTiming), "event"))
-            return ZLM_NULL_HANDLE;
-        memcpy(d->h_bx, x, k * sizeof(float));
-        if (!ok(d, hipMemcpyAsync(d->d_bx, d->h_bx, k * sizeof(float), hipMemcpyHostToDevice, d->stream),
-                "stage burst x") ||
-            !ok(d, hipEventRecord(d->bx_copied, d->stream), "record")) {
-            d->burst_open = false;
-            return ZLM_NULL_HANDLE;
-        }
-        d->burst_src = x;
-        d->burst_len = k;
-        d->burst_open = true;
-    } else if (!d->burst_open || x != d->burst_src || x_len != d->burst_len) {
-        return fail(d, "burst member does not match the burst's activation"), ZLM_NULL_HANDLE;
-    }
-    if (!submit_into_slot(d, s, r, quant, rows, k, d->d_bx)) return ZLM_NULL_HANDLE;
+    const float* xd = stage_burst(d, x, x_len, first);
+    if (!xd) return ZLM_NULL_HANDLE;
+    if (!submit_into_slot(d, s, r, quant, rows, k, xd)) return ZLM_NULL_HANDLE;
     return make_handle(d, s);
 }
 
@@ -821,26 +985,74 @@ extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void*
     return ran;
 }
 
-extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, zlm_resident*, zlm_resident*,
-                                                                uint32_t, size_t, size_t, const float*, size_t,
-                                                                uint32_t, uint32_t, bool) {
-    if (d && d->avail) fail(d, "fused gate_up not built");
-    return ZLM_NULL_HANDLE;
+// The variant argument of the fused ops selects Vulkan shader variants in the
+// reference; here every variant runs the pair-tile kernel (results differ
+// only by fp32 summation order), so it is accepted and not used.
+extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, zlm_resident* rg, zlm_resident* ru,
+                                                                uint32_t quant, size_t rows, size_t k,
+                                                                const float* x, size_t x_len, uint32_t act,
+                                                                uint32_t variant, bool first) {
+    (void)variant;
+    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
+    if (act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", act), ZLM_NULL_HANDLE;
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu), ZLM_NULL_HANDLE;
+    if (!check_resident(d, rg, qi, rows, k) || !check_resident(d, ru, qi, rows, k)) return ZLM_NULL_HANDLE;
+    const int s = find_free_slot(d);
+    if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
+    if (!prepare_slot(d, s, rows)) return ZLM_NULL_HANDLE;
+    const float* xd = stage_burst(d, x, x_len, first);
+    if (!xd) return ZLM_NULL_HANDLE;
+    zlm_gemv_op op = {};
+    op.form = ZLM_FORM_PAIR;
+    op.quant = quant;
+    op.w = rg;
+    op.w_up = ru;
+    op.rows = rows;
+    op.k = k;
+    op.x = xd;
+    op.act = act;
+    op.y = d->slots[s].d_y;
+    if (!enqueue_op(d, op) || !finish_slot(d, s, rows)) return ZLM_NULL_HANDLE;
+    return make_handle(d, s);
 }
 
-extern "C" int32_t zlm_gpu_mat_vec_mlp_resident_burst_async(zlm_device* d, zlm_resident*, zlm_resident*,
-                                                            zlm_resident*, uint32_t, size_t, size_t, size_t,
-                                                            const float*, size_t, uint32_t, uint32_t, bool) {
-    if (d && d->avail) fail(d, "fused mlp not built");
-    return ZLM_NULL_HANDLE;
+extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, zlm_resident* rg,
+                                                                 zlm_resident* ru, zlm_resident* rd,
+                                                                 uint32_t gu_quant, uint32_t down_quant,
+                                                                 size_t rows, size_t k, size_t ffn, const float* x,
+                                                                 size_t x_len, uint32_t act, uint32_t variant,
+                                                                 bool first) {
+    (void)variant;
+    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
+    if (act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", act), ZLM_NULL_HANDLE;
+    const QuantInfo* gq = quant_info(gu_quant);
+    const QuantInfo* dq = quant_info(down_quant);
+    if (!gq || !dq) return fail(d, "unsupported quant"), ZLM_NULL_HANDLE;
+    if (!check_resident(d, rg, gq, ffn, k) || !check_resident(d, ru, gq, ffn, k) ||
+        !check_resident(d, rd, dq, rows, ffn))
+        return ZLM_NULL_HANDLE;
+    const int s = find_free_slot(d);
+    if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
+    if (!prepare_slot(d, s, rows)) return ZLM_NULL_HANDLE;
+    const float* xd = stage_burst(d, x, x_len, first);
+    if (!xd) return ZLM_NULL_HANDLE;
+    if (!enqueue_mlp(d, s, rg, ru, rd, gu_quant, down_quant, rows, k, ffn, xd, act) || !finish_slot(d, s, rows))
+        return ZLM_NULL_HANDLE;
+    return make_handle(d, s);
 }
 
-extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, zlm_resident*, zlm_resident*,
-                                                                 zlm_resident*, uint32_t, uint32_t, size_t,
-                                                                 size_t, size_t, const float*, size_t, uint32_t,
-                                                                 uint32_t, bool) {
-    if (d && d->avail) fail(d, "mlp pair not built");
-    return ZLM_NULL_HANDLE;
+// The reference's single-dispatch fused MLP (one workgroup, vulkan
+// pipeline.zig:1565-1635) is the same computation as the two-kernel form; on
+// gfx950 the two full-grid kernels are the faster shape, so both ops run it.
+extern "C" int32_t zlm_gpu_mat_vec_mlp_resident_burst_async(zlm_device* d, zlm_resident* rg, zlm_resident* ru,
+                                                            zlm_resident* rd, uint32_t quant, size_t rows, size_t k,
+                                                            size_t ffn, const float* x, size_t x_len, uint32_t act,
+                                                            uint32_t variant, bool first) {
+    return zlm_gpu_mat_vec_mlp_pair_resident_burst_async(d, rg, ru, rd, quant, quant, rows, k, ffn, x, x_len, act,
+                                                         variant, first);
 }
 
 extern "C" void zlm_gpu_sync(zlm_device* d) {
@@ -977,6 +1189,12 @@ extern "C" bool zlm_gpu_time_gemv_sequence(zlm_device* d, const zlm_gemv_desc* d
     hipEventDestroy(e1);
     *ms = t;
     return good;
+}
+
+extern "C" bool zlm_gpu_gemv_op_enqueue(zlm_device* d, const zlm_gemv_op* op) {
+    if (!d || !d->avail) return false;
+    if (!op) return fail(d, "null op");
+    return enqueue_op(d, *op);
 }
 
 extern "C" bool zlm_gpu_dequant_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t n, float* out) {

@@ -1,635 +1,10 @@
-// zlm_kernels.hip -- CDNA4 (gfx950) kernels for zlm's quantized GEMV/GEMM path.
-//
-// Built as a device-only code object (hipcc --genco) and loaded by the host
-// library with hipModuleLoad; every entry point is extern "C" so the host can
-// look it up by name.
-//
-// Weight layouts in HBM (produced once by the repack kernels from the raw GGUF
-// blocks of reference src/kernels/linear/quant/types.zig:6-53):
-//   q4_0  payload [rows][nb][16 B nibbles]        + scales [rows][nb] f16
-//   q8_0  payload [rows][nb][32 B int8]           + scales [rows][nb] f16
-//   q6_k  payload [rows][nb][208 B ql|qh|sc]      + scales [rows][nb] f16
-//   q4_k  raw     [rows][nb][144 B]  (already a multiple of 16 B per block)
-// Every payload block is a whole number of 16-byte chunks, so the GEMV
-// streams it with 128-bit loads; a wavefront's 64 lanes read 1 KiB of
-// consecutive payload per load instruction.
-//
-// GEMV scheme (one kernel per quant, templated on the row tile RT, the chunk
-// steps per row STEPS and the x capacity KCAP):
-//   * each wave owns tiles of RT rows (grid-stride over tiles); lane l covers
-//     the row's 16-byte chunks l, l+64, ... (STEPS of them), and the wave
-//     issues all of a tile's loads before computing any, so a tile is one
-//     memory round trip;
-//   * the workgroup stages x (fp32) once into LDS, padded by one float4 per 32
-//     floats so 128-bit LDS reads of neighbouring lanes fall in distinct banks,
-//     plus the fp32 sum of every 16-element run of x.  x's global loads are
-//     issued before the first tile's weight loads and the prologue has no
-//     branches, so the staging barrier waits for x alone;
-//   * the x values a chunk needs are read from LDS once and applied to all RT
-//     rows; the nibble/byte bias (-8 for q4_0, -32 for q6_k) is folded
-//     through the run sums, so the inner loop is extract -> cvt -> fma in fp32;
-//   * the RT per-lane partials are reduced with a transposing butterfly (each
-//     shuffle stage halves the live values), one lane per row writes y.
-#include <hip/hip_runtime.h>
-#include <stdint.h>
+// zlm_kernels.hip -- CDNA4 (gfx950) kernels besides the GEMVs: layout
+// conversion, dequant, the activation quantizer, the prefill GEMM and the
+// decode-step glue.  Built as a device-only code object (hipcc --genco) and
+// loaded by the host library with hipModuleLoad; every entry point is
+// extern "C" so the host can look it up by name.
+#include "gemv_impl.h"
 
-namespace {
-
-constexpr int kWave = 64;
-
-enum QType : int { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
-
-__device__ __forceinline__ float h2f(uint32_t bits) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
-}
-
-__device__ __forceinline__ float ub(uint32_t w, int i) { return static_cast<float>((w >> (8 * i)) & 0xffu); }
-__device__ __forceinline__ float sb(uint32_t w, int i) {
-    return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * i)) >> 24);
-}
-
-// LDS position of x element e: one float4 of padding after every 32 floats.
-__device__ __forceinline__ int xpad(int e) { return e + ((e >> 5) << 2); }
-
-// LDS footprint of a staged x of capacity KCAP: the padded values plus one
-// dummy float4 (kDummy) and the run sums plus one dummy slot (index kRuns),
-// the targets of out-of-range threads' stores.
-template <int KCAP>
-struct XTile {
-    static constexpr int kDummy = KCAP + KCAP / 8;
-    static constexpr int kFloats = kDummy + 4;
-    static constexpr int kRuns = KCAP / 16;
-};
-
-// Stage x[0..k) into LDS (padded) and the sums of its 16-element runs.  x is
-// read from global memory once: thread i holds float4 i, and the four
-// consecutive lanes that hold one run add their partials with two shuffles.
-// k is a multiple of 32 and blockDim a multiple of 64, so every loop trip is
-// wave-uniform and a run never straddles two waves.
-template <int KCAP>
-__device__ __forceinline__ void stage_x(const float* __restrict__ x, int k, float* xl, float* xs) {
-    const int n4 = k >> 2;
-    for (int base = 0; base < n4; base += blockDim.x) {
-        const int i = base + threadIdx.x;
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (i < n4) {
-            v = reinterpret_cast<const float4*>(x)[i];
-            *reinterpret_cast<float4*>(xl + xpad(i << 2)) = v;
-        }
-        float s = (v.x + v.y) + (v.z + v.w);
-        s += __shfl_xor(s, 1, kWave);
-        s += __shfl_xor(s, 2, kWave);
-        if (i < n4 && (i & 3) == 0) xs[i >> 2] = s;
-    }
-    __syncthreads();
-}
-
-// The same staging split in two phases, so a kernel can issue x's global loads
-// first, then its weight loads, and only then wait for x: loads complete in
-// issue order, so x must be requested before the weights or the LDS store
-// would wait for the whole weight tile.  NX = float4s of x per thread.
-template <int NX>
-struct XRegs {
-    float4 v[NX];
-};
-
-// Both phases are branch-free (clamped loads, selects, a dummy LDS slot for
-// out-of-range threads): a branch here would make the compiler wait for every
-// outstanding load, weights included, before the barrier.
-template <int NX>
-__device__ __forceinline__ void xload(const float* __restrict__ x, int k, XRegs<NX>& r) {
-    const int n4 = k >> 2;
-#pragma unroll
-    for (int j = 0; j < NX; j++) {
-        const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
-        r.v[j] = reinterpret_cast<const float4*>(x)[min(i, n4 - 1)];
-    }
-}
-
-template <int KCAP, int NX>
-__device__ __forceinline__ void xstore(const XRegs<NX>& r, int k, float* xl, float* xs) {
-    const int n4 = k >> 2;
-#pragma unroll
-    for (int j = 0; j < NX; j++) {
-        const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
-        const bool valid = i < n4;
-        float4 v = r.v[j];
-        v.x = valid ? v.x : 0.0f;
-        v.y = valid ? v.y : 0.0f;
-        v.z = valid ? v.z : 0.0f;
-        v.w = valid ? v.w : 0.0f;
-        *reinterpret_cast<float4*>(xl + (valid ? xpad(i << 2) : XTile<KCAP>::kDummy)) = v;
-        float s = (v.x + v.y) + (v.z + v.w);
-        s += __shfl_xor(s, 1, kWave);
-        s += __shfl_xor(s, 2, kWave);
-        xs[(valid && (i & 3) == 0) ? (i >> 2) : XTile<KCAP>::kRuns] = s;
-    }
-    __syncthreads();
-}
-
-__device__ __forceinline__ float4 lds4(const float* p) { return *reinterpret_cast<const float4*>(p); }
-
-// ---- per-quant fragments --------------------------------------------------
-// A fragment is what one lane loads for one 16-byte chunk position `c` of RT
-// rows; `load_frag` only issues global loads, `compute_frag` only touches
-// registers and LDS, so the main loop can keep the next fragment's loads in
-// flight while it computes the current one.
-
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-typedef unsigned int v2u __attribute__((ext_vector_type(2)));
-
-template <bool NT>
-__device__ __forceinline__ uint4 ld16(const uint8_t* p) {
-    if constexpr (NT) {
-        const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
-        return make_uint4(t.x, t.y, t.z, t.w);
-    } else {
-        return *reinterpret_cast<const uint4*>(p);
-    }
-}
-
-template <bool NT>
-__device__ __forceinline__ uint2 ld8(const uint8_t* p) {
-    if constexpr (NT) {
-        const v2u t = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
-        return make_uint2(t.x, t.y);
-    } else {
-        return *reinterpret_cast<const uint2*>(p);
-    }
-}
-
-template <bool NT>
-__device__ __forceinline__ uint32_t ld2(const uint16_t* p) {
-    if constexpr (NT) return __builtin_nontemporal_load(p);
-    else return *p;
-}
-
-template <int QT, int RT>
-struct Frag;
-
-template <int RT>
-struct Frag<Q4_0, RT> {
-    uint4 q[RT];
-    uint32_t d[RT];
-};
-template <int RT>
-struct Frag<Q8_0, RT> {
-    uint4 q[RT];
-    uint32_t d[RT];
-};
-template <int RT>
-struct Frag<Q4_K, RT> {
-    uint4 hd[RT];
-    uint4 q[RT];
-};
-template <int RT>
-struct Frag<Q6_K, RT> {
-    uint4 ql[RT];
-    uint4 qh[RT];
-    uint2 sc[RT];
-    uint32_t d[RT];
-};
-
-// q4_0: chunk c = block c (16 nibble bytes).  q8_0: chunk c = half block c
-// (16 int8; block c/2 holds the scale).  q4_k / q6_k: 8 chunks per 256-element
-// super-block (c>>3), see the compute steps.
-template <int QT, int RT, bool NT>
-__device__ __forceinline__ void load_frag(Frag<QT, RT>& f, const uint8_t* __restrict__ w,
-                                          const uint16_t* __restrict__ dsc, const uint32_t* rr, uint32_t nb, int c) {
-#pragma unroll
-    for (int r = 0; r < RT; r++) {
-        const size_t row = rr[r];
-        if constexpr (QT == Q4_0) {
-            const size_t bi = row * nb + c;
-            f.q[r] = ld16<NT>(w + bi * 16);
-            f.d[r] = ld2<NT>(dsc + bi);
-        } else if constexpr (QT == Q8_0) {
-            f.q[r] = ld16<NT>(w + (row * (2 * nb) + c) * 16);
-            f.d[r] = ld2<NT>(dsc + row * nb + (c >> 1));
-        } else if constexpr (QT == Q4_K) {
-            const uint8_t* blk = w + (row * nb + (c >> 3)) * 144;
-            f.hd[r] = ld16<false>(blk);
-            f.q[r] = ld16<NT>(blk + 16 + 16 * (c & 7));
-        } else {
-            const int p = c & 7, n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
-            const size_t bi = row * nb + (c >> 3);
-            const uint8_t* blk = w + bi * 208;
-            f.ql[r] = ld16<NT>(blk + 64 * n + 32 * ws + 16 * h);
-            f.qh[r] = ld16<false>(blk + 128 + 32 * n + 16 * h);
-            f.sc[r] = ld8<false>(blk + 192 + 8 * n);
-            f.d[r] = ld2<false>(dsc + bi);
-        }
-    }
-}
-
-// Byte j of a q4_0 block holds element j (low nibble) and j+16 (high);
-// value (nib-8)*d, and Sum (nib-8)*x = Sum nib*x - 8*Sum x.
-template <int RT>
-__device__ __forceinline__ void compute_q4_0(const Frag<Q4_0, RT>& f, const float* xl, const float* xs, int c,
-                                             bool valid, float* acc) {
-    const float* xb = xl + xpad(c << 5);
-    const float xsum = xs[2 * c] + xs[2 * c + 1];
-    float s[RT];
-#pragma unroll
-    for (int r = 0; r < RT; r++) s[r] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 xa = lds4(xb + 4 * i);
-        const float4 xh = lds4(xb + 16 + 4 * i);
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const uint32_t wv = (&f.q[r].x)[i];
-            const uint32_t lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
-            s[r] = fmaf(ub(lo, 0), xa.x, s[r]);
-            s[r] = fmaf(ub(lo, 1), xa.y, s[r]);
-            s[r] = fmaf(ub(lo, 2), xa.z, s[r]);
-            s[r] = fmaf(ub(lo, 3), xa.w, s[r]);
-            s[r] = fmaf(ub(hi, 0), xh.x, s[r]);
-            s[r] = fmaf(ub(hi, 1), xh.y, s[r]);
-            s[r] = fmaf(ub(hi, 2), xh.z, s[r]);
-            s[r] = fmaf(ub(hi, 3), xh.w, s[r]);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, fmaf(-8.0f, xsum, s[r]), acc[r]);
-}
-
-template <int RT>
-__device__ __forceinline__ void compute_q8_0(const Frag<Q8_0, RT>& f, const float* xl, const float*, int c,
-                                             bool valid, float* acc) {
-    const float* xb = xl + xpad(c << 4);
-    float s[RT];
-#pragma unroll
-    for (int r = 0; r < RT; r++) s[r] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 xa = lds4(xb + 4 * i);
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const uint32_t wv = (&f.q[r].x)[i];
-            s[r] = fmaf(sb(wv, 0), xa.x, s[r]);
-            s[r] = fmaf(sb(wv, 1), xa.y, s[r]);
-            s[r] = fmaf(sb(wv, 2), xa.z, s[r]);
-            s[r] = fmaf(sb(wv, 3), xa.w, s[r]);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, s[r], acc[r]);
-}
-
-// getScaleMinK4 (reference quant/k_quants.zig:24-32) on the 12 packed bytes
-// held as three dwords; j in 0..7, any lane-varying j.
-__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, float& sc, float& mn) {
-    const int t = (j & 3) * 8;
-    const uint32_t b0 = (s0 >> t) & 0xffu, b1 = (s1 >> t) & 0xffu, b2 = (s2 >> t) & 0xffu;
-    uint32_t d, m;
-    if (j < 4) {
-        d = b0 & 63u;
-        m = b1 & 63u;
-    } else {
-        d = (b2 & 15u) | ((b0 >> 6) << 4);
-        m = (b2 >> 4) | ((b1 >> 6) << 4);
-    }
-    sc = static_cast<float>(d);
-    mn = static_cast<float>(m);
-}
-
-// q4_k piece p = c&7 of super-block c>>3 (16 qs bytes of group g = p/2): low
-// nibbles are elements 64g + 16(p%2) + j (scale 2g), high nibbles +32 (scale
-// 2g+1); value d*sc*nib - dmin*mn.
-template <int RT>
-__device__ __forceinline__ void compute_q4_k(const Frag<Q4_K, RT>& f, const float* xl, const float* xs, int c,
-                                             bool valid, float* acc) {
-    const int sbk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
-    const int elo = 256 * sbk + 64 * g + 16 * h, ehi = elo + 32;
-    const float* xa_p = xl + xpad(elo);
-    const float* xb_p = xl + xpad(ehi);
-    const float xs_lo = xs[elo >> 4], xs_hi = xs[ehi >> 4];
-    float slo[RT], shi[RT];
-#pragma unroll
-    for (int r = 0; r < RT; r++) slo[r] = shi[r] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 xa = lds4(xa_p + 4 * i);
-        const float4 xb = lds4(xb_p + 4 * i);
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const uint32_t wv = (&f.q[r].x)[i];
-            const uint32_t lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
-            slo[r] = fmaf(ub(lo, 0), xa.x, slo[r]);
-            slo[r] = fmaf(ub(lo, 1), xa.y, slo[r]);
-            slo[r] = fmaf(ub(lo, 2), xa.z, slo[r]);
-            slo[r] = fmaf(ub(lo, 3), xa.w, slo[r]);
-            shi[r] = fmaf(ub(hi, 0), xb.x, shi[r]);
-            shi[r] = fmaf(ub(hi, 1), xb.y, shi[r]);
-            shi[r] = fmaf(ub(hi, 2), xb.z, shi[r]);
-            shi[r] = fmaf(ub(hi, 3), xb.w, shi[r]);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RT; r++) {
-        const uint32_t dd = valid ? f.hd[r].x : 0u;
-        const float d = h2f(dd), dmin = h2f(dd >> 16);
-        float sc1, mn1, sc2, mn2;
-        scale_min_k4(2 * g, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc1, mn1);
-        scale_min_k4(2 * g + 1, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc2, mn2);
-        float t = (d * sc1) * slo[r];
-        t = fmaf(d * sc2, shi[r], t);
-        t = fmaf(-(dmin * mn1), xs_lo, t);
-        t = fmaf(-(dmin * mn2), xs_hi, t);
-        acc[r] += t;
-    }
-}
-
-// q6_k part p = c&7 of super-block c>>3: half n = p/4, 16-run h, ql half ws;
-// low nibbles + qh bits 2ws are elements 128n + 32ws + 16h + j, high nibbles +
-// qh bits 4+2ws are those +64.  value d*sc*(q-32); Sum (q-32)*x = Sum q*x - 32*Sum x.
-template <int RT>
-__device__ __forceinline__ void compute_q6_k(const Frag<Q6_K, RT>& f, const float* xl, const float* xs, int c,
-                                             bool valid, float* acc) {
-    const int sbk = c >> 3, p = c & 7, n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
-    const int ea = 256 * sbk + 128 * n + 32 * ws + 16 * h, eb = ea + 64;
-    const float* xa_p = xl + xpad(ea);
-    const float* xb_p = xl + xpad(eb);
-    const float xs_a = xs[ea >> 4], xs_b = xs[eb >> 4];
-    const int sh_lo = 2 * ws, sh_hi = 4 + 2 * ws, sci = 8 * (h + 2 * ws);
-    float sa[RT], sbv[RT];
-#pragma unroll
-    for (int r = 0; r < RT; r++) sa[r] = sbv[r] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 xa = lds4(xa_p + 4 * i);
-        const float4 xb = lds4(xb_p + 4 * i);
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
-            const uint32_t lo = (lw & 0x0F0F0F0Fu) | (((hw >> sh_lo) & 0x03030303u) << 4);
-            const uint32_t hi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> sh_hi) & 0x03030303u) << 4);
-            sa[r] = fmaf(ub(lo, 0), xa.x, sa[r]);
-            sa[r] = fmaf(ub(lo, 1), xa.y, sa[r]);
-            sa[r] = fmaf(ub(lo, 2), xa.z, sa[r]);
-            sa[r] = fmaf(ub(lo, 3), xa.w, sa[r]);
-            sbv[r] = fmaf(ub(hi, 0), xb.x, sbv[r]);
-            sbv[r] = fmaf(ub(hi, 1), xb.y, sbv[r]);
-            sbv[r] = fmaf(ub(hi, 2), xb.z, sbv[r]);
-            sbv[r] = fmaf(ub(hi, 3), xb.w, sbv[r]);
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RT; r++) {
-        const float d = valid ? h2f(f.d[r]) : 0.0f;
-        const float sc_a = static_cast<float>(static_cast<int32_t>(f.sc[r].x << (24 - sci)) >> 24);
-        const float sc_b = static_cast<float>(static_cast<int32_t>(f.sc[r].y << (24 - sci)) >> 24);
-        float t = (d * sc_a) * fmaf(-32.0f, xs_a, sa[r]);
-        t = fmaf(d * sc_b, fmaf(-32.0f, xs_b, sbv[r]), t);
-        acc[r] += t;
-    }
-}
-
-template <int QT, int RT>
-__device__ __forceinline__ void compute_frag(const Frag<QT, RT>& f, const float* xl, const float* xs, int c,
-                                             bool valid, float* acc) {
-    if constexpr (QT == Q4_0) compute_q4_0<RT>(f, xl, xs, c, valid, acc);
-    if constexpr (QT == Q8_0) compute_q8_0<RT>(f, xl, xs, c, valid, acc);
-    if constexpr (QT == Q4_K) compute_q4_k<RT>(f, xl, xs, c, valid, acc);
-    if constexpr (QT == Q6_K) compute_q6_k<RT>(f, xl, xs, c, valid, acc);
-}
-
-// Reduce RT per-lane partials over the wavefront and write y[r0 .. r0+RT).
-// Stage s exchanges across lane bit (5-s) and keeps half of the live values,
-// so RT values cost RT-1 + (6-log2 RT) shuffles instead of 6*RT.
-template <int RT>
-__device__ __forceinline__ void reduce_write(float* v, float* __restrict__ y, uint32_t r0, uint32_t rows,
-                                             int lane) {
-    constexpr int LOG = (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
-#pragma unroll
-    for (int st = 0; st < LOG; st++) {
-        const int half = (RT >> st) >> 1;
-        const int bit = 32 >> st;
-        const bool upper = (lane & bit) != 0;
-#pragma unroll
-        for (int i = 0; i < half; i++) {
-            const float keep = upper ? v[half + i] : v[i];
-            const float send = upper ? v[i] : v[half + i];
-            v[i] = keep + __shfl_xor(send, bit, kWave);
-        }
-    }
-    float s = v[0];
-#pragma unroll
-    for (int off = 32 >> LOG; off >= 1; off >>= 1) s += __shfl_xor(s, off, kWave);
-    if ((lane & ((64 >> LOG) - 1)) == 0) {
-        const uint32_t row = r0 + (lane >> (6 - LOG));
-        if (row < rows) y[row] = s;
-    }
-}
-
-template <int QT>
-__device__ __forceinline__ int chunks_per_row(uint32_t nb) {
-    return (QT == Q4_0) ? static_cast<int>(nb) : (QT == Q8_0) ? static_cast<int>(2 * nb) : static_cast<int>(8 * nb);
-}
-
-template <int QT>
-__device__ __forceinline__ int elems_per_block() {
-    return (QT == Q4_0 || QT == Q8_0) ? 32 : 256;
-}
-
-// Issue the loads of every chunk step of row tile `t`.  Rows past the end are
-// clamped to the last row and chunk positions past the row's end to its last
-// chunk, so the loads are branch-free; compute_tile gives those a zero scale.
-// With EXACT the caller guarantees STEPS == ceil(C/64); otherwise steps that
-// start past the row's end are skipped by a wave-uniform test.
-template <int QT, int RT, int STEPS, bool EXACT, bool NT>
-__device__ __forceinline__ void load_tile(Frag<QT, RT> (&f)[STEPS], const uint8_t* __restrict__ w,
-                                          const uint16_t* __restrict__ dsc, uint32_t t, uint32_t rows, uint32_t nb,
-                                          int C, int lane) {
-    uint32_t rr[RT];
-#pragma unroll
-    for (int r = 0; r < RT; r++) rr[r] = min(t * RT + r, rows - 1);
-#pragma unroll
-    for (int s = 0; s < STEPS; s++)
-        if (EXACT || s * kWave < C) load_frag<QT, RT, NT>(f[s], w, dsc, rr, nb, min(lane + s * kWave, C - 1));
-}
-
-template <int QT, int RT, int STEPS, bool EXACT>
-__device__ __forceinline__ void compute_tile(const Frag<QT, RT> (&f)[STEPS], const float* xl, const float* xs,
-                                             int C, int lane, float* acc) {
-#pragma unroll
-    for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < STEPS; s++) {
-        const int c = lane + s * kWave;
-        if (EXACT || s * kWave < C) compute_frag<QT, RT>(f[s], xl, xs, min(c, C - 1), c < C, acc);
-    }
-}
-
-// One GEMV: y[r] = sum_k w[r,k] * x[k] for r < rows, k = nb * block_elems.
-// A wave owns row tiles blockIdx*WAVES + wid + j*gridDim*WAVES.  For each tile
-// it issues the loads of every chunk step (64 consecutive 16-byte chunks per
-// row per step) before it computes any of them, so a tile costs one memory
-// round trip.  The first tile is peeled and kept branch-free: x's loads, then
-// the tile's loads, then x's LDS store and the barrier, so the barrier waits
-// for x only and step s computes as soon as its own loads land.  Occupancy
-// (several waves per SIMD) overlaps one wave's compute with others' loads.
-template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT>
-__device__ __forceinline__ void gemv(const uint8_t* __restrict__ w, const uint16_t* __restrict__ dsc,
-                                     const float* __restrict__ x, float* __restrict__ y, uint32_t rows,
-                                     uint32_t nb) {
-    __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
-    __shared__ float xs[XTile<KCAP>::kRuns + 1];
-    const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t wid = threadIdx.x / kWave;
-    const int C = chunks_per_row<QT>(nb);
-    const uint32_t ntiles = (rows + RT - 1) / RT;
-    const uint32_t tstride = gridDim.x * WAVES;
-    uint32_t tile = blockIdx.x * WAVES + wid;
-
-    const int k = static_cast<int>(nb) * elems_per_block<QT>();
-    XRegs<(KCAP / 4 + WAVES * kWave - 1) / (WAVES * kWave)> xr;
-    xload(x, k, xr);
-    Frag<QT, RT> f[STEPS];
-    load_tile<QT, RT, STEPS, EXACT, NT>(f, w, dsc, min(tile, ntiles - 1), rows, nb, C, lane);
-    xstore<KCAP>(xr, k, xl, xs);
-
-    float acc[RT];
-    compute_tile<QT, RT, STEPS, EXACT>(f, xl, xs, C, lane, acc);
-    if (tile < ntiles) reduce_write<RT>(acc, y, tile * RT, rows, lane);
-    for (tile += tstride; tile < ntiles; tile += tstride) {
-        load_tile<QT, RT, STEPS, EXACT, NT>(f, w, dsc, tile, rows, nb, C, lane);
-        compute_tile<QT, RT, STEPS, EXACT>(f, xl, xs, C, lane, acc);
-        reduce_write<RT>(acc, y, tile * RT, rows, lane);
-    }
-}
-
-// The software-pipelined form: each wave walks a flat sequence of (row tile,
-// chunk step) items and issues every item's loads one item ahead of its
-// compute.  Kept for launch-shape comparisons.
-template <int QT, int KCAP, int WAVES, int RT, bool NT>
-__device__ __forceinline__ void gemv_pipe(const uint8_t* __restrict__ w, const uint16_t* __restrict__ dsc,
-                                          const float* __restrict__ x, float* __restrict__ y, uint32_t rows,
-                                          uint32_t nb) {
-    __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
-    __shared__ float xs[XTile<KCAP>::kRuns + 1];
-    const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t wid = threadIdx.x / kWave;
-    const int C = chunks_per_row<QT>(nb);
-    const int steps = (C + kWave - 1) / kWave;
-    const uint32_t ntiles = (rows + RT - 1) / RT;
-    const uint32_t tstride = gridDim.x * WAVES;
-    uint32_t tile = blockIdx.x * WAVES + wid;
-    const uint32_t my_tiles = tile < ntiles ? (ntiles - 1 - tile) / tstride + 1 : 0;
-    const uint32_t items = my_tiles * static_cast<uint32_t>(steps);
-
-    uint32_t rr[RT];
-    auto set_rows = [&](uint32_t t) {
-#pragma unroll
-        for (int r = 0; r < RT; r++) rr[r] = min(t * RT + r, rows - 1);
-    };
-    Frag<QT, RT> cur;
-    if (items > 0) {
-        set_rows(tile);
-        load_frag<QT, RT, NT>(cur, w, dsc, rr, nb, min(lane, C - 1));
-    }
-    stage_x<KCAP>(x, static_cast<int>(nb) * elems_per_block<QT>(), xl, xs);
-
-    float acc[RT];
-#pragma unroll
-    for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-    int step = 0;
-    for (uint32_t it = 0; it < items; it++) {
-        // next item: same tile, next step; or the wave's next tile, step 0
-        const bool last_step = (step == steps - 1);
-        const uint32_t ntile = last_step ? tile + tstride : tile;
-        const int nstep = last_step ? 0 : step + 1;
-        Frag<QT, RT> nxt;
-        if (it + 1 < items) {
-            uint32_t nrr[RT];
-#pragma unroll
-            for (int r = 0; r < RT; r++) nrr[r] = min(ntile * RT + r, rows - 1);
-            load_frag<QT, RT, NT>(nxt, w, dsc, nrr, nb, min(lane + nstep * kWave, C - 1));
-        }
-        const int c = lane + step * kWave;
-        compute_frag<QT, RT>(cur, xl, xs, min(c, C - 1), c < C, acc);
-        if (last_step) {
-            reduce_write<RT>(acc, y, tile * RT, rows, lane);
-#pragma unroll
-            for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-        }
-        tile = ntile;
-        step = nstep;
-        cur = nxt;
-    }
-}
-
-}  // namespace
-
-// ---- GEMV entry points ---------------------------------------------------
-// zlm_gemv_<quant>_r<RT>_s<STEPS>: STEPS == ceil(chunks per row / 64) exactly
-// (q4_0 and the K-quants have k/32 chunks per row, q8_0 k/16), x capacity the
-// smallest of 4096/8192/16384/32768 that holds STEPS steps.
-// zlm_gemv_<quant>_r1_g<STEPS>: the generic form for any other k up to 32768.
-// Every instance runs 4 waves (256 threads) per workgroup.
-
-#define ZLM_GEMV(NAME, QT, KCAP, RT, STEPS, EXACT)                                                        \
-    extern "C" __global__ void __launch_bounds__(256)                                                    \
-        NAME(const uint8_t* __restrict__ w, const uint16_t* __restrict__ dsc, const float* __restrict__ x, \
-             float* __restrict__ y, uint32_t rows, uint32_t nb) {                                        \
-        gemv<QT, KCAP, 4, RT, STEPS, EXACT, true>(w, dsc, x, y, rows, nb);                               \
-    }
-
-// q4_0 / q4_k / q6_k: KCAP = 2048 * STEPS rounded up to a tier.
-#define ZLM_GEMV_Q4(QN, QT)                                         \
-    ZLM_GEMV_Q4_COMMON(QN, QT)                                      \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s6, QT, 16384, 2, 6, true)          \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s8, QT, 16384, 2, 8, true)
-
-// The K-quants keep RT 1 from 6 steps up (their fragments are larger).
-#define ZLM_GEMV_Q4_COMMON(QN, QT)                                  \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s1, QT, 4096, 1, 1, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s1, QT, 4096, 2, 1, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s1, QT, 4096, 4, 1, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s2, QT, 4096, 1, 2, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s2, QT, 4096, 2, 2, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s2, QT, 4096, 4, 2, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s3, QT, 8192, 1, 3, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s3, QT, 8192, 2, 3, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s3, QT, 8192, 4, 3, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s4, QT, 8192, 1, 4, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s4, QT, 8192, 2, 4, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s4, QT, 8192, 4, 4, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s6, QT, 16384, 1, 6, true)          \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s8, QT, 16384, 1, 8, true)          \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_g16, QT, 32768, 1, 16, false)
-
-// q8_0: KCAP = 1024 * STEPS rounded up to a tier.
-#define ZLM_GEMV_Q8(QN, QT)                                         \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s1, QT, 4096, 1, 1, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s1, QT, 4096, 2, 1, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s1, QT, 4096, 4, 1, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s2, QT, 4096, 1, 2, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s2, QT, 4096, 2, 2, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s2, QT, 4096, 4, 2, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s3, QT, 4096, 1, 3, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s3, QT, 4096, 2, 3, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s3, QT, 4096, 4, 3, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s4, QT, 4096, 1, 4, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s4, QT, 4096, 2, 4, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r4_s4, QT, 4096, 4, 4, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s6, QT, 8192, 1, 6, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s6, QT, 8192, 2, 6, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s8, QT, 8192, 1, 8, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s8, QT, 8192, 2, 8, true)           \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s12, QT, 16384, 1, 12, true)        \
-    ZLM_GEMV(zlm_gemv_##QN##_r2_s12, QT, 16384, 2, 12, true)        \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s15, QT, 16384, 1, 15, true)        \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_s16, QT, 16384, 1, 16, true)        \
-    ZLM_GEMV(zlm_gemv_##QN##_r1_g32, QT, 32768, 1, 32, false)
-
-#ifndef ZLM_NO_ENTRY_POINTS
-ZLM_GEMV_Q4(q4_0, Q4_0)
-ZLM_GEMV_Q4_COMMON(q4_k, Q4_K)
-ZLM_GEMV_Q4_COMMON(q6_k, Q6_K)
-ZLM_GEMV_Q8(q8_0, Q8_0)
-#endif
 
 // ---- repack: raw GGUF blocks -> aligned payload + separate f16 scales -----
 // One thread per block; `bb` raw block bytes, the scale at `soff` within the

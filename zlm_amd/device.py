@@ -24,6 +24,9 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(_HERE, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libzlm_gpu_hip.so")
 CODE_OBJECT_PATH = os.path.join(LIB_DIR, "zlm_kernels_gfx950.hsaco")
+# Every code object the library loads: the common kernels and one GEMV object per quant.
+CODE_OBJECT_PATHS = [CODE_OBJECT_PATH] + [os.path.join(LIB_DIR, f"zlm_gemv_{q}_gfx950.hsaco")
+                                          for q in ("q4_0", "q8_0", "q4_k", "q6_k")]
 
 RING_SIZE = 8
 NULL_HANDLE = -1
@@ -35,6 +38,8 @@ PLAIN, U4, U8, SUB, UN2, UN4, W32, W128 = range(8)
 VARIANT_NAMES = ("plain", "u4", "u8", "sub", "un2", "un4", "w32", "w128")
 # GateUpAct (reference gpu/backend/root.zig:225).
 SILU, GELU = 0, 1
+# GEMV forms of zlm_gemv_op (device-level; see include/zlm_gpu_hip.h).
+FORM_PLAIN, FORM_PAIR, FORM_NORM, FORM_NORMPAIR, FORM_RESID = range(5)
 
 
 def quant(ggml_type: int, variant: int = PLAIN) -> int:
@@ -60,6 +65,23 @@ class _GemvDesc(ctypes.Structure):
         ("k", ctypes.c_size_t),
         ("x_dev", ctypes.c_void_p),
         ("y_dev", ctypes.c_void_p),
+    ]
+
+
+class _GemvOp(ctypes.Structure):
+    _fields_ = [
+        ("form", ctypes.c_uint32),
+        ("quant", ctypes.c_uint32),
+        ("w", ctypes.c_void_p),
+        ("w_up", ctypes.c_void_p),
+        ("rows", ctypes.c_size_t),
+        ("k", ctypes.c_size_t),
+        ("x", ctypes.c_void_p),
+        ("norm_w", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("act", ctypes.c_uint32),
+        ("res", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
     ]
 
 
@@ -140,6 +162,7 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_time_mat_mul": (B, [P, P, S, U, S, S, S, P, P, ctypes.c_int, P]),
         "zlm_gpu_time_gemv_sequence": (B, [P, P, S, ctypes.c_int, P]),
         "zlm_gpu_dequant_resident": (B, [P, P, U, S, P]),
+        "zlm_gpu_gemv_op_enqueue": (B, [P, P]),
         "zlm_gpu_quantize_act_q8": (B, [P, P, S, P, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -396,6 +419,14 @@ class Device:
                                                   ctypes.addressof(ms)):
             raise RuntimeError(self.last_error())
         return ms.value
+
+    def gemv_op_enqueue(self, form: int, quant: int, w: Resident, rows: int, k: int, x_dev: int, y_dev: int,
+                        w_up: Optional[Resident] = None, norm_w: int = 0, eps: float = 0.0, act: int = SILU,
+                        res: int = 0) -> bool:
+        """Enqueue one GEMV form on device buffers (no wait); see zlm_gemv_op."""
+        op = _GemvOp(form, quant, w.ptr if w else None, w_up.ptr if w_up else None, rows, k, x_dev,
+                     norm_w or None, eps, act, res or None, y_dev)
+        return bool(self._L.zlm_gpu_gemv_op_enqueue(self._h, ctypes.byref(op)))
 
     def dequant_resident(self, res: Resident, quant: int, n: int) -> Optional[np.ndarray]:
         out = np.zeros(n, np.float32)
