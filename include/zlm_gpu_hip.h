@@ -194,6 +194,8 @@ bool zlm_gpu_dev_download(zlm_device *dev, void *dst, const void *src, size_t by
 /* Copy `bytes` (a multiple of 16, 16-byte aligned pointers) device to device
  * with the library's own copy kernel, and wait. */
 bool zlm_gpu_dev_copy(zlm_device *dev, void *dst, const void *src, size_t bytes);
+/* The same copy, enqueued on the device stream without waiting. */
+bool zlm_gpu_dev_copy_enqueue(zlm_device *dev, void *dst, const void *src, size_t bytes);
 /* Enqueue y_dev[0..rows) = W * x_dev on the device stream; no host copies. */
 bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
                              const float *x_dev, float *y_dev);
@@ -244,6 +246,45 @@ typedef struct {
 } zlm_gemv_op;
 /* Enqueue one GEMV op on the device stream (no host copies, no wait). */
 bool zlm_gpu_gemv_op_enqueue(zlm_device *dev, const zlm_gemv_op *op);
+/* ---- decode-step glue (device buffers; the ops between a layer's GEMVs) ----
+ * Per-head q/k RMSNorm + rotate-half RoPE at *pos and the K/V cache append
+ * (reference transformer/norm.zig:116-160, rope.zig:4-104, attention.zig:6-28).
+ * qkv = [q: n_heads*hd | k: n_kv_heads*hd | v: n_kv_heads*hd] fp32; q_out
+ * receives the rotated q; caches are [n_kv_heads][max_seq][hd] f16; *pos is
+ * read on the device (a position >= max_seq appends nothing).  hd even, <= 256. */
+bool zlm_gpu_qk_norm_rope_kv_enqueue(zlm_device *dev, const float *qkv, float *q_out, const float *q_norm_w,
+                                     const float *k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                     uint32_t head_dim, float eps, float freq_base, const int32_t *pos,
+                                     uint16_t *k_cache, uint16_t *v_cache, uint32_t max_seq);
+/* Attention of every q head over positions [0, min(*pos + 1, max_seq)) of the
+ * f16 caches (reference attention.zig:86-170; GQA by n_heads / n_kv_heads <= 4,
+ * head_dim 128), scores scaled by `scale`; out: n_heads*128 fp32.  Split over
+ * 64-position ranges, then merged; the partials live in library scratch that
+ * the first call sizes (call once before capturing it into a graph). */
+bool zlm_gpu_attention_enqueue(zlm_device *dev, const float *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                               uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, const int32_t *pos,
+                               uint32_t max_seq, float scale, float *out);
+
+/* ---- HIP graphs over the device stream ----
+ * Everything enqueued between capture_begin and capture_end is recorded, not
+ * run.  Ops that allocate or convert layouts on first use must have run once
+ * eagerly before their capture. */
+typedef struct zlm_graph zlm_graph;
+bool zlm_gpu_capture_begin(zlm_device *dev);
+zlm_graph *zlm_gpu_capture_end(zlm_device *dev);
+/* Launch the graph `iters` times back to back and wait; *ms (optional) = GPU
+ * milliseconds between events around the launches. */
+bool zlm_gpu_graph_launch(zlm_device *dev, zlm_graph *graph, int iters, double *ms);
+void zlm_gpu_graph_destroy(zlm_device *dev, zlm_graph *graph);
+
+/* ---- synthetic data generated in HBM (benchmark, large-shape tests) ----
+ * A resident of `n_blocks` raw GGUF blocks (q4_0: f16 d + 16 random bytes;
+ * q8_0: f16 d + 32 int8 uniform in [-127, 127]) with d = |N(0,1)| * scale. */
+zlm_resident *zlm_gpu_synth_resident(zlm_device *dev, uint32_t ggml_type, size_t n_blocks, uint64_t seed,
+                                     float scale);
+/* n f16 values N(0,1) * scale into device memory. */
+bool zlm_gpu_synth_f16(zlm_device *dev, uint16_t *dst, size_t n, uint64_t seed, float scale);
+
 /* Dequantize the first n_elements of a resident from its device layout into host `out`. */
 bool zlm_gpu_dequant_resident(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t n_elements, float *out);
 /* Quantize host x (n floats, n % 32 == 0) to q8 blocks on the device. */

@@ -140,6 +140,16 @@ struct zlm_device {
     hipFunction_t tile_q4_0 = nullptr;
     hipFunction_t copy16 = nullptr;
     hipFunction_t gemm_q4_0 = nullptr;
+    hipFunction_t qk_norm_rope_kv = nullptr;
+    hipFunction_t attn_partial = nullptr;
+    hipFunction_t attn_combine = nullptr;
+    hipFunction_t synth_blocks = nullptr;
+    hipFunction_t synth_f16 = nullptr;
+
+    // attention partials (per q head and 64-position split: 128 acc + m + l)
+    float* attn_part = nullptr;
+    size_t attn_part_cap = 0;
+    bool capturing = false;
 
     // prefill scratch: quantized activations (qx, dx, sums) and staged x/out
     uint8_t* q_scratch = nullptr;
@@ -235,6 +245,16 @@ bool load_kernels(zlm_device* d) {
     if (!ok(d, hipModuleGetFunction(&d->tile_q4_0, d->mod, "zlm_tile_q4_0"), "zlm_tile_q4_0")) return false;
     if (!ok(d, hipModuleGetFunction(&d->copy16, d->mod, "zlm_copy16"), "zlm_copy16")) return false;
     if (!ok(d, hipModuleGetFunction(&d->gemm_q4_0, d->mod, "zlm_gemm_q4_0_q8"), "zlm_gemm_q4_0_q8")) return false;
+    const struct {
+        hipFunction_t* f;
+        const char* name;
+    } more[] = {{&d->qk_norm_rope_kv, "zlm_qk_norm_rope_kv"},
+                {&d->attn_partial, "zlm_attn_partial"},
+                {&d->attn_combine, "zlm_attn_combine"},
+                {&d->synth_blocks, "zlm_synth_blocks"},
+                {&d->synth_f16, "zlm_synth_f16"}};
+    for (const auto& m : more)
+        if (!ok(d, hipModuleGetFunction(m.f, d->mod, m.name), m.name)) return false;
     return true;
 }
 
@@ -708,6 +728,7 @@ extern "C" void zlm_gpu_deinit(zlm_device* d) {
         if (d->h_x) hipHostFree(d->h_x);
         if (d->d_y) hipFree(d->d_y);
         if (d->h_y) hipHostFree(d->h_y);
+        if (d->attn_part) hipFree(d->attn_part);
         if (d->d_mid) hipFree(d->d_mid);
         if (d->h_mid) hipHostFree(d->h_mid);
         if (d->d_bx) hipFree(d->d_bx);
@@ -1095,7 +1116,7 @@ extern "C" bool zlm_gpu_dev_download(zlm_device* d, void* dst, const void* src, 
     return ok(d, hipStreamSynchronize(d->stream), "sync");
 }
 
-extern "C" bool zlm_gpu_dev_copy(zlm_device* d, void* dst, const void* src, size_t bytes) {
+extern "C" bool zlm_gpu_dev_copy_enqueue(zlm_device* d, void* dst, const void* src, size_t bytes) {
     if (!d || !d->avail || !dst || !src) return false;
     if (bytes % 16 || reinterpret_cast<uintptr_t>(dst) % 16 || reinterpret_cast<uintptr_t>(src) % 16)
         return fail(d, "dev_copy needs 16-byte granules");
@@ -1103,7 +1124,11 @@ extern "C" bool zlm_gpu_dev_copy(zlm_device* d, void* dst, const void* src, size
     uint64_t n16 = bytes / 16;
     const unsigned grid = static_cast<unsigned>(std::min<uint64_t>((n16 + 255) / 256, static_cast<uint64_t>(d->cus) * 8));
     void* args[] = {const_cast<void**>(&src), &dst, &n16};
-    return launch(d, d->copy16, grid, 256, args, "copy") && ok(d, hipStreamSynchronize(d->stream), "sync");
+    return launch(d, d->copy16, grid, 256, args, "copy");
+}
+
+extern "C" bool zlm_gpu_dev_copy(zlm_device* d, void* dst, const void* src, size_t bytes) {
+    return zlm_gpu_dev_copy_enqueue(d, dst, src, bytes) && ok(d, hipStreamSynchronize(d->stream), "sync");
 }
 
 extern "C" bool zlm_gpu_mat_vec_enqueue(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
@@ -1195,6 +1220,158 @@ extern "C" bool zlm_gpu_gemv_op_enqueue(zlm_device* d, const zlm_gemv_op* op) {
     if (!d || !d->avail) return false;
     if (!op) return fail(d, "null op");
     return enqueue_op(d, *op);
+}
+
+// ---- decode-step glue, graphs and synthetic data ----
+
+extern "C" bool zlm_gpu_qk_norm_rope_kv_enqueue(zlm_device* d, const float* qkv, float* q_out, const float* q_norm_w,
+                                                const float* k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                                uint32_t head_dim, float eps, float freq_base, const int32_t* pos,
+                                                uint16_t* k_cache, uint16_t* v_cache, uint32_t max_seq) {
+    if (!d || !d->avail) return false;
+    if (!qkv || !q_out || !q_norm_w || !k_norm_w || !pos || !k_cache || !v_cache) return fail(d, "null buffer");
+    if (n_heads == 0 || n_kv_heads == 0 || head_dim == 0 || head_dim % 2 || head_dim > 256 || max_seq == 0)
+        return fail(d, "bad attention shape");
+    uint16_t* kc = k_cache;
+    uint16_t* vc = v_cache;
+    void* args[] = {&qkv, &q_out, &q_norm_w, &k_norm_w, &n_heads, &n_kv_heads, &head_dim, &eps, &freq_base,
+                    &pos, &kc, &vc, &max_seq};
+    return launch(d, d->qk_norm_rope_kv, n_heads + 2 * n_kv_heads, 64, args, "qk norm rope");
+}
+
+extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const uint16_t* k_cache,
+                                          const uint16_t* v_cache, uint32_t n_heads, uint32_t n_kv_heads,
+                                          uint32_t head_dim, const int32_t* pos, uint32_t max_seq, float scale,
+                                          float* out) {
+    if (!d || !d->avail) return false;
+    if (!q || !k_cache || !v_cache || !pos || !out) return fail(d, "null buffer");
+    if (head_dim != 128) return fail(d, "attention supports head_dim 128 (got %u)", head_dim);
+    if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 4 || max_seq == 0)
+        return fail(d, "attention supports 1-4 q heads per kv head");
+    uint32_t nsplit = (max_seq + 63) / 64;
+    const size_t need = static_cast<size_t>(n_heads) * nsplit * 130;
+    if (need > d->attn_part_cap) {
+        if (d->capturing) return fail(d, "attention scratch must be sized by an eager call before capture");
+        if (d->attn_part) {
+            hipStreamSynchronize(d->stream);
+            hipFree(d->attn_part);
+        }
+        d->attn_part = nullptr;
+        d->attn_part_cap = 0;
+        if (!ok(d, hipMalloc(reinterpret_cast<void**>(&d->attn_part), need * sizeof(float)), "hipMalloc attn"))
+            return false;
+        d->attn_part_cap = need;
+    }
+    float* part = d->attn_part;
+    {
+        void* args[] = {&q, &k_cache, &v_cache, &n_heads, &n_kv_heads, &pos, &max_seq, &scale, &part, &nsplit};
+        if (!ok(d, hipModuleLaunchKernel(d->attn_partial, n_kv_heads, nsplit, 1, 256, 1, 1, 0, d->stream, args,
+                                         nullptr),
+                "attention"))
+            return false;
+    }
+    void* args[] = {&part, &nsplit, &out};
+    return launch(d, d->attn_combine, n_heads, 64, args, "attention combine");
+}
+
+struct zlm_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" bool zlm_gpu_capture_begin(zlm_device* d) {
+    if (!d || !d->avail) return false;
+    if (d->capturing) return fail(d, "already capturing");
+    if (!ok(d, hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed), "begin capture")) return false;
+    d->capturing = true;
+    return true;
+}
+
+extern "C" zlm_graph* zlm_gpu_capture_end(zlm_device* d) {
+    if (!d || !d->avail || !d->capturing) return nullptr;
+    d->capturing = false;
+    zlm_graph* g = new (std::nothrow) zlm_graph();
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(d->stream, &graph);
+    if (!g || !ok(d, e, "end capture") || !graph) {
+        if (graph) hipGraphDestroy(graph);
+        delete g;
+        return nullptr;
+    }
+    g->graph = graph;
+    if (!ok(d, hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0), "instantiate")) {
+        hipGraphDestroy(graph);
+        delete g;
+        return nullptr;
+    }
+    return g;
+}
+
+extern "C" bool zlm_gpu_graph_launch(zlm_device* d, zlm_graph* g, int iters, double* ms) {
+    if (!d || !d->avail || !g || iters < 1) return false;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (ms) {
+        if (!ok(d, hipEventCreate(&e0), "event") || !ok(d, hipEventCreate(&e1), "event")) return false;
+        hipEventRecord(e0, d->stream);
+    }
+    bool good = true;
+    for (int i = 0; i < iters && good; i++) good = ok(d, hipGraphLaunch(g->exec, d->stream), "graph launch");
+    if (ms) hipEventRecord(e1, d->stream);
+    good = ok(d, hipStreamSynchronize(d->stream), "sync") && good;
+    if (ms) {
+        float t = 0.0f;
+        hipEventElapsedTime(&t, e0, e1);
+        *ms = t;
+        hipEventDestroy(e0);
+        hipEventDestroy(e1);
+    }
+    return good;
+}
+
+extern "C" void zlm_gpu_graph_destroy(zlm_device* d, zlm_graph* g) {
+    if (!g) return;
+    if (d && d->avail) hipStreamSynchronize(d->stream);
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+}
+
+extern "C" zlm_resident* zlm_gpu_synth_resident(zlm_device* d, uint32_t ggml_type, size_t nblocks, uint64_t seed,
+                                                float scale) {
+    if (!d || !d->avail) return nullptr;
+    if (ggml_type != ZLM_GGML_Q4_0 && ggml_type != ZLM_GGML_Q8_0) {
+        fail(d, "synthetic blocks exist for q4_0 and q8_0");
+        return nullptr;
+    }
+    const QuantInfo* qi = quant_info(ggml_type);
+    zlm_resident* r = new (std::nothrow) zlm_resident();
+    if (!r) return nullptr;
+    r->owner = d;
+    r->bytes = nblocks * qi->block_bytes;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&r->raw), r->bytes ? r->bytes : 1), "hipMalloc resident")) {
+        delete r;
+        return nullptr;
+    }
+    uint8_t* raw = r->raw;
+    uint64_t n = nblocks;
+    void* args[] = {&raw, &ggml_type, &n, &seed, &scale};
+    if (nblocks && (!launch(d, d->synth_blocks, static_cast<unsigned>((nblocks + 255) / 256), 256, args, "synth") ||
+                    !ok(d, hipStreamSynchronize(d->stream), "sync"))) {
+        hipFree(r->raw);
+        delete r;
+        return nullptr;
+    }
+    return r;
+}
+
+extern "C" bool zlm_gpu_synth_f16(zlm_device* d, uint16_t* dst, size_t n, uint64_t seed, float scale) {
+    if (!d || !d->avail) return false;
+    if (!dst) return fail(d, "null buffer");
+    if (n == 0) return true;
+    uint64_t nn = n;
+    void* args[] = {&dst, &nn, &seed, &scale};
+    return launch(d, d->synth_f16, static_cast<unsigned>((n + 255) / 256), 256, args, "synth f16") &&
+           ok(d, hipStreamSynchronize(d->stream), "sync");
 }
 
 extern "C" bool zlm_gpu_dequant_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t n, float* out) {

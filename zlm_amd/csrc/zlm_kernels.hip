@@ -332,3 +332,303 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
     }
 }
 
+
+// ---- decode-step glue -------------------------------------------------------
+// The non-GEMV ops of one Qwen3 decode layer (reference
+// architectures/impl/qwen3/block.zig:20-41), so activations stay in HBM
+// between the GEMVs: per-head q/k RMSNorm + RoPE + the K/V cache append, and
+// split-K attention over the fp16 cache.  KV cache layout (reference
+// transformer/attention.zig:6-28): [n_kv_heads][max_seq][head_dim] f16.  The
+// position is read from device memory (*pos), so a captured step can be
+// replayed for another position without re-recording.
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// qkv = [q: nh*hd | k: nkv*hd | v: nkv*hd] fp32 (the fused q/k/v GEMV's
+// output).  One 64-lane workgroup per head: heads [0, nh) are q heads (out to
+// q_out), [nh, nh+nkv) k heads (to the K cache at *pos), the rest v heads (to
+// the V cache).  q and k: RMSNorm with the head weight (norm.zig:39-54,
+// qkNormHeads :116-126), then the rotate-half RoPE (rope.zig:4-33 with the
+// RopeTable frequencies :46-104: inv_freq_i = base^(-2i/hd), angle = pos *
+// inv_freq_i; pair (i, i + hd/2) -> (x0 c - x1 s, x0 s + x1 c)).  Lane l owns
+// pairs i = l and l + 64 (hd <= 256).  Every global load (position, head
+// values, norm weights) is issued before the first use, so the kernel is one
+// memory round trip.  A position at or past max_seq writes nothing.
+extern "C" __global__ void __launch_bounds__(64)
+    zlm_qk_norm_rope_kv(const float* __restrict__ qkv, float* __restrict__ q_out, const float* __restrict__ qn_w,
+                        const float* __restrict__ kn_w, uint32_t nh, uint32_t nkv, uint32_t hd, float eps,
+                        float freq_base, const int32_t* __restrict__ pos_p, _Float16* __restrict__ kc,
+                        _Float16* __restrict__ vc, uint32_t max_seq) {
+    const uint32_t head = blockIdx.x;
+    const uint32_t lane = threadIdx.x;
+    const uint32_t half = hd / 2;
+    const bool is_v = head >= nh + nkv;
+    const bool is_q = head < nh;
+    const float* src = qkv + static_cast<size_t>(head) * hd;  // q, k and v heads are consecutive
+    const float* w = is_q ? qn_w : kn_w;
+    const int32_t pos_i = *pos_p;
+    float x0[2], x1[2], w0[2], w1[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const uint32_t i = min(lane + kWave * p, half - 1);
+        x0[p] = src[i];
+        x1[p] = src[i + half];
+        w0[p] = w[i];
+        w1[p] = w[i + half];
+    }
+    const bool pos_ok = pos_i >= 0 && static_cast<uint32_t>(pos_i) < max_seq;
+    const uint32_t pos = pos_ok ? static_cast<uint32_t>(pos_i) : 0u;
+    if (is_v) {  // the cache append only
+        _Float16* dst = vc + (static_cast<size_t>(head - nh - nkv) * max_seq + pos) * hd;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint32_t i = lane + kWave * p;
+            if (pos_ok && i < half) {
+                dst[i] = static_cast<_Float16>(x0[p]);
+                dst[i + half] = static_cast<_Float16>(x1[p]);
+            }
+        }
+        return;
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        if (lane + kWave * p < half) {
+            ss = fmaf(x0[p], x0[p], ss);
+            ss = fmaf(x1[p], x1[p], ss);
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(ss) / static_cast<float>(hd) + eps);
+    const float t = static_cast<float>(pos_i);
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const uint32_t i = lane + kWave * p;
+        if (i >= half) continue;
+        const float a = x0[p] * inv * w0[p];
+        const float b = x1[p] * inv * w1[p];
+        const float angle = t * powf(freq_base, -2.0f * static_cast<float>(i) / static_cast<float>(hd));
+        const float c = cosf(angle), s = sinf(angle);
+        const float r0 = fmaf(b, -s, a * c);
+        const float r1 = fmaf(b, c, a * s);
+        if (is_q) {
+            q_out[static_cast<size_t>(head) * hd + i] = r0;
+            q_out[static_cast<size_t>(head) * hd + i + half] = r1;
+        } else if (pos_ok) {
+            _Float16* dst = kc + (static_cast<size_t>(head - nh) * max_seq + pos) * hd;
+            dst[i] = static_cast<_Float16>(r0);
+            dst[i + half] = static_cast<_Float16>(r1);
+        }
+    }
+}
+
+// Split-K decode attention, head_dim 128 (reference attention.zig:86-170, the
+// per-q-head online softmax, here split over position ranges and merged by
+// zlm_attn_combine).  Grid (nkv, nsplit), 256 threads.  Workgroup (h, s)
+// handles the G = nh/nkv q heads of kv head h (G <= 4) over positions
+// [64 s, 64 s + 64) clipped to L = min(*pos + 1, max_seq):
+//   scores: thread t takes position t/4 and dims 32*(t%4)..+31 for all G heads
+//           (4 lanes reduce a dot with two shuffles), score = (q.k) * scale;
+//   softmax: wave g (< G) takes head g's 64 scores: m = max, p = exp(s - m),
+//           l = sum p;
+//   values:  wave g accumulates sum_t p_t V[t] with lane l owning dims 2l, 2l+1;
+//           the split's V loads (one 256-byte row per position) are all issued
+//           before the first FMA, so the split costs one memory round trip.
+// Output part[(qh*nsplit + s)*130 + d] = unnormalised acc (d < 128), then m, l.
+constexpr int kAttnHd = 128;
+constexpr int kAttnSplit = 64;
+constexpr int kAttnPart = kAttnHd + 2;
+
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_attn_partial(const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
+                     uint32_t nh, uint32_t nkv, const int32_t* __restrict__ pos_p, uint32_t max_seq, float scale,
+                     float* __restrict__ part, uint32_t nsplit) {
+    __shared__ float qs[4][kAttnHd];
+    __shared__ float sc[4][kAttnSplit];
+    const uint32_t h = blockIdx.x, s = blockIdx.y;
+    const uint32_t G = nh / nkv;
+    const uint32_t tid = threadIdx.x, wid = tid / kWave, lane = tid & (kWave - 1);
+    const int32_t pos_i = *pos_p;
+    // q (scaled) for the G heads into LDS; thread tid holds 2 of the 4*128 values
+    float qv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t i = tid + 256u * j, g = i / kAttnHd, d = i % kAttnHd;
+        qv[j] = q[static_cast<size_t>(h * G + min(g, G - 1)) * kAttnHd + d];
+    }
+    const uint32_t L = pos_i < 0 ? 0u : min(static_cast<uint32_t>(pos_i) + 1u, max_seq);
+    const uint32_t t0 = s * kAttnSplit;
+    const uint32_t n = t0 < L ? min(static_cast<uint32_t>(kAttnSplit), L - t0) : 0u;
+    const uint32_t p = tid / 4, qd = tid % 4;
+    const bool valid = p < n;
+    uint4 kraw[4];
+    {
+        const _Float16* kr = kc + (static_cast<size_t>(h) * max_seq + t0 + (valid ? p : 0u)) * kAttnHd + 32 * qd;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            kraw[c] = valid ? *reinterpret_cast<const uint4*>(kr + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t i = tid + 256u * j, g = i / kAttnHd;
+        qs[g][i % kAttnHd] = g < G ? qv[j] * scale : 0.0f;
+    }
+    __syncthreads();
+    {
+        float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t wv[4] = {kraw[c].x, kraw[c].y, kraw[c].z, kraw[c].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float k0 = h2f(wv[j]), k1 = h2f(wv[j] >> 16);
+                const int d = 32 * qd + 8 * c + 2 * j;
+#pragma unroll
+                for (int g = 0; g < 4; g++) dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            dot[g] += __shfl_xor(dot[g], 1, kWave);
+            dot[g] += __shfl_xor(dot[g], 2, kWave);
+        }
+        if (qd == 0) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) sc[g][p] = valid ? dot[g] : -INFINITY;
+        }
+    }
+    __syncthreads();
+    if (wid >= G) return;  // no barrier follows
+    const uint32_t g = wid;
+    // the split's V rows: position j's two dims of this lane, all loads first
+    uint32_t vv[kAttnSplit];
+    {
+        const _Float16* vr = vc + (static_cast<size_t>(h) * max_seq + t0) * kAttnHd + 2 * lane;
+#pragma unroll
+        for (int j = 0; j < kAttnSplit; j++)
+            vv[j] = static_cast<uint32_t>(j) < n ? *reinterpret_cast<const uint32_t*>(vr + static_cast<size_t>(j) * kAttnHd)
+                                                 : 0u;
+    }
+    const float sv = sc[g][lane];
+    const float m = wave_max(sv);
+    const float e = (sv == -INFINITY) ? 0.0f : expf(sv - m);
+    const float l = wave_sum(e);
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kAttnSplit; j++) {
+        const float pe = __shfl(e, j, kWave);  // position j's weight, held by lane j (0 past n)
+        a0 = fmaf(pe, h2f(vv[j]), a0);
+        a1 = fmaf(pe, h2f(vv[j] >> 16), a1);
+    }
+    float* out = part + (static_cast<size_t>(h * G + g) * nsplit + s) * kAttnPart;
+    out[2 * lane] = a0;
+    out[2 * lane + 1] = a1;
+    if (lane == 0) {
+        out[kAttnHd] = m;
+        out[kAttnHd + 1] = l;
+    }
+}
+
+// Merge the nsplit partials of each q head: M = max m_s, w_s = exp(m_s - M)
+// (0 for an empty split), out = sum w_s acc_s / sum w_s l_s.  One 64-lane
+// workgroup per q head: lane s holds split s's (m, l) (64 splits per pass),
+// lane l owns dims 2l, 2l+1 of the accumulators, whose loads are issued 16
+// splits at a time ahead of their FMAs.
+extern "C" __global__ void __launch_bounds__(64)
+    zlm_attn_combine(const float* __restrict__ part, uint32_t nsplit, float* __restrict__ out) {
+    const uint32_t qh = blockIdx.x, lane = threadIdx.x;
+    const float* base = part + static_cast<size_t>(qh) * nsplit * kAttnPart;
+    float M = -INFINITY;
+    for (uint32_t s0 = 0; s0 < nsplit; s0 += kWave) {
+        const uint32_t s = s0 + lane;
+        M = fmaxf(M, wave_max(s < nsplit ? base[static_cast<size_t>(s) * kAttnPart + kAttnHd] : -INFINITY));
+    }
+    float a0 = 0.0f, a1 = 0.0f, den = 0.0f;
+    for (uint32_t s0 = 0; s0 < nsplit; s0 += kWave) {
+        const uint32_t s = s0 + lane;
+        const bool sv = s < nsplit;
+        const float ms = sv ? base[static_cast<size_t>(s) * kAttnPart + kAttnHd] : -INFINITY;
+        const float ls = sv ? base[static_cast<size_t>(s) * kAttnPart + kAttnHd + 1] : 0.0f;
+        const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+        den += wave_sum(w * ls);
+        const uint32_t cnt = min(static_cast<uint32_t>(kWave), nsplit - s0);
+        for (uint32_t j0 = 0; j0 < cnt; j0 += 16) {
+            float2 acc[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const uint32_t sj = s0 + min(j0 + j, cnt - 1);
+                acc[j] = *reinterpret_cast<const float2*>(base + static_cast<size_t>(sj) * kAttnPart + 2 * lane);
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float wj = __shfl(w, static_cast<int>(j0 + j) & (kWave - 1), kWave);
+                const float use = (j0 + j < cnt) ? wj : 0.0f;
+                a0 = fmaf(use, acc[j].x, a0);
+                a1 = fmaf(use, acc[j].y, a1);
+            }
+        }
+    }
+    const float inv = 1.0f / den;
+    *reinterpret_cast<float2*>(out + static_cast<size_t>(qh) * kAttnHd + 2 * lane) = make_float2(a0 * inv, a1 * inv);
+}
+
+// ---- synthetic data on the device (benchmark and large-shape tests) ---------
+// splitmix64 of (seed, index): the same counter-based generator as the
+// repository's Python synthesiser, used here to fill raw GGUF blocks in HBM so
+// multi-GB synthetic models need no host generation or upload.
+__device__ __forceinline__ uint64_t smix(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// |N(0,1)| from two uniforms (Box-Muller).
+__device__ __forceinline__ float abs_normal(uint64_t r) {
+    const float u1 = (static_cast<float>(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = static_cast<float>((r >> 16) & 0xffffffu) * (1.0f / 16777216.0f);
+    return fabsf(sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2));
+}
+
+// One thread per raw block of type `type` (2 = q4_0: f16 d + 16 random bytes;
+// 8 = q8_0: f16 d + 32 int8 uniform in [-127, 127]); d = f16(|N(0,1)| * scale).
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_synth_blocks(uint8_t* __restrict__ raw, uint32_t type, uint64_t nblocks, uint64_t seed, float scale) {
+    const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint32_t bb = type == 8u ? 34u : 18u;
+    uint8_t* dst = raw + b * bb;
+    const uint64_t base = smix(seed ^ (b * 0xD1B54A32D192ED03ull));
+    const _Float16 d = static_cast<_Float16>(abs_normal(smix(base)) * scale);
+    const uint16_t db = __builtin_bit_cast(uint16_t, d);
+    dst[0] = static_cast<uint8_t>(db & 0xffu);
+    dst[1] = static_cast<uint8_t>(db >> 8);
+    const uint32_t nq = bb - 2;
+    for (uint32_t i = 0; i < nq; i += 8) {
+        const uint64_t r = smix(base + 1 + i);
+        for (uint32_t j = 0; j < 8 && i + j < nq; j++) {
+            const uint32_t byte = static_cast<uint32_t>(r >> (8 * j)) & 0xffu;
+            dst[2 + i + j] = type == 8u ? static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(byte % 255u) - 127))
+                                        : static_cast<uint8_t>(byte);
+        }
+    }
+}
+
+// n f16 values N(0,1) * scale (signed), e.g. a KV cache's history.
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_synth_f16(_Float16* __restrict__ out, uint64_t n, uint64_t seed, float scale) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t r = smix(seed ^ (i * 0xD1B54A32D192ED03ull));
+    const float v = abs_normal(r) * scale;
+    out[i] = static_cast<_Float16>((r & 1u) ? -v : v);
+}

@@ -156,6 +156,7 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_dev_upload": (B, [P, P, P, S]),
         "zlm_gpu_dev_download": (B, [P, P, P, S]),
         "zlm_gpu_dev_copy": (B, [P, P, P, S]),
+        "zlm_gpu_dev_copy_enqueue": (B, [P, P, P, S]),
         "zlm_gpu_mat_vec_enqueue": (B, [P, P, U, S, S, P, P]),
         "zlm_gpu_time_mat_vec": (B, [P, P, S, U, S, S, P, P, ctypes.c_int, P]),
         "zlm_gpu_mat_mul_enqueue": (B, [P, P, U, S, S, S, P, P]),
@@ -163,6 +164,15 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_time_gemv_sequence": (B, [P, P, S, ctypes.c_int, P]),
         "zlm_gpu_dequant_resident": (B, [P, P, U, S, P]),
         "zlm_gpu_gemv_op_enqueue": (B, [P, P]),
+        "zlm_gpu_qk_norm_rope_kv_enqueue": (B, [P, P, P, P, P, U, U, U, ctypes.c_float, ctypes.c_float, P, P, P,
+                                                U]),
+        "zlm_gpu_attention_enqueue": (B, [P, P, P, P, U, U, U, P, U, ctypes.c_float, P]),
+        "zlm_gpu_capture_begin": (B, [P]),
+        "zlm_gpu_capture_end": (P, [P]),
+        "zlm_gpu_graph_launch": (B, [P, P, ctypes.c_int, P]),
+        "zlm_gpu_graph_destroy": (None, [P, P]),
+        "zlm_gpu_synth_resident": (P, [P, U, S, ctypes.c_uint64, ctypes.c_float]),
+        "zlm_gpu_synth_f16": (B, [P, P, S, ctypes.c_uint64, ctypes.c_float]),
         "zlm_gpu_quantize_act_q8": (B, [P, P, S, P, P, P]),
     }
     for name, (res, args) in sig.items():
@@ -383,6 +393,9 @@ class Device:
         if not self._L.zlm_gpu_dev_copy(self._h, dst, src, nbytes):
             raise RuntimeError(self.last_error())
 
+    def dev_copy_enqueue(self, dst: int, src: int, nbytes: int) -> bool:
+        return bool(self._L.zlm_gpu_dev_copy_enqueue(self._h, dst, src, nbytes))
+
     def mat_vec_enqueue(self, res: Resident, quant: int, rows: int, k: int, x_dev: int, y_dev: int) -> bool:
         return bool(self._L.zlm_gpu_mat_vec_enqueue(self._h, res.ptr, quant, rows, k, x_dev, y_dev))
 
@@ -427,6 +440,44 @@ class Device:
         op = _GemvOp(form, quant, w.ptr if w else None, w_up.ptr if w_up else None, rows, k, x_dev,
                      norm_w or None, eps, act, res or None, y_dev)
         return bool(self._L.zlm_gpu_gemv_op_enqueue(self._h, ctypes.byref(op)))
+
+    # -- decode-step glue, graphs, synthetic data ------------------------------
+    def qk_norm_rope_kv_enqueue(self, qkv: int, q_out: int, q_norm_w: int, k_norm_w: int, n_heads: int,
+                                n_kv_heads: int, head_dim: int, eps: float, freq_base: float, pos: int,
+                                k_cache: int, v_cache: int, max_seq: int) -> bool:
+        return bool(self._L.zlm_gpu_qk_norm_rope_kv_enqueue(self._h, qkv, q_out, q_norm_w, k_norm_w, n_heads,
+                                                            n_kv_heads, head_dim, eps, freq_base, pos, k_cache,
+                                                            v_cache, max_seq))
+
+    def attention_enqueue(self, q: int, k_cache: int, v_cache: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                          pos: int, max_seq: int, scale: float, out: int) -> bool:
+        return bool(self._L.zlm_gpu_attention_enqueue(self._h, q, k_cache, v_cache, n_heads, n_kv_heads, head_dim,
+                                                      pos, max_seq, scale, out))
+
+    def capture_begin(self) -> bool:
+        return bool(self._L.zlm_gpu_capture_begin(self._h))
+
+    def capture_end(self) -> Optional[int]:
+        g = self._L.zlm_gpu_capture_end(self._h)
+        return g or None
+
+    def graph_launch(self, graph: int, iters: int = 1) -> float:
+        """Launch a captured graph `iters` times; returns GPU milliseconds for all of them."""
+        ms = ctypes.c_double(0.0)
+        if not self._L.zlm_gpu_graph_launch(self._h, graph, iters, ctypes.addressof(ms)):
+            raise RuntimeError(self.last_error())
+        return ms.value
+
+    def graph_destroy(self, graph: int) -> None:
+        self._L.zlm_gpu_graph_destroy(self._h, graph)
+
+    def synth_resident(self, ggml_type: int, n_blocks: int, seed: int, scale: float) -> Optional[Resident]:
+        p = self._L.zlm_gpu_synth_resident(self._h, ggml_type, n_blocks, seed & 0xFFFFFFFFFFFFFFFF, scale)
+        return Resident(self, p) if p else None
+
+    def synth_f16(self, dst: int, n: int, seed: int, scale: float) -> None:
+        if not self._L.zlm_gpu_synth_f16(self._h, dst, n, seed & 0xFFFFFFFFFFFFFFFF, scale):
+            raise RuntimeError(self.last_error())
 
     def dequant_resident(self, res: Resident, quant: int, n: int) -> Optional[np.ndarray]:
         out = np.zeros(n, np.float32)
