@@ -265,6 +265,18 @@ bool zlm_gpu_attention_enqueue(zlm_device *dev, const float *q, const uint16_t *
                                uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, const int32_t *pos,
                                uint32_t max_seq, float scale, float *out);
 
+/* The fused decode attention block: q/k head norm + RoPE, the K/V append at
+ * *pos and the attention over [0, *pos] in one launch (the two calls above,
+ * with `scale` and the q/k norms of the same reference routines), then the
+ * split merge; qkv as for zlm_gpu_qk_norm_rope_kv_enqueue, out: n_heads*128
+ * fp32.  head_dim 128, n_heads / n_kv_heads <= 4.  Uses the library scratch
+ * of zlm_gpu_attention_enqueue (call once before capture). */
+bool zlm_gpu_attention_decode_enqueue(zlm_device *dev, const float *qkv, const float *q_norm_w,
+                                      const float *k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                      uint32_t head_dim, float eps, float freq_base, const int32_t *pos,
+                                      uint16_t *k_cache, uint16_t *v_cache, uint32_t max_seq, float scale,
+                                      float *out);
+
 /* ---- HIP graphs over the device stream ----
  * Everything enqueued between capture_begin and capture_end is recorded, not
  * run.  Ops that allocate or convert layouts on first use must have run once

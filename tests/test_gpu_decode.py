@@ -94,6 +94,41 @@ def test_attention_matches_oracle(dev, nh, nkv, L):
         dev.dev_free(p)
 
 
+@pytest.mark.parametrize("nh,nkv,pos", [(32, 8, 0), (32, 8, 63), (32, 8, 64), (32, 8, 700), (32, 8, 2047),
+                                        (8, 4, 129), (16, 16, 5)])
+def test_fused_attention_decode_matches_oracle(dev, nh, nkv, pos):
+    """q/k head norm + RoPE, K/V append at pos and attention in one launch, then the merge."""
+    hd, max_seq, eps, base = 128, 2048, 1e-6, 1e6
+    _say(f"attention_decode nh={nh} nkv={nkv} pos={pos}")
+    rng = np.random.default_rng(pos + nh)
+    qkv = (rng.standard_normal((nh + 2 * nkv) * hd) * 2).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kc0 = rng.standard_normal((nkv, max_seq, hd)).astype(np.float16)
+    vc0 = rng.standard_normal((nkv, max_seq, hd)).astype(np.float16)
+    scale = 1.0 / math.sqrt(hd)
+    d_qkv, d_qn, d_kn, d_kc, d_vc = (_vec(dev, a) for a in (qkv, qn, kn, kc0, vc0))
+    d_pos = _vec(dev, np.array([pos, 0, 0, 0], np.int32))
+    d_out = dev.dev_malloc(nh * hd * 4)
+    q, k, v = od.qk_norm_rope(qkv, qn, kn, nh, nkv, hd, eps, base, pos)
+    kref, vref = kc0.copy(), vc0.copy()
+    od.write_kv(k, v, kref, vref, pos)
+    want = od.attend(q, kref, vref, nh, pos, scale)
+    for rep in range(2):  # a second call over the appended caches gives the same result
+        assert dev.attention_decode_enqueue(d_qkv, d_qn, d_kn, nh, nkv, hd, eps, base, d_pos, d_kc, d_vc, max_seq,
+                                            scale, d_out), dev.last_error()
+        out = np.zeros(nh * hd, np.float32)
+        dev.dev_download(out, d_out)
+        assert rel_l2(out, want) <= 1e-4, rep
+    kc, vc = np.zeros_like(kc0), np.zeros_like(vc0)
+    dev.dev_download(kc, d_kc)
+    dev.dev_download(vc, d_vc)
+    np.testing.assert_array_equal(vc, vref)
+    np.testing.assert_allclose(kc.astype(np.float32), kref.astype(np.float32), rtol=2e-3, atol=1e-3)
+    for p in (d_qkv, d_qn, d_kn, d_kc, d_vc, d_pos, d_out):
+        dev.dev_free(p)
+
+
 def test_attention_rejects_unsupported_shapes(dev):
     p = dev.dev_malloc(1 << 16)
     assert not dev.attention_enqueue(p, p, p, 32, 8, 64, p, 16, 1.0, p)  # head_dim

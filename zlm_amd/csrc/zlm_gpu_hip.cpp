@@ -143,6 +143,7 @@ struct zlm_device {
     hipFunction_t qk_norm_rope_kv = nullptr;
     hipFunction_t attn_partial = nullptr;
     hipFunction_t attn_combine = nullptr;
+    hipFunction_t attn_decode = nullptr;
     hipFunction_t synth_blocks = nullptr;
     hipFunction_t synth_f16 = nullptr;
 
@@ -251,6 +252,7 @@ bool load_kernels(zlm_device* d) {
     } more[] = {{&d->qk_norm_rope_kv, "zlm_qk_norm_rope_kv"},
                 {&d->attn_partial, "zlm_attn_partial"},
                 {&d->attn_combine, "zlm_attn_combine"},
+                {&d->attn_decode, "zlm_attn_decode"},
                 {&d->synth_blocks, "zlm_synth_blocks"},
                 {&d->synth_f16, "zlm_synth_f16"}};
     for (const auto& m : more)
@@ -1239,17 +1241,11 @@ extern "C" bool zlm_gpu_qk_norm_rope_kv_enqueue(zlm_device* d, const float* qkv,
     return launch(d, d->qk_norm_rope_kv, n_heads + 2 * n_kv_heads, 64, args, "qk norm rope");
 }
 
-extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const uint16_t* k_cache,
-                                          const uint16_t* v_cache, uint32_t n_heads, uint32_t n_kv_heads,
-                                          uint32_t head_dim, const int32_t* pos, uint32_t max_seq, float scale,
-                                          float* out) {
-    if (!d || !d->avail) return false;
-    if (!q || !k_cache || !v_cache || !pos || !out) return fail(d, "null buffer");
-    if (head_dim != 128) return fail(d, "attention supports head_dim 128 (got %u)", head_dim);
-    if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 4 || max_seq == 0)
-        return fail(d, "attention supports 1-4 q heads per kv head");
-    uint32_t nsplit = (max_seq + 63) / 64;
-    const size_t need = static_cast<size_t>(n_heads) * nsplit * 130;
+namespace {
+
+// Size the attention partials (floats).  Allocation happens on an eager call;
+// a call under capture that would need it fails.
+bool ensure_attn_scratch(zlm_device* d, size_t need) {
     if (need > d->attn_part_cap) {
         if (d->capturing) return fail(d, "attention scratch must be sized by an eager call before capture");
         if (d->attn_part) {
@@ -1262,6 +1258,47 @@ extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const u
             return false;
         d->attn_part_cap = need;
     }
+    return true;
+}
+
+}  // namespace
+
+extern "C" bool zlm_gpu_attention_decode_enqueue(zlm_device* d, const float* qkv, const float* q_norm_w,
+                                                 const float* k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                                 uint32_t head_dim, float eps, float freq_base, const int32_t* pos,
+                                                 uint16_t* k_cache, uint16_t* v_cache, uint32_t max_seq, float scale,
+                                                 float* out) {
+    if (!d || !d->avail) return false;
+    if (!qkv || !q_norm_w || !k_norm_w || !pos || !k_cache || !v_cache || !out) return fail(d, "null buffer");
+    if (head_dim != 128) return fail(d, "attention supports head_dim 128 (got %u)", head_dim);
+    if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 4 || max_seq == 0)
+        return fail(d, "attention supports 1-4 q heads per kv head");
+    uint32_t nsplit = (max_seq + 63) / 64;
+    if (!ensure_attn_scratch(d, static_cast<size_t>(n_heads) * nsplit * 130)) return false;
+    float* part = d->attn_part;
+    {
+        void* args[] = {&qkv, &q_norm_w, &k_norm_w, &n_heads, &n_kv_heads, &eps, &freq_base, &pos, &k_cache,
+                        &v_cache, &max_seq, &scale, &part, &nsplit};
+        if (!ok(d, hipModuleLaunchKernel(d->attn_decode, n_kv_heads, nsplit, 1, 256, 1, 1, 0, d->stream, args,
+                                         nullptr),
+                "attention decode"))
+            return false;
+    }
+    void* args[] = {&part, &nsplit, &out};
+    return launch(d, d->attn_combine, n_heads, 64, args, "attention combine");
+}
+
+extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const uint16_t* k_cache,
+                                          const uint16_t* v_cache, uint32_t n_heads, uint32_t n_kv_heads,
+                                          uint32_t head_dim, const int32_t* pos, uint32_t max_seq, float scale,
+                                          float* out) {
+    if (!d || !d->avail) return false;
+    if (!q || !k_cache || !v_cache || !pos || !out) return fail(d, "null buffer");
+    if (head_dim != 128) return fail(d, "attention supports head_dim 128 (got %u)", head_dim);
+    if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 4 || max_seq == 0)
+        return fail(d, "attention supports 1-4 q heads per kv head");
+    uint32_t nsplit = (max_seq + 63) / 64;
+    if (!ensure_attn_scratch(d, static_cast<size_t>(n_heads) * nsplit * 130)) return false;
     float* part = d->attn_part;
     {
         void* args[] = {&q, &k_cache, &v_cache, &n_heads, &n_kv_heads, &pos, &max_seq, &scale, &part, &nsplit};

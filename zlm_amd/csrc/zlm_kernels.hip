@@ -538,15 +538,11 @@ extern "C" __global__ void __launch_bounds__(256)
     }
 }
 
-// Merge the nsplit partials of each q head: M = max m_s, w_s = exp(m_s - M)
-// (0 for an empty split), out = sum w_s acc_s / sum w_s l_s.  One 64-lane
-// workgroup per q head: lane s holds split s's (m, l) (64 splits per pass),
-// lane l owns dims 2l, 2l+1 of the accumulators, whose loads are issued 16
-// splits at a time ahead of their FMAs.
-extern "C" __global__ void __launch_bounds__(64)
-    zlm_attn_combine(const float* __restrict__ part, uint32_t nsplit, float* __restrict__ out) {
-    const uint32_t qh = blockIdx.x, lane = threadIdx.x;
-    const float* base = part + static_cast<size_t>(qh) * nsplit * kAttnPart;
+// Merge the partials of one q head into lane l's dims 2l, 2l+1: lane s holds
+// split s's (m, l) (64 splits per pass); the accumulator loads are issued 16
+// splits at a time ahead of their FMAs.  `base` points at the head's nsplit
+// partials.
+__device__ __forceinline__ float2 combine_head(const float* __restrict__ base, uint32_t nsplit, uint32_t lane) {
     float M = -INFINITY;
     for (uint32_t s0 = 0; s0 < nsplit; s0 += kWave) {
         const uint32_t s = s0 + lane;
@@ -578,7 +574,165 @@ extern "C" __global__ void __launch_bounds__(64)
         }
     }
     const float inv = 1.0f / den;
-    *reinterpret_cast<float2*>(out + static_cast<size_t>(qh) * kAttnHd + 2 * lane) = make_float2(a0 * inv, a1 * inv);
+    return make_float2(a0 * inv, a1 * inv);
+}
+
+// Merge the nsplit partials of each q head: M = max m_s, w_s = exp(m_s - M)
+// (0 for an empty split), out = sum w_s acc_s / sum w_s l_s.  One 64-lane
+// workgroup per q head (combine_head).
+extern "C" __global__ void __launch_bounds__(64)
+    zlm_attn_combine(const float* __restrict__ part, uint32_t nsplit, float* __restrict__ out) {
+    const uint32_t qh = blockIdx.x, lane = threadIdx.x;
+    const float2 r = combine_head(part + static_cast<size_t>(qh) * nsplit * kAttnPart, nsplit, lane);
+    *reinterpret_cast<float2*>(out + static_cast<size_t>(qh) * kAttnHd + 2 * lane) = r;
+}
+
+// The decode layer's whole attention block in one launch (reference
+// block.zig:24-31: q_norm/k_norm, rope, write_kv, attention), head_dim 128,
+// G = nh/nkv <= 4.  Grid (nkv, nsplit), 256 threads; workgroup (h, s) owns kv
+// head h's G q heads over positions [64 s, 64 s + 64) of L = *pos + 1:
+//   * every global load it needs (its K and V rows, the raw q / k / v head
+//     values, the norm weights) is issued first;
+//   * the cos/sin of the 64 rotary pairs at *pos go to LDS once;
+//   * wave g normalises and rotates q head g (the same arithmetic as
+//     zlm_qk_norm_rope_kv); the workgroup whose range holds *pos also
+//     normalises and rotates k head h, appends the f16 K and V rows to the
+//     caches and uses those same f16 values for position *pos (no read back);
+//   * scores, softmax and values as zlm_attn_partial, into the same partials,
+//     which zlm_attn_combine merges.  (Merging in the last workgroup of each kv
+//     head instead, behind a device-scope fence and counter, measured 3x
+//     slower on gfx950: every workgroup's release fence writes back its L2.)
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_attn_decode(const float* __restrict__ qkv, const float* __restrict__ qn_w, const float* __restrict__ kn_w,
+                    uint32_t nh, uint32_t nkv, float eps, float freq_base, const int32_t* __restrict__ pos_p,
+                    _Float16* __restrict__ kc, _Float16* __restrict__ vc, uint32_t max_seq, float scale,
+                    float* __restrict__ part, uint32_t nsplit) {
+    __shared__ float qs[4][kAttnHd];
+    __shared__ float sc[4][kAttnSplit];
+    __shared__ float cs[kAttnHd / 2], sn[kAttnHd / 2];
+    __shared__ float kn[kAttnHd], vn[kAttnHd];
+    const uint32_t h = blockIdx.x, s = blockIdx.y;
+    const uint32_t G = nh / nkv;
+    const uint32_t tid = threadIdx.x, wid = tid / kWave, lane = tid & (kWave - 1);
+    constexpr uint32_t half = kAttnHd / 2;
+    const int32_t pos_i = *pos_p;
+    const bool pos_ok = pos_i >= 0 && static_cast<uint32_t>(pos_i) < max_seq;
+    const uint32_t L = pos_i < 0 ? 0u : min(static_cast<uint32_t>(pos_i) + 1u, max_seq);
+    const uint32_t t0 = s * kAttnSplit;
+    const uint32_t n = t0 < L ? min(static_cast<uint32_t>(kAttnSplit), L - t0) : 0u;
+    const bool own = pos_ok && static_cast<uint32_t>(pos_i) >= t0 && static_cast<uint32_t>(pos_i) < t0 + kAttnSplit;
+    const uint32_t prow = own ? static_cast<uint32_t>(pos_i) - t0 : kAttnSplit;  // the new row's slot, or none
+
+    // loads: this wave's q head (raw) and norm weights, k/v of the new row,
+    // the split's K rows (scores mapping) and V rows (values mapping)
+    const uint32_t g = min(wid, G - 1);
+    const float* qh = qkv + static_cast<size_t>(h * G + g) * kAttnHd;
+    const float q0 = qh[lane], q1 = qh[lane + half];
+    const float wq0 = qn_w[lane], wq1 = qn_w[lane + half];
+    const float* kh = qkv + static_cast<size_t>(nh + h) * kAttnHd;
+    const float* vh = qkv + static_cast<size_t>(nh + nkv + h) * kAttnHd;
+    const float k0 = kh[lane], k1 = kh[lane + half], wk0 = kn_w[lane], wk1 = kn_w[lane + half];
+    const float v0 = vh[lane], v1 = vh[lane + half];
+    const uint32_t p = tid / 4, qd = tid % 4;
+    const bool valid = p < n;
+    uint4 kraw[4];
+    {
+        const _Float16* kr = kc + (static_cast<size_t>(h) * max_seq + t0 + (valid ? p : 0u)) * kAttnHd + 32 * qd;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            kraw[c] = valid ? *reinterpret_cast<const uint4*>(kr + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    uint32_t vv[kAttnSplit];
+    {
+        const _Float16* vr = vc + (static_cast<size_t>(h) * max_seq + t0) * kAttnHd + 2 * lane;
+#pragma unroll
+        for (int j = 0; j < kAttnSplit; j++)
+            vv[j] = static_cast<uint32_t>(j) < n ? *reinterpret_cast<const uint32_t*>(vr + static_cast<size_t>(j) * kAttnHd)
+                                                 : 0u;
+    }
+    if (tid < half) {
+        const float angle = static_cast<float>(pos_i) *
+                            powf(freq_base, -2.0f * static_cast<float>(tid) / static_cast<float>(kAttnHd));
+        cs[tid] = cosf(angle);
+        sn[tid] = sinf(angle);
+    }
+    __syncthreads();
+    // q head g: RMSNorm, rotate, scale (lane l owns the pair (l, l + 64))
+    if (wid < G) {
+        const float inv = 1.0f / sqrtf(wave_sum(fmaf(q0, q0, q1 * q1)) / static_cast<float>(kAttnHd) + eps);
+        const float a = q0 * inv * wq0, b = q1 * inv * wq1;
+        qs[wid][lane] = fmaf(b, -sn[lane], a * cs[lane]) * scale;
+        qs[wid][lane + half] = fmaf(b, cs[lane], a * sn[lane]) * scale;
+    } else {
+        qs[wid][lane] = 0.0f;
+        qs[wid][lane + half] = 0.0f;
+    }
+    // the new position's K and V rows: kept as the f16 values the caches hold
+    if (own && wid == 0) {
+        const float inv = 1.0f / sqrtf(wave_sum(fmaf(k0, k0, k1 * k1)) / static_cast<float>(kAttnHd) + eps);
+        const float a = k0 * inv * wk0, b = k1 * inv * wk1;
+        const _Float16 r0 = static_cast<_Float16>(fmaf(b, -sn[lane], a * cs[lane]));
+        const _Float16 r1 = static_cast<_Float16>(fmaf(b, cs[lane], a * sn[lane]));
+        const _Float16 e0 = static_cast<_Float16>(v0), e1 = static_cast<_Float16>(v1);
+        _Float16* kd = kc + (static_cast<size_t>(h) * max_seq + pos_i) * kAttnHd;
+        _Float16* vd = vc + (static_cast<size_t>(h) * max_seq + pos_i) * kAttnHd;
+        kd[lane] = r0;
+        kd[lane + half] = r1;
+        vd[lane] = e0;
+        vd[lane + half] = e1;
+        kn[lane] = static_cast<float>(r0);
+        kn[lane + half] = static_cast<float>(r1);
+        vn[lane] = static_cast<float>(e0);
+        vn[lane + half] = static_cast<float>(e1);
+    }
+    __syncthreads();
+    {
+        float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        const bool newrow = p == prow;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint32_t wv[4] = {kraw[c].x, kraw[c].y, kraw[c].z, kraw[c].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = 32 * qd + 8 * c + 2 * j;
+                const float x0 = newrow ? kn[d] : h2f(wv[j]);
+                const float x1 = newrow ? kn[d + 1] : h2f(wv[j] >> 16);
+#pragma unroll
+                for (int gg = 0; gg < 4; gg++) dot[gg] = fmaf(qs[gg][d + 1], x1, fmaf(qs[gg][d], x0, dot[gg]));
+            }
+        }
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) {
+            dot[gg] += __shfl_xor(dot[gg], 1, kWave);
+            dot[gg] += __shfl_xor(dot[gg], 2, kWave);
+        }
+        if (qd == 0) {
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) sc[gg][p] = valid ? dot[gg] : -INFINITY;
+        }
+    }
+    __syncthreads();
+    if (wid < G) {
+        const float sv = sc[wid][lane];
+        const float m = wave_max(sv);
+        const float e = (sv == -INFINITY) ? 0.0f : expf(sv - m);
+        const float l = wave_sum(e);
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kAttnSplit; j++) {
+            const float pe = __shfl(e, j, kWave);
+            const bool nr = static_cast<uint32_t>(j) == prow;
+            a0 = fmaf(pe, nr ? vn[2 * lane] : h2f(vv[j]), a0);
+            a1 = fmaf(pe, nr ? vn[2 * lane + 1] : h2f(vv[j] >> 16), a1);
+        }
+        float* o = part + (static_cast<size_t>(h * G + wid) * nsplit + s) * kAttnPart;
+        o[2 * lane] = a0;
+        o[2 * lane + 1] = a1;
+        if (lane == 0) {
+            o[kAttnHd] = m;
+            o[kAttnHd + 1] = l;
+        }
+    }
 }
 
 // ---- synthetic data on the device (benchmark and large-shape tests) ---------

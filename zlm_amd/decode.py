@@ -8,8 +8,9 @@ runs through this backend's GEMV kernels, fused where the sequence allows:
     h <- x_in                                        (the token's embedding row)
     per layer:
       qkv  = W_qkv . RMSNorm(h, attn_norm)           GEMV, norm form (q;k;v rows)
-      q, K/V cache <- q/k head RMSNorm + RoPE, append at pos
-      attn = attention(q, K, V)                      split-K + merge
+      attn = attention(RoPE(RMSNorm_head(q)), K, V)  q/k head norm + RoPE, K/V append
+                                                     at pos and split-K attention in
+                                                     one launch, the merge in a second
       h    = h + W_o . attn                          GEMV, residual form
       mid  = silu(W_gate . n) * (W_up . n),  n = RMSNorm(h, ffn_norm)
                                                      GEMV, normed gate_up form
@@ -161,7 +162,6 @@ class DecodeModel:
         self.x_in = buf(c.hidden * 4)
         self.h = buf(c.hidden * 4)
         self.qkv = buf(c.qkv_rows * 4)
-        self.q = buf(c.n_heads * c.head_dim * 4)
         self.attn = buf(c.n_heads * c.head_dim * 4)
         self.mid = buf(c.ffn * 4)
         self.logits = buf(c.vocab * 4)
@@ -182,10 +182,9 @@ class DecodeModel:
         for L in self.layers:
             ok(d.gemv_op_enqueue(zd.FORM_NORM, q, L.qkv, c.qkv_rows, c.hidden, self.h, self.qkv,
                                  norm_w=L.attn_norm, eps=c.eps), "qkv")
-            ok(d.qk_norm_rope_kv_enqueue(self.qkv, self.q, L.q_norm, L.k_norm, c.n_heads, c.n_kv_heads, c.head_dim,
-                                         c.eps, c.freq_base, self.pos, L.k_cache, L.v_cache, c.max_seq), "rope")
-            ok(d.attention_enqueue(self.q, L.k_cache, L.v_cache, c.n_heads, c.n_kv_heads, c.head_dim, self.pos,
-                                   c.max_seq, self.scale, self.attn), "attention")
+            ok(d.attention_decode_enqueue(self.qkv, L.q_norm, L.k_norm, c.n_heads, c.n_kv_heads, c.head_dim, c.eps,
+                                          c.freq_base, self.pos, L.k_cache, L.v_cache, c.max_seq, self.scale,
+                                          self.attn), "attention")
             ok(d.gemv_op_enqueue(zd.FORM_RESID, q, L.o, c.hidden, c.n_heads * c.head_dim, self.attn, self.h,
                                  res=self.h), "o")
             ok(d.gemv_op_enqueue(zd.FORM_NORMPAIR, q, L.gate, c.ffn, c.hidden, self.h, self.mid, w_up=L.up,
