@@ -187,6 +187,13 @@ uint64_t zlm_gpu_resident_bytes(const zlm_resident *res);
 const char *zlm_gpu_last_error(const zlm_device *dev);
 /* Number of compute units, 0 when inert. */
 int zlm_gpu_cu_count(const zlm_device *dev);
+/* Free and total HBM bytes of the device, for the caller's residency budget
+ * (the plan packs its resident set into `--vram` minus a driver headroom,
+ * reference plan/root.zig:36-38, and uploads it with uploadResident,
+ * runtime/session.zig:452-474).  A resident holds its raw bytes until the
+ * first op names its quant; the conversion to the device layout briefly holds
+ * both copies. */
+bool zlm_gpu_vram_info(zlm_device *dev, uint64_t *free_bytes, uint64_t *total_bytes);
 void *zlm_gpu_dev_malloc(zlm_device *dev, size_t bytes);
 void zlm_gpu_dev_free(zlm_device *dev, void *ptr);
 bool zlm_gpu_dev_upload(zlm_device *dev, void *dst, const void *src, size_t bytes);

@@ -92,6 +92,7 @@ def test_inert_device_refuses_everything():
                                                     True) is None
     assert not dev.wait_resident(0, out, rows)
     assert not dev.mat_vec_resident_batch(k, x, [zd.ResidentOp(fake, zd.quant(zd.Q4_0), rows, out)])
+    assert dev.vram_info() is None
     p = dev.probe_gpu(rows, k, 2)
     assert p.gemv_gbps == 0 and p.matmul_gbps == 0 and p.q4_0_variant == 0
     dev.sync()

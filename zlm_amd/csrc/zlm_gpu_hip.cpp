@@ -30,6 +30,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <vector>
 
 namespace {
 
@@ -1082,9 +1083,180 @@ extern "C" void zlm_gpu_sync(zlm_device* d) {
     if (d && d->avail) hipStreamSynchronize(d->stream);
 }
 
-extern "C" void zlm_gpu_probe(zlm_device* d, size_t, size_t, size_t, zlm_probe* out) {
-    if (out) memset(out, 0, sizeof *out);
-    (void)d;
+// ---- probeGpu (reference gpu/backend/root.zig:357-498) ----
+// Each rate is min-of-5 host wall time of one contract op (as the reference
+// measures it: staging, dispatch and read-back included), in GB/s over the
+// weight bytes.  Variants are measured interleaved and the fastest recorded;
+// every GpuVariant maps to one of this backend's row tiles (rt_for_variant).
+// Quants this backend does not run (q4_1, f32, f16, bf16) keep rate 0 and
+// variant `plain`, the contract's "unmeasured".
+
+namespace {
+
+constexpr int kProbeSamples = 5;
+constexpr size_t kProbeMaxRows = 12 * 1024;
+constexpr size_t kProbeMaxK = 4 * 1024;
+constexpr uint32_t kAllVariants[] = {ZLM_VARIANT_PLAIN, ZLM_VARIANT_U4, ZLM_VARIANT_U8, ZLM_VARIANT_SUB,
+                                     ZLM_VARIANT_UN2,   ZLM_VARIANT_UN4, ZLM_VARIANT_W32, ZLM_VARIANT_W128};
+
+// fillWeights (gpu/backend/root.zig:734-786): random bytes with the scale
+// fields overwritten (q4_0/q8_0 d = 0.05, q4_k d = 0.05 and dmin = 0.02, q6_k
+// d = 0.02).  The bytes come from a splitmix64 stream, not Zig's PRNG.
+std::vector<uint8_t> probe_weights(uint32_t type, size_t rows, size_t k) {
+    const QuantInfo* qi = quant_info(type);
+    const size_t nblk = rows * (k / qi->block_elems);
+    std::vector<uint8_t> w(nblk * qi->block_bytes);
+    uint64_t z = 0x9e3779b97f4a7c15ull;
+    for (size_t i = 0; i < w.size(); i += 8) {
+        z += 0x9E3779B97F4A7C15ull;
+        uint64_t r = z;
+        r = (r ^ (r >> 30)) * 0xBF58476D1CE4E5B9ull;
+        r = (r ^ (r >> 27)) * 0x94D049BB133111EBull;
+        r ^= r >> 31;
+        for (size_t j = 0; j < 8 && i + j < w.size(); j++) w[i + j] = static_cast<uint8_t>(r >> (8 * j));
+    }
+    const uint16_t h005 = 0x2A66, h002 = 0x251F;  // f16(0.05), f16(0.02)
+    for (size_t b = 0; b < nblk; b++) {
+        uint8_t* blk = w.data() + b * qi->block_bytes;
+        auto put = [&](size_t off, uint16_t v) {
+            blk[off] = static_cast<uint8_t>(v & 0xff);
+            blk[off + 1] = static_cast<uint8_t>(v >> 8);
+        };
+        if (type == ZLM_GGML_Q4_0 || type == ZLM_GGML_Q8_0) put(0, h005);
+        if (type == ZLM_GGML_Q4_K) {
+            put(0, h005);
+            put(2, h002);
+        }
+        if (type == ZLM_GGML_Q6_K) put(208, h002);
+    }
+    return w;
+}
+
+uint8_t fastest(const double* rates) {
+    uint8_t best = ZLM_VARIANT_PLAIN;
+    double rate = 0.0;
+    for (uint32_t v : kAllVariants)
+        if (rates[v] > rate) {
+            rate = rates[v];
+            best = static_cast<uint8_t>(v);
+        }
+    return best;
+}
+
+// Interleaved min-of-N resident GEMV rates of every variant (probeResidentVariants).
+void probe_resident_variants(zlm_device* d, uint32_t type, size_t rows, size_t k, const float* x, float* out,
+                             double* rates) {
+    for (int v = 0; v < 8; v++) rates[v] = 0.0;
+    if (k % quant_info(type)->block_elems) return;
+    std::vector<uint8_t> w = probe_weights(type, rows, k);
+    zlm_resident* r = zlm_gpu_upload_resident(d, w.data(), w.size());
+    if (!r) return;
+    double best[8];
+    for (double& b : best) b = 1e300;
+    for (uint32_t v : kAllVariants) zlm_gpu_mat_vec_resident(d, r, ZLM_QUANT(type, v), rows, k, x, k, out, rows);
+    for (int i = 0; i < kProbeSamples; i++)
+        for (uint32_t v : kAllVariants) {
+            const double t0 = now_ns();
+            const bool ran = zlm_gpu_mat_vec_resident(d, r, ZLM_QUANT(type, v), rows, k, x, k, out, rows);
+            const double t1 = now_ns();
+            if (ran && t1 > t0) best[v] = std::min(best[v], t1 - t0);
+        }
+    for (uint32_t v : kAllVariants)
+        if (best[v] < 1e300) rates[v] = static_cast<double>(w.size()) / best[v];
+    zlm_gpu_free_resident(d, r);
+}
+
+// Interleaved min-of-N fused gate_up rates over both weights' bytes (probeGateUpRates).
+void probe_gate_up(zlm_device* d, uint32_t type, size_t rows, size_t k, const float* x, float* out, double* rates) {
+    for (int v = 0; v < 8; v++) rates[v] = 0.0;
+    std::vector<uint8_t> w = probe_weights(type, rows, k);
+    zlm_resident* rg = zlm_gpu_upload_resident(d, w.data(), w.size());
+    zlm_resident* ru = zlm_gpu_upload_resident(d, w.data(), w.size());
+    if (rg && ru) {
+        double best[8];
+        for (double& b : best) b = 1e300;
+        for (int i = 0; i <= kProbeSamples; i++)  // the first pass warms up
+            for (uint32_t v : kAllVariants) {
+                const double t0 = now_ns();
+                const int32_t h =
+                    zlm_gpu_mat_vec_gate_up_resident_burst_async(d, rg, ru, type, rows, k, x, k, ZLM_ACT_GELU, v, true);
+                const bool ran = h != ZLM_NULL_HANDLE && zlm_gpu_wait_resident(d, h, out, rows, rows);
+                const double t1 = now_ns();
+                if (i > 0 && ran && t1 > t0) best[v] = std::min(best[v], t1 - t0);
+            }
+        for (uint32_t v : kAllVariants)
+            if (best[v] < 1e300) rates[v] = 2.0 * static_cast<double>(w.size()) / best[v];
+    }
+    if (rg) zlm_gpu_free_resident(d, rg);
+    if (ru) zlm_gpu_free_resident(d, ru);
+}
+
+}  // namespace
+
+extern "C" void zlm_gpu_probe(zlm_device* d, size_t rows_in, size_t k_in, size_t m_in, zlm_probe* out) {
+    if (!out) return;
+    memset(out, 0, sizeof *out);
+    if (!d || !d->avail) return;
+    const size_t rows = std::min(rows_in, kProbeMaxRows);
+    size_t k = std::min(k_in, kProbeMaxK);
+    k -= k % 32;
+    const size_t m = std::max<size_t>(m_in, 2);
+    if (rows == 0 || k == 0) return;
+    std::vector<float> x(k), y(rows), xm(m * k), ym(m * rows);
+    for (size_t i = 0; i < k; i++) x[i] = static_cast<float>(static_cast<int>((i * 7 + 3) % 17) - 8) * 0.125f;
+    for (size_t j = 0; j < m; j++)
+        for (size_t i = 0; i < k; i++) xm[j * k + i] = x[i] * static_cast<float>(j + 1);
+    const std::vector<uint8_t> w = probe_weights(ZLM_GGML_Q4_0, rows, k);
+    const uint32_t q40 = ZLM_QUANT(ZLM_GGML_Q4_0, ZLM_VARIANT_PLAIN);
+    // warm-up of the streamed and GEMM paths, then min-of-N of each
+    zlm_gpu_mat_vec(d, q40, w.data(), w.size(), rows, k, x.data(), k, y.data(), rows);
+    zlm_gpu_mat_mul_batch(d, q40, w.data(), w.size(), rows, k, m, xm.data(), m * k, ym.data(), m * rows);
+    double best_s = 1e300, best_m = 1e300;
+    for (int i = 0; i < kProbeSamples; i++) {
+        double t0 = now_ns();
+        bool ran = zlm_gpu_mat_vec(d, q40, w.data(), w.size(), rows, k, x.data(), k, y.data(), rows);
+        double t1 = now_ns();
+        if (ran && t1 > t0) best_s = std::min(best_s, t1 - t0);
+        t0 = now_ns();
+        ran = zlm_gpu_mat_mul_batch(d, q40, w.data(), w.size(), rows, k, m, xm.data(), m * k, ym.data(), m * rows);
+        t1 = now_ns();
+        if (ran && t1 > t0) best_m = std::min(best_m, t1 - t0);
+    }
+    const double wb = static_cast<double>(w.size());
+    if (best_s < 1e300) out->gemv_streamed_gbps = wb / best_s;
+    if (best_m < 1e300) out->matmul_gbps = wb / best_m;
+
+    double rates[8];
+    probe_resident_variants(d, ZLM_GGML_Q4_0, rows, k, x.data(), y.data(), rates);
+    out->gemv_gbps = rates[ZLM_VARIANT_PLAIN];
+    out->q4_0_u4_gbps = rates[ZLM_VARIANT_U4];
+    out->q4_0_sub_gbps = rates[ZLM_VARIANT_SUB];
+    out->q4_0_un2_gbps = rates[ZLM_VARIANT_UN2];
+    out->q4_0_un4_gbps = rates[ZLM_VARIANT_UN4];
+    out->q4_0_w32_gbps = rates[ZLM_VARIANT_W32];
+    out->q4_0_w128_gbps = rates[ZLM_VARIANT_W128];
+    out->q4_0_variant = fastest(rates);
+
+    probe_gate_up(d, ZLM_GGML_Q4_0, rows, k, x.data(), y.data(), rates);
+    out->gate_up_gbps = rates[ZLM_VARIANT_PLAIN];
+    out->gate_up_u4_gbps = rates[ZLM_VARIANT_U4];
+    out->gate_up_variant = fastest(rates);
+    probe_gate_up(d, ZLM_GGML_Q8_0, rows, k, x.data(), y.data(), rates);
+    out->gate_up_q8_0_variant = fastest(rates);
+
+    // the K-quants need k in whole 256-element super-blocks
+    const size_t kk = k - k % 256;
+    if (kk) {
+        probe_resident_variants(d, ZLM_GGML_Q4_K, rows, kk, x.data(), y.data(), rates);
+        out->q4_k_gbps = rates[ZLM_VARIANT_PLAIN];
+        out->q4_k_u4_gbps = rates[ZLM_VARIANT_U4];
+        out->q4_k_variant = fastest(rates);
+        probe_resident_variants(d, ZLM_GGML_Q6_K, rows, kk, x.data(), y.data(), rates);
+        out->q6_k_variant = fastest(rates);
+    }
+    probe_resident_variants(d, ZLM_GGML_Q8_0, rows, k, x.data(), y.data(), rates);
+    out->q8_0_variant = fastest(rates);
+    zlm_gpu_sync(d);
 }
 
 // ======================= device-level entry points =======================
@@ -1092,6 +1264,15 @@ extern "C" void zlm_gpu_probe(zlm_device* d, size_t, size_t, size_t, zlm_probe* 
 extern "C" const char* zlm_gpu_last_error(const zlm_device* d) { return d ? d->err.c_str() : "null device"; }
 
 extern "C" int zlm_gpu_cu_count(const zlm_device* d) { return (d && d->avail) ? d->cus : 0; }
+
+extern "C" bool zlm_gpu_vram_info(zlm_device* d, uint64_t* free_bytes, uint64_t* total_bytes) {
+    if (!d || !d->avail || !free_bytes || !total_bytes) return false;
+    size_t f = 0, t = 0;
+    if (!ok(d, hipMemGetInfo(&f, &t), "hipMemGetInfo")) return false;
+    *free_bytes = f;
+    *total_bytes = t;
+    return true;
+}
 
 extern "C" void* zlm_gpu_dev_malloc(zlm_device* d, size_t bytes) {
     if (!d || !d->avail) return nullptr;

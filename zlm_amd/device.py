@@ -151,6 +151,7 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_resident_bytes": (ctypes.c_uint64, [P]),
         "zlm_gpu_last_error": (ctypes.c_char_p, [P]),
         "zlm_gpu_cu_count": (ctypes.c_int, [P]),
+        "zlm_gpu_vram_info": (B, [P, P, P]),
         "zlm_gpu_dev_malloc": (P, [P, S]),
         "zlm_gpu_dev_free": (None, [P, P]),
         "zlm_gpu_dev_upload": (B, [P, P, P, S]),
@@ -273,6 +274,13 @@ class Device:
 
     def last_error(self) -> str:
         return self._L.zlm_gpu_last_error(self._h).decode()
+
+    def vram_info(self) -> Optional[tuple]:
+        """(free, total) HBM bytes, or None when inert."""
+        f, t = ctypes.c_uint64(0), ctypes.c_uint64(0)
+        if not self._L.zlm_gpu_vram_info(self._h, ctypes.addressof(f), ctypes.addressof(t)):
+            return None
+        return f.value, t.value
 
     def cu_count(self) -> int:
         return int(self._L.zlm_gpu_cu_count(self._h))
