@@ -207,7 +207,7 @@ bool zlm_gpu_dev_copy_enqueue(zlm_device *dev, void *dst, const void *src, size_
 bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
                              const float *x_dev, float *y_dev);
 /* Enqueue the prefill GEMM out_dev[t*rows + r] (x_dev: m x k fp32, token-major):
- * the q8 activation quantizer, then the int8-MFMA GEMM.  Q4_0 only. */
+ * the q8 activation quantizer, then the int8-MFMA GEMM.  Q4_0 and Q8_0 weights. */
 bool zlm_gpu_mat_mul_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k, size_t m,
                              const float *x_dev, float *out_dev);
 /* Enqueue `iters` prefill GEMMs (quantizer + GEMM each), rotating over `n_res`

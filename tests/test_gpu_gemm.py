@@ -1,7 +1,8 @@
 """GPU parity of the prefill GEMM (q8 activations, int8 MFMA) through the C ABI.
 
-The oracle is zlm's int path (reference kernels/quantized.zig:49-55 over the
-activation quantizer of matvec/layout.zig:458-476) applied per token:
+The oracle is zlm's int path (reference matvec/kernels/quantized.zig:49-55 for
+Q4_0, :149-156 for Q8_0, over the activation quantizer of
+matvec/layout.zig:458-476) applied per token:
 relative L2 <= 1e-3 (the block dots are exact integers; only fp32 scaling and
 summation order differ).  Against the fp32 GEMM the reference's own int-vs-fp
 bound applies, |int - fp| <= 0.02 * sum|w*x| (kernels/quantized_test.zig:61).
@@ -24,23 +25,29 @@ def _say(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("rows,k,m", [(64, 256, 4), (100, 512, 37), (64, 1024, 64), (130, 4096, 70), (48, 16384, 3), (70, 4096, 129), (64, 4096, 1)])
-def test_gemm_matches_int_oracle(dev, rows, k, m):
-    _say(f"gemm q4_0 rows={rows} k={k} m={m}")
-    w = synth.weights(synth.Q4_0, rows, k, seed=rows + k + m)
+SHAPES = [(64, 256, 4), (100, 512, 37), (64, 1024, 64), (130, 4096, 70), (48, 16384, 3), (70, 4096, 129),
+          (64, 4096, 1)]
+GEMM_QUANTS = [(synth.Q4_0, zd.Q4_0), (synth.Q8_0, zd.Q8_0)]
+
+
+@pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("rows,k,m", SHAPES)
+def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
+    _say(f"gemm type={qt} rows={rows} k={k} m={m}")
+    w = synth.weights(qt, rows, k, seed=rows + k + m)
     x = synth.activation(m + 5, m * k)
-    want = oracle.matmul_int(synth.Q4_0, w, k, rows, m, x)
+    want = oracle.matmul_int(qt, w, k, rows, m, x)
     out = np.full(m * rows, np.nan, np.float32)
-    assert dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x, out), dev.last_error()
+    assert dev.mat_mul_batch(zd.quant(zq), w, rows, k, m, x, out), dev.last_error()
     got = out.reshape(m, rows)
     assert rel_l2(got, want) <= 1e-3
     res = dev.upload_resident(w)
     out2 = np.zeros(m * rows, np.float32)
-    assert dev.mat_mul_resident(res, zd.quant(zd.Q4_0), rows, k, m, x, out2), dev.last_error()
+    assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, out2), dev.last_error()
     np.testing.assert_array_equal(out2, out)
     # the int path stays within the reference's bound of the fp32 GEMM
-    fp = oracle.matmul_rows(synth.Q4_0, w, k, rows, m, x)
-    dq = np.abs(oracle.dequant(synth.Q4_0, w, rows * k).reshape(rows, k).astype(np.float64))
+    fp = oracle.matmul_rows(qt, w, k, rows, m, x)
+    dq = np.abs(oracle.dequant(qt, w, rows * k).reshape(rows, k).astype(np.float64))
     mag = np.abs(x.reshape(m, k).astype(np.float64)) @ dq.T
     assert np.all(np.abs(got - fp) <= 0.02 * mag + 1e-6)
     dev.free_resident(res)
@@ -69,7 +76,7 @@ def test_gemm_unsupported_quants_fall_back(dev):
     rows, k, m = 32, 256, 4
     x = synth.activation(1, m * k)
     out = np.zeros(m * rows, np.float32)
-    for qt in (synth.Q6_K, synth.Q4_K, synth.Q8_0):
+    for qt in (synth.Q6_K, synth.Q4_K):
         w = synth.weights(qt, rows, k, seed=2)
         assert not dev.mat_mul_batch(zd.quant(qt), w, rows, k, m, x, out)
     w = synth.weights(synth.Q4_0, rows, k, seed=2)

@@ -115,8 +115,9 @@ struct zlm_resident {
     uint16_t* scales = nullptr;    // device layout scales (split quants)
     uint32_t layout = kNoLayout;   // GGML type of the device layout
     uint64_t blocks = 0;           // whole blocks in the layout
-    // The prefill GEMM's tiled copy of a Q4_0 weight ([rows/32][nb][32][16 B]
-    // + scales [rows/32][nb][32]), built on the first GEMM for a given nb.
+    // The prefill GEMM's tiled copy of a Q4_0 / Q8_0 weight ([rows/32][nb][32]
+    // [16 or 32 B] + scales [rows/32][nb][32]), built on the first GEMM for a
+    // given nb.
     uint8_t* gemm_payload = nullptr;
     uint16_t* gemm_scales = nullptr;
     uint64_t gemm_nb = 0;
@@ -139,8 +140,10 @@ struct zlm_device {
     hipFunction_t quantize_q8 = nullptr;
     hipFunction_t quantize_q8_tiled = nullptr;
     hipFunction_t tile_q4_0 = nullptr;
+    hipFunction_t tile_q8_0 = nullptr;
     hipFunction_t copy16 = nullptr;
     hipFunction_t gemm_q4_0 = nullptr;
+    hipFunction_t gemm_q8_0 = nullptr;
     hipFunction_t qk_norm_rope_kv = nullptr;
     hipFunction_t attn_partial = nullptr;
     hipFunction_t attn_combine = nullptr;
@@ -247,6 +250,8 @@ bool load_kernels(zlm_device* d) {
     if (!ok(d, hipModuleGetFunction(&d->tile_q4_0, d->mod, "zlm_tile_q4_0"), "zlm_tile_q4_0")) return false;
     if (!ok(d, hipModuleGetFunction(&d->copy16, d->mod, "zlm_copy16"), "zlm_copy16")) return false;
     if (!ok(d, hipModuleGetFunction(&d->gemm_q4_0, d->mod, "zlm_gemm_q4_0_q8"), "zlm_gemm_q4_0_q8")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->tile_q8_0, d->mod, "zlm_tile_q8_0"), "zlm_tile_q8_0")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->gemm_q8_0, d->mod, "zlm_gemm_q8_0_q8"), "zlm_gemm_q8_0_q8")) return false;
     const struct {
         hipFunction_t* f;
         const char* name;
@@ -398,12 +403,15 @@ bool check_resident(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t 
 // Grid of a GEMV launch: one wave per tile up to a per-CU cap.  Measured on
 // gfx950: up to 4 steps per row (k <= 4096 for q8_0, 8192 for the others) a
 // grid of 4 workgroups per CU is best; wider rows stage a larger x in LDS and
-// one workgroup per CU looping over tiles is best.  steps 0 = the generic
+// one workgroup per CU looping over tiles is best.  Tall launches (>= 64K row
+// tiles, the lm_heads) with a 4096-float x capacity (19 KB of LDS) run 8
+// workgroups per CU: 262144 x 3840 q6_k 222 -> 190 us.  steps 0 = the generic
 // instance (32768-float x capacity, one workgroup per CU).
-unsigned gemv_grid(const zlm_device* d, uint64_t tiles, int steps) {
+unsigned gemv_grid(const zlm_device* d, const QuantInfo* qi, uint64_t tiles, int steps) {
     const uint64_t wgs = (tiles + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
-    const uint64_t cap = static_cast<uint64_t>(d->cus) * ((steps == 0 || steps > 4) ? 1 : 4);
-    return static_cast<unsigned>(std::min<uint64_t>(wgs, cap));
+    const bool small_x = steps > 0 && steps <= (qi->type == ZLM_GGML_Q8_0 ? 4 : 2);
+    const uint64_t per_cu = (steps == 0 || steps > 4) ? 1 : (small_x && tiles >= 65536) ? 8 : 4;
+    return static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->cus) * per_cu));
 }
 
 // Validate a GEMV over resident `r` and pick its kernel.
@@ -416,7 +424,7 @@ bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     const GemvKernel* gk = pick_gemv(d, qi, k, rt_for_variant(variant_of(quant)));
     if (!gk) return fail(d, "no GEMV kernel for quant %u k=%zu", qi->type, k);
     *f = gk->fn;
-    *grid = gemv_grid(d, (rows + gk->rt - 1) / gk->rt, gk->steps);
+    *grid = gemv_grid(d, qi, (rows + gk->rt - 1) / gk->rt, gk->steps);
     *block = kGemvThreads;
     return true;
 }
@@ -506,7 +514,7 @@ bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     a.eps = op.eps;
     a.act = op.act;
     void* args[] = {&a};
-    return launch(d, gk->fn, gemv_grid(d, op.rows, gk->steps), kGemvThreads, args, kFormNames[op.form]);
+    return launch(d, gk->fn, gemv_grid(d, qi, op.rows, gk->steps), kGemvThreads, args, kFormNames[op.form]);
 }
 
 zlm_resident* new_resident(zlm_device* d, const void* bytes, size_t len) {
@@ -594,10 +602,11 @@ double now_ns() {
     return static_cast<double>(ts.tv_sec) * 1e9 + static_cast<double>(ts.tv_nsec);
 }
 
-// Build (once per row length) the GEMM's tiled copy of a resident Q4_0 weight
-// from its split layout: payload [rt][nb][32 rows][16 B] and scales
-// [rt][nb][32 rows] over all whole rows the resident holds, rows padded to 32.
-bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, uint64_t nb) {
+// Build (once per row length) the GEMM's tiled copy of a resident Q4_0 or
+// Q8_0 weight from its split layout: payload [rt][nb][32 rows][16 or 32 B] and
+// scales [rt][nb][32 rows] over all whole rows the resident holds, rows padded
+// to 32.  The resident's layout type never changes, so nb keys the copy.
+bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint64_t nb) {
     if (r->gemm_payload && r->gemm_nb == nb) return true;
     if (r->gemm_payload) hipFree(r->gemm_payload);
     r->gemm_payload = nullptr;
@@ -607,7 +616,7 @@ bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, uint64_t nb) {
     const uint64_t rows_total = r->blocks / nb;
     const uint64_t rt = (rows_total + 31) / 32;
     if (rt == 0 || rt * 32 > 0xffffffffu) return fail(d, "GEMM weight shape out of range");
-    const uint64_t pbytes = rt * nb * 512;
+    const uint64_t pbytes = rt * nb * 32 * qi->payload_bytes;
     const uint64_t sbytes = rt * nb * 32 * 2;
     uint8_t* p = nullptr;
     if (!ok(d, hipMalloc(reinterpret_cast<void**>(&p), pbytes + sbytes), "hipMalloc gemm tiles")) return false;
@@ -619,7 +628,8 @@ bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, uint64_t nb) {
              rt32 = static_cast<uint32_t>(rt);
     void* args[] = {&payload, &scales, &tp, &ts, &rows32, &nb32, &rt32};
     const uint64_t n = rt * 32 * nb;
-    if (!launch(d, d->tile_q4_0, static_cast<unsigned>((n + 255) / 256), 256, args, "tile q4_0")) {
+    hipFunction_t tile = qi->type == ZLM_GGML_Q8_0 ? d->tile_q8_0 : d->tile_q4_0;
+    if (!launch(d, tile, static_cast<unsigned>((n + 255) / 256), 256, args, "tile weights")) {
         hipFree(p);
         return false;
     }
@@ -630,22 +640,24 @@ bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, uint64_t nb) {
     return true;
 }
 
-// Enqueue the prefill GEMM out_dev[t*rows + r] over a resident Q4_0 weight and
-// device activations x_dev (m x k, token-major): quantize x to q8 blocks into
-// the tiled device scratch, then the int8-MFMA GEMM over the tiled weights.
+// Enqueue the prefill GEMM out_dev[t*rows + r] over a resident Q4_0 or Q8_0
+// weight and device activations x_dev (m x k, token-major): quantize x to q8
+// blocks into the tiled device scratch, then the int8-MFMA GEMM over the tiled
+// weights.
 bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, size_t m,
                   const float* x_dev, float* out_dev) {
     if (!d || !d->avail) return fail(d, "device unavailable");
     const QuantInfo* qi = quant_info(quant);
     if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
-    if (qi->type != ZLM_GGML_Q4_0) return fail(d, "no GEMM kernel for quant %u", qi->type);
+    if (qi->type != ZLM_GGML_Q4_0 && qi->type != ZLM_GGML_Q8_0)
+        return fail(d, "no GEMM kernel for quant %u", qi->type);
     if (!r || rows == 0 || k == 0 || m == 0 || k % 32) return fail(d, "bad GEMM shape");
     if (rows > 0x7fffffffu || m > 0x7fffffffu || k / 32 > 0xffffffu) return fail(d, "GEMM shape too large");
     const uint64_t nb = k / 32;
     if (r->bytes < rows * nb * qi->block_bytes) return fail(d, "resident too short");
     if (!ensure_layout(d, r, qi)) return false;
     if (r->blocks < rows * nb) return fail(d, "resident layout too short");
-    if (!ensure_gemm_tiles(d, r, nb)) return false;
+    if (!ensure_gemm_tiles(d, r, qi, nb)) return false;
     if (r->gemm_rt * 32 < rows) return fail(d, "GEMM tiles too short");
     const uint64_t mt = (static_cast<uint64_t>(m) + 31) / 32;
     const uint64_t qbytes = mt * 32 * k;  // a multiple of 1024
@@ -665,7 +677,8 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     const uint16_t* wd = r->gemm_scales;
     void* args[] = {&wq, &wd, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
     return ok(d,
-              hipModuleLaunchKernel(d->gemm_q4_0, static_cast<unsigned>((rows + 63) / 64),
+              hipModuleLaunchKernel(qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0 : d->gemm_q4_0,
+                                    static_cast<unsigned>((rows + 63) / 64),
                                     static_cast<unsigned>((m + 127) / 128), 1, 256, 1, 1, 0, d->stream, args, nullptr),
               "gemm");
 }
@@ -988,7 +1001,8 @@ extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void*
     if (!d || !d->avail) return false;
     const QuantInfo* qi = quant_info(quant);
     if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
-    if (qi->type != ZLM_GGML_Q4_0) return fail(d, "no GEMM kernel for quant %u", qi->type);
+    if (qi->type != ZLM_GGML_Q4_0 && qi->type != ZLM_GGML_Q8_0)
+        return fail(d, "no GEMM kernel for quant %u", qi->type);
     if (!w || rows == 0 || k == 0 || k % qi->block_elems) return fail(d, "bad shape");
     const uint64_t nblk = static_cast<uint64_t>(rows) * (k / qi->block_elems);
     const uint64_t need = nblk * qi->block_bytes;

@@ -164,25 +164,42 @@ extern "C" __global__ void __launch_bounds__(256)
                    reinterpret_cast<uint4*>(qx + slot * 32), dx + slot, nullptr);
 }
 
-// The prefill GEMM's tiled Q4_0 weight layout, rows padded to rt*32:
-// payload [rt][nb][32 rows][16 B], scales [rt][nb][32 rows]; padding rows have
-// zero scales.  One thread per (row, block) of the padded matrix.
-extern "C" __global__ void __launch_bounds__(256)
-    zlm_tile_q4_0(const uint8_t* __restrict__ payload, const uint16_t* __restrict__ scales,
-                  uint8_t* __restrict__ tpayload, uint16_t* __restrict__ tscales, uint32_t rows, uint32_t nb,
-                  uint32_t rt) {
+// The prefill GEMM's tiled weight layout, rows padded to rt*32: payload
+// [rt][nb][32 rows][PB bytes] (PB = 16 for q4_0, 32 for q8_0), scales
+// [rt][nb][32 rows]; padding rows have zero scales.  One thread per (row,
+// block) of the padded matrix.
+template <int PB>
+__device__ __forceinline__ void tile_blocks(const uint8_t* __restrict__ payload, const uint16_t* __restrict__ scales,
+                                            uint8_t* __restrict__ tpayload, uint16_t* __restrict__ tscales,
+                                            uint32_t rows, uint32_t nb, uint32_t rt) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<uint64_t>(rt) * 32 * nb) return;
     const uint32_t r = static_cast<uint32_t>(i / nb), b = static_cast<uint32_t>(i % nb);
     const uint64_t slot = (static_cast<uint64_t>(r / 32) * nb + b) * 32 + (r % 32);
-    uint4 q = make_uint4(0u, 0u, 0u, 0u);
+    const uint64_t src = static_cast<uint64_t>(r) * nb + b;
     uint16_t d = 0;
-    if (r < rows) {
-        q = reinterpret_cast<const uint4*>(payload)[static_cast<uint64_t>(r) * nb + b];
-        d = scales[static_cast<uint64_t>(r) * nb + b];
+#pragma unroll
+    for (int j = 0; j < PB / 16; j++) {
+        uint4 q = make_uint4(0u, 0u, 0u, 0u);
+        if (r < rows) q = reinterpret_cast<const uint4*>(payload)[src * (PB / 16) + j];
+        reinterpret_cast<uint4*>(tpayload)[slot * (PB / 16) + j] = q;
     }
-    reinterpret_cast<uint4*>(tpayload)[slot] = q;
+    if (r < rows) d = scales[src];
     tscales[slot] = d;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_tile_q4_0(const uint8_t* __restrict__ payload, const uint16_t* __restrict__ scales,
+                  uint8_t* __restrict__ tpayload, uint16_t* __restrict__ tscales, uint32_t rows, uint32_t nb,
+                  uint32_t rt) {
+    tile_blocks<16>(payload, scales, tpayload, tscales, rows, nb, rt);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_tile_q8_0(const uint8_t* __restrict__ payload, const uint16_t* __restrict__ scales,
+                  uint8_t* __restrict__ tpayload, uint16_t* __restrict__ tscales, uint32_t rows, uint32_t nb,
+                  uint32_t rt) {
+    tile_blocks<32>(payload, scales, tpayload, tscales, rows, nb, rt);
 }
 
 // ---- device copy (16-byte granules; the traffic-counter calibration kernel) --
@@ -194,11 +211,15 @@ extern "C" __global__ void __launch_bounds__(256)
         dst[i] = src[i];
 }
 
-// ---- prefill GEMM: Q4_0 weights x Q8_0-quantized activations, int8 MFMA ----
+// ---- prefill GEMM: Q4_0 / Q8_0 weights x Q8_0-quantized activations, int8 MFMA ----
 //
-// out[t*rows + r] = sum_b dw[r,b] * dx[t,b] * sum_j (nib[r,b,j] - 8) * qx[t,b,j]
-// (the int path of reference kernels/quantized.zig:49-55 over the activation
+// out[t*rows + r] = sum_b dw[r,b] * dx[t,b] * sum_j w[r,b,j] * qx[t,b,j], with
+// w = nib - 8 for q4_0 and the int8 quant for q8_0 (the int paths of
+// reference kernels/quantized.zig:49-55 and :149-156 over the activation
 // quantizer of matvec/layout.zig:458-476, i.e. zlm_quantize_q8's output).
+// q8_0 is the same kernel with the weight bytes taken as they are (lanes 0-31
+// hold bytes 0..15 of a row's block, lanes 32-63 bytes 16..31, the B operand's
+// k split) and no nibble factor.
 //
 // v_mfma_i32_32x32x32_i8 computes one 32-element block for a 32-token x
 // 32-row tile: A = activations (lane l: token l%32, block elements
@@ -235,23 +256,30 @@ struct GemmBlk {
 #endif
 constexpr int kGemmDepth = ZLM_GEMM_DEPTH;  // blocks per register set
 
+template <int QT>
 __device__ __forceinline__ void gemm_load(GemmBlk& g, const int8_t* a0, const int8_t* a1, const uint8_t* wr,
                                           const uint16_t* dr, const float* x0, const float* x1, uint32_t b) {
+    constexpr size_t kWStride = QT == Q8_0 ? 1024 : 512;  // tiled weight bytes per block
     g.a0 = *reinterpret_cast<const uint4*>(a0 + static_cast<size_t>(b) * 1024);
     g.a1 = *reinterpret_cast<const uint4*>(a1 + static_cast<size_t>(b) * 1024);
-    g.w = *reinterpret_cast<const uint4*>(wr + static_cast<size_t>(b) * 512);
+    g.w = *reinterpret_cast<const uint4*>(wr + static_cast<size_t>(b) * kWStride);
     g.d = dr[static_cast<size_t>(b) * 32];
     g.x0 = x0[static_cast<size_t>(b) * 32];
     g.x1 = x1[static_cast<size_t>(b) * 32];
 }
 
+template <int QT>
 __device__ __forceinline__ void gemm_block(const GemmBlk& g, bool valid, bool lo_half, int sh, v16f& acc0,
                                            v16f& acc1) {
     v4i bv;
-    bv.x = static_cast<int>(((g.w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
-    bv.y = static_cast<int>(((g.w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
-    bv.z = static_cast<int>(((g.w.z << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
-    bv.w = static_cast<int>(((g.w.w << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+    if constexpr (QT == Q8_0) {
+        bv = v4i{static_cast<int>(g.w.x), static_cast<int>(g.w.y), static_cast<int>(g.w.z), static_cast<int>(g.w.w)};
+    } else {
+        bv.x = static_cast<int>(((g.w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+        bv.y = static_cast<int>(((g.w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+        bv.z = static_cast<int>(((g.w.z << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+        bv.w = static_cast<int>(((g.w.w << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+    }
     const v4i a0 = {static_cast<int>(g.a0.x), static_cast<int>(g.a0.y), static_cast<int>(g.a0.z),
                     static_cast<int>(g.a0.w)};
     const v4i a1 = {static_cast<int>(g.a1.x), static_cast<int>(g.a1.y), static_cast<int>(g.a1.z),
@@ -261,7 +289,7 @@ __device__ __forceinline__ void gemm_block(const GemmBlk& g, bool valid, bool lo
     const v16i i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv, zi, 0, 0, 0);
     const bool use = valid && lo_half;
     const float bw = use ? h2f(g.d) : 0.0f;
-    const float s0 = use ? g.x0 : 0.0f;  // the 16 of the nibble encoding is divided out at the store
+    const float s0 = use ? g.x0 : 0.0f;  // q4_0: the 16 of the nibble encoding is divided out at the store
     const float s1 = use ? g.x1 : 0.0f;
     const v16f zf = {};
     const v16f c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(s0, bw, zf, 0, 0, 0);
@@ -273,13 +301,15 @@ __device__ __forceinline__ void gemm_block(const GemmBlk& g, bool valid, bool lo
     }
 }
 
-// Operands come from the tiled layouts (zlm_quantize_q8_tiled, zlm_tile_q4_0),
-// so each per-block load of a wave is one contiguous run: 1 KiB of qx per
-// 32-token tile, 512 B of weights and 64 B of scales per 32-row tile.
-extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
-    zlm_gemm_q4_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
-                     const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
-                     uint32_t mt) {
+// Operands come from the tiled layouts (zlm_quantize_q8_tiled, zlm_tile_q4_0 /
+// zlm_tile_q8_0), so each per-block load of a wave is one contiguous run: 1 KiB
+// of qx per 32-token tile, 512 B (q4_0) or 1 KiB (q8_0) of weights and 64 B of
+// scales per 32-row tile.
+template <int QT>
+__device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                                           const int8_t* __restrict__ qx, const float* __restrict__ dx,
+                                           float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
+                                           uint32_t mt) {
     const int lane = threadIdx.x & 63;
     const int wid = threadIdx.x >> 6;
     const uint32_t tok0 = blockIdx.y * 128 + 64 * (wid & 1);  // multiple of 32
@@ -290,7 +320,8 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
     const uint32_t rt = min(row0 / 32, (rows + 31) / 32 - 1);  // a wave past the last tile re-reads it, stores nothing
     const int8_t* a0 = qx + static_cast<size_t>(tt0) * nb * 1024 + l32 * 32 + 16 * half;
     const int8_t* a1 = qx + static_cast<size_t>(tt1) * nb * 1024 + l32 * 32 + 16 * half;
-    const uint8_t* wr = wq + static_cast<size_t>(rt) * nb * 512 + l32 * 16;
+    const uint8_t* wr = QT == Q8_0 ? wq + static_cast<size_t>(rt) * nb * 1024 + l32 * 32 + 16 * half
+                                   : wq + static_cast<size_t>(rt) * nb * 512 + l32 * 16;
     const uint16_t* dr = wd + static_cast<size_t>(rt) * nb * 32 + l32;
     const float* x0 = dx + static_cast<size_t>(tt0) * nb * 32 + l32;
     const float* x1 = dx + static_cast<size_t>(tt1) * nb * 32 + l32;
@@ -304,32 +335,48 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
     // next to their uses), and the ping-pong needs no register copies.
     GemmBlk A[kGemmDepth], B[kGemmDepth];
 #pragma unroll
-    for (int p = 0; p < kGemmDepth; p++) gemm_load(A[p], a0, a1, wr, dr, x0, x1, min(static_cast<uint32_t>(p), nb - 1));
+    for (int p = 0; p < kGemmDepth; p++)
+        gemm_load<QT>(A[p], a0, a1, wr, dr, x0, x1, min(static_cast<uint32_t>(p), nb - 1));
     for (uint32_t b = 0; b < nb; b += 2 * kGemmDepth) {
 #pragma unroll
         for (int p = 0; p < kGemmDepth; p++)
-            gemm_load(B[p], a0, a1, wr, dr, x0, x1, min(b + kGemmDepth + p, nb - 1));
+            gemm_load<QT>(B[p], a0, a1, wr, dr, x0, x1, min(b + kGemmDepth + p, nb - 1));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = 0; p < kGemmDepth; p++) gemm_block(A[p], b + p < nb, lo_half, sh, acc0, acc1);
+        for (int p = 0; p < kGemmDepth; p++) gemm_block<QT>(A[p], b + p < nb, lo_half, sh, acc0, acc1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < kGemmDepth; p++)
-            gemm_load(A[p], a0, a1, wr, dr, x0, x1, min(b + 2 * kGemmDepth + p, nb - 1));
+            gemm_load<QT>(A[p], a0, a1, wr, dr, x0, x1, min(b + 2 * kGemmDepth + p, nb - 1));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = 0; p < kGemmDepth; p++) gemm_block(B[p], b + kGemmDepth + p < nb, lo_half, sh, acc0, acc1);
+        for (int p = 0; p < kGemmDepth; p++) gemm_block<QT>(B[p], b + kGemmDepth + p < nb, lo_half, sh, acc0, acc1);
         __builtin_amdgcn_sched_barrier(0);
     }
+    constexpr float kOut = QT == Q8_0 ? 1.0f : 0.0625f;
     const uint32_t r = row0 + l32;
     if (r < rows) {
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const uint32_t t = tok0 + 8 * (i / 4) + 4 * half + (i % 4);
-            if (t < m) out[static_cast<size_t>(t) * rows + r] = acc0[i] * 0.0625f;
-            if (t + 32 < m) out[static_cast<size_t>(t + 32) * rows + r] = acc1[i] * 0.0625f;
+            if (t < m) out[static_cast<size_t>(t) * rows + r] = acc0[i] * kOut;
+            if (t + 32 < m) out[static_cast<size_t>(t + 32) * rows + r] = acc1[i] * kOut;
         }
     }
+}
+
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q4_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
+                     const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
+                     uint32_t mt) {
+    gemm_tiles<Q4_0>(wq, wd, qx, dx, out, rows, m, nb, mt);
+}
+
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q8_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
+                     const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
+                     uint32_t mt) {
+    gemm_tiles<Q8_0>(wq, wd, qx, dx, out, rows, m, nb, mt);
 }
 
 
