@@ -161,9 +161,11 @@ def _dev_vec(dev, a):
 
 
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
-@pytest.mark.parametrize("rows,k", [(256, 4096), (100, 3840), (64, 2048)])
+@pytest.mark.parametrize("rows,k", [(256, 4096), (100, 3840), (64, 2048), (5000, 4096), (4133, 12288), (77, 11264)])
 def test_device_forms_match_oracle(dev, qt, rows, k):
-    """norm / resid / normpair forms on device buffers (the decode step's ops)."""
+    """norm / resid / normpair forms on device buffers (the decode step's ops);
+    the larger shapes give the prefetching instances several row tiles per
+    wave and a ragged last tile."""
     if k % synth.BLOCK_ELEMS[qt]:
         pytest.skip("k not a multiple of the block")
     _say(f"forms {NAMES[qt]} rows={rows} k={k}")

@@ -519,6 +519,61 @@ __device__ __forceinline__ void reduce_store(float* v, const GemvArgs& a, uint32
     }
 }
 
+// The row of fragment-row group `fr` of tile t and, for EPI_RESID, the
+// residual value its lanes add (loaded together with the tile's weights, so
+// waiting for the weights covers it).
+template <int RT, int EPI>
+__device__ __forceinline__ uint32_t store_row(const GemvArgs& a, uint32_t t, int lane) {
+    constexpr int LOG = (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
+    const uint32_t fr = static_cast<uint32_t>(lane >> (6 - LOG));
+    const uint32_t row = (EPI == EPI_PAIR) ? t * (RT / 2) + (fr % (RT / 2 > 0 ? RT / 2 : 1)) : t * RT + fr;
+    return min(row, a.rows - 1);
+}
+
+// reduce_store for the prefetching loop: the same butterfly, then every lane
+// stores its fragment row's value to the row clamped into range, with no
+// branch.  A store behind a branch makes the compiler wait for every
+// outstanding load (the next tile's included) before the next tile's compute;
+// an unconditional one keeps the load counter exact.  Lanes of one row store
+// the same value; a fragment row past the end (clamped to the last row) is a
+// duplicate of the last row in the same wave and store instruction, so it
+// stores that row's value too.  For EPI_PAIR both halves of the wave form
+// act(gate, up) (the up half swaps its operands) and store it.
+template <int RT, int EPI>
+__device__ __forceinline__ void reduce_store_all(float* v, const GemvArgs& a, uint32_t t, float scale, int lane,
+                                                 float rv) {
+    constexpr int LOG = (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
+#pragma unroll
+    for (int st = 0; st < LOG; st++) {
+        const int half = (RT >> st) >> 1;
+        const int bit = 32 >> st;
+        const bool upper = (lane & bit) != 0;
+#pragma unroll
+        for (int i = 0; i < half; i++) {
+            const float keep = upper ? v[half + i] : v[i];
+            const float send = upper ? v[i] : v[half + i];
+            v[i] = keep + __shfl_xor(send, bit, kWave);
+        }
+    }
+    float s = v[0];
+#pragma unroll
+    for (int off = 32 >> LOG; off >= 1; off >>= 1) s += __shfl_xor(s, off, kWave);
+    s *= scale;
+    const uint32_t row = store_row<RT, EPI>(a, t, lane);
+    float val;
+    if constexpr (EPI == EPI_PAIR) {
+        static_assert(RT >= 2, "a pair tile holds a gate and an up row");
+        const float o = __shfl_xor(s, 32, kWave);
+        const bool lo = lane < 32;
+        val = gate_act(a.act, lo ? s : o, lo ? o : s);
+    } else if constexpr (EPI == EPI_RESID) {
+        val = rv + s;
+    } else {
+        val = s;
+    }
+    a.y[row] = val;
+}
+
 template <int QT>
 __device__ __forceinline__ int chunks_per_row(uint32_t nb) {
     return (QT == Q4_0) ? static_cast<int>(nb) : (QT == Q8_0) ? static_cast<int>(2 * nb) : static_cast<int>(8 * nb);
@@ -543,13 +598,16 @@ __device__ __forceinline__ void load_group(Frag<QT, RT> (&f)[STEPS], const TileR
         if (EXACT || cb + s * kWave < C) load_frag<QT, RT, NT>(f[s], tr, nb, min(cb + lane + s * kWave, C - 1));
 }
 
-template <int QT, int RT, int STEPS, bool EXACT>
+// FENCE: a scheduling barrier after each step keeps the compiler from
+// hoisting later steps' LDS reads (which costs registers, hence occupancy).
+template <int QT, int RT, int STEPS, bool EXACT, bool FENCE = false>
 __device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], const float* xl, const float* xs,
                                               int C, int cb, int lane, float* acc) {
 #pragma unroll
     for (int s = 0; s < STEPS; s++) {
         const int c = cb + lane + s * kWave;
         if (EXACT || cb + s * kWave < C) compute_frag<QT, RT>(f[s], xl, xs, min(c, C - 1), c < C, acc);
+        if constexpr (FENCE) __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -564,7 +622,13 @@ __device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], co
 // so the barrier waits for x only and step s computes as soon as its own loads
 // land.  Occupancy (several waves per SIMD) overlaps one wave's compute with
 // others' loads.
-template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT, int PRO, int EPI>
+//
+// PF (exact instances only): the wave loads its next tile while it computes
+// the current one (two fragment sets used in turn, the last tile's prefetch
+// clamped to a valid tile and dropped), stores with reduce_store_all.
+// FENCE: see compute_group.
+template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT, int PRO, int EPI, bool PF = false,
+          bool FENCE = false>
 __device__ __forceinline__ void gemv(const GemvArgs& a) {
     __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
     __shared__ float xs[XTile<KCAP>::kRuns + 1];
@@ -592,6 +656,37 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
     else xstore<KCAP>(xr, k, xl, xs);
 
     float acc[RT];
+    if constexpr (PF) {
+        static_assert(EXACT, "the prefetching loop needs one step group per tile");
+        Frag<QT, RT> g[STEPS];
+        float rf = 0.0f, rg = 0.0f;
+        if constexpr (EPI == EPI_RESID) rf = a.res[store_row<RT, EPI>(a, min(tile, ntiles - 1), lane)];
+        uint32_t t = tile;
+        while (t < ntiles) {
+            const uint32_t t1 = t + tstride;
+            {
+                const uint32_t tc = min(t1, ntiles - 1);
+                load_group<QT, RT, STEPS, EXACT, NT>(g, tile_rows<RT, PAIR>(a, tc), a.nb, C, 0, lane);
+                if constexpr (EPI == EPI_RESID) rg = a.res[store_row<RT, EPI>(a, tc, lane)];
+            }
+#pragma unroll
+            for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+            compute_group<QT, RT, STEPS, EXACT, FENCE>(f, xl, xs, C, 0, lane, acc);
+            reduce_store_all<RT, EPI>(acc, a, t, scale, lane, rf);
+            if (t1 >= ntiles) break;
+            t = t1 + tstride;
+            {
+                const uint32_t tc = min(t, ntiles - 1);
+                load_group<QT, RT, STEPS, EXACT, NT>(f, tile_rows<RT, PAIR>(a, tc), a.nb, C, 0, lane);
+                if constexpr (EPI == EPI_RESID) rf = a.res[store_row<RT, EPI>(a, tc, lane)];
+            }
+#pragma unroll
+            for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+            compute_group<QT, RT, STEPS, EXACT, FENCE>(g, xl, xs, C, 0, lane, acc);
+            reduce_store_all<RT, EPI>(acc, a, t1, scale, lane, rg);
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = 0.0f;
     compute_group<QT, RT, STEPS, EXACT>(f, xl, xs, C, 0, lane, acc);
@@ -640,6 +735,13 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
 #define ZLM_GEMVX(NAME, QT, KCAP, RT, STEPS, EXACT, PRO, EPI)                        \
     extern "C" __global__ void __launch_bounds__(256) NAME(GemvArgs a) {            \
         gemv<QT, KCAP, 4, RT, STEPS, EXACT, true, PRO, EPI>(a);                     \
+    }
+// Prefetching instances zlm_gemv_<quant>_<form>_s<STEPS>_pf: WAVES waves per
+// workgroup, launched at 8 waves per CU (the host reads the block size from
+// the kernel's launch bounds).
+#define ZLM_GEMVX_PF(NAME, QT, KCAP, WAVES, RT, STEPS, PRO, EPI, FENCE)                       \
+    extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {              \
+        gemv<QT, KCAP, WAVES, RT, STEPS, true, true, PRO, EPI, true, FENCE>(a);             \
     }
 #define ZLM_GEMVX_FORMS(QN, QT, KCAP, STEPS, EXACT, SFX)                                           \
     ZLM_GEMVX(zlm_gemv_##QN##_pair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_PLAIN, EPI_PAIR)           \

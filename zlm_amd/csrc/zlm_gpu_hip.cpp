@@ -64,8 +64,8 @@ const QuantInfo* quant_info(uint32_t quant) {
 
 uint32_t variant_of(uint32_t quant) { return (quant >> 8) & 0xffu; }
 
-// GEMV kernels: 4 waves (256 threads) per workgroup; k up to 32768.
-constexpr int kGemvThreads = 256;
+// GEMV kernels: 4 waves (256 threads) per workgroup unless an instance's launch
+// bounds say otherwise; k up to 32768.
 constexpr size_t kMaxK = 32768;
 
 // GpuVariant -> rows per wave tile.  The reference's variants are Vulkan
@@ -91,6 +91,8 @@ struct GemvKernel {
     hipFunction_t fn = nullptr;
     int rt = 0;
     int steps = 0;
+    int threads = 256;     // the kernel's launch bounds
+    int waves_per_cu = 0;  // grid target of a prefetching instance; 0 = gemv_grid's rule
 };
 
 struct Slot {
@@ -352,14 +354,21 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
     return true;
 }
 
-// Look up (and cache) a GEMV entry point by name in its quant's code object.
-const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps) {
+// Look up (and cache) a GEMV entry point by name in its quant's code object;
+// the block size is the kernel's launch bound.
+const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps, int waves_per_cu = 0) {
     auto it = d->gemv.find(name);
     if (it == d->gemv.end()) {
         GemvKernel g;
         if (hipModuleGetFunction(&g.fn, d->gemv_mod[slot], name) == hipSuccess) {
             g.rt = rt;
             g.steps = steps;
+            g.waves_per_cu = waves_per_cu;
+            int mt = 0;
+            if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g.fn) == hipSuccess && mt >= 64)
+                g.threads = mt;
+            else
+                hipGetLastError();
         } else {
             g.fn = nullptr;
             hipGetLastError();
@@ -407,11 +416,16 @@ bool check_resident(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t 
 // tiles, the lm_heads) with a 4096-float x capacity (19 KB of LDS) run 8
 // workgroups per CU: 262144 x 3840 q6_k 222 -> 190 us.  steps 0 = the generic
 // instance (32768-float x capacity, one workgroup per CU).
-unsigned gemv_grid(const zlm_device* d, const QuantInfo* qi, uint64_t tiles, int steps) {
-    const uint64_t wgs = (tiles + kGemvThreads / 64 - 1) / (kGemvThreads / 64);
+// A prefetching instance (waves_per_cu set) runs that many waves per CU.
+unsigned gemv_grid(const zlm_device* d, const QuantInfo* qi, uint64_t tiles, const GemvKernel* gk) {
+    const uint64_t waves = static_cast<uint64_t>(gk->threads / 64);
+    const uint64_t wgs = (tiles + waves - 1) / waves;
+    const int steps = gk->steps;
     const bool small_x = steps > 0 && steps <= (qi->type == ZLM_GGML_Q8_0 ? 4 : 2);
-    const uint64_t per_cu = (steps == 0 || steps > 4) ? 1 : (small_x && tiles >= 65536) ? 8 : 4;
-    return static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->cus) * per_cu));
+    uint64_t cap = static_cast<uint64_t>(d->cus) * ((steps == 0 || steps > 4) ? 1 : (small_x && tiles >= 65536) ? 8 : 4);
+    if (gk->waves_per_cu > 0)
+        cap = std::max<uint64_t>(1, static_cast<uint64_t>(d->cus) * static_cast<uint64_t>(gk->waves_per_cu) / waves);
+    return static_cast<unsigned>(std::min<uint64_t>(wgs, cap));
 }
 
 // Validate a GEMV over resident `r` and pick its kernel.
@@ -424,8 +438,8 @@ bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     const GemvKernel* gk = pick_gemv(d, qi, k, rt_for_variant(variant_of(quant)));
     if (!gk) return fail(d, "no GEMV kernel for quant %u k=%zu", qi->type, k);
     *f = gk->fn;
-    *grid = gemv_grid(d, qi, (rows + gk->rt - 1) / gk->rt, gk->steps);
-    *block = kGemvThreads;
+    *grid = gemv_grid(d, qi, (rows + gk->rt - 1) / gk->rt, gk);
+    *block = static_cast<unsigned>(gk->threads);
     return true;
 }
 
@@ -467,14 +481,16 @@ struct GemvArgsHost {
 };
 static_assert(sizeof(GemvArgsHost) == 80, "GemvArgs layout");
 
-// The fused-form kernel for a shape: the exact-steps instance, else the
-// generic one.
+// The fused-form kernel for a shape: the prefetching exact-steps instance if
+// the quant has one, else the exact-steps instance, else the generic one.
 const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form) {
     const size_t chunks = (qi->type == ZLM_GGML_Q8_0) ? k / 16 : k / 32;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const int rt = form_is_pair(form) ? 2 : 1;
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d_pf", qn, kFormNames[form], steps);
+    if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 8)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d", qn, kFormNames[form], steps);
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_g", qn, kFormNames[form]);
@@ -514,7 +530,8 @@ bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     a.eps = op.eps;
     a.act = op.act;
     void* args[] = {&a};
-    return launch(d, gk->fn, gemv_grid(d, qi, op.rows, gk->steps), kGemvThreads, args, kFormNames[op.form]);
+    return launch(d, gk->fn, gemv_grid(d, qi, op.rows, gk), static_cast<unsigned>(gk->threads), args,
+                  kFormNames[op.form]);
 }
 
 zlm_resident* new_resident(zlm_device* d, const void* bytes, size_t len) {

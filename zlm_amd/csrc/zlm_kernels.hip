@@ -483,28 +483,150 @@ extern "C" __global__ void __launch_bounds__(64)
 // zlm_attn_combine).  Grid (nkv, nsplit), 256 threads.  Workgroup (h, s)
 // handles the G = nh/nkv q heads of kv head h (G <= 4) over positions
 // [64 s, 64 s + 64) clipped to L = min(*pos + 1, max_seq):
-//   scores: thread t takes position t/4 and dims 32*(t%4)..+31 for all G heads
-//           (4 lanes reduce a dot with two shuffles), score = (q.k) * scale;
-//   softmax: wave g (< G) takes head g's 64 scores: m = max, p = exp(s - m),
-//           l = sum p;
-//   values:  wave g accumulates sum_t p_t V[t] with lane l owning dims 2l, 2l+1;
-//           the split's V loads (one 256-byte row per position) are all issued
-//           before the first FMA, so the split costs one memory round trip.
+//   loads:   thread t loads 64 bytes of K and of V: position t/4, dims
+//            32*(t%4)..+31.  The row addresses do not depend on *pos (rows
+//            are clamped to the cache, positions past L masked afterwards), so
+//            the K/V loads go out together with the position's own load and a
+//            split costs one memory round trip;
+//   scores:  thread t takes its K slice for all G heads (4 lanes reduce a dot
+//            with two shuffles), score = (q.k) * scale;
+//   values:  the V slices go to LDS transposed (dword column c = dims 2c, 2c+1
+//            holds the 64 positions contiguously; zeros past L), wave g (< G)
+//            takes head g's 64 scores: m = max, p = exp(s - m), l = sum p, and
+//            lane l accumulates sum_t p_t V[t][2l..2l+1], reading its column
+//            four positions per 128-bit LDS read and each weight with a
+//            readlane.
 // Output part[(qh*nsplit + s)*130 + d] = unnormalised acc (d < 128), then m, l.
 constexpr int kAttnHd = 128;
 constexpr int kAttnSplit = 64;
 constexpr int kAttnPart = kAttnHd + 2;
 
+// V tile row stride in dwords: 64 positions + 4, so the 16 lanes of one
+// 128-bit LDS read pass (columns l..l+15, same positions) cover all 64 banks.
+constexpr int kAttnVStride = kAttnSplit + 4;
+
+struct alignas(16) AttnLds {
+    float qs[4][kAttnHd];                          // scaled q of the G heads (zeros past G)
+    float sc[4][kAttnSplit];                       // scores
+    uint32_t vt[kAttnHd / 2][kAttnVStride];        // V transposed: [dim pair][position] f16 pairs
+};
+
+// Position-independent K and V loads of thread (p, qd) of split t0.
+__device__ __forceinline__ void attn_load_kv(const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
+                                             uint32_t h, uint32_t max_seq, uint32_t t0, uint32_t p, uint32_t qd,
+                                             uint4 (&kraw)[4], uint4 (&vraw)[4]) {
+    const size_t row = static_cast<size_t>(h) * max_seq + min(t0 + p, max_seq - 1);
+    const _Float16* kr = kc + row * kAttnHd + 32 * qd;
+    const _Float16* vr = vc + row * kAttnHd + 32 * qd;
+#pragma unroll
+    for (int c = 0; c < 4; c++) kraw[c] = *reinterpret_cast<const uint4*>(kr + 8 * c);
+#pragma unroll
+    for (int c = 0; c < 4; c++) vraw[c] = *reinterpret_cast<const uint4*>(vr + 8 * c);
+}
+
+// Thread (p, qd)'s V slice (dword columns 16 qd..+15) into the transposed
+// LDS tile: zeros for a position past L (its weight is 0, and 0 * a stale NaN
+// would not be), nothing for the row `skip` (the caller writes that row).
+__device__ __forceinline__ void attn_stage_v(const uint4 (&vraw)[4], uint32_t p, uint32_t qd, bool valid,
+                                             uint32_t skip, AttnLds& sm) {
+    if (p == skip) return;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t w[4] = {vraw[c].x, vraw[c].y, vraw[c].z, vraw[c].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) sm.vt[16 * qd + 4 * c + i][p] = valid ? w[i] : 0u;
+    }
+}
+
+// Scores of thread (p, qd)'s position for all 4 head slots into sm.sc; with
+// NEWROW the position `prow` takes its K values from kn (fp32 of the f16 row
+// just appended) instead of the loaded slice.
+template <bool NEWROW>
+__device__ __forceinline__ void attn_scores(const uint4 (&kraw)[4], uint32_t p, uint32_t qd, bool valid,
+                                            uint32_t prow, const float* kn, AttnLds& sm) {
+    float kf[32];  // dims 32 qd .. +31 of position p
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const uint32_t wv[4] = {kraw[c].x, kraw[c].y, kraw[c].z, kraw[c].w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            kf[8 * c + 2 * j] = h2f(wv[j]);
+            kf[8 * c + 2 * j + 1] = h2f(wv[j] >> 16);
+        }
+    }
+    if constexpr (NEWROW) {
+        if (p == prow) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 t = lds4(kn + 32 * qd + 4 * i);
+                kf[4 * i] = t.x;
+                kf[4 * i + 1] = t.y;
+                kf[4 * i + 2] = t.z;
+                kf[4 * i + 3] = t.w;
+            }
+        }
+    }
+    float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const float4 qv = lds4(&sm.qs[g][32 * qd + 4 * i]);
+            dot[g] = fmaf(qv.x, kf[4 * i], dot[g]);
+            dot[g] = fmaf(qv.y, kf[4 * i + 1], dot[g]);
+            dot[g] = fmaf(qv.z, kf[4 * i + 2], dot[g]);
+            dot[g] = fmaf(qv.w, kf[4 * i + 3], dot[g]);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        dot[g] += __shfl_xor(dot[g], 1, kWave);
+        dot[g] += __shfl_xor(dot[g], 2, kWave);
+    }
+    if (qd == 0) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) sm.sc[g][p] = valid ? dot[g] : -INFINITY;
+    }
+}
+
+// Wave g's softmax over its head's 64 scores and the weighted V sum from LDS;
+// writes the split's partial (acc[128], m, l).
+__device__ __forceinline__ void attn_values(const AttnLds& sm, uint32_t g, uint32_t lane, float* __restrict__ out) {
+    const float sv = sm.sc[g][lane];
+    const float m = wave_max(sv);
+    const float e = (sv == -INFINITY) ? 0.0f : expf(sv - m);
+    const float l = wave_sum(e);
+    const int eb = __builtin_bit_cast(int, e);
+    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+    for (int j4 = 0; j4 < kAttnSplit; j4 += 4) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&sm.vt[lane][j4]);
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            // position j's weight, held by lane j (0 past n)
+            const float pe = __builtin_bit_cast(float, __builtin_amdgcn_readlane(eb, j4 + i));
+            a0 = fmaf(pe, h2f(vw[i]), a0);
+            a1 = fmaf(pe, h2f(vw[i] >> 16), a1);
+        }
+    }
+    *reinterpret_cast<float2*>(out + 2 * lane) = make_float2(a0, a1);
+    if (lane == 0) {
+        out[kAttnHd] = m;
+        out[kAttnHd + 1] = l;
+    }
+}
+
 extern "C" __global__ void __launch_bounds__(256)
     zlm_attn_partial(const float* __restrict__ q, const _Float16* __restrict__ kc, const _Float16* __restrict__ vc,
                      uint32_t nh, uint32_t nkv, const int32_t* __restrict__ pos_p, uint32_t max_seq, float scale,
                      float* __restrict__ part, uint32_t nsplit) {
-    __shared__ float qs[4][kAttnHd];
-    __shared__ float sc[4][kAttnSplit];
+    __shared__ AttnLds sm;
     const uint32_t h = blockIdx.x, s = blockIdx.y;
     const uint32_t G = nh / nkv;
     const uint32_t tid = threadIdx.x, wid = tid / kWave, lane = tid & (kWave - 1);
-    const int32_t pos_i = *pos_p;
+    const uint32_t t0 = s * kAttnSplit;
+    const uint32_t p = tid / 4, qd = tid % 4;
     // q (scaled) for the G heads into LDS; thread tid holds 2 of the 4*128 values
     float qv[2];
 #pragma unroll
@@ -512,84 +634,56 @@ extern "C" __global__ void __launch_bounds__(256)
         const uint32_t i = tid + 256u * j, g = i / kAttnHd, d = i % kAttnHd;
         qv[j] = q[static_cast<size_t>(h * G + min(g, G - 1)) * kAttnHd + d];
     }
+    uint4 kraw[4], vraw[4];
+    attn_load_kv(kc, vc, h, max_seq, t0, p, qd, kraw, vraw);
+    const int32_t pos_i = *pos_p;
     const uint32_t L = pos_i < 0 ? 0u : min(static_cast<uint32_t>(pos_i) + 1u, max_seq);
-    const uint32_t t0 = s * kAttnSplit;
     const uint32_t n = t0 < L ? min(static_cast<uint32_t>(kAttnSplit), L - t0) : 0u;
-    const uint32_t p = tid / 4, qd = tid % 4;
     const bool valid = p < n;
-    uint4 kraw[4];
-    {
-        const _Float16* kr = kc + (static_cast<size_t>(h) * max_seq + t0 + (valid ? p : 0u)) * kAttnHd + 32 * qd;
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            kraw[c] = valid ? *reinterpret_cast<const uint4*>(kr + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
-    }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const uint32_t i = tid + 256u * j, g = i / kAttnHd;
-        qs[g][i % kAttnHd] = g < G ? qv[j] * scale : 0.0f;
+        sm.qs[g][i % kAttnHd] = g < G ? qv[j] * scale : 0.0f;
     }
+    attn_stage_v(vraw, p, qd, valid, kAttnSplit, sm);
     __syncthreads();
-    {
-        float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t wv[4] = {kraw[c].x, kraw[c].y, kraw[c].z, kraw[c].w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float k0 = h2f(wv[j]), k1 = h2f(wv[j] >> 16);
-                const int d = 32 * qd + 8 * c + 2 * j;
-#pragma unroll
-                for (int g = 0; g < 4; g++) dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
-            }
-        }
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            dot[g] += __shfl_xor(dot[g], 1, kWave);
-            dot[g] += __shfl_xor(dot[g], 2, kWave);
-        }
-        if (qd == 0) {
-#pragma unroll
-            for (int g = 0; g < 4; g++) sc[g][p] = valid ? dot[g] : -INFINITY;
-        }
-    }
+    attn_scores<false>(kraw, p, qd, valid, kAttnSplit, nullptr, sm);
     __syncthreads();
-    if (wid >= G) return;  // no barrier follows
-    const uint32_t g = wid;
-    // the split's V rows: position j's two dims of this lane, all loads first
-    uint32_t vv[kAttnSplit];
-    {
-        const _Float16* vr = vc + (static_cast<size_t>(h) * max_seq + t0) * kAttnHd + 2 * lane;
-#pragma unroll
-        for (int j = 0; j < kAttnSplit; j++)
-            vv[j] = static_cast<uint32_t>(j) < n ? *reinterpret_cast<const uint32_t*>(vr + static_cast<size_t>(j) * kAttnHd)
-                                                 : 0u;
-    }
-    const float sv = sc[g][lane];
-    const float m = wave_max(sv);
-    const float e = (sv == -INFINITY) ? 0.0f : expf(sv - m);
-    const float l = wave_sum(e);
-    float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kAttnSplit; j++) {
-        const float pe = __shfl(e, j, kWave);  // position j's weight, held by lane j (0 past n)
-        a0 = fmaf(pe, h2f(vv[j]), a0);
-        a1 = fmaf(pe, h2f(vv[j] >> 16), a1);
-    }
-    float* out = part + (static_cast<size_t>(h * G + g) * nsplit + s) * kAttnPart;
-    out[2 * lane] = a0;
-    out[2 * lane + 1] = a1;
-    if (lane == 0) {
-        out[kAttnHd] = m;
-        out[kAttnHd + 1] = l;
-    }
+    if (wid < G) attn_values(sm, wid, lane, part + (static_cast<size_t>(h * G + wid) * nsplit + s) * kAttnPart);
 }
 
 // Merge the partials of one q head into lane l's dims 2l, 2l+1: lane s holds
-// split s's (m, l) (64 splits per pass); the accumulator loads are issued 16
-// splits at a time ahead of their FMAs.  `base` points at the head's nsplit
-// partials.
+// split s's (m, l).  Up to 32 splits (a 2048-position cache) every load is
+// issued before the first use, one memory round trip; more splits loop in
+// passes of 64 (m first, then the accumulators 16 splits at a time).  `base`
+// points at the head's nsplit partials.
 __device__ __forceinline__ float2 combine_head(const float* __restrict__ base, uint32_t nsplit, uint32_t lane) {
+    if (nsplit <= 32) {
+        const bool sv = lane < nsplit;
+        const uint32_t sl = sv ? lane : 0u;
+        const float ms_raw = base[static_cast<size_t>(sl) * kAttnPart + kAttnHd];
+        const float ls_raw = base[static_cast<size_t>(sl) * kAttnPart + kAttnHd + 1];
+        float2 acc[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const uint32_t sj = min(static_cast<uint32_t>(j), nsplit - 1);
+            acc[j] = *reinterpret_cast<const float2*>(base + static_cast<size_t>(sj) * kAttnPart + 2 * lane);
+        }
+        const float ms = sv ? ms_raw : -INFINITY;
+        const float M = wave_max(ms);
+        const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+        const float den = wave_sum(sv ? w * ls_raw : 0.0f);
+        float a0 = 0.0f, a1 = 0.0f;
+        const int wb = __builtin_bit_cast(int, w);
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(wb, j));  // 0 past nsplit
+            a0 = fmaf(wj, acc[j].x, a0);
+            a1 = fmaf(wj, acc[j].y, a1);
+        }
+        const float inv = 1.0f / den;
+        return make_float2(a0 * inv, a1 * inv);
+    }
     float M = -INFINITY;
     for (uint32_t s0 = 0; s0 < nsplit; s0 += kWave) {
         const uint32_t s = s0 + lane;
@@ -638,13 +732,16 @@ extern "C" __global__ void __launch_bounds__(64)
 // block.zig:24-31: q_norm/k_norm, rope, write_kv, attention), head_dim 128,
 // G = nh/nkv <= 4.  Grid (nkv, nsplit), 256 threads; workgroup (h, s) owns kv
 // head h's G q heads over positions [64 s, 64 s + 64) of L = *pos + 1:
-//   * every global load it needs (its K and V rows, the raw q / k / v head
-//     values, the norm weights) is issued first;
+//   * every global load it needs (its K and V slices, the raw q / k / v head
+//     values, the norm weights, the position) is issued first, none waiting
+//     on another;
 //   * the cos/sin of the 64 rotary pairs at *pos go to LDS once;
 //   * wave g normalises and rotates q head g (the same arithmetic as
 //     zlm_qk_norm_rope_kv); the workgroup whose range holds *pos also
 //     normalises and rotates k head h, appends the f16 K and V rows to the
-//     caches and uses those same f16 values for position *pos (no read back);
+//     caches and uses those same f16 values for position *pos (no read back:
+//     the V row goes straight into the LDS V tile, the K row replaces the
+//     loaded slice in the scores);
 //   * scores, softmax and values as zlm_attn_partial, into the same partials,
 //     which zlm_attn_combine merges.  (Merging in the last workgroup of each kv
 //     head instead, behind a device-scope fence and counter, measured 3x
@@ -654,24 +751,19 @@ extern "C" __global__ void __launch_bounds__(256)
                     uint32_t nh, uint32_t nkv, float eps, float freq_base, const int32_t* __restrict__ pos_p,
                     _Float16* __restrict__ kc, _Float16* __restrict__ vc, uint32_t max_seq, float scale,
                     float* __restrict__ part, uint32_t nsplit) {
-    __shared__ float qs[4][kAttnHd];
-    __shared__ float sc[4][kAttnSplit];
+    __shared__ AttnLds sm;
     __shared__ float cs[kAttnHd / 2], sn[kAttnHd / 2];
-    __shared__ float kn[kAttnHd], vn[kAttnHd];
+    __shared__ __attribute__((aligned(16))) float kn[kAttnHd];
     const uint32_t h = blockIdx.x, s = blockIdx.y;
     const uint32_t G = nh / nkv;
     const uint32_t tid = threadIdx.x, wid = tid / kWave, lane = tid & (kWave - 1);
     constexpr uint32_t half = kAttnHd / 2;
-    const int32_t pos_i = *pos_p;
-    const bool pos_ok = pos_i >= 0 && static_cast<uint32_t>(pos_i) < max_seq;
-    const uint32_t L = pos_i < 0 ? 0u : min(static_cast<uint32_t>(pos_i) + 1u, max_seq);
     const uint32_t t0 = s * kAttnSplit;
-    const uint32_t n = t0 < L ? min(static_cast<uint32_t>(kAttnSplit), L - t0) : 0u;
-    const bool own = pos_ok && static_cast<uint32_t>(pos_i) >= t0 && static_cast<uint32_t>(pos_i) < t0 + kAttnSplit;
-    const uint32_t prow = own ? static_cast<uint32_t>(pos_i) - t0 : kAttnSplit;  // the new row's slot, or none
+    const uint32_t p = tid / 4, qd = tid % 4;
 
-    // loads: this wave's q head (raw) and norm weights, k/v of the new row,
-    // the split's K rows (scores mapping) and V rows (values mapping)
+    // loads: the position, this wave's q head (raw) and norm weights, k/v of
+    // the new row, the split's K and V slices
+    const int32_t pos_i = *pos_p;
     const uint32_t g = min(wid, G - 1);
     const float* qh = qkv + static_cast<size_t>(h * G + g) * kAttnHd;
     const float q0 = qh[lane], q1 = qh[lane + half];
@@ -680,106 +772,58 @@ extern "C" __global__ void __launch_bounds__(256)
     const float* vh = qkv + static_cast<size_t>(nh + nkv + h) * kAttnHd;
     const float k0 = kh[lane], k1 = kh[lane + half], wk0 = kn_w[lane], wk1 = kn_w[lane + half];
     const float v0 = vh[lane], v1 = vh[lane + half];
-    const uint32_t p = tid / 4, qd = tid % 4;
+    uint4 kraw[4], vraw[4];
+    attn_load_kv(kc, vc, h, max_seq, t0, p, qd, kraw, vraw);
+
+    const bool pos_ok = pos_i >= 0 && static_cast<uint32_t>(pos_i) < max_seq;
+    const uint32_t L = pos_i < 0 ? 0u : min(static_cast<uint32_t>(pos_i) + 1u, max_seq);
+    const uint32_t n = t0 < L ? min(static_cast<uint32_t>(kAttnSplit), L - t0) : 0u;
+    const bool own = pos_ok && static_cast<uint32_t>(pos_i) >= t0 && static_cast<uint32_t>(pos_i) < t0 + kAttnSplit;
+    const uint32_t prow = own ? static_cast<uint32_t>(pos_i) - t0 : kAttnSplit;  // the new row's slot, or none
     const bool valid = p < n;
-    uint4 kraw[4];
-    {
-        const _Float16* kr = kc + (static_cast<size_t>(h) * max_seq + t0 + (valid ? p : 0u)) * kAttnHd + 32 * qd;
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            kraw[c] = valid ? *reinterpret_cast<const uint4*>(kr + 8 * c) : make_uint4(0u, 0u, 0u, 0u);
-    }
-    uint32_t vv[kAttnSplit];
-    {
-        const _Float16* vr = vc + (static_cast<size_t>(h) * max_seq + t0) * kAttnHd + 2 * lane;
-#pragma unroll
-        for (int j = 0; j < kAttnSplit; j++)
-            vv[j] = static_cast<uint32_t>(j) < n ? *reinterpret_cast<const uint32_t*>(vr + static_cast<size_t>(j) * kAttnHd)
-                                                 : 0u;
-    }
     if (tid < half) {
         const float angle = static_cast<float>(pos_i) *
                             powf(freq_base, -2.0f * static_cast<float>(tid) / static_cast<float>(kAttnHd));
         cs[tid] = cosf(angle);
         sn[tid] = sinf(angle);
     }
+    attn_stage_v(vraw, p, qd, valid, prow, sm);
+    if (own && wid == 1) {  // the new V row, as the f16 values the cache holds
+        const _Float16 e0 = static_cast<_Float16>(v0), e1 = static_cast<_Float16>(v1);
+        _Float16* vd = vc + (static_cast<size_t>(h) * max_seq + pos_i) * kAttnHd;
+        vd[lane] = e0;
+        vd[lane + half] = e1;
+        // dim d sits in half d%2 of dword column d/2 at position prow
+        reinterpret_cast<_Float16*>(&sm.vt[lane / 2][prow])[lane % 2] = e0;
+        reinterpret_cast<_Float16*>(&sm.vt[(lane + half) / 2][prow])[lane % 2] = e1;
+    }
     __syncthreads();
     // q head g: RMSNorm, rotate, scale (lane l owns the pair (l, l + 64))
     if (wid < G) {
         const float inv = 1.0f / sqrtf(wave_sum(fmaf(q0, q0, q1 * q1)) / static_cast<float>(kAttnHd) + eps);
         const float a = q0 * inv * wq0, b = q1 * inv * wq1;
-        qs[wid][lane] = fmaf(b, -sn[lane], a * cs[lane]) * scale;
-        qs[wid][lane + half] = fmaf(b, cs[lane], a * sn[lane]) * scale;
+        sm.qs[wid][lane] = fmaf(b, -sn[lane], a * cs[lane]) * scale;
+        sm.qs[wid][lane + half] = fmaf(b, cs[lane], a * sn[lane]) * scale;
     } else {
-        qs[wid][lane] = 0.0f;
-        qs[wid][lane + half] = 0.0f;
+        sm.qs[wid][lane] = 0.0f;
+        sm.qs[wid][lane + half] = 0.0f;
     }
-    // the new position's K and V rows: kept as the f16 values the caches hold
+    // the new position's K row: kept as the f16 values the cache holds
     if (own && wid == 0) {
         const float inv = 1.0f / sqrtf(wave_sum(fmaf(k0, k0, k1 * k1)) / static_cast<float>(kAttnHd) + eps);
         const float a = k0 * inv * wk0, b = k1 * inv * wk1;
         const _Float16 r0 = static_cast<_Float16>(fmaf(b, -sn[lane], a * cs[lane]));
         const _Float16 r1 = static_cast<_Float16>(fmaf(b, cs[lane], a * sn[lane]));
-        const _Float16 e0 = static_cast<_Float16>(v0), e1 = static_cast<_Float16>(v1);
         _Float16* kd = kc + (static_cast<size_t>(h) * max_seq + pos_i) * kAttnHd;
-        _Float16* vd = vc + (static_cast<size_t>(h) * max_seq + pos_i) * kAttnHd;
         kd[lane] = r0;
         kd[lane + half] = r1;
-        vd[lane] = e0;
-        vd[lane + half] = e1;
         kn[lane] = static_cast<float>(r0);
         kn[lane + half] = static_cast<float>(r1);
-        vn[lane] = static_cast<float>(e0);
-        vn[lane + half] = static_cast<float>(e1);
     }
     __syncthreads();
-    {
-        float dot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        const bool newrow = p == prow;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const uint32_t wv[4] = {kraw[c].x, kraw[c].y, kraw[c].z, kraw[c].w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int d = 32 * qd + 8 * c + 2 * j;
-                const float x0 = newrow ? kn[d] : h2f(wv[j]);
-                const float x1 = newrow ? kn[d + 1] : h2f(wv[j] >> 16);
-#pragma unroll
-                for (int gg = 0; gg < 4; gg++) dot[gg] = fmaf(qs[gg][d + 1], x1, fmaf(qs[gg][d], x0, dot[gg]));
-            }
-        }
-#pragma unroll
-        for (int gg = 0; gg < 4; gg++) {
-            dot[gg] += __shfl_xor(dot[gg], 1, kWave);
-            dot[gg] += __shfl_xor(dot[gg], 2, kWave);
-        }
-        if (qd == 0) {
-#pragma unroll
-            for (int gg = 0; gg < 4; gg++) sc[gg][p] = valid ? dot[gg] : -INFINITY;
-        }
-    }
+    attn_scores<true>(kraw, p, qd, valid, prow, kn, sm);
     __syncthreads();
-    if (wid < G) {
-        const float sv = sc[wid][lane];
-        const float m = wave_max(sv);
-        const float e = (sv == -INFINITY) ? 0.0f : expf(sv - m);
-        const float l = wave_sum(e);
-        float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kAttnSplit; j++) {
-            const float pe = __shfl(e, j, kWave);
-            const bool nr = static_cast<uint32_t>(j) == prow;
-            a0 = fmaf(pe, nr ? vn[2 * lane] : h2f(vv[j]), a0);
-            a1 = fmaf(pe, nr ? vn[2 * lane + 1] : h2f(vv[j] >> 16), a1);
-        }
-        float* o = part + (static_cast<size_t>(h * G + wid) * nsplit + s) * kAttnPart;
-        o[2 * lane] = a0;
-        o[2 * lane + 1] = a1;
-        if (lane == 0) {
-            o[kAttnHd] = m;
-            o[kAttnHd + 1] = l;
-        }
-    }
+    if (wid < G) attn_values(sm, wid, lane, part + (static_cast<size_t>(h * G + wid) * nsplit + s) * kAttnPart);
 }
 
 // ---- synthetic data on the device (benchmark and large-shape tests) ---------
