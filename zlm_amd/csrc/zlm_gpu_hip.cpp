@@ -1497,7 +1497,7 @@ extern "C" bool zlm_gpu_attention_decode_enqueue(zlm_device* d, const float* qkv
             return false;
     }
     void* args[] = {&part, &nsplit, &out};
-    return launch(d, d->attn_combine, n_heads, 64, args, "attention combine");
+    return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
 }
 
 extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const uint16_t* k_cache,
@@ -1520,7 +1520,7 @@ extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const u
             return false;
     }
     void* args[] = {&part, &nsplit, &out};
-    return launch(d, d->attn_combine, n_heads, 64, args, "attention combine");
+    return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
 }
 
 struct zlm_graph {

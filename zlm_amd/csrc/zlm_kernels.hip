@@ -652,80 +652,63 @@ extern "C" __global__ void __launch_bounds__(256)
     if (wid < G) attn_values(sm, wid, lane, part + (static_cast<size_t>(h * G + wid) * nsplit + s) * kAttnPart);
 }
 
-// Merge the partials of one q head into lane l's dims 2l, 2l+1: lane s holds
-// split s's (m, l).  Up to 32 splits (a 2048-position cache) every load is
-// issued before the first use, one memory round trip; more splits loop in
-// passes of 64 (m first, then the accumulators 16 splits at a time).  `base`
-// points at the head's nsplit partials.
-__device__ __forceinline__ float2 combine_head(const float* __restrict__ base, uint32_t nsplit, uint32_t lane) {
-    if (nsplit <= 32) {
-        const bool sv = lane < nsplit;
-        const uint32_t sl = sv ? lane : 0u;
-        const float ms_raw = base[static_cast<size_t>(sl) * kAttnPart + kAttnHd];
-        const float ls_raw = base[static_cast<size_t>(sl) * kAttnPart + kAttnHd + 1];
-        float2 acc[32];
-#pragma unroll
-        for (int j = 0; j < 32; j++) {
-            const uint32_t sj = min(static_cast<uint32_t>(j), nsplit - 1);
-            acc[j] = *reinterpret_cast<const float2*>(base + static_cast<size_t>(sj) * kAttnPart + 2 * lane);
-        }
-        const float ms = sv ? ms_raw : -INFINITY;
-        const float M = wave_max(ms);
-        const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);
-        const float den = wave_sum(sv ? w * ls_raw : 0.0f);
-        float a0 = 0.0f, a1 = 0.0f;
-        const int wb = __builtin_bit_cast(int, w);
-#pragma unroll
-        for (int j = 0; j < 32; j++) {
-            const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(wb, j));  // 0 past nsplit
-            a0 = fmaf(wj, acc[j].x, a0);
-            a1 = fmaf(wj, acc[j].y, a1);
-        }
-        const float inv = 1.0f / den;
-        return make_float2(a0 * inv, a1 * inv);
-    }
+// Merge the nsplit partials of each q head: M = max m_s, w_s = exp(m_s - M)
+// (0 for an empty split), out = sum w_s acc_s / sum w_s l_s.  One 256-thread
+// workgroup per q head, in passes of 64 splits: lane s of every wave holds
+// split s's (m, l) and w_s; wave g accumulates the pass's splits g, g+4, ...
+// into lane l's dims 2l, 2l+1 (16 splits, every load issued before the first
+// use, so a pass is one memory round trip), and the four waves' sums merge in
+// LDS.
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_attn_combine(const float* __restrict__ part, uint32_t nsplit, float* __restrict__ out) {
+    __shared__ float2 red[4][kWave];
+    const uint32_t qh = blockIdx.x, tid = threadIdx.x, wid = tid / kWave, lane = tid & (kWave - 1);
+    const float* base = part + static_cast<size_t>(qh) * nsplit * kAttnPart;
     float M = -INFINITY;
-    for (uint32_t s0 = 0; s0 < nsplit; s0 += kWave) {
-        const uint32_t s = s0 + lane;
-        M = fmaxf(M, wave_max(s < nsplit ? base[static_cast<size_t>(s) * kAttnPart + kAttnHd] : -INFINITY));
+    if (nsplit > kWave) {
+        for (uint32_t s0 = 0; s0 < nsplit; s0 += kWave) {
+            const uint32_t s = s0 + lane;
+            M = fmaxf(M, wave_max(s < nsplit ? base[static_cast<size_t>(s) * kAttnPart + kAttnHd] : -INFINITY));
+        }
     }
     float a0 = 0.0f, a1 = 0.0f, den = 0.0f;
     for (uint32_t s0 = 0; s0 < nsplit; s0 += kWave) {
-        const uint32_t s = s0 + lane;
-        const bool sv = s < nsplit;
-        const float ms = sv ? base[static_cast<size_t>(s) * kAttnPart + kAttnHd] : -INFINITY;
-        const float ls = sv ? base[static_cast<size_t>(s) * kAttnPart + kAttnHd + 1] : 0.0f;
-        const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);
-        den += wave_sum(w * ls);
         const uint32_t cnt = min(static_cast<uint32_t>(kWave), nsplit - s0);
-        for (uint32_t j0 = 0; j0 < cnt; j0 += 16) {
-            float2 acc[16];
+        const bool sv = lane < cnt;
+        const size_t sl = s0 + (sv ? lane : 0u);
+        const float ms_raw = base[sl * kAttnPart + kAttnHd];
+        const float ls_raw = base[sl * kAttnPart + kAttnHd + 1];
+        float2 acc[16];
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const uint32_t sj = s0 + min(j0 + j, cnt - 1);
-                acc[j] = *reinterpret_cast<const float2*>(base + static_cast<size_t>(sj) * kAttnPart + 2 * lane);
-            }
+        for (int j = 0; j < 16; j++) {
+            const uint32_t sj = s0 + min(wid + 4u * j, cnt - 1);
+            acc[j] = *reinterpret_cast<const float2*>(base + static_cast<size_t>(sj) * kAttnPart + 2 * lane);
+        }
+        const float ms = sv ? ms_raw : -INFINITY;
+        if (nsplit <= kWave) M = wave_max(ms);
+        const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+        den += wave_sum(sv ? w * ls_raw : 0.0f);
+        const int wb = __builtin_bit_cast(int, w);
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float wj = __shfl(w, static_cast<int>(j0 + j) & (kWave - 1), kWave);
-                const float use = (j0 + j < cnt) ? wj : 0.0f;
-                a0 = fmaf(use, acc[j].x, a0);
-                a1 = fmaf(use, acc[j].y, a1);
-            }
+        for (int j = 0; j < 16; j++) {
+            const uint32_t idx = wid + 4u * j;  // 0 weight past cnt
+            const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(wb, idx));
+            a0 = fmaf(wj, acc[j].x, a0);
+            a1 = fmaf(wj, acc[j].y, a1);
         }
     }
-    const float inv = 1.0f / den;
-    return make_float2(a0 * inv, a1 * inv);
-}
-
-// Merge the nsplit partials of each q head: M = max m_s, w_s = exp(m_s - M)
-// (0 for an empty split), out = sum w_s acc_s / sum w_s l_s.  One 64-lane
-// workgroup per q head (combine_head).
-extern "C" __global__ void __launch_bounds__(64)
-    zlm_attn_combine(const float* __restrict__ part, uint32_t nsplit, float* __restrict__ out) {
-    const uint32_t qh = blockIdx.x, lane = threadIdx.x;
-    const float2 r = combine_head(part + static_cast<size_t>(qh) * nsplit * kAttnPart, nsplit, lane);
-    *reinterpret_cast<float2*>(out + static_cast<size_t>(qh) * kAttnHd + 2 * lane) = r;
+    red[wid][lane] = make_float2(a0, a1);
+    __syncthreads();
+    if (wid == 0) {
+        float2 t = red[0][lane];
+#pragma unroll
+        for (int g = 1; g < 4; g++) {
+            t.x += red[g][lane].x;
+            t.y += red[g][lane].y;
+        }
+        const float inv = 1.0f / den;
+        *reinterpret_cast<float2*>(out + static_cast<size_t>(qh) * kAttnHd + 2 * lane) = make_float2(t.x * inv, t.y * inv);
+    }
 }
 
 // The decode layer's whole attention block in one launch (reference
