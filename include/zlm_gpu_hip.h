@@ -20,6 +20,10 @@
  * 0..7 and the GpuVariant code (reference gpu/kernels/grid.zig:14) in bits
  * 8..15.  A variant never changes the byte layout, only the kernel.
  *
+ * Device kernels: GEMVs (every form) for q4_0, q4_1, q8_0, q4_k, q6_k, f32,
+ * f16 and bf16 (the float types need k % 32 == 0), prefill GEMMs for q4_0 and
+ * q8_0; any other quant or shape returns false.
+ *
  * Weight bytes are always the raw GGUF blocks (row-major, `rows` rows of
  * `k / block_elems` blocks).  The device keeps its own layout in HBM.
  */

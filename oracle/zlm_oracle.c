@@ -404,18 +404,82 @@ ALWAYS_INLINE void sweep_fp(int L, uint32_t t, const uint8_t *w, size_t k, const
 
 static int check_shape(uint32_t t, size_t w_len, size_t k, size_t rows, size_t begin, size_t end) {
     size_t be = orc_block_elems(t), bb = orc_block_bytes(t);
-    if (be == 0 || t == ORC_F32 || t == ORC_F16 || t == ORC_BF16) return ORC_E_UNSUPPORTED;
+    if (be == 0) return ORC_E_UNSUPPORTED;
     if (k % be != 0) return ORC_E_SHAPE;
     if (w_len < rows * (k / be) * bb) return ORC_E_TRUNCATED;
     if (begin > end || end > rows) return ORC_E_RANGE;
     return ORC_OK;
 }
 
-/* matVecRowsWithPlan(.production) (single.zig:168-205) for the quant types. */
+/* One weight element of a float row (F32 / F16 / BF16) widened to f32. */
+ALWAYS_INLINE float float_elem(uint32_t t, const uint8_t *row, size_t j) {
+    if (t == ORC_F32) {
+        float v;
+        memcpy(&v, row + 4 * j, 4);
+        return v;
+    }
+    uint16_t h = (uint16_t)(row[2 * j] | ((uint16_t)row[2 * j + 1] << 8));
+    if (t == ORC_F16) return orc_f16_to_f32(h);
+    uint32_t bits = (uint32_t)h << 16;
+    float v;
+    memcpy(&v, &bits, 4);
+    return v;
+}
+
+/*
+ * matVecF32 / matVecF16 (matvec/kernels/float.zig:67-95), the float types'
+ * production_fp: per row one f32 accumulator, acc += w * x[j] (a product and a
+ * sum, two roundings), in element order.
+ */
+static void matvec_float_seq(uint32_t t, const uint8_t *w, size_t k, const float *x, float *out,
+                             size_t begin, size_t end) {
+    size_t rowb = k * orc_block_bytes(t);
+    for (size_t i = begin; i < end; i++) {
+        const uint8_t *row = w + i * rowb;
+        float acc = 0.0f;
+        for (size_t j = 0; j < k; j++) acc += float_elem(t, row, j) * x[j];
+        out[i] = acc;
+    }
+}
+
+/*
+ * matVecBF16 (matvec/kernels/bfloat.zig:44-67): two 8-lane accumulators over
+ * 16-element steps (acc0 += w[j..j+8]*x, acc1 += w[j+8..j+16]*x, products and
+ * sums rounded separately), acc = reduce(acc0) + reduce(acc1), then the tail
+ * elements one by one.
+ */
+static void matvec_bf16(const uint8_t *w, size_t k, const float *x, float *out, size_t begin,
+                        size_t end) {
+    size_t rowb = k * 2;
+    for (size_t i = begin; i < end; i++) {
+        const uint8_t *row = w + i * rowb;
+        float a0[8] = {0}, a1[8] = {0};
+        size_t j = 0;
+        for (; j + 16 <= k; j += 16) {
+            for (int l = 0; l < 8; l++) {
+                a0[l] += float_elem(ORC_BF16, row, j + l) * x[j + l];
+                a1[l] += float_elem(ORC_BF16, row, j + 8 + l) * x[j + 8 + l];
+            }
+        }
+        float acc = lane_sum(a0, 8) + lane_sum(a1, 8);
+        for (; j < k; j++) acc += float_elem(ORC_BF16, row, j) * x[j];
+        out[i] = acc;
+    }
+}
+
+/* matVecRowsWithPlan(.production) (single.zig:168-205): each type's production_fp. */
 int orc_matvec(uint32_t t, const uint8_t *w, size_t w_len, size_t k, size_t rows, const float *x,
                float *out, size_t begin, size_t end, int lanes) {
     int rc = check_shape(t, w_len, k, rows, begin, end);
     if (rc) return rc;
+    if (t == ORC_F32 || t == ORC_F16) {
+        matvec_float_seq(t, w, k, x, out, begin, end);
+        return ORC_OK;
+    }
+    if (t == ORC_BF16) {
+        matvec_bf16(w, k, x, out, begin, end);
+        return ORC_OK;
+    }
     float *xsum = NULL;
     if (t == ORC_Q4_K || t == ORC_Q4_1) {
         /* The bounded activation cache (types.zig:8, single.zig:76-80). */
@@ -510,6 +574,23 @@ ALWAYS_INLINE void int_q8_0(int L, const uint8_t *b, const int8_t *qx, float dx,
     for (int j = 0; j < L; j++) acc[j] = fmaf(s, ivf[j], acc[j]);
 }
 
+/*
+ * Q4_1.intBlock (quantized.zig:79-87) over q4_1IntBlockVec (layout.zig:185-210):
+ * unsigned nibble times q8 activation folded into lanes;
+ * acc = fma(d*dx, f32(iv), acc); corr += (mn*dx) * f32(sums).
+ */
+ALWAYS_INLINE void int_q4_1(int L, const uint8_t *b, const int8_t *qx, float dx, int32_t sum,
+                            float *acc, float *corr) {
+    int32_t p[16];
+    float ivf[16];
+    for (int j = 0; j < 16; j++) p[j] = (int32_t)(b[4 + j] & 0x0F) * qx[j] + (int32_t)(b[4 + j] >> 4) * qx[16 + j];
+    fold_lanes(L, p, 16, ivf);
+    float d = rd_f16(b), mn = rd_f16(b + 2);
+    float s = d * dx;
+    for (int j = 0; j < L; j++) acc[j] = fmaf(s, ivf[j], acc[j]);
+    *corr += mn * dx * (float)sum;
+}
+
 /* q4KBlockIntAccum (layout.zig:349-387) as Q4_K.intBlock (quantized.zig:111-123). */
 ALWAYS_INLINE void int_q4_k(int L, const uint8_t *b, const int8_t *qx, const float *dx,
                             const int32_t *sums, float *acc, float *corr) {
@@ -550,6 +631,7 @@ ALWAYS_INLINE void sweep_int(int L, uint32_t t, const uint8_t *w, size_t k, cons
             switch (t) {
             case ORC_Q4_0: int_q4_0(L, b, qx + rb * 32, dx[rb], sums[rb], acc, &corr); break;
             case ORC_Q8_0: int_q8_0(L, b, qx + rb * 32, dx[rb], acc); break;
+            case ORC_Q4_1: int_q4_1(L, b, qx + rb * 32, dx[rb], sums[rb], acc, &corr); break;
             case ORC_Q4_K: int_q4_k(L, b, qx + rb * 256, dx + rb * 8, sums + rb * 8, acc, &corr); break;
             default: break;
             }
@@ -560,7 +642,7 @@ ALWAYS_INLINE void sweep_int(int L, uint32_t t, const uint8_t *w, size_t k, cons
 
 int orc_matvec_int(uint32_t t, const uint8_t *w, size_t w_len, size_t k, size_t rows,
                    const float *x, float *out, size_t begin, size_t end, int lanes) {
-    if (t != ORC_Q4_0 && t != ORC_Q8_0 && t != ORC_Q4_K) return ORC_E_UNSUPPORTED;
+    if (t != ORC_Q4_0 && t != ORC_Q8_0 && t != ORC_Q4_1 && t != ORC_Q4_K) return ORC_E_UNSUPPORTED;
     int rc = check_shape(t, w_len, k, rows, begin, end);
     if (rc) return rc;
     size_t chunks = k / 32;

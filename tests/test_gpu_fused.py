@@ -23,8 +23,8 @@ from zlm_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K]
-NAMES = {synth.Q4_0: "q4_0", synth.Q8_0: "q8_0", synth.Q4_K: "q4_k", synth.Q6_K: "q6_k"}
+TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K, synth.Q4_1, synth.F32, synth.F16, synth.BF16]
+NAMES = synth.TYPE_NAMES
 REL_L2 = 1e-3
 
 
@@ -84,6 +84,9 @@ def test_gate_up_reference_shape(dev):
     (synth.Q8_0, synth.Q4_0, 256, 1024, 3072),
     (synth.Q4_K, synth.Q6_K, 128, 3840, 15360),
     (synth.Q6_K, synth.Q8_0, 96, 2048, 768),
+    (synth.Q4_1, synth.Q4_1, 256, 4096, 1024),
+    (synth.F16, synth.BF16, 128, 1024, 2048),
+    (synth.F32, synth.Q4_1, 64, 512, 1536),
 ])
 def test_mlp_pair_matches_oracle(dev, gq, dq, rows, k, ffn):
     _say(f"mlp {NAMES[gq]}/{NAMES[dq]} rows={rows} k={k} ffn={ffn}")

@@ -20,8 +20,8 @@ from zlm_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K]
-NAMES = {synth.Q4_0: "q4_0", synth.Q8_0: "q8_0", synth.Q4_K: "q4_k", synth.Q6_K: "q6_k"}
+TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K, synth.Q4_1, synth.F32, synth.F16, synth.BF16]
+NAMES = synth.TYPE_NAMES
 REL_L2 = 1e-3
 
 
@@ -173,8 +173,9 @@ def test_rejections_fall_back(dev):
     w = synth.weights(synth.Q4_0, rows, k, seed=1)
     x = synth.activation(1, k)
     out = np.zeros(rows, np.float32)
-    assert not dev.mat_vec(zd.quant(zd.Q4_1), np.zeros(rows * 8 * 20, np.uint8), rows, k, x, out)
-    assert not dev.mat_vec(zd.quant(zd.F32), np.zeros(rows * k * 4, np.uint8), rows, k, x, out)
+    assert not dev.mat_vec(6, np.zeros(rows * 8 * 22, np.uint8), rows, k, x, out)  # q5_0: no kernel
+    xf = synth.activation(2, 40)  # float rows must be a multiple of 32 elements (16-byte rows)
+    assert not dev.mat_vec(zd.quant(zd.F32), np.zeros(rows * 40 * 4, np.uint8), rows, 40, xf, out)
     assert not dev.mat_vec(zd.quant(zd.Q4_0), w, rows, k + 16, np.zeros(k + 16, np.float32), out)  # k % 32
     assert not dev.mat_vec(zd.quant(zd.Q4_0), w[:-1], rows, k, x, out)  # short weight
     assert not dev.mat_vec(zd.quant(zd.Q4_0), w, 0, k, x, out)  # rows == 0

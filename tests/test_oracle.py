@@ -22,7 +22,7 @@ from tests.helpers import rel_l2
 from zlm_amd import synth
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")
-TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K]
+TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q6_K, synth.Q4_1, synth.F32, synth.F16, synth.BF16]
 
 
 def f16b(v: float) -> list:
@@ -139,6 +139,18 @@ def test_dequant_closed_form_f64(qt):
         elif qt == synth.Q8_0:
             d = f32(blk[0:2].view(np.float16)[0])
             want = (blk[2:34].view(np.int8).astype(f32) * d).astype(f32)
+        elif qt == synth.Q4_1:
+            # standard.zig:138-148: q*d + m, the product and the sum rounded
+            d = f32(blk[0:2].view(np.float16)[0])
+            m = f32(blk[2:4].view(np.float16)[0])
+            q = np.concatenate([blk[4:20] & 15, blk[4:20] >> 4]).astype(f32)
+            want = ((q * d).astype(f32) + m).astype(f32)
+        elif qt == synth.F32:
+            want = blk.view(np.float32).copy()
+        elif qt == synth.F16:
+            want = blk.view(np.float16).astype(f32)
+        elif qt == synth.BF16:
+            want = (blk.view(np.uint16).astype(np.uint32) << 16).view(f32)
         elif qt == synth.Q4_K:
             d = f32(blk[0:2].view(np.float16)[0])
             dm = f32(blk[2:4].view(np.float16)[0])
@@ -255,7 +267,7 @@ def test_quantizer_invariants():
     np.testing.assert_array_equal(sums, qb.sum(axis=1))
 
 
-@pytest.mark.parametrize("qt", [synth.Q4_0, synth.Q8_0, synth.Q4_K])
+@pytest.mark.parametrize("qt", [synth.Q4_0, synth.Q8_0, synth.Q4_K, synth.Q4_1])
 def test_int_path_exact_reconstruction_and_fp_bound(qt):
     rows, k = 64, 1024
     w = synth.weights(qt, rows, k, seed=12)

@@ -4,9 +4,12 @@
 // Weight layouts in HBM (produced once by the repack kernels from the raw GGUF
 // blocks of reference src/kernels/linear/quant/types.zig:6-53):
 //   q4_0  payload [rows][nb][16 B nibbles]        + scales [rows][nb] f16
+//   q4_1  payload [rows][nb][16 B nibbles]        + scales [rows][nb] (f16 d, f16 m)
 //   q8_0  payload [rows][nb][32 B int8]           + scales [rows][nb] f16
 //   q6_k  payload [rows][nb][208 B ql|qh|sc]      + scales [rows][nb] f16
 //   q4_k  raw     [rows][nb][144 B]  (already a multiple of 16 B per block)
+//   f32 / f16 / bf16  raw [rows][k] (k a multiple of 32, so rows stay 16-byte
+//         aligned; the kernels count nb = k/32 "blocks" of 32 elements)
 // Every payload block is a whole number of 16-byte chunks, so the GEMV
 // streams it with 128-bit loads; a wavefront's 64 lanes read 1 KiB of
 // consecutive payload per load instruction.
@@ -35,7 +38,10 @@ namespace {
 
 constexpr int kWave = 64;
 
-enum QType : int { Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14 };
+// GGML type codes (reference gguf/format.zig:41-77).
+enum QType : int { F32 = 0, F16 = 1, Q4_0 = 2, Q4_1 = 3, Q8_0 = 8, Q4_K = 12, Q6_K = 14, BF16 = 30 };
+
+constexpr bool is_float_type(int qt) { return qt == F32 || qt == F16 || qt == BF16; }
 
 __device__ __forceinline__ float h2f(uint32_t bits) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
@@ -182,6 +188,12 @@ __device__ __forceinline__ uint2 ld8(const uint8_t* p) {
 }
 
 template <bool NT>
+__device__ __forceinline__ uint32_t ld4(const uint32_t* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+
+template <bool NT>
 __device__ __forceinline__ uint32_t ld2(const uint16_t* p) {
     if constexpr (NT) return __builtin_nontemporal_load(p);
     else return *p;
@@ -201,6 +213,23 @@ struct Frag<Q8_0, RT> {
     uint32_t d[RT];
 };
 template <int RT>
+struct Frag<Q4_1, RT> {
+    uint4 q[RT];
+    uint32_t dm[RT];  // f16 d (low half), f16 m (high half)
+};
+template <int RT>
+struct Frag<F32, RT> {
+    uint4 q[RT];
+};
+template <int RT>
+struct Frag<F16, RT> {
+    uint4 q[RT];
+};
+template <int RT>
+struct Frag<BF16, RT> {
+    uint4 q[RT];
+};
+template <int RT>
 struct Frag<Q4_K, RT> {
     uint4 hd[RT];
     uint4 q[RT];
@@ -213,9 +242,10 @@ struct Frag<Q6_K, RT> {
     uint32_t d[RT];
 };
 
-// q4_0: chunk c = block c (16 nibble bytes).  q8_0: chunk c = half block c
-// (16 int8; block c/2 holds the scale).  q4_k / q6_k: 8 chunks per 256-element
-// super-block (c>>3), see the compute steps.
+// q4_0 / q4_1: chunk c = block c (16 nibble bytes).  q8_0: chunk c = half
+// block c (16 int8; block c/2 holds the scale).  q4_k / q6_k: 8 chunks per
+// 256-element super-block (c>>3), see the compute steps.  f32: chunk c =
+// elements 4c..4c+3; f16 / bf16: elements 8c..8c+7.
 // The rows a wave tile covers: for each of its RT fragment rows, the matrix
 // (payload and scales) and the row index.  A plain tile is RT consecutive rows
 // of one matrix; a pair tile (fused gate_up) is RT/2 rows of the gate matrix
@@ -238,6 +268,14 @@ __device__ __forceinline__ void load_frag(Frag<QT, RT>& f, const TileRows<RT>& t
             const size_t bi = row * nb + c;
             f.q[r] = ld16<NT>(w + bi * 16);
             f.d[r] = ld2<NT>(dsc + bi);
+        } else if constexpr (QT == Q4_1) {
+            const size_t bi = row * nb + c;
+            f.q[r] = ld16<NT>(w + bi * 16);
+            f.dm[r] = ld4<NT>(reinterpret_cast<const uint32_t*>(dsc) + bi);
+        } else if constexpr (QT == F32) {
+            f.q[r] = ld16<NT>(w + (row * (8 * static_cast<size_t>(nb)) + c) * 16);
+        } else if constexpr (QT == F16 || QT == BF16) {
+            f.q[r] = ld16<NT>(w + (row * (4 * static_cast<size_t>(nb)) + c) * 16);
         } else if constexpr (QT == Q8_0) {
             f.q[r] = ld16<NT>(w + (row * (2 * nb) + c) * 16);
             f.d[r] = ld2<NT>(dsc + row * nb + (c >> 1));
@@ -287,6 +325,90 @@ __device__ __forceinline__ void compute_q4_0(const Frag<Q4_0, RT>& f, const floa
     }
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, fmaf(-8.0f, xsum, s[r]), acc[r]);
+}
+
+// Byte j of a q4_1 block holds element j (low nibble) and j+16 (high); value
+// nib*d + m, and Sum (nib*d + m)*x = d*Sum nib*x + m*Sum x (the reference's
+// fpBlock splits it the same way: quantized.zig:71-77).
+template <int RT>
+__device__ __forceinline__ void compute_q4_1(const Frag<Q4_1, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    const float* xb = xl + xpad(c << 5);
+    const float xsum = xs[2 * c] + xs[2 * c + 1];
+    float s[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) s[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = lds4(xb + 4 * i);
+        const float4 xh = lds4(xb + 16 + 4 * i);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint32_t wv = (&f.q[r].x)[i];
+            const uint32_t lo = wv & 0x0F0F0F0Fu, hi = (wv >> 4) & 0x0F0F0F0Fu;
+            s[r] = fmaf(ub(lo, 0), xa.x, s[r]);
+            s[r] = fmaf(ub(lo, 1), xa.y, s[r]);
+            s[r] = fmaf(ub(lo, 2), xa.z, s[r]);
+            s[r] = fmaf(ub(lo, 3), xa.w, s[r]);
+            s[r] = fmaf(ub(hi, 0), xh.x, s[r]);
+            s[r] = fmaf(ub(hi, 1), xh.y, s[r]);
+            s[r] = fmaf(ub(hi, 2), xh.z, s[r]);
+            s[r] = fmaf(ub(hi, 3), xh.w, s[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const uint32_t dm = valid ? f.dm[r] : 0u;
+        acc[r] = fmaf(h2f(dm), s[r], fmaf(h2f(dm >> 16), xsum, acc[r]));
+    }
+}
+
+// Raw float rows: f32 chunk = 4 elements, f16 / bf16 chunk = 8 (bf16 is the
+// top half of an f32, reference bfloat.zig:24-34).
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+template <int QT, int RT>
+__device__ __forceinline__ void compute_float(const Frag<QT, RT>& f, const float* xl, int c, bool valid, float* acc) {
+    if constexpr (QT == F32) {
+        const float4 xa = lds4(xl + xpad(c << 2));
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            float s = __builtin_bit_cast(float, f.q[r].x) * xa.x;
+            s = fmaf(__builtin_bit_cast(float, f.q[r].y), xa.y, s);
+            s = fmaf(__builtin_bit_cast(float, f.q[r].z), xa.z, s);
+            s = fmaf(__builtin_bit_cast(float, f.q[r].w), xa.w, s);
+            acc[r] += valid ? s : 0.0f;
+        }
+    } else {
+        const float* xb = xl + xpad(c << 3);
+        const float4 xa = lds4(xb), xc = lds4(xb + 4);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint32_t w0 = f.q[r].x, w1 = f.q[r].y, w2 = f.q[r].z, w3 = f.q[r].w;
+            float s;
+            if constexpr (QT == F16) {
+                s = h2f(w0) * xa.x;
+                s = fmaf(h2f(w0 >> 16), xa.y, s);
+                s = fmaf(h2f(w1), xa.z, s);
+                s = fmaf(h2f(w1 >> 16), xa.w, s);
+                s = fmaf(h2f(w2), xc.x, s);
+                s = fmaf(h2f(w2 >> 16), xc.y, s);
+                s = fmaf(h2f(w3), xc.z, s);
+                s = fmaf(h2f(w3 >> 16), xc.w, s);
+            } else {
+                s = bf16lo(w0) * xa.x;
+                s = fmaf(bf16hi(w0), xa.y, s);
+                s = fmaf(bf16lo(w1), xa.z, s);
+                s = fmaf(bf16hi(w1), xa.w, s);
+                s = fmaf(bf16lo(w2), xc.x, s);
+                s = fmaf(bf16hi(w2), xc.y, s);
+                s = fmaf(bf16lo(w3), xc.z, s);
+                s = fmaf(bf16hi(w3), xc.w, s);
+            }
+            acc[r] += valid ? s : 0.0f;
+        }
+    }
 }
 
 template <int RT>
@@ -425,6 +547,8 @@ template <int QT, int RT>
 __device__ __forceinline__ void compute_frag(const Frag<QT, RT>& f, const float* xl, const float* xs, int c,
                                              bool valid, float* acc) {
     if constexpr (QT == Q4_0) compute_q4_0<RT>(f, xl, xs, c, valid, acc);
+    if constexpr (QT == Q4_1) compute_q4_1<RT>(f, xl, xs, c, valid, acc);
+    if constexpr (is_float_type(QT)) compute_float<QT, RT>(f, xl, c, valid, acc);
     if constexpr (QT == Q8_0) compute_q8_0<RT>(f, xl, xs, c, valid, acc);
     if constexpr (QT == Q4_K) compute_q4_k<RT>(f, xl, xs, c, valid, acc);
     if constexpr (QT == Q6_K) compute_q6_k<RT>(f, xl, xs, c, valid, acc);
@@ -576,12 +700,15 @@ __device__ __forceinline__ void reduce_store_all(float* v, const GemvArgs& a, ui
 
 template <int QT>
 __device__ __forceinline__ int chunks_per_row(uint32_t nb) {
-    return (QT == Q4_0) ? static_cast<int>(nb) : (QT == Q8_0) ? static_cast<int>(2 * nb) : static_cast<int>(8 * nb);
+    if constexpr (QT == Q4_0 || QT == Q4_1) return static_cast<int>(nb);
+    if constexpr (QT == Q8_0) return static_cast<int>(2 * nb);
+    if constexpr (QT == F16 || QT == BF16) return static_cast<int>(4 * nb);
+    return static_cast<int>(8 * nb);  // q4_k, q6_k, f32
 }
 
 template <int QT>
 __device__ __forceinline__ int elems_per_block() {
-    return (QT == Q4_0 || QT == Q8_0) ? 32 : 256;
+    return (QT == Q4_K || QT == Q6_K) ? 256 : 32;
 }
 
 // Issue the loads of chunk group `cb` (chunks cb + lane + 64*s, s < STEPS) of
@@ -812,4 +939,45 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
     ZLM_GEMVX_FORMS(QN, QT, 8192, 6, true, s6)        \
     ZLM_GEMVX_FORMS(QN, QT, 8192, 8, true, s8)        \
     ZLM_GEMVX_FORMS(QN, QT, 16384, 12, true, s12)     \
+    ZLM_GEMVX_FORMS(QN, QT, 32768, 8, false, g)
+
+// f16 / bf16 (8 elements per 16-byte chunk): KCAP = 512 * STEPS rounded up to
+// a tier.
+#define ZLM_GEMV_F16(QN, QT)                                        \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s1, QT, 4096, 1, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s1, QT, 4096, 2, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s1, QT, 4096, 4, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s2, QT, 4096, 1, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s2, QT, 4096, 2, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r4_s2, QT, 4096, 4, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s4, QT, 4096, 1, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s4, QT, 4096, 2, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s6, QT, 4096, 1, 6, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s8, QT, 4096, 1, 8, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s8, QT, 4096, 2, 8, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s12, QT, 8192, 1, 12, true)         \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s16, QT, 8192, 1, 16, true)         \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_g, QT, 32768, 1, 8, false)
+#define ZLM_GEMVX_F16(QN, QT)                         \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 2, true, s2)        \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 4, true, s4)        \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 8, true, s8)        \
+    ZLM_GEMVX_FORMS(QN, QT, 32768, 8, false, g)
+
+// f32 (4 elements per chunk): KCAP = 256 * STEPS rounded up to a tier.
+#define ZLM_GEMV_F32(QN, QT)                                        \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s1, QT, 4096, 1, 1, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s2, QT, 4096, 1, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s2, QT, 4096, 2, 2, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s4, QT, 4096, 1, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s4, QT, 4096, 2, 4, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s8, QT, 4096, 1, 8, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r2_s8, QT, 4096, 2, 8, true)           \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s12, QT, 4096, 1, 12, true)         \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_s16, QT, 4096, 1, 16, true)         \
+    ZLM_GEMV(zlm_gemv_##QN##_r1_g, QT, 32768, 1, 8, false)
+#define ZLM_GEMVX_F32(QN, QT)                         \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 4, true, s4)        \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 8, true, s8)        \
+    ZLM_GEMVX_FORMS(QN, QT, 4096, 16, true, s16)      \
     ZLM_GEMVX_FORMS(QN, QT, 32768, 8, false, g)

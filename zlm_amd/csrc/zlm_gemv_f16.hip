@@ -1,0 +1,7 @@
+// zlm_gemv_f16.hip -- the f16 GEMV entry points (plain and fused forms),
+// built as their own gfx950 code object so the instance files compile in
+// parallel.
+#include "gemv_impl.h"
+
+ZLM_GEMV_F16(f16, F16)
+ZLM_GEMVX_F16(f16, F16)

@@ -1,0 +1,7 @@
+// zlm_gemv_q4_1.hip -- the q4_1 GEMV entry points (plain and fused forms),
+// built as their own gfx950 code object so the instance files compile in
+// parallel.
+#include "gemv_impl.h"
+
+ZLM_GEMV_Q4_COMMON(q4_1, Q4_1)
+ZLM_GEMVX_Q4(q4_1, Q4_1)

@@ -37,23 +37,33 @@ namespace {
 constexpr int kRing = ZLM_RING_SIZE;
 constexpr uint32_t kNoLayout = 0xffffffffu;
 
-// Supported GEMV quants and their GGUF block geometry.
+// Supported GEMV quants and their GGUF block geometry (the contract's
+// blockElems/blockBytes, reference gpu/backend/root.zig:198-220: the float
+// types count one element per block).
 struct QuantInfo {
     uint32_t type;
     uint32_t block_elems;
     uint32_t block_bytes;
-    uint32_t payload_bytes;  // bytes per block in the device layout (scale split out)
-    uint32_t scale_offset;   // offset of the f16 scale inside the raw block, or kNoLayout
+    uint32_t payload_bytes;  // bytes per block in the device layout (scales split out)
+    uint32_t scale_offset;   // offset of the f16 scales inside the raw block, or kNoLayout (raw layout)
     int slot;                // index into the kernel tables
+    uint32_t scale_count;    // f16 scales per block in the split layout (q4_1: d and m)
+    uint32_t chunk_elems;    // elements per 16-byte payload chunk of a row (the GEMV's unit)
+    uint32_t kblock;         // elements per kernel block: the kernels take nb = k / kblock
 };
 
 const QuantInfo kQuants[] = {
-    {ZLM_GGML_Q4_0, 32, 18, 16, 0, 0},
-    {ZLM_GGML_Q8_0, 32, 34, 32, 0, 1},
-    {ZLM_GGML_Q4_K, 256, 144, 144, kNoLayout, 2},
-    {ZLM_GGML_Q6_K, 256, 210, 208, 208, 3},
+    {ZLM_GGML_Q4_0, 32, 18, 16, 0, 0, 1, 32, 32},
+    {ZLM_GGML_Q8_0, 32, 34, 32, 0, 1, 1, 16, 32},
+    {ZLM_GGML_Q4_K, 256, 144, 144, kNoLayout, 2, 0, 32, 256},
+    {ZLM_GGML_Q6_K, 256, 210, 208, 208, 3, 1, 32, 256},
+    {ZLM_GGML_Q4_1, 32, 20, 16, 0, 4, 2, 32, 32},
+    {ZLM_GGML_F32, 1, 4, 4, kNoLayout, 5, 0, 4, 32},
+    {ZLM_GGML_F16, 1, 2, 2, kNoLayout, 6, 0, 8, 32},
+    {ZLM_GGML_BF16, 1, 2, 2, kNoLayout, 7, 0, 8, 32},
 };
-const char* const kQuantNames[] = {"q4_0", "q8_0", "q4_k", "q6_k"};
+constexpr int kNumQuants = 8;
+const char* const kQuantNames[kNumQuants] = {"q4_0", "q8_0", "q4_k", "q6_k", "q4_1", "f32", "f16", "bf16"};
 
 const QuantInfo* quant_info(uint32_t quant) {
     const uint32_t t = quant & 0xffu;
@@ -135,10 +145,10 @@ struct zlm_device {
     std::string err;
 
     hipModule_t mod = nullptr;          // zlm_kernels_gfx950.hsaco
-    hipModule_t gemv_mod[4] = {};       // zlm_gemv_<quant>_gfx950.hsaco, by QuantInfo::slot
+    hipModule_t gemv_mod[kNumQuants] = {};  // zlm_gemv_<quant>_gfx950.hsaco, by QuantInfo::slot
     std::map<std::string, GemvKernel> gemv;  // by entry-point name; null fn = absent
     hipFunction_t repack = nullptr;
-    hipFunction_t dequant[4] = {};
+    hipFunction_t dequant[kNumQuants] = {};
     hipFunction_t quantize_q8 = nullptr;
     hipFunction_t quantize_q8_tiled = nullptr;
     hipFunction_t tile_q4_0 = nullptr;
@@ -237,11 +247,11 @@ bool load_kernels(zlm_device* d) {
     const std::string path = env ? std::string(env) : dir + "/zlm_kernels_gfx950.hsaco";
     if (!ok(d, hipModuleLoad(&d->mod, path.c_str()), path.c_str())) return false;
     char nm[128];
-    for (int q = 0; q < 4; q++) {
+    for (int q = 0; q < kNumQuants; q++) {
         const std::string gp = dir + "/zlm_gemv_" + kQuantNames[q] + "_gfx950.hsaco";
         if (!ok(d, hipModuleLoad(&d->gemv_mod[q], gp.c_str()), gp.c_str())) return false;
     }
-    for (int q = 0; q < 4; q++) {
+    for (int q = 0; q < kNumQuants; q++) {
         snprintf(nm, sizeof nm, "zlm_dequant_%s", kQuantNames[q]);
         if (!ok(d, hipModuleGetFunction(&d->dequant[q], d->mod, nm), nm)) return false;
     }
@@ -307,7 +317,7 @@ bool launch(zlm_device* d, hipFunction_t f, unsigned grid, unsigned block, void*
 // Bytes of the device layout of `nblk` blocks: payload rounded to 256 B, then scales.
 uint64_t layout_bytes(const QuantInfo* qi, uint64_t nblk) {
     const uint64_t p = (nblk * qi->payload_bytes + 255) & ~static_cast<uint64_t>(255);
-    return p + nblk * 2 + 256;
+    return p + nblk * 2 * qi->scale_count + 256;
 }
 
 // Enqueue the raw -> device-layout conversion of `nblk` blocks into `dst`.
@@ -317,9 +327,9 @@ bool convert_blocks(zlm_device* d, const uint8_t* raw, uint64_t nblk, const Quan
     uint16_t* scales = reinterpret_cast<uint16_t*>(dst + p);
     *scales_out = scales;
     if (nblk == 0) return true;
-    uint32_t bb = qi->block_bytes, so = qi->scale_offset;
+    uint32_t bb = qi->block_bytes, so = qi->scale_offset, ns = qi->scale_count;
     uint64_t n = nblk;
-    void* args[] = {&raw, &dst, &scales, &n, &bb, &so};
+    void* args[] = {&raw, &dst, &scales, &n, &bb, &so, &ns};
     return launch(d, d->repack, static_cast<unsigned>((nblk + 255) / 256), 256, args, "repack");
 }
 
@@ -380,10 +390,11 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
 
 // The GEMV kernel for a shape: the instance whose step count equals
 // ceil(chunks per row / 64) with the requested row tile, else with a 1-row
-// tile, else the generic bounded instance.  Chunks per row: k/16 for q8_0,
-// k/32 for q4_0 and the K-quants.
+// tile, else the generic bounded instance.  Chunks per row: k / chunk_elems
+// (k/16 for q8_0, k/32 for q4_0, q4_1 and the K-quants, k/8 for f16 / bf16,
+// k/4 for f32).
 const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt) {
-    const size_t chunks = (qi->type == ZLM_GGML_Q8_0) ? k / 16 : k / 32;
+    const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
@@ -399,7 +410,8 @@ const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt
 // device layout exists.
 bool check_resident(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t rows, size_t k) {
     if (!r) return fail(d, "null resident");
-    if (rows == 0 || k == 0 || k % qi->block_elems != 0) return fail(d, "bad shape rows=%zu k=%zu", rows, k);
+    if (rows == 0 || k == 0 || k % qi->block_elems != 0 || k % qi->kblock != 0)
+        return fail(d, "bad shape rows=%zu k=%zu", rows, k);
     if (rows > 0xffffffffu) return fail(d, "rows too large");
     if (k > kMaxK) return fail(d, "k=%zu exceeds the LDS-staged activation capacity", k);
     const uint64_t nb = k / qi->block_elems;
@@ -410,9 +422,9 @@ bool check_resident(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t 
 }
 
 // Grid of a GEMV launch: one wave per tile up to a per-CU cap.  Measured on
-// gfx950: up to 4 steps per row (k <= 4096 for q8_0, 8192 for the others) a
-// grid of 4 workgroups per CU is best; wider rows stage a larger x in LDS and
-// one workgroup per CU looping over tiles is best.  Tall launches (>= 64K row
+// gfx950: rows up to k = 4096 for q8_0, 8192 for the others (the float types
+// follow the same x-size rule) run best at 4 workgroups per CU; wider rows
+// stage a larger x in LDS and one workgroup per CU looping over tiles is best.  Tall launches (>= 64K row
 // tiles, the lm_heads) with a 4096-float x capacity (19 KB of LDS) run 8
 // workgroups per CU: 262144 x 3840 q6_k 222 -> 190 us.  steps 0 = the generic
 // instance (32768-float x capacity, one workgroup per CU).
@@ -421,8 +433,10 @@ unsigned gemv_grid(const zlm_device* d, const QuantInfo* qi, uint64_t tiles, con
     const uint64_t waves = static_cast<uint64_t>(gk->threads / 64);
     const uint64_t wgs = (tiles + waves - 1) / waves;
     const int steps = gk->steps;
-    const bool small_x = steps > 0 && steps <= (qi->type == ZLM_GGML_Q8_0 ? 4 : 2);
-    uint64_t cap = static_cast<uint64_t>(d->cus) * ((steps == 0 || steps > 4) ? 1 : (small_x && tiles >= 65536) ? 8 : 4);
+    const uint64_t xk = static_cast<uint64_t>(steps) * 64 * qi->chunk_elems;  // elements of x a row covers
+    const bool small_x = steps > 0 && xk <= 4096;
+    const bool wide = steps == 0 || xk > (qi->type == ZLM_GGML_Q8_0 ? 4096u : 8192u);
+    uint64_t cap = static_cast<uint64_t>(d->cus) * (wide ? 1 : (small_x && tiles >= 65536) ? 8 : 4);
     if (gk->waves_per_cu > 0)
         cap = std::max<uint64_t>(1, static_cast<uint64_t>(d->cus) * static_cast<uint64_t>(gk->waves_per_cu) / waves);
     return static_cast<unsigned>(std::min<uint64_t>(wgs, cap));
@@ -451,7 +465,7 @@ bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     const QuantInfo* qi = quant_info(quant);
     const uint8_t* w = r->payload;
     const uint16_t* s = r->scales;
-    uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->block_elems);
+    uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->kblock);
     void* args[] = {&w, &s, &x_dev, &y_dev, &rows32, &nb};
     return launch(d, f, grid, block, args, "gemv");
 }
@@ -484,7 +498,7 @@ static_assert(sizeof(GemvArgsHost) == 80, "GemvArgs layout");
 // The fused-form kernel for a shape: the prefetching exact-steps instance if
 // the quant has one, else the exact-steps instance, else the generic one.
 const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form) {
-    const size_t chunks = (qi->type == ZLM_GGML_Q8_0) ? k / 16 : k / 32;
+    const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const int rt = form_is_pair(form) ? 2 : 1;
     const char* qn = kQuantNames[qi->slot];
@@ -526,7 +540,7 @@ bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     a.y = op.y;
     a.res = op.form == ZLM_FORM_RESID ? op.res : op.y;
     a.rows = static_cast<uint32_t>(op.rows);
-    a.nb = static_cast<uint32_t>(op.k / qi->block_elems);
+    a.nb = static_cast<uint32_t>(op.k / qi->kblock);
     a.eps = op.eps;
     a.act = op.act;
     void* args[] = {&a};
@@ -726,7 +740,7 @@ extern "C" zlm_device* zlm_gpu_init(void) {
         return d;
     }
     d->cus = props.multiProcessorCount;
-    snprintf(d->name, sizeof d->name, "%s (%s)", props.name, props.gcnArchName);
+    snprintf(d->name, sizeof d->name, "%.200s (%.40s)", props.name, props.gcnArchName);
     if (hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking) != hipSuccess) {
         fail(d, "hipStreamCreate failed");
         snprintf(d->name, sizeof d->name, "off");

@@ -7,21 +7,23 @@
 
 
 // ---- repack: raw GGUF blocks -> aligned payload + separate f16 scales -----
-// One thread per block; `bb` raw block bytes, the scale at `soff` within the
-// raw block, the payload is the remaining bytes in order.
+// One thread per block; `bb` raw block bytes, `ns` f16 scales (1, or 2 for
+// q4_1's d and m) at `soff` within the raw block; the payload is the remaining
+// bytes in order, the scales go to dsc[b*ns ..].
 
 extern "C" __global__ void __launch_bounds__(256)
     zlm_repack_split(const uint8_t* __restrict__ raw, uint8_t* __restrict__ payload, uint16_t* __restrict__ dsc,
-                     uint64_t nblocks, uint32_t bb, uint32_t soff) {
+                     uint64_t nblocks, uint32_t bb, uint32_t soff, uint32_t ns) {
     const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
     const uint8_t* src = raw + b * bb;
-    const uint32_t pb = bb - 2;
-    uint8_t* dst = payload + b * pb;
-    dsc[b] = static_cast<uint16_t>(src[soff] | (static_cast<uint16_t>(src[soff + 1]) << 8));
+    const uint32_t send = soff + 2 * ns;
+    uint8_t* dst = payload + b * (bb - 2 * ns);
+    for (uint32_t i = 0; i < ns; i++)
+        dsc[b * ns + i] = static_cast<uint16_t>(src[soff + 2 * i] | (static_cast<uint16_t>(src[soff + 2 * i + 1]) << 8));
     uint32_t o = 0;
     for (uint32_t i = 0; i < bb; i++) {
-        if (i == soff || i == soff + 1) continue;
+        if (i >= soff && i < send) continue;
         dst[o++] = src[i];
     }
 }
@@ -43,6 +45,45 @@ extern "C" __global__ void __launch_bounds__(256)
         o[j] = static_cast<float>(static_cast<int>(q[j] & 15) - 8) * d;
         o[16 + j] = static_cast<float>(static_cast<int>(q[j] >> 4) - 8) * d;
     }
+}
+
+// standard.dequantQ4_1Block (reference quant/standard.zig:138-148): q*d + m,
+// the product and the sum rounded separately.
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_dequant_q4_1(const uint8_t* __restrict__ w, const uint16_t* __restrict__ dsc, float* __restrict__ out,
+                     uint64_t nblocks) {
+    const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint8_t* q = w + b * 16;
+    const float d = h2f(dsc[2 * b]), m = h2f(dsc[2 * b + 1]);
+    float* o = out + b * 32;
+    for (int j = 0; j < 16; j++) {
+        o[j] = static_cast<float>(q[j] & 15) * d + m;
+        o[16 + j] = static_cast<float>(q[j] >> 4) * d + m;
+    }
+}
+
+// The float types, one element per "block" (reference quant/floats.zig):
+// f32 as is, f16 widened exactly, bf16 as the top half of an f32.
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_dequant_f32(const uint8_t* __restrict__ w, const uint16_t* __restrict__, float* __restrict__ out,
+                    uint64_t n) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = reinterpret_cast<const float*>(w)[i];
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_dequant_f16(const uint8_t* __restrict__ w, const uint16_t* __restrict__, float* __restrict__ out,
+                    uint64_t n) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = h2f(reinterpret_cast<const uint16_t*>(w)[i]);
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_dequant_bf16(const uint8_t* __restrict__ w, const uint16_t* __restrict__, float* __restrict__ out,
+                     uint64_t n) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = __builtin_bit_cast(float, static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(w)[i]) << 16);
 }
 
 extern "C" __global__ void __launch_bounds__(256)

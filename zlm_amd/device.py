@@ -26,7 +26,7 @@ LIB_PATH = os.path.join(LIB_DIR, "libzlm_gpu_hip.so")
 CODE_OBJECT_PATH = os.path.join(LIB_DIR, "zlm_kernels_gfx950.hsaco")
 # Every code object the library loads: the common kernels and one GEMV object per quant.
 CODE_OBJECT_PATHS = [CODE_OBJECT_PATH] + [os.path.join(LIB_DIR, f"zlm_gemv_{q}_gfx950.hsaco")
-                                          for q in ("q4_0", "q8_0", "q4_k", "q6_k")]
+                                          for q in ("q4_0", "q8_0", "q4_k", "q6_k", "q4_1", "f32", "f16", "bf16")]
 
 RING_SIZE = 8
 NULL_HANDLE = -1

@@ -13,6 +13,8 @@ Distributions follow the benchmark configurations:
   * Q4_K: ``d``, ``dmin`` = ``f16(|N(0,1)| * 0.02)``; 12 scale bytes and 128
     quant bytes uniform.
   * Q6_K: ``ql``, ``qh`` and ``sc`` uniform bytes, ``d = f16(|N(0,1)| * 0.02)``.
+  * F32 / F16 / BF16: elements ``N(0,1) * 0.02`` rounded to the type
+    (round-to-nearest-even).
   * activations: fp32 N(0, 1).
 
 The raw byte layout is GGUF's (block formats as in the reference's
@@ -28,10 +30,11 @@ _M2 = np.uint64(0x94D049BB133111EB)
 _STREAM = np.uint64(0xD1B54A32D192ED03)
 
 # GGML type codes (reference gguf/format.zig:41-77).
-Q4_0, Q4_1, Q8_0, Q4_K, Q6_K = 2, 3, 8, 12, 14
-BLOCK_ELEMS = {Q4_0: 32, Q4_1: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q4_0: 18, Q4_1: 20, Q8_0: 34, Q4_K: 144, Q6_K: 210}
-TYPE_NAMES = {Q4_0: "q4_0", Q4_1: "q4_1", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 14, 30
+BLOCK_ELEMS = {Q4_0: 32, Q4_1: 32, Q8_0: 32, Q4_K: 256, Q6_K: 256, F32: 1, F16: 1, BF16: 1}
+BLOCK_BYTES = {Q4_0: 18, Q4_1: 20, Q8_0: 34, Q4_K: 144, Q6_K: 210, F32: 4, F16: 2, BF16: 2}
+TYPE_NAMES = {Q4_0: "q4_0", Q4_1: "q4_1", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k", F32: "f32", F16: "f16",
+              BF16: "bf16"}
 
 
 def _mix(z: np.ndarray) -> np.ndarray:
@@ -83,6 +86,13 @@ def _f16_bytes(v: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(v.astype(np.float16)).view(np.uint8).reshape(-1, 2)
 
 
+def _bf16_bytes(v: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16, round to nearest even (finite inputs)."""
+    b = np.ascontiguousarray(v.astype(np.float32)).view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    return r.view(np.uint8).reshape(-1, 2)
+
+
 def weights(qtype: int, rows: int, k: int, seed: int) -> np.ndarray:
     """Raw GGUF bytes of a ``rows x k`` weight (row-major blocks), uint8."""
     be, bb = BLOCK_ELEMS[qtype], BLOCK_BYTES[qtype]
@@ -109,6 +119,12 @@ def weights(qtype: int, rows: int, k: int, seed: int) -> np.ndarray:
     elif qtype == Q6_K:
         out[:, 0:208] = random_bytes(seed, 2, nblk * 208).reshape(nblk, 208)
         out[:, 208:210] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
+    elif qtype == F32:
+        out[:] = np.ascontiguousarray((normal(seed, 1, nblk) * 0.02).astype(np.float32)).view(np.uint8).reshape(nblk, 4)
+    elif qtype == F16:
+        out[:] = _f16_bytes(normal(seed, 1, nblk) * 0.02)
+    elif qtype == BF16:
+        out[:] = _bf16_bytes(normal(seed, 1, nblk) * 0.02)
     else:
         raise ValueError(f"unsupported type {qtype}")
     return out.reshape(-1)
