@@ -21,8 +21,8 @@
  * 8..15.  A variant never changes the byte layout, only the kernel.
  *
  * Device kernels: GEMVs (every form) for q4_0, q4_1, q8_0, q4_k, q6_k, f32,
- * f16 and bf16 (the float types need k % 32 == 0), prefill GEMMs for q4_0 and
- * q8_0; any other quant or shape returns false.
+ * f16 and bf16 (the float types need k % 32 == 0), prefill GEMMs for q4_0,
+ * q8_0, q4_1 and q4_k; any other quant or shape returns false.
  *
  * Weight bytes are always the raw GGUF blocks (row-major, `rows` rows of
  * `k / block_elems` blocks).  The device keeps its own layout in HBM.
@@ -211,7 +211,8 @@ bool zlm_gpu_dev_copy_enqueue(zlm_device *dev, void *dst, const void *src, size_
 bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
                              const float *x_dev, float *y_dev);
 /* Enqueue the prefill GEMM out_dev[t*rows + r] (x_dev: m x k fp32, token-major):
- * the q8 activation quantizer, then the int8-MFMA GEMM.  Q4_0 and Q8_0 weights. */
+ * the q8 activation quantizer, then the int8-MFMA GEMM.  Q4_0, Q8_0, Q4_1 and
+ * Q4_K weights. */
 bool zlm_gpu_mat_mul_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k, size_t m,
                              const float *x_dev, float *out_dev);
 /* Enqueue `iters` prefill GEMMs (quantizer + GEMM each), rotating over `n_res`

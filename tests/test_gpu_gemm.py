@@ -1,8 +1,8 @@
 """GPU parity of the prefill GEMM (q8 activations, int8 MFMA) through the C ABI.
 
 The oracle is zlm's int path (reference matvec/kernels/quantized.zig:49-55 for
-Q4_0, :149-156 for Q8_0, over the activation quantizer of
-matvec/layout.zig:458-476) applied per token:
+Q4_0, :79-87 for Q4_1, :111-123 for Q4_K, :149-156 for Q8_0, over the
+activation quantizer of matvec/layout.zig:458-476) applied per token:
 relative L2 <= 1e-3 (the block dots are exact integers; only fp32 scaling and
 summation order differ).  Against the fp32 GEMM the reference's own int-vs-fp
 bound applies, |int - fp| <= 0.02 * sum|w*x| (kernels/quantized_test.zig:61).
@@ -27,10 +27,10 @@ def _say(msg):
 
 SHAPES = [(64, 256, 4), (100, 512, 37), (64, 1024, 64), (130, 4096, 70), (48, 16384, 3), (70, 4096, 129),
           (64, 4096, 1)]
-GEMM_QUANTS = [(synth.Q4_0, zd.Q4_0), (synth.Q8_0, zd.Q8_0)]
+GEMM_QUANTS = [(synth.Q4_0, zd.Q4_0), (synth.Q8_0, zd.Q8_0), (synth.Q4_1, zd.Q4_1), (synth.Q4_K, zd.Q4_K)]
 
 
-@pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0"])
+@pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0", "q4_1", "q4_k"])
 @pytest.mark.parametrize("rows,k,m", SHAPES)
 def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     _say(f"gemm type={qt} rows={rows} k={k} m={m}")
@@ -76,10 +76,28 @@ def test_gemm_unsupported_quants_fall_back(dev):
     rows, k, m = 32, 256, 4
     x = synth.activation(1, m * k)
     out = np.zeros(m * rows, np.float32)
-    for qt in (synth.Q6_K, synth.Q4_K):
+    for qt in (synth.Q6_K, synth.F32, synth.F16):
         w = synth.weights(qt, rows, k, seed=2)
         assert not dev.mat_mul_batch(zd.quant(qt), w, rows, k, m, x, out)
     w = synth.weights(synth.Q4_0, rows, k, seed=2)
     assert not dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x[:-1].copy(), out)  # x length
     assert not dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x, out[:-1].copy())  # short out
     assert dev.mat_mul_batch(zd.quant(zd.Q4_0), w, rows, k, m, x, out)  # still healthy
+
+
+def test_gemm_q4_k_c3_shape_rows_subset(dev):
+    """A configs[3]-shaped Q4_K prefill (15360 x 3840, 96 tokens): row slices
+    against the int oracle."""
+    rows, k, m = 15360, 3840, 96
+    _say("gemm q4_k 15360x3840 m=96")
+    w = synth.weights(synth.Q4_K, rows, k, seed=0x5A4C4D03)
+    x = synth.activation(0x5A4C4D0C, m * k)
+    res = dev.upload_resident(w)
+    out = np.zeros(m * rows, np.float32)
+    assert dev.mat_mul_resident(res, zd.quant(zd.Q4_K), rows, k, m, x, out), dev.last_error()
+    got = out.reshape(m, rows)
+    rb = synth.row_bytes(synth.Q4_K, k)
+    for r0, r1 in ((0, 96), (7000, 7064), (15296, 15360)):
+        want = oracle.matmul_int(synth.Q4_K, w[r0 * rb:r1 * rb], k, r1 - r0, m, x)
+        assert rel_l2(got[:, r0:r1], want) <= 1e-3, (r0, r1)
+    dev.free_resident(res)

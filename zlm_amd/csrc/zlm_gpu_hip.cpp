@@ -131,7 +131,7 @@ struct zlm_resident {
     // [16 or 32 B] + scales [rows/32][nb][32]), built on the first GEMM for a
     // given nb.
     uint8_t* gemm_payload = nullptr;
-    uint16_t* gemm_scales = nullptr;
+    void* gemm_scales = nullptr;  // f16 (q4_0, q8_0) or float2 (scale, min) (q4_1, q4_k)
     uint64_t gemm_nb = 0;
     uint64_t gemm_rt = 0;  // 32-row tiles
     zlm_device* owner = nullptr;
@@ -153,6 +153,10 @@ struct zlm_device {
     hipFunction_t quantize_q8_tiled = nullptr;
     hipFunction_t tile_q4_0 = nullptr;
     hipFunction_t tile_q8_0 = nullptr;
+    hipFunction_t tile_q4_1 = nullptr;
+    hipFunction_t tile_q4_k = nullptr;
+    hipFunction_t gemm_q4_1 = nullptr;
+    hipFunction_t gemm_q4_k = nullptr;
     hipFunction_t copy16 = nullptr;
     hipFunction_t gemm_q4_0 = nullptr;
     hipFunction_t gemm_q8_0 = nullptr;
@@ -264,6 +268,10 @@ bool load_kernels(zlm_device* d) {
     if (!ok(d, hipModuleGetFunction(&d->gemm_q4_0, d->mod, "zlm_gemm_q4_0_q8"), "zlm_gemm_q4_0_q8")) return false;
     if (!ok(d, hipModuleGetFunction(&d->tile_q8_0, d->mod, "zlm_tile_q8_0"), "zlm_tile_q8_0")) return false;
     if (!ok(d, hipModuleGetFunction(&d->gemm_q8_0, d->mod, "zlm_gemm_q8_0_q8"), "zlm_gemm_q8_0_q8")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->tile_q4_1, d->mod, "zlm_tile_q4_1"), "zlm_tile_q4_1")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->tile_q4_k, d->mod, "zlm_tile_q4_k"), "zlm_tile_q4_k")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->gemm_q4_1, d->mod, "zlm_gemm_q4_1_q8"), "zlm_gemm_q4_1_q8")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->gemm_q4_k, d->mod, "zlm_gemm_q4_k_q8"), "zlm_gemm_q4_k_q8")) return false;
     const struct {
         hipFunction_t* f;
         const char* name;
@@ -633,10 +641,20 @@ double now_ns() {
     return static_cast<double>(ts.tv_sec) * 1e9 + static_cast<double>(ts.tv_nsec);
 }
 
-// Build (once per row length) the GEMM's tiled copy of a resident Q4_0 or
-// Q8_0 weight from its split layout: payload [rt][nb][32 rows][16 or 32 B] and
-// scales [rt][nb][32 rows] over all whole rows the resident holds, rows padded
-// to 32.  The resident's layout type never changes, so nb keys the copy.
+// The quants with a prefill GEMM and whether their tiles carry a min term.
+bool gemm_supported(uint32_t type) {
+    return type == ZLM_GGML_Q4_0 || type == ZLM_GGML_Q8_0 || type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K;
+}
+bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K; }
+
+// Build (once per row length) the GEMM's tiled copy of a resident weight, over
+// all whole rows it holds, rows padded to 32; nb = 32-element blocks per row:
+//   q4_0 / q8_0  payload [rt][nb][32 rows][16 / 32 B] + f16 scales [rt][nb][32]
+//                (from the split layout);
+//   q4_1 / q4_k  payload [rt][nb][32 rows][16 B nibbles] + (scale, min) float2
+//                [rt][nb][32] (q4_1 from its split layout, q4_k from its raw
+//                super-blocks).
+// The resident's layout type never changes, so nb keys the copy.
 bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint64_t nb) {
     if (r->gemm_payload && r->gemm_nb == nb) return true;
     if (r->gemm_payload) hipFree(r->gemm_payload);
@@ -644,23 +662,35 @@ bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint
     r->gemm_scales = nullptr;
     r->gemm_nb = 0;
     r->gemm_rt = 0;
-    const uint64_t rows_total = r->blocks / nb;
+    const uint64_t wblocks = nb * 32 / qi->block_elems;  // layout blocks per row
+    const uint64_t rows_total = r->blocks / wblocks;
     const uint64_t rt = (rows_total + 31) / 32;
     if (rt == 0 || rt * 32 > 0xffffffffu) return fail(d, "GEMM weight shape out of range");
-    const uint64_t pbytes = rt * nb * 32 * qi->payload_bytes;
-    const uint64_t sbytes = rt * nb * 32 * 2;
+    const bool with_min = gemm_has_min(qi->type);
+    const uint64_t pbytes = rt * nb * 32 * (qi->type == ZLM_GGML_Q8_0 ? 32 : 16);
+    const uint64_t sbytes = rt * nb * 32 * (with_min ? 8 : 2);
     uint8_t* p = nullptr;
     if (!ok(d, hipMalloc(reinterpret_cast<void**>(&p), pbytes + sbytes), "hipMalloc gemm tiles")) return false;
     uint8_t* payload = r->payload;
     uint16_t* scales = r->scales;
     uint8_t* tp = p;
-    uint16_t* ts = reinterpret_cast<uint16_t*>(p + pbytes);
+    void* ts = p + pbytes;
     uint32_t rows32 = static_cast<uint32_t>(rows_total), nb32 = static_cast<uint32_t>(nb),
              rt32 = static_cast<uint32_t>(rt);
-    void* args[] = {&payload, &scales, &tp, &ts, &rows32, &nb32, &rt32};
     const uint64_t n = rt * 32 * nb;
-    hipFunction_t tile = qi->type == ZLM_GGML_Q8_0 ? d->tile_q8_0 : d->tile_q4_0;
-    if (!launch(d, tile, static_cast<unsigned>((n + 255) / 256), 256, args, "tile weights")) {
+    const unsigned grid = static_cast<unsigned>((n + 255) / 256);
+    bool good;
+    if (qi->type == ZLM_GGML_Q4_K) {
+        void* args[] = {&payload, &tp, &ts, &rows32, &nb32, &rt32};
+        good = launch(d, d->tile_q4_k, grid, 256, args, "tile weights");
+    } else {
+        void* args[] = {&payload, &scales, &tp, &ts, &rows32, &nb32, &rt32};
+        hipFunction_t tile = qi->type == ZLM_GGML_Q8_0   ? d->tile_q8_0
+                             : qi->type == ZLM_GGML_Q4_1 ? d->tile_q4_1
+                                                         : d->tile_q4_0;
+        good = launch(d, tile, grid, 256, args, "tile weights");
+    }
+    if (!good) {
         hipFree(p);
         return false;
     }
@@ -671,47 +701,52 @@ bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint
     return true;
 }
 
-// Enqueue the prefill GEMM out_dev[t*rows + r] over a resident Q4_0 or Q8_0
-// weight and device activations x_dev (m x k, token-major): quantize x to q8
-// blocks into the tiled device scratch, then the int8-MFMA GEMM over the tiled
-// weights.
+// Enqueue the prefill GEMM out_dev[t*rows + r] over a resident Q4_0, Q8_0,
+// Q4_1 or Q4_K weight and device activations x_dev (m x k, token-major):
+// quantize x to q8 blocks into the tiled device scratch (plus dx*sum(q) for
+// the min-carrying types), then the int8-MFMA GEMM over the tiled weights.
 bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, size_t m,
                   const float* x_dev, float* out_dev) {
     if (!d || !d->avail) return fail(d, "device unavailable");
     const QuantInfo* qi = quant_info(quant);
     if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
-    if (qi->type != ZLM_GGML_Q4_0 && qi->type != ZLM_GGML_Q8_0)
-        return fail(d, "no GEMM kernel for quant %u", qi->type);
-    if (!r || rows == 0 || k == 0 || m == 0 || k % 32) return fail(d, "bad GEMM shape");
+    if (!gemm_supported(qi->type)) return fail(d, "no GEMM kernel for quant %u", qi->type);
+    if (!r || rows == 0 || k == 0 || m == 0 || k % qi->block_elems || k % 32) return fail(d, "bad GEMM shape");
     if (rows > 0x7fffffffu || m > 0x7fffffffu || k / 32 > 0xffffffu) return fail(d, "GEMM shape too large");
-    const uint64_t nb = k / 32;
-    if (r->bytes < rows * nb * qi->block_bytes) return fail(d, "resident too short");
+    const uint64_t nb = k / 32, wblocks = k / qi->block_elems;
+    if (r->bytes < rows * wblocks * qi->block_bytes) return fail(d, "resident too short");
     if (!ensure_layout(d, r, qi)) return false;
-    if (r->blocks < rows * nb) return fail(d, "resident layout too short");
+    if (r->blocks < rows * wblocks) return fail(d, "resident layout too short");
     if (!ensure_gemm_tiles(d, r, qi, nb)) return false;
     if (r->gemm_rt * 32 < rows) return fail(d, "GEMM tiles too short");
+    const bool with_min = gemm_has_min(qi->type);
     const uint64_t mt = (static_cast<uint64_t>(m) + 31) / 32;
     const uint64_t qbytes = mt * 32 * k;  // a multiple of 1024
-    const uint64_t need = qbytes + mt * 32 * nb * 4;
+    const uint64_t fbytes = mt * 32 * nb * 4;
+    const uint64_t need = qbytes + fbytes * (with_min ? 2 : 1);
     if (!ensure_bytes(d, d->q_scratch, d->q_scratch_cap, need)) return false;
     int8_t* qx = reinterpret_cast<int8_t*>(d->q_scratch);
     float* dx = reinterpret_cast<float*>(d->q_scratch + qbytes);
+    float* ds = with_min ? reinterpret_cast<float*>(d->q_scratch + qbytes + fbytes) : nullptr;
     uint32_t rows32 = static_cast<uint32_t>(rows), m32 = static_cast<uint32_t>(m), nb32 = static_cast<uint32_t>(nb),
              mt32 = static_cast<uint32_t>(mt);
     {
         const uint64_t n = mt * 32 * nb;
-        void* args[] = {const_cast<float**>(&x_dev), &qx, &dx, &m32, &nb32, &mt32};
+        void* args[] = {const_cast<float**>(&x_dev), &qx, &dx, &m32, &nb32, &mt32, &ds};
         if (!launch(d, d->quantize_q8_tiled, static_cast<unsigned>((n + 255) / 256), 256, args, "quantize tiled"))
             return false;
     }
     const uint8_t* wq = r->gemm_payload;
-    const uint16_t* wd = r->gemm_scales;
-    void* args[] = {&wq, &wd, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
-    return ok(d,
-              hipModuleLaunchKernel(qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0 : d->gemm_q4_0,
-                                    static_cast<unsigned>((rows + 63) / 64),
-                                    static_cast<unsigned>((m + 127) / 128), 1, 256, 1, 1, 0, d->stream, args, nullptr),
-              "gemm");
+    const void* ws = r->gemm_scales;
+    const unsigned gx = static_cast<unsigned>((rows + 63) / 64), gy = static_cast<unsigned>((m + 127) / 128);
+    if (with_min) {
+        void* args[] = {&wq, &ws, &qx, &dx, &ds, &out_dev, &rows32, &m32, &nb32, &mt32};
+        hipFunction_t f = qi->type == ZLM_GGML_Q4_1 ? d->gemm_q4_1 : d->gemm_q4_k;
+        return ok(d, hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d->stream, args, nullptr), "gemm");
+    }
+    void* args[] = {&wq, &ws, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
+    hipFunction_t f = qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0 : d->gemm_q4_0;
+    return ok(d, hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d->stream, args, nullptr), "gemm");
 }
 
 }  // namespace
@@ -1032,8 +1067,7 @@ extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void*
     if (!d || !d->avail) return false;
     const QuantInfo* qi = quant_info(quant);
     if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
-    if (qi->type != ZLM_GGML_Q4_0 && qi->type != ZLM_GGML_Q8_0)
-        return fail(d, "no GEMM kernel for quant %u", qi->type);
+    if (!gemm_supported(qi->type)) return fail(d, "no GEMM kernel for quant %u", qi->type);
     if (!w || rows == 0 || k == 0 || k % qi->block_elems) return fail(d, "bad shape");
     const uint64_t nblk = static_cast<uint64_t>(rows) * (k / qi->block_elems);
     const uint64_t need = nblk * qi->block_bytes;

@@ -192,17 +192,23 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 // The prefill GEMM's tiled output for m tokens of nb blocks, tokens padded to
-// mt*32: qx [mt][nb][32 tokens][32 B], dx [mt][nb][32 tokens]; padding tokens
-// are zeros.  One thread per (token, block).
+// mt*32: qx [mt][nb][32 tokens][32 B], dx [mt][nb][32 tokens] and, when `ds`
+// is not null, ds = dx * f32(sum of the block's q) in the same order (the
+// min-term factor of q4_1 / q4_k); padding tokens are zeros.  One thread per
+// (token, block).
 extern "C" __global__ void __launch_bounds__(256)
     zlm_quantize_q8_tiled(const float* __restrict__ x, int8_t* __restrict__ qx, float* __restrict__ dx,
-                          uint32_t m, uint32_t nb, uint32_t mt) {
+                          uint32_t m, uint32_t nb, uint32_t mt, float* __restrict__ ds) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<uint64_t>(mt) * 32 * nb) return;
     const uint32_t t = static_cast<uint32_t>(i / nb), b = static_cast<uint32_t>(i % nb);
     const uint64_t slot = (static_cast<uint64_t>(t / 32) * nb + b) * 32 + (t % 32);
+    float d;
+    int32_t sum;
     quantize_block(t < m ? x + (static_cast<uint64_t>(t) * nb + b) * 32 : nullptr,
-                   reinterpret_cast<uint4*>(qx + slot * 32), dx + slot, nullptr);
+                   reinterpret_cast<uint4*>(qx + slot * 32), &d, &sum);
+    dx[slot] = d;
+    if (ds) ds[slot] = d * static_cast<float>(sum);
 }
 
 // The prefill GEMM's tiled weight layout, rows padded to rt*32: payload
@@ -241,6 +247,63 @@ extern "C" __global__ void __launch_bounds__(256)
                   uint8_t* __restrict__ tpayload, uint16_t* __restrict__ tscales, uint32_t rows, uint32_t nb,
                   uint32_t rt) {
     tile_blocks<32>(payload, scales, tpayload, tscales, rows, nb, rt);
+}
+
+// The tiled layout of the min-carrying types (q4_1, q4_k): per 32-element
+// block of a row, 16 nibble bytes in q4_0 order (byte j: element j low,
+// element j+16 high) and a float2 (scale, min) such that the block's values
+// are scale * nib + min: payload [rt][nb][32 rows][16 B], sm [rt][nb][32 rows].
+// Padding rows are zeros.  One thread per (row, 32-element block).
+//
+// q4_1 (split layout, reference quant/standard.zig:138-148): the payload as
+// is, (d, m).
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_tile_q4_1(const uint8_t* __restrict__ payload, const uint16_t* __restrict__ scales,
+                  uint8_t* __restrict__ tpayload, float2* __restrict__ tsm, uint32_t rows, uint32_t nb, uint32_t rt) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<uint64_t>(rt) * 32 * nb) return;
+    const uint32_t r = static_cast<uint32_t>(i / nb), b = static_cast<uint32_t>(i % nb);
+    const uint64_t slot = (static_cast<uint64_t>(r / 32) * nb + b) * 32 + (r % 32);
+    const uint64_t src = static_cast<uint64_t>(r) * nb + b;
+    uint4 q = make_uint4(0u, 0u, 0u, 0u);
+    float2 sm = make_float2(0.0f, 0.0f);
+    if (r < rows) {
+        q = reinterpret_cast<const uint4*>(payload)[src];
+        sm = make_float2(h2f(scales[2 * src]), h2f(scales[2 * src + 1]));
+    }
+    reinterpret_cast<uint4*>(tpayload)[slot] = q;
+    tsm[slot] = sm;
+}
+
+// q4_k (raw 144-byte super-blocks, reference quant/k_quants.zig:34-72):
+// 32-element block b of a row is sub-block j = b%8 of super-block b/8, the low
+// (j even) or high (j odd) nibbles of qs[32*(j/2) .. +32]; scale = d*sc_j,
+// min = -(dmin*mn_j) (getScaleMinK4, the products of the reference's int path,
+// quantized.zig:111-123).
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_tile_q4_k(const uint8_t* __restrict__ raw, uint8_t* __restrict__ tpayload, float2* __restrict__ tsm,
+                  uint32_t rows, uint32_t nb, uint32_t rt) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<uint64_t>(rt) * 32 * nb) return;
+    const uint32_t r = static_cast<uint32_t>(i / nb), b = static_cast<uint32_t>(i % nb);
+    const uint64_t slot = (static_cast<uint64_t>(r / 32) * nb + b) * 32 + (r % 32);
+    uint32_t packed[4] = {0u, 0u, 0u, 0u};
+    float2 sm = make_float2(0.0f, 0.0f);
+    if (r < rows) {
+        const uint8_t* blk = raw + (static_cast<uint64_t>(r) * (nb / 8) + b / 8) * 144;
+        const uint32_t j = b % 8, sh = 4 * (j & 1);
+        const uint32_t* hd = reinterpret_cast<const uint32_t*>(blk);
+        float sc, mn;
+        scale_min_k4(static_cast<int>(j), hd[1], hd[2], hd[3], sc, mn);
+        sm = make_float2(h2f(hd[0]) * sc, -(h2f(hd[0] >> 16) * mn));
+        const uint8_t* qs = blk + 16 + 32 * (j / 2);
+        for (int e = 0; e < 16; e++) {
+            const uint32_t lo = (qs[e] >> sh) & 15u, hi = (qs[e + 16] >> sh) & 15u;
+            packed[e / 4] |= (lo | (hi << 4)) << (8 * (e % 4));
+        }
+    }
+    reinterpret_cast<uint4*>(tpayload)[slot] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    tsm[slot] = sm;
 }
 
 // ---- device copy (16-byte granules; the traffic-counter calibration kernel) --
@@ -282,8 +345,21 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 struct GemmBlk {
     uint4 a0, a1, w;
-    uint32_t d;
-    float x0, x1;
+    uint32_t d;      // q4_0 / q8_0: the f16 weight scale
+    float x0, x1;    // dx of the two token tiles
+    float2 sm;       // q4_1 / q4_k: (scale, min)
+    float s0, s1;    // q4_1 / q4_k: dx * sum(q) of the two token tiles
+};
+
+constexpr bool gemm_has_min(int qt) { return qt == Q4_1 || qt == Q4_K; }
+
+// Per-wave operand pointers of the GEMM (lane offsets applied).
+struct GemmPtrs {
+    const int8_t *a0, *a1;
+    const uint8_t* wr;
+    const uint16_t* dr;  // q4_0 / q8_0 scales
+    const float2* smr;   // q4_1 / q4_k (scale, min)
+    const float *x0, *x1, *s0, *s1;
 };
 
 // Depth 1 keeps the kernel at 129 VGPRs, so the 3 waves per SIMD that the
@@ -298,23 +374,34 @@ struct GemmBlk {
 constexpr int kGemmDepth = ZLM_GEMM_DEPTH;  // blocks per register set
 
 template <int QT>
-__device__ __forceinline__ void gemm_load(GemmBlk& g, const int8_t* a0, const int8_t* a1, const uint8_t* wr,
-                                          const uint16_t* dr, const float* x0, const float* x1, uint32_t b) {
+__device__ __forceinline__ void gemm_load(GemmBlk& g, const GemmPtrs& p, uint32_t b) {
     constexpr size_t kWStride = QT == Q8_0 ? 1024 : 512;  // tiled weight bytes per block
-    g.a0 = *reinterpret_cast<const uint4*>(a0 + static_cast<size_t>(b) * 1024);
-    g.a1 = *reinterpret_cast<const uint4*>(a1 + static_cast<size_t>(b) * 1024);
-    g.w = *reinterpret_cast<const uint4*>(wr + static_cast<size_t>(b) * kWStride);
-    g.d = dr[static_cast<size_t>(b) * 32];
-    g.x0 = x0[static_cast<size_t>(b) * 32];
-    g.x1 = x1[static_cast<size_t>(b) * 32];
+    g.a0 = *reinterpret_cast<const uint4*>(p.a0 + static_cast<size_t>(b) * 1024);
+    g.a1 = *reinterpret_cast<const uint4*>(p.a1 + static_cast<size_t>(b) * 1024);
+    g.w = *reinterpret_cast<const uint4*>(p.wr + static_cast<size_t>(b) * kWStride);
+    if constexpr (gemm_has_min(QT)) {
+        g.sm = p.smr[static_cast<size_t>(b) * 32];
+        g.s0 = p.s0[static_cast<size_t>(b) * 32];
+        g.s1 = p.s1[static_cast<size_t>(b) * 32];
+    } else {
+        g.d = p.dr[static_cast<size_t>(b) * 32];
+    }
+    g.x0 = p.x0[static_cast<size_t>(b) * 32];
+    g.x1 = p.x1[static_cast<size_t>(b) * 32];
 }
 
 template <int QT>
 __device__ __forceinline__ void gemm_block(const GemmBlk& g, bool valid, bool lo_half, int sh, v16f& acc0,
-                                           v16f& acc1) {
+                                           v16f& acc1, v16f& accm0, v16f& accm1) {
     v4i bv;
     if constexpr (QT == Q8_0) {
         bv = v4i{static_cast<int>(g.w.x), static_cast<int>(g.w.y), static_cast<int>(g.w.z), static_cast<int>(g.w.w)};
+    } else if constexpr (gemm_has_min(QT)) {  // unsigned nibbles 0..15 as int8: lanes 0-31 low, 32-63 high
+        const int rs = lo_half ? 0 : 4;
+        bv.x = static_cast<int>((g.w.x >> rs) & 0x0F0F0F0Fu);
+        bv.y = static_cast<int>((g.w.y >> rs) & 0x0F0F0F0Fu);
+        bv.z = static_cast<int>((g.w.z >> rs) & 0x0F0F0F0Fu);
+        bv.w = static_cast<int>((g.w.w >> rs) & 0x0F0F0F0Fu);
     } else {
         bv.x = static_cast<int>(((g.w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
         bv.y = static_cast<int>(((g.w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
@@ -329,7 +416,17 @@ __device__ __forceinline__ void gemm_block(const GemmBlk& g, bool valid, bool lo
     const v16i i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bv, zi, 0, 0, 0);
     const v16i i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv, zi, 0, 0, 0);
     const bool use = valid && lo_half;
-    const float bw = use ? h2f(g.d) : 0.0f;
+    float bw;
+    if constexpr (gemm_has_min(QT)) {
+        bw = use ? g.sm.x : 0.0f;
+        // the min term sum_t' (dx*sum q)[t] * min[r]: an outer product the matrix
+        // pipe accumulates by itself
+        const float bm = use ? g.sm.y : 0.0f;
+        accm0 = __builtin_amdgcn_mfma_f32_32x32x2f32(use ? g.s0 : 0.0f, bm, accm0, 0, 0, 0);
+        accm1 = __builtin_amdgcn_mfma_f32_32x32x2f32(use ? g.s1 : 0.0f, bm, accm1, 0, 0, 0);
+    } else {
+        bw = use ? h2f(g.d) : 0.0f;
+    }
     const float s0 = use ? g.x0 : 0.0f;  // q4_0: the 16 of the nibble encoding is divided out at the store
     const float s1 = use ? g.x1 : 0.0f;
     const v16f zf = {};
@@ -346,11 +443,13 @@ __device__ __forceinline__ void gemm_block(const GemmBlk& g, bool valid, bool lo
 // zlm_tile_q8_0), so each per-block load of a wave is one contiguous run: 1 KiB
 // of qx per 32-token tile, 512 B (q4_0) or 1 KiB (q8_0) of weights and 64 B of
 // scales per 32-row tile.
+// q4_1 / q4_k take the (scale, min) tiles (zlm_tile_q4_1 / zlm_tile_q4_k) and
+// the quantizer's dx*sum(q): out = sum_b scale*dx*dot(nib, q) + min*dx*sum(q).
 template <int QT>
-__device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+__device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const void* __restrict__ wsc,
                                            const int8_t* __restrict__ qx, const float* __restrict__ dx,
-                                           float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
-                                           uint32_t mt) {
+                                           const float* __restrict__ ds, float* __restrict__ out, uint32_t rows,
+                                           uint32_t m, uint32_t nb, uint32_t mt) {
     const int lane = threadIdx.x & 63;
     const int wid = threadIdx.x >> 6;
     const uint32_t tok0 = blockIdx.y * 128 + 64 * (wid & 1);  // multiple of 32
@@ -359,17 +458,21 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
     const int l32 = lane & 31;
     const uint32_t tt0 = min(tok0 / 32, mt - 1), tt1 = min(tok0 / 32 + 1, mt - 1);
     const uint32_t rt = min(row0 / 32, (rows + 31) / 32 - 1);  // a wave past the last tile re-reads it, stores nothing
-    const int8_t* a0 = qx + static_cast<size_t>(tt0) * nb * 1024 + l32 * 32 + 16 * half;
-    const int8_t* a1 = qx + static_cast<size_t>(tt1) * nb * 1024 + l32 * 32 + 16 * half;
-    const uint8_t* wr = QT == Q8_0 ? wq + static_cast<size_t>(rt) * nb * 1024 + l32 * 32 + 16 * half
-                                   : wq + static_cast<size_t>(rt) * nb * 512 + l32 * 16;
-    const uint16_t* dr = wd + static_cast<size_t>(rt) * nb * 32 + l32;
-    const float* x0 = dx + static_cast<size_t>(tt0) * nb * 32 + l32;
-    const float* x1 = dx + static_cast<size_t>(tt1) * nb * 32 + l32;
-    const int sh = half ? 0 : 4;  // lanes 0-31 take the low nibbles, 32-63 the high
+    GemmPtrs ptr;
+    ptr.a0 = qx + static_cast<size_t>(tt0) * nb * 1024 + l32 * 32 + 16 * half;
+    ptr.a1 = qx + static_cast<size_t>(tt1) * nb * 1024 + l32 * 32 + 16 * half;
+    ptr.wr = QT == Q8_0 ? wq + static_cast<size_t>(rt) * nb * 1024 + l32 * 32 + 16 * half
+                      : wq + static_cast<size_t>(rt) * nb * 512 + l32 * 16;
+    ptr.dr = static_cast<const uint16_t*>(wsc) + static_cast<size_t>(rt) * nb * 32 + l32;
+    ptr.smr = static_cast<const float2*>(wsc) + static_cast<size_t>(rt) * nb * 32 + l32;
+    ptr.x0 = dx + static_cast<size_t>(tt0) * nb * 32 + l32;
+    ptr.x1 = dx + static_cast<size_t>(tt1) * nb * 32 + l32;
+    ptr.s0 = gemm_has_min(QT) ? ds + static_cast<size_t>(tt0) * nb * 32 + l32 : nullptr;
+    ptr.s1 = gemm_has_min(QT) ? ds + static_cast<size_t>(tt1) * nb * 32 + l32 : nullptr;
+    const int sh = half ? 0 : 4;  // q4_0: lanes 0-31 take the low nibbles, 32-63 the high
     const bool lo_half = half == 0;
 
-    v16f acc0 = {}, acc1 = {};
+    v16f acc0 = {}, acc1 = {}, accm0 = {}, accm1 = {};
     // Two register sets, A and B, alternate: one set's loads are in flight
     // while the other's blocks are computed.  The scheduling barriers keep each
     // set's loads ahead of the compute (the scheduler would otherwise sink them
@@ -377,31 +480,38 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
     GemmBlk A[kGemmDepth], B[kGemmDepth];
 #pragma unroll
     for (int p = 0; p < kGemmDepth; p++)
-        gemm_load<QT>(A[p], a0, a1, wr, dr, x0, x1, min(static_cast<uint32_t>(p), nb - 1));
+        gemm_load<QT>(A[p], ptr, min(static_cast<uint32_t>(p), nb - 1));
     for (uint32_t b = 0; b < nb; b += 2 * kGemmDepth) {
 #pragma unroll
         for (int p = 0; p < kGemmDepth; p++)
-            gemm_load<QT>(B[p], a0, a1, wr, dr, x0, x1, min(b + kGemmDepth + p, nb - 1));
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int p = 0; p < kGemmDepth; p++) gemm_block<QT>(A[p], b + p < nb, lo_half, sh, acc0, acc1);
+            gemm_load<QT>(B[p], ptr, min(b + kGemmDepth + p, nb - 1));
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < kGemmDepth; p++)
-            gemm_load<QT>(A[p], a0, a1, wr, dr, x0, x1, min(b + 2 * kGemmDepth + p, nb - 1));
+            gemm_block<QT>(A[p], b + p < nb, lo_half, sh, acc0, acc1, accm0, accm1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = 0; p < kGemmDepth; p++) gemm_block<QT>(B[p], b + kGemmDepth + p < nb, lo_half, sh, acc0, acc1);
+        for (int p = 0; p < kGemmDepth; p++)
+            gemm_load<QT>(A[p], ptr, min(b + 2 * kGemmDepth + p, nb - 1));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < kGemmDepth; p++)
+            gemm_block<QT>(B[p], b + kGemmDepth + p < nb, lo_half, sh, acc0, acc1, accm0, accm1);
         __builtin_amdgcn_sched_barrier(0);
     }
-    constexpr float kOut = QT == Q8_0 ? 1.0f : 0.0625f;
+    constexpr float kOut = QT == Q4_0 ? 0.0625f : 1.0f;
     const uint32_t r = row0 + l32;
     if (r < rows) {
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const uint32_t t = tok0 + 8 * (i / 4) + 4 * half + (i % 4);
-            if (t < m) out[static_cast<size_t>(t) * rows + r] = acc0[i] * kOut;
-            if (t + 32 < m) out[static_cast<size_t>(t + 32) * rows + r] = acc1[i] * kOut;
+            float v0 = acc0[i] * kOut, v1 = acc1[i] * kOut;
+            if constexpr (gemm_has_min(QT)) {
+                v0 += accm0[i];
+                v1 += accm1[i];
+            }
+            if (t < m) out[static_cast<size_t>(t) * rows + r] = v0;
+            if (t + 32 < m) out[static_cast<size_t>(t + 32) * rows + r] = v1;
         }
     }
 }
@@ -410,14 +520,29 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
     zlm_gemm_q4_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
                      const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
                      uint32_t mt) {
-    gemm_tiles<Q4_0>(wq, wd, qx, dx, out, rows, m, nb, mt);
+    gemm_tiles<Q4_0>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
 }
 
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
     zlm_gemm_q8_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
                      const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
                      uint32_t mt) {
-    gemm_tiles<Q8_0>(wq, wd, qx, dx, out, rows, m, nb, mt);
+    gemm_tiles<Q8_0>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
+}
+
+// q4_1 / q4_k: nb is the row's 32-element block count (k/32 for both).
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q4_1_q8(const uint8_t* __restrict__ wq, const float2* __restrict__ wsm, const int8_t* __restrict__ qx,
+                     const float* __restrict__ dx, const float* __restrict__ ds, float* __restrict__ out,
+                     uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q4_1>(wq, wsm, qx, dx, ds, out, rows, m, nb, mt);
+}
+
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q4_k_q8(const uint8_t* __restrict__ wq, const float2* __restrict__ wsm, const int8_t* __restrict__ qx,
+                     const float* __restrict__ dx, const float* __restrict__ ds, float* __restrict__ out,
+                     uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q4_K>(wq, wsm, qx, dx, ds, out, rows, m, nb, mt);
 }
 
 
