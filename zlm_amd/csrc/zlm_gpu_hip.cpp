@@ -103,6 +103,7 @@ struct GemvKernel {
     int steps = 0;
     int threads = 256;     // the kernel's launch bounds
     int waves_per_cu = 0;  // grid target of a prefetching instance; 0 = gemv_grid's rule
+    bool struct_args = false;  // takes one GemvArgs (fused forms, prefetching instances)
 };
 
 struct Slot {
@@ -374,7 +375,8 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
 
 // Look up (and cache) a GEMV entry point by name in its quant's code object;
 // the block size is the kernel's launch bound.
-const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps, int waves_per_cu = 0) {
+const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps, int waves_per_cu = 0,
+                            bool struct_args = false) {
     auto it = d->gemv.find(name);
     if (it == d->gemv.end()) {
         GemvKernel g;
@@ -382,6 +384,7 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
             g.rt = rt;
             g.steps = steps;
             g.waves_per_cu = waves_per_cu;
+            g.struct_args = struct_args;
             int mt = 0;
             if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g.fn) == hipSuccess && mt >= 64)
                 g.threads = mt;
@@ -396,16 +399,23 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
     return it->second.fn ? &it->second : nullptr;
 }
 
-// The GEMV kernel for a shape: the instance whose step count equals
-// ceil(chunks per row / 64) with the requested row tile, else with a 1-row
-// tile, else the generic bounded instance.  Chunks per row: k / chunk_elems
-// (k/16 for q8_0, k/32 for q4_0, q4_1 and the K-quants, k/8 for f16 / bf16,
-// k/4 for f32).
-const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt) {
+// The GEMV kernel for a shape: for a 1-row tile and fewer than 65536 rows
+// the prefetching instance of the exact step count if the quant has one
+// (zlm_gemv_<quant>_r1_s<steps>_pf); else the instance whose step count
+// equals ceil(chunks per row / 64) with the requested row tile, else with a
+// 1-row tile, else the generic bounded instance.  Chunks per row:
+// k / chunk_elems (k/16 for q8_0, k/32 for q4_0, q4_1 and the K-quants, k/8
+// for f16 / bf16, k/4 for f32).  Tall launches (the lm_heads) keep the plain
+// instances at 8 workgroups per CU (gemv_grid).
+const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows) {
     const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
+    if (rt == 1 && rows < 65536) {
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d_pf", qn, steps);
+        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps, 8, true)) return g;
+    }
     snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d", qn, rt, steps);
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d", qn, steps);
@@ -452,38 +462,19 @@ unsigned gemv_grid(const zlm_device* d, const QuantInfo* qi, uint64_t tiles, con
 
 // Validate a GEMV over resident `r` and pick its kernel.
 bool prepare_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, hipFunction_t* f,
-                  unsigned* grid, unsigned* block) {
+                  unsigned* grid, unsigned* block, const GemvKernel** picked = nullptr) {
     if (!d || !d->avail) return fail(d, "device unavailable");
     const QuantInfo* qi = quant_info(quant);
     if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
     if (!check_resident(d, r, qi, rows, k)) return false;
-    const GemvKernel* gk = pick_gemv(d, qi, k, rt_for_variant(variant_of(quant)));
+    const GemvKernel* gk = pick_gemv(d, qi, k, rt_for_variant(variant_of(quant)), rows);
     if (!gk) return fail(d, "no GEMV kernel for quant %u k=%zu", qi->type, k);
     *f = gk->fn;
     *grid = gemv_grid(d, qi, (rows + gk->rt - 1) / gk->rt, gk);
     *block = static_cast<unsigned>(gk->threads);
+    if (picked) *picked = gk;
     return true;
 }
-
-bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, const float* x_dev,
-                  float* y_dev) {
-    hipFunction_t f;
-    unsigned grid, block;
-    if (!prepare_gemv(d, r, quant, rows, k, &f, &grid, &block)) return false;
-    const QuantInfo* qi = quant_info(quant);
-    const uint8_t* w = r->payload;
-    const uint16_t* s = r->scales;
-    uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->kblock);
-    void* args[] = {&w, &s, &x_dev, &y_dev, &rows32, &nb};
-    return launch(d, f, grid, block, args, "gemv");
-}
-
-// ---- fused GEMV forms (prologue/epilogue variants of the same kernel) ----
-
-const char* const kFormNames[] = {"plain", "pair", "norm", "normpair", "resid"};
-
-bool form_is_pair(uint32_t form) { return form == ZLM_FORM_PAIR || form == ZLM_FORM_NORMPAIR; }
-bool form_is_norm(uint32_t form) { return form == ZLM_FORM_NORM || form == ZLM_FORM_NORMPAIR; }
 
 // Kernel-argument block of the fused forms; the same layout as GemvArgs in
 // gemv_impl.h (passed by value as the kernel's only argument).
@@ -503,6 +494,32 @@ struct GemvArgsHost {
 };
 static_assert(sizeof(GemvArgsHost) == 80, "GemvArgs layout");
 
+bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, const float* x_dev,
+                  float* y_dev) {
+    hipFunction_t f;
+    unsigned grid, block;
+    const GemvKernel* gk = nullptr;
+    if (!prepare_gemv(d, r, quant, rows, k, &f, &grid, &block, &gk)) return false;
+    const QuantInfo* qi = quant_info(quant);
+    const uint8_t* w = r->payload;
+    const uint16_t* s = r->scales;
+    uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->kblock);
+    if (gk->struct_args) {
+        GemvArgsHost a = {w, s, w, s, x_dev, x_dev, y_dev, y_dev, rows32, nb, 0.0f, 0u};
+        void* args[] = {&a};
+        return launch(d, f, grid, block, args, "gemv");
+    }
+    void* args[] = {&w, &s, &x_dev, &y_dev, &rows32, &nb};
+    return launch(d, f, grid, block, args, "gemv");
+}
+
+// ---- fused GEMV forms (prologue/epilogue variants of the same kernel) ----
+
+const char* const kFormNames[] = {"plain", "pair", "norm", "normpair", "resid"};
+
+bool form_is_pair(uint32_t form) { return form == ZLM_FORM_PAIR || form == ZLM_FORM_NORMPAIR; }
+bool form_is_norm(uint32_t form) { return form == ZLM_FORM_NORM || form == ZLM_FORM_NORMPAIR; }
+
 // The fused-form kernel for a shape: the prefetching exact-steps instance if
 // the quant has one, else the exact-steps instance, else the generic one.
 const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form) {
@@ -512,7 +529,7 @@ const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint3
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d_pf", qn, kFormNames[form], steps);
-    if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 8)) return g;
+    if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 8, true)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d", qn, kFormNames[form], steps);
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_g", qn, kFormNames[form]);
