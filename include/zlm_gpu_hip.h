@@ -210,6 +210,11 @@ bool zlm_gpu_dev_copy_enqueue(zlm_device *dev, void *dst, const void *src, size_
 /* Enqueue y_dev[0..rows) = W * x_dev on the device stream; no host copies. */
 bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k,
                              const float *x_dev, float *y_dev);
+/* The device-side form of matVecResidentBatch: n <= ZLM_RING_SIZE GEMVs over
+ * one x_dev (k floats), res[i] (rows[i] x k, all of one quant type) into
+ * y_dev[i], enqueued as one launch (no wait). */
+bool zlm_gpu_mat_vec_batch_enqueue(zlm_device *dev, zlm_resident *const *res, uint32_t quant, const size_t *rows,
+                                   size_t n, size_t k, const float *x_dev, float *const *y_dev);
 /* Enqueue the prefill GEMM out_dev[t*rows + r] (x_dev: m x k fp32, token-major):
  * the q8 activation quantizer, then the int8-MFMA GEMM.  Q4_0, Q8_0, Q4_1 and
  * Q4_K weights. */
@@ -223,7 +228,9 @@ bool zlm_gpu_time_mat_mul(zlm_device *dev, zlm_resident *const *res, size_t n_re
  * on the device stream; *ms = elapsed GPU milliseconds between the events. */
 bool zlm_gpu_time_mat_vec(zlm_device *dev, zlm_resident *const *res, size_t n_res, uint32_t quant, size_t rows,
                           size_t k, const float *x_dev, float *y_dev, int iters, double *ms);
-/* One GEMV of a timed sequence (device pointers). */
+/* One GEMV of a timed sequence (device pointers).  with_next != 0 joins this
+ * GEMV and the next into one batch launch (zlm_gpu_mat_vec_batch_enqueue);
+ * joined GEMVs share quant type, k and x_dev. */
 typedef struct {
     zlm_resident *res;
     uint32_t quant;
@@ -231,6 +238,7 @@ typedef struct {
     size_t k;
     const float *x_dev;
     float *y_dev;
+    uint32_t with_next;
 } zlm_gemv_desc;
 /* Enqueue descs[0..n) in order, `iters` times, between two HIP events on the
  * device stream; *ms = elapsed GPU milliseconds between the events. */

@@ -128,6 +128,42 @@ def test_async_burst_batch_agree(dev):
         dev.free_resident(res)
 
 
+@pytest.mark.parametrize("qt,k", [(synth.Q8_0, 4096), (synth.Q4_K, 3840), (synth.F16, 1024), (synth.Q4_1, 12288)],
+                         ids=["q8_0", "q4_k", "f16", "q4_1"])
+def test_batch_one_launch_matches_single_ops(dev, qt, k):
+    """A same-quant batch runs as one launch of the batch kernel; every op's
+    rows equal the single-op GEMV's bit for bit (same per-lane order and
+    reduction), including eight ops of ragged row counts."""
+    _say(f"batch {NAMES[qt]} k={k}")
+    shapes = [1, 77, 4096, 130, 33, 1024, 2, 513]
+    ws = [synth.weights(qt, r, k, seed=300 + i) for i, r in enumerate(shapes)]
+    x = synth.activation(31, k)
+    ress = [dev.upload_resident(w) for w in ws]
+    ref = []
+    for r, res in zip(shapes, ress):
+        o = np.zeros(r, np.float32)
+        assert dev.mat_vec_resident(res, zd.quant(qt), r, k, x, o), dev.last_error()
+        ref.append(o)
+    outs = [np.full(r, np.nan, np.float32) for r in shapes]
+    ops = [zd.ResidentOp(res, zd.quant(qt), r, o) for res, r, o in zip(ress, shapes, outs)]
+    assert dev.mat_vec_resident_batch(k, x, ops), dev.last_error()
+    for o, want in zip(outs, ref):
+        np.testing.assert_array_equal(o, want)
+    assert rel_l2(outs[2], oracle.matvec(qt, ws[2], k, shapes[2], x)) <= REL_L2
+    # a mixed-quant batch runs op by op and agrees too
+    wq = synth.weights(synth.Q4_0, 64, k, seed=399)
+    rq = dev.upload_resident(wq)
+    oq = np.zeros(64, np.float32)
+    assert dev.mat_vec_resident(rq, zd.quant(zd.Q4_0), 64, k, x, oq)
+    mixed = [np.zeros(shapes[0], np.float32), np.zeros(64, np.float32)]
+    ops = [zd.ResidentOp(ress[0], zd.quant(qt), shapes[0], mixed[0]), zd.ResidentOp(rq, zd.quant(zd.Q4_0), 64, mixed[1])]
+    assert dev.mat_vec_resident_batch(k, x, ops), dev.last_error()
+    np.testing.assert_array_equal(mixed[0], ref[0])
+    np.testing.assert_array_equal(mixed[1], oq)
+    for res in ress + [rq]:
+        dev.free_resident(res)
+
+
 def test_ring_refuses_ninth_inflight_and_stale_handles(dev):
     qt, rows, k = synth.Q8_0, 128, 256
     w = synth.weights(qt, rows, k, seed=3)

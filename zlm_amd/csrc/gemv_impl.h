@@ -158,6 +158,12 @@ __device__ __forceinline__ float xstore_norm(const XRegs<NX>& r, const XRegs<NX>
 
 __device__ __forceinline__ float4 lds4(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
+__device__ __forceinline__ float wave_sum_all(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
 // ---- per-quant fragments --------------------------------------------------
 // A fragment is what one lane loads for one 16-byte chunk position `c` of RT
 // rows; `load_frag` only issues global loads, `compute_frag` only touches
@@ -835,6 +841,76 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
         reduce_store<RT, EPI>(acc, a, tile, scale, lane);
     }
 }
+// ---- several matrices over one x in one launch -------------------------------
+// The contract's matVecResidentBatch (reference gpu/backend/root.zig:249-254,
+// vulkan/pipeline.zig:1770-1802) runs up to RingSize GEMVs that share k and x.
+// One launch covers all of them: the row tiles of op i are global tiles
+// [first[i], first[i+1]), a wave finds its op by a wave-uniform scan, and
+// everything else is the plain GEMV (1-row tiles), so the launch's fixed cost
+// is paid once for the whole batch.
+constexpr int kMultiMax = 8;
+
+struct GemvMultiArgs {
+    const uint8_t* w[kMultiMax];
+    const uint16_t* d[kMultiMax];
+    float* y[kMultiMax];
+    uint32_t first[kMultiMax + 1];  // first global row of op i; first[n] = all rows
+    const float* x;
+    uint32_t n;
+    uint32_t nb;
+};
+
+__device__ __forceinline__ TileRows<1> multi_row(const GemvMultiArgs& a, uint32_t t, uint32_t& op) {
+    op = 0;
+#pragma unroll
+    for (int i = 1; i < kMultiMax; i++)
+        if (static_cast<uint32_t>(i) < a.n && t >= a.first[i]) op = static_cast<uint32_t>(i);
+    TileRows<1> tr;
+    tr.w[0] = a.w[op];
+    tr.d[0] = a.d[op];
+    tr.r[0] = t - a.first[op];
+    return tr;
+}
+
+template <int QT, int KCAP, int WAVES, int STEPS, bool EXACT>
+__device__ __forceinline__ void gemv_multi(const GemvMultiArgs& a) {
+    __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
+    __shared__ float xs[XTile<KCAP>::kRuns + 1];
+    constexpr int NX = (KCAP / 4 + WAVES * kWave - 1) / (WAVES * kWave);
+    constexpr int GROUP = STEPS * kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wid = threadIdx.x / kWave;
+    const int C = chunks_per_row<QT>(a.nb);
+    const uint32_t ntiles = a.first[a.n];
+    const uint32_t tstride = gridDim.x * WAVES;
+    uint32_t tile = blockIdx.x * WAVES + wid;
+    const int k = static_cast<int>(a.nb) * elems_per_block<QT>();
+    XRegs<NX> xr;
+    xload(a.x, k, xr);
+    Frag<QT, 1> f[STEPS];
+    uint32_t op;
+    TileRows<1> tr = multi_row(a, min(tile, ntiles - 1), op);
+    load_group<QT, 1, STEPS, EXACT, true>(f, tr, a.nb, C, 0, lane);
+    xstore<KCAP>(xr, k, xl, xs);
+    float acc[1];
+    for (;;) {
+        acc[0] = 0.0f;
+        compute_group<QT, 1, STEPS, EXACT>(f, xl, xs, C, 0, lane, acc);
+        if constexpr (!EXACT) {
+            for (int cb = GROUP; cb < C; cb += GROUP) {
+                load_group<QT, 1, STEPS, EXACT, true>(f, tr, a.nb, C, cb, lane);
+                compute_group<QT, 1, STEPS, EXACT>(f, xl, xs, C, cb, lane, acc);
+            }
+        }
+        const float sum = wave_sum_all(acc[0]);
+        if (tile < ntiles && lane == 0) a.y[op][tr.r[0]] = sum;
+        tile += tstride;
+        if (tile >= ntiles) break;
+        tr = multi_row(a, tile, op);
+        load_group<QT, 1, STEPS, EXACT, true>(f, tr, a.nb, C, 0, lane);
+    }
+}
+
 }  // namespace
 
 // ---- GEMV entry points ---------------------------------------------------
@@ -981,3 +1057,28 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
     ZLM_GEMVX_FORMS(QN, QT, 4096, 8, true, s8)        \
     ZLM_GEMVX_FORMS(QN, QT, 4096, 16, true, s16)      \
     ZLM_GEMVX_FORMS(QN, QT, 32768, 8, false, g)
+
+// zlm_gemv_<quant>_multi_s<STEPS> (exact steps) and zlm_gemv_<quant>_multi_g
+// (any k up to 32768): the batch kernel over GemvMultiArgs.
+#define ZLM_GEMV_MULTI(NAME, QT, KCAP, STEPS, EXACT)                                 \
+    extern "C" __global__ void __launch_bounds__(256) NAME(GemvMultiArgs a) {        \
+        gemv_multi<QT, KCAP, 4, STEPS, EXACT>(a);                                   \
+    }
+// Batch instances: q4_0 / q4_1 / q4_k / q6_k (32 elements per chunk), q8_0
+// (16), f16 / bf16 (8), f32 (4); exact steps at the common k, else generic.
+#define ZLM_GEMV_MULTI_Q4(QN, QT)                                   \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s1, QT, 4096, 1, true)     \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s2, QT, 4096, 2, true)     \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s4, QT, 8192, 4, true)     \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_g, QT, 32768, 4, false)
+#define ZLM_GEMV_MULTI_Q8(QN, QT)                                   \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s2, QT, 4096, 2, true)     \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s4, QT, 4096, 4, true)     \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s8, QT, 8192, 8, true)     \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_g, QT, 32768, 8, false)
+#define ZLM_GEMV_MULTI_F16(QN, QT)                                  \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s8, QT, 4096, 8, true)     \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_g, QT, 32768, 8, false)
+#define ZLM_GEMV_MULTI_F32(QN, QT)                                  \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_s16, QT, 4096, 16, true)   \
+    ZLM_GEMV_MULTI(zlm_gemv_##QN##_multi_g, QT, 32768, 8, false)

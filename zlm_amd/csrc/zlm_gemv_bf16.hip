@@ -5,3 +5,5 @@
 
 ZLM_GEMV_F16(bf16, BF16)
 ZLM_GEMVX_F16(bf16, BF16)
+
+ZLM_GEMV_MULTI_F16(bf16, BF16)

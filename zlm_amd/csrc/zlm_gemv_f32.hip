@@ -5,3 +5,5 @@
 
 ZLM_GEMV_F32(f32, F32)
 ZLM_GEMVX_F32(f32, F32)
+
+ZLM_GEMV_MULTI_F32(f32, F32)

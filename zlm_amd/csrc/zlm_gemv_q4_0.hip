@@ -14,3 +14,5 @@ ZLM_GEMVX_FORMS(q4_0, Q4_0, 16384, 6, true, s6)
 ZLM_GEMVX_PF(zlm_gemv_q4_0_pair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PAIR, false)
 ZLM_GEMVX_PF(zlm_gemv_q4_0_normpair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_NORM, EPI_PAIR, false)
 ZLM_GEMVX_PF(zlm_gemv_q4_0_resid_s6_pf, Q4_0, 12288, 4, 1, 6, PRO_PLAIN, EPI_RESID, true)
+
+ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)

@@ -5,3 +5,5 @@
 
 ZLM_GEMV_Q4_COMMON(q4_1, Q4_1)
 ZLM_GEMVX_Q4(q4_1, Q4_1)
+
+ZLM_GEMV_MULTI_Q4(q4_1, Q4_1)

@@ -9,3 +9,5 @@ ZLM_GEMVX_Q4(q6_k, Q6_K)
 // Prefetching plain instance for k <= 4096 (measured on gfx950 at 15360 x
 // 3840: 16.3 -> 12.9 us with 8-wave workgroups at 8 waves per CU).
 ZLM_GEMVX_PF(zlm_gemv_q6_k_r1_s2_pf, Q6_K, 4096, 8, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
+
+ZLM_GEMV_MULTI_Q4(q6_k, Q6_K)

@@ -5,3 +5,5 @@
 
 ZLM_GEMV_Q8(q8_0, Q8_0)
 ZLM_GEMVX_Q8(q8_0, Q8_0)
+
+ZLM_GEMV_MULTI_Q8(q8_0, Q8_0)

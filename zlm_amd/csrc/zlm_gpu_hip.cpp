@@ -520,6 +520,54 @@ const char* const kFormNames[] = {"plain", "pair", "norm", "normpair", "resid"};
 bool form_is_pair(uint32_t form) { return form == ZLM_FORM_PAIR || form == ZLM_FORM_NORMPAIR; }
 bool form_is_norm(uint32_t form) { return form == ZLM_FORM_NORM || form == ZLM_FORM_NORMPAIR; }
 
+// Kernel-argument block of the batch kernel (GemvMultiArgs in gemv_impl.h).
+constexpr int kMultiMax = 8;
+struct GemvMultiArgsHost {
+    const uint8_t* w[kMultiMax];
+    const uint16_t* d[kMultiMax];
+    float* y[kMultiMax];
+    uint32_t first[kMultiMax + 1];
+    const float* x;
+    uint32_t n;
+    uint32_t nb;
+};
+static_assert(sizeof(GemvMultiArgsHost) == 248, "GemvMultiArgs layout");
+static_assert(kMultiMax == kRing, "a batch holds at most RingSize ops");
+
+// Enqueue up to kMultiMax GEMVs that share quant `qi`, k and x_dev as one
+// launch of the batch kernel, op i's rows into ys[i].  The residents are
+// validated by the caller (check_resident).
+bool enqueue_multi(zlm_device* d, const QuantInfo* qi, size_t k, const float* x_dev, zlm_resident* const* res,
+                   const size_t* rows, float* const* ys, size_t n) {
+    const size_t chunks = k / qi->chunk_elems;
+    const int steps = static_cast<int>((chunks + 63) / 64);
+    const char* qn = kQuantNames[qi->slot];
+    char nm[96];
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_multi_s%d", qn, steps);
+    const GemvKernel* gk = find_gemv(d, qi->slot, nm, 1, steps);
+    if (!gk) {
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_multi_g", qn);
+        gk = find_gemv(d, qi->slot, nm, 1, 0);
+    }
+    if (!gk) return fail(d, "no batch GEMV kernel for quant %u", qi->type);
+    GemvMultiArgsHost a = {};
+    uint64_t total = 0;
+    for (size_t i = 0; i < n; i++) {
+        a.w[i] = res[i]->payload;
+        a.d[i] = res[i]->scales;
+        a.y[i] = ys[i];
+        a.first[i] = static_cast<uint32_t>(total);
+        total += rows[i];
+    }
+    if (total > 0xffffffffu) return fail(d, "batch too large");
+    for (size_t i = n; i <= static_cast<size_t>(kMultiMax); i++) a.first[i] = static_cast<uint32_t>(total);
+    a.x = x_dev;
+    a.n = static_cast<uint32_t>(n);
+    a.nb = static_cast<uint32_t>(k / qi->kblock);
+    void* args[] = {&a};
+    return launch(d, gk->fn, gemv_grid(d, qi, total, gk), static_cast<unsigned>(gk->threads), args, "gemv batch");
+}
+
 // The fused-form kernel for a shape: the prefetching exact-steps instance if
 // the quant has one, else the exact-steps instance, else the generic one.
 const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form) {
@@ -1044,13 +1092,33 @@ extern "C" bool zlm_gpu_mat_vec_resident_batch(zlm_device* d, size_t k, const fl
     }
     if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, total)) return false;
     if (!stage_x_sync(d, x, k)) return false;
+    // Ops of one quant go out as one launch of the batch kernel; a mixed batch
+    // runs op by op.
+    bool same = n > 1;
+    for (size_t i = 1; i < n; i++) same = same && (ops[i].quant & 0xffu) == (ops[0].quant & 0xffu);
     size_t off = 0;
-    for (size_t i = 0; i < n; i++) {
-        if (!enqueue_gemv(d, ops[i].res, ops[i].quant, ops[i].rows, k, d->d_x, d->d_y + off)) {
+    if (same) {
+        zlm_resident* res[kMultiMax];
+        size_t rows[kMultiMax];
+        float* ys[kMultiMax];
+        for (size_t i = 0; i < n; i++) {
+            res[i] = ops[i].res;
+            rows[i] = ops[i].rows;
+            ys[i] = d->d_y + off;
+            off += ops[i].rows;
+        }
+        if (!enqueue_multi(d, quant_info(ops[0].quant), k, d->d_x, res, rows, ys, n)) {
             hipStreamSynchronize(d->stream);
             return false;
         }
-        off += ops[i].rows;
+    } else {
+        for (size_t i = 0; i < n; i++) {
+            if (!enqueue_gemv(d, ops[i].res, ops[i].quant, ops[i].rows, k, d->d_x, d->d_y + off)) {
+                hipStreamSynchronize(d->stream);
+                return false;
+            }
+            off += ops[i].rows;
+        }
     }
     if (!ok(d, hipMemcpyAsync(d->h_y, d->d_y, total * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y") ||
         !ok(d, hipStreamSynchronize(d->stream), "sync"))
@@ -1416,6 +1484,21 @@ extern "C" bool zlm_gpu_mat_vec_enqueue(zlm_device* d, zlm_resident* r, uint32_t
     return enqueue_gemv(d, r, quant, rows, k, x_dev, y_dev);
 }
 
+extern "C" bool zlm_gpu_mat_vec_batch_enqueue(zlm_device* d, zlm_resident* const* res, uint32_t quant,
+                                              const size_t* rows, size_t n, size_t k, const float* x_dev,
+                                              float* const* y_dev) {
+    if (!d || !d->avail) return false;
+    if (!res || !rows || !y_dev || !x_dev || n == 0 || n > static_cast<size_t>(kMultiMax)) return fail(d, "bad batch");
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
+    for (size_t i = 0; i < n; i++) {
+        if (!y_dev[i]) return fail(d, "null y");
+        if (!check_resident(d, res[i], qi, rows[i], k)) return false;
+    }
+    if (n == 1) return enqueue_gemv(d, res[0], quant, rows[0], k, x_dev, y_dev[0]);
+    return enqueue_multi(d, qi, k, x_dev, res, rows, y_dev, n);
+}
+
 extern "C" bool zlm_gpu_mat_mul_enqueue(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
                                         size_t m, const float* x_dev, float* out_dev) {
     if (!d || !d->avail) return false;
@@ -1483,9 +1566,26 @@ extern "C" bool zlm_gpu_time_gemv_sequence(zlm_device* d, const zlm_gemv_desc* d
     }
     bool good = ok(d, hipEventRecord(e0, d->stream), "record");
     for (int it = 0; good && it < iters; it++)
-        for (size_t i = 0; good && i < n; i++)
-            good = enqueue_gemv(d, descs[i].res, descs[i].quant, descs[i].rows, descs[i].k, descs[i].x_dev,
-                                descs[i].y_dev);
+        for (size_t i = 0; good && i < n;) {
+            size_t j = i + 1;  // [i, j): one launch
+            while (descs[j - 1].with_next && j < n && j - i < static_cast<size_t>(kMultiMax)) j++;
+            if (j - i == 1) {
+                good = enqueue_gemv(d, descs[i].res, descs[i].quant, descs[i].rows, descs[i].k, descs[i].x_dev,
+                                    descs[i].y_dev);
+            } else {
+                zlm_resident* res[kMultiMax];
+                size_t rows[kMultiMax];
+                float* ys[kMultiMax];
+                for (size_t t = i; t < j; t++) {
+                    res[t - i] = descs[t].res;
+                    rows[t - i] = descs[t].rows;
+                    ys[t - i] = descs[t].y_dev;
+                }
+                good = zlm_gpu_mat_vec_batch_enqueue(d, res, descs[i].quant, rows, j - i, descs[i].k, descs[i].x_dev,
+                                                     ys);
+            }
+            i = j;
+        }
     good = good && ok(d, hipEventRecord(e1, d->stream), "record") && ok(d, hipEventSynchronize(e1), "sync");
     float t = 0.0f;
     good = good && ok(d, hipEventElapsedTime(&t, e0, e1), "elapsed");

@@ -65,6 +65,7 @@ class _GemvDesc(ctypes.Structure):
         ("k", ctypes.c_size_t),
         ("x_dev", ctypes.c_void_p),
         ("y_dev", ctypes.c_void_p),
+        ("with_next", ctypes.c_uint32),
     ]
 
 
@@ -159,6 +160,7 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_dev_copy": (B, [P, P, P, S]),
         "zlm_gpu_dev_copy_enqueue": (B, [P, P, P, S]),
         "zlm_gpu_mat_vec_enqueue": (B, [P, P, U, S, S, P, P]),
+        "zlm_gpu_mat_vec_batch_enqueue": (B, [P, P, U, P, S, S, P, P]),
         "zlm_gpu_time_mat_vec": (B, [P, P, S, U, S, S, P, P, ctypes.c_int, P]),
         "zlm_gpu_mat_mul_enqueue": (B, [P, P, U, S, S, S, P, P]),
         "zlm_gpu_time_mat_mul": (B, [P, P, S, U, S, S, S, P, P, ctypes.c_int, P]),
@@ -409,6 +411,16 @@ class Device:
     def mat_vec_enqueue(self, res: Resident, quant: int, rows: int, k: int, x_dev: int, y_dev: int) -> bool:
         return bool(self._L.zlm_gpu_mat_vec_enqueue(self._h, res.ptr, quant, rows, k, x_dev, y_dev))
 
+    def mat_vec_batch_enqueue(self, residents: Sequence[Resident], quant: int, rows: Sequence[int], k: int,
+                              x_dev: int, y_devs: Sequence[int]) -> bool:
+        """One launch of up to RING_SIZE GEMVs over one device x (no wait)."""
+        n = len(residents)
+        ra = (ctypes.c_void_p * max(1, n))(*[r.ptr for r in residents])
+        rw = (ctypes.c_size_t * max(1, n))(*rows)
+        ya = (ctypes.c_void_p * max(1, n))(*y_devs)
+        return bool(self._L.zlm_gpu_mat_vec_batch_enqueue(self._h, ctypes.addressof(ra), quant, ctypes.addressof(rw),
+                                                          n, k, x_dev, ctypes.addressof(ya)))
+
     def time_mat_vec(self, residents: Sequence[Resident], quant: int, rows: int, k: int, x_dev: int, y_dev: int,
                      iters: int) -> float:
         """GPU milliseconds for `iters` GEMVs rotating over `residents` (HIP events)."""
@@ -433,10 +445,12 @@ class Device:
         return ms.value
 
     def time_gemv_sequence(self, descs: Sequence[tuple], iters: int) -> float:
-        """GPU milliseconds for `iters` passes over descs = [(res, quant, rows, k, x_dev, y_dev), ...]."""
+        """GPU milliseconds for `iters` passes over descs = [(res, quant, rows, k, x_dev, y_dev[, with_next]), ...];
+        with_next joins a GEMV and the next into one batch launch."""
         arr = (_GemvDesc * len(descs))()
-        for i, (res, q, rows, k, xd, yd) in enumerate(descs):
-            arr[i] = _GemvDesc(res.ptr, q, rows, k, xd, yd)
+        for i, d in enumerate(descs):
+            res, q, rows, k, xd, yd = d[:6]
+            arr[i] = _GemvDesc(res.ptr, q, rows, k, xd, yd, int(d[6]) if len(d) > 6 else 0)
         ms = ctypes.c_double(0.0)
         if not self._L.zlm_gpu_time_gemv_sequence(self._h, ctypes.addressof(arr), len(descs), iters,
                                                   ctypes.addressof(ms)):
