@@ -91,7 +91,56 @@ __device__ __forceinline__ void xload(const float* __restrict__ x, int k, XRegs<
     }
 }
 
-template <int KCAP, int NX>
+// With XQ the LDS tile holds x in three int8 planes instead of fp32: per
+// 32-element block a power-of-two scale s = 2^(5-e) (e = exponent of the
+// block's amax, so |x*s| < 64), q0 = rint(x*s), q1 = rint(128*(x*s - q0)),
+// q2 = rint(128*(128*(x*s - q0) - q1)); x = (q0 + q1/128 + q2/16384) / s to
+// within amax * 2^-20.  Plane p is KCAP bytes at byte offset p*KCAP of the
+// tile, then the per-block 1/s (KCAP/32 floats); the dummy slot takes
+// out-of-range threads' stores.  The 8 lanes that hold one block's float4s
+// share its amax with three shuffles.
+template <int KCAP>
+struct XQTile {
+    static constexpr int kScales = 3 * KCAP / 4;         // float index of 1/s
+    static constexpr int kDummy = kScales + KCAP / 32;   // float index of the dummy slot
+    static_assert(kDummy + 4 <= XTile<KCAP>::kFloats, "the int8 planes fit the fp32 tile");
+};
+
+template <int KCAP, bool XQ>
+__device__ __forceinline__ void xput(float4 v, int i, bool valid, float* xl) {
+    if constexpr (!XQ) {
+        *reinterpret_cast<float4*>(xl + (valid ? xpad(i << 2) : XTile<KCAP>::kDummy)) = v;
+    } else {
+        float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        am = fmaxf(am, __shfl_xor(am, 1, kWave));
+        am = fmaxf(am, __shfl_xor(am, 2, kWave));
+        am = fmaxf(am, __shfl_xor(am, 4, kWave));
+        const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, am) >> 23) & 0xffu);
+        const int e = min(max(eb - 127, -122), 127);
+        const float s = ldexpf(1.0f, 5 - e);
+        const float t[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
+        uint32_t p0 = 0, p1 = 0, p2 = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float q0 = rintf(t[j]);
+            const float u = (t[j] - q0) * 128.0f;
+            const float q1 = rintf(u);
+            const float q2 = rintf((u - q1) * 128.0f);
+            p0 |= (static_cast<uint32_t>(static_cast<int>(q0)) & 0xffu) << (8 * j);
+            p1 |= (static_cast<uint32_t>(static_cast<int>(q1)) & 0xffu) << (8 * j);
+            p2 |= (static_cast<uint32_t>(static_cast<int>(q2)) & 0xffu) << (8 * j);
+        }
+        uint32_t* w = reinterpret_cast<uint32_t*>(xl);
+        const int slot = valid ? i : XQTile<KCAP>::kDummy;
+        w[slot] = p0;
+        w[valid ? KCAP / 4 + i : XQTile<KCAP>::kDummy + 1] = p1;
+        w[valid ? KCAP / 2 + i : XQTile<KCAP>::kDummy + 2] = p2;
+        xl[(valid && (i & 7) == 0) ? XQTile<KCAP>::kScales + (i >> 3) : XQTile<KCAP>::kDummy + 3] =
+            ldexpf(1.0f, e - 5);
+    }
+}
+
+template <int KCAP, int NX, bool XQ = false>
 __device__ __forceinline__ void xstore(const XRegs<NX>& r, int k, float* xl, float* xs) {
     const int n4 = k >> 2;
 #pragma unroll
@@ -103,7 +152,7 @@ __device__ __forceinline__ void xstore(const XRegs<NX>& r, int k, float* xl, flo
         v.y = valid ? v.y : 0.0f;
         v.z = valid ? v.z : 0.0f;
         v.w = valid ? v.w : 0.0f;
-        *reinterpret_cast<float4*>(xl + (valid ? xpad(i << 2) : XTile<KCAP>::kDummy)) = v;
+        xput<KCAP, XQ>(v, i, valid, xl);
         float s = (v.x + v.y) + (v.z + v.w);
         s += __shfl_xor(s, 1, kWave);
         s += __shfl_xor(s, 2, kWave);
@@ -118,7 +167,7 @@ __device__ __forceinline__ void xstore(const XRegs<NX>& r, int k, float* xl, flo
 // costs no pass of its own.  Every workgroup reduces the same per-wave partials
 // in the same order, so all of them use the same scale.  `red` holds one float
 // per wave.
-template <int KCAP, int NX, int WAVES>
+template <int KCAP, int NX, int WAVES, bool XQ = false>
 __device__ __forceinline__ float xstore_norm(const XRegs<NX>& r, const XRegs<NX>& g, int k, float eps, float* xl,
                                              float* xs, float* red) {
     const int n4 = k >> 2;
@@ -140,7 +189,7 @@ __device__ __forceinline__ float xstore_norm(const XRegs<NX>& r, const XRegs<NX>
         v.y *= g.v[j].y;
         v.z *= g.v[j].z;
         v.w *= g.v[j].w;
-        *reinterpret_cast<float4*>(xl + (valid ? xpad(i << 2) : XTile<KCAP>::kDummy)) = v;
+        xput<KCAP, XQ>(v, i, valid, xl);
         float s = (v.x + v.y) + (v.z + v.w);
         s += __shfl_xor(s, 1, kWave);
         s += __shfl_xor(s, 2, kWave);
@@ -417,6 +466,41 @@ __device__ __forceinline__ void compute_float(const Frag<QT, RT>& f, const float
     }
 }
 
+// q4_0 against the int8 planes (XQ): per plane the 32 nibble-times-q products
+// by v_dot4_i32_i8 (nibbles 0..15 are valid int8), the planes combined in
+// fp32, the nibble bias -8 through the block's fp32 run sums.
+template <int RT, int KCAP>
+__device__ __forceinline__ void compute_q4_0_xq(const Frag<Q4_0, RT>& f, const float* xl, const float* xs, int c,
+                                                bool valid, float* acc) {
+    const int8_t* xq = reinterpret_cast<const int8_t*>(xl);
+    const float d1 = xl[XQTile<KCAP>::kScales + c];
+    const float xsum = xs[2 * c] + xs[2 * c + 1];
+    uint4 pl[3], ph[3];
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        pl[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + 32 * c);
+        ph[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + 32 * c + 16);
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t wv = (&f.q[r].x)[i];
+            const int lo = static_cast<int>(wv & 0x0F0F0F0Fu), hi = static_cast<int>((wv >> 4) & 0x0F0F0F0Fu);
+            s0 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&pl[0].x)[i]), s0, false);
+            s0 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&ph[0].x)[i]), s0, false);
+            s1 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&pl[1].x)[i]), s1, false);
+            s1 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&ph[1].x)[i]), s1, false);
+            s2 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&pl[2].x)[i]), s2, false);
+            s2 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&ph[2].x)[i]), s2, false);
+        }
+        const float v =
+            fmaf(static_cast<float>(s2), 1.0f / 16384.0f, fmaf(static_cast<float>(s1), 1.0f / 128.0f, static_cast<float>(s0)));
+        acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, fmaf(v, d1, -8.0f * xsum), acc[r]);
+    }
+}
+
 template <int RT>
 __device__ __forceinline__ void compute_q8_0(const Frag<Q8_0, RT>& f, const float* xl, const float*, int c,
                                              bool valid, float* acc) {
@@ -549,10 +633,12 @@ __device__ __forceinline__ void compute_q6_k(const Frag<Q6_K, RT>& f, const floa
     }
 }
 
-template <int QT, int RT>
+template <int QT, int RT, int KCAP = 0, bool XQ = false>
 __device__ __forceinline__ void compute_frag(const Frag<QT, RT>& f, const float* xl, const float* xs, int c,
                                              bool valid, float* acc) {
-    if constexpr (QT == Q4_0) compute_q4_0<RT>(f, xl, xs, c, valid, acc);
+    static_assert(!XQ || QT == Q4_0, "the int8-plane x is implemented for q4_0");
+    if constexpr (QT == Q4_0 && XQ) compute_q4_0_xq<RT, KCAP>(f, xl, xs, c, valid, acc);
+    if constexpr (QT == Q4_0 && !XQ) compute_q4_0<RT>(f, xl, xs, c, valid, acc);
     if constexpr (QT == Q4_1) compute_q4_1<RT>(f, xl, xs, c, valid, acc);
     if constexpr (is_float_type(QT)) compute_float<QT, RT>(f, xl, c, valid, acc);
     if constexpr (QT == Q8_0) compute_q8_0<RT>(f, xl, xs, c, valid, acc);
@@ -733,13 +819,13 @@ __device__ __forceinline__ void load_group(Frag<QT, RT> (&f)[STEPS], const TileR
 
 // FENCE: a scheduling barrier after each step keeps the compiler from
 // hoisting later steps' LDS reads (which costs registers, hence occupancy).
-template <int QT, int RT, int STEPS, bool EXACT, bool FENCE = false>
+template <int QT, int RT, int STEPS, bool EXACT, bool FENCE = false, int KCAP = 0, bool XQ = false>
 __device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], const float* xl, const float* xs,
                                               int C, int cb, int lane, float* acc) {
 #pragma unroll
     for (int s = 0; s < STEPS; s++) {
         const int c = cb + lane + s * kWave;
-        if (EXACT || cb + s * kWave < C) compute_frag<QT, RT>(f[s], xl, xs, min(c, C - 1), c < C, acc);
+        if (EXACT || cb + s * kWave < C) compute_frag<QT, RT, KCAP, XQ>(f[s], xl, xs, min(c, C - 1), c < C, acc);
         if constexpr (FENCE) __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -761,7 +847,7 @@ __device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], co
 // clamped to a valid tile and dropped), stores with reduce_store_all.
 // FENCE: see compute_group.
 template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT, int PRO, int EPI, bool PF = false,
-          bool FENCE = false>
+          bool FENCE = false, bool XQ = false>
 __device__ __forceinline__ void gemv(const GemvArgs& a) {
     __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
     __shared__ float xs[XTile<KCAP>::kRuns + 1];
@@ -785,8 +871,8 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
     TileRows<RT> tr = tile_rows<RT, PAIR>(a, min(tile, ntiles - 1));
     load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, 0, lane);
     float scale = 1.0f;
-    if constexpr (PRO == PRO_NORM) scale = xstore_norm<KCAP, NX, WAVES>(xr, gr, k, a.eps, xl, xs, red);
-    else xstore<KCAP>(xr, k, xl, xs);
+    if constexpr (PRO == PRO_NORM) scale = xstore_norm<KCAP, NX, WAVES, XQ>(xr, gr, k, a.eps, xl, xs, red);
+    else xstore<KCAP, NX, XQ>(xr, k, xl, xs);
 
     float acc[RT];
     if constexpr (PF) {
@@ -804,7 +890,7 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
             }
 #pragma unroll
             for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-            compute_group<QT, RT, STEPS, EXACT, FENCE>(f, xl, xs, C, 0, lane, acc);
+            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, 0, lane, acc);
             reduce_store_all<RT, EPI>(acc, a, t, scale, lane, rf);
             if (t1 >= ntiles) break;
             t = t1 + tstride;
@@ -815,18 +901,18 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
             }
 #pragma unroll
             for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-            compute_group<QT, RT, STEPS, EXACT, FENCE>(g, xl, xs, C, 0, lane, acc);
+            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(g, xl, xs, C, 0, lane, acc);
             reduce_store_all<RT, EPI>(acc, a, t1, scale, lane, rg);
         }
         return;
     }
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-    compute_group<QT, RT, STEPS, EXACT>(f, xl, xs, C, 0, lane, acc);
+    compute_group<QT, RT, STEPS, EXACT, false, KCAP, XQ>(f, xl, xs, C, 0, lane, acc);
     if constexpr (!EXACT) {
         for (int cb = GROUP; cb < C; cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute_group<QT, RT, STEPS, EXACT>(f, xl, xs, C, cb, lane, acc);
+            compute_group<QT, RT, STEPS, EXACT, false, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
         }
     }
     if (tile < ntiles) reduce_store<RT, EPI>(acc, a, tile, scale, lane);
@@ -836,7 +922,7 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
         for (int r = 0; r < RT; r++) acc[r] = 0.0f;
         for (int cb = 0; cb < (EXACT ? 1 : C); cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute_group<QT, RT, STEPS, EXACT>(f, xl, xs, C, cb, lane, acc);
+            compute_group<QT, RT, STEPS, EXACT, false, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
         }
         reduce_store<RT, EPI>(acc, a, tile, scale, lane);
     }
@@ -939,12 +1025,17 @@ __device__ __forceinline__ void gemv_multi(const GemvMultiArgs& a) {
     extern "C" __global__ void __launch_bounds__(256) NAME(GemvArgs a) {            \
         gemv<QT, KCAP, 4, RT, STEPS, EXACT, true, PRO, EPI>(a);                     \
     }
-// Prefetching instances zlm_gemv_<quant>_<form>_s<STEPS>_pf: WAVES waves per
-// workgroup, launched at 8 waves per CU (the host reads the block size from
-// the kernel's launch bounds).
+// Prefetching instances zlm_gemv_<quant>_<form>_s<STEPS>_pf (launched at 8
+// waves per CU) and ..._pfw16 (16 waves per CU): WAVES waves per workgroup
+// (the host reads the block size from the kernel's launch bounds); XQ stages
+// x as int8 planes (q4_0).
 #define ZLM_GEMVX_PF(NAME, QT, KCAP, WAVES, RT, STEPS, PRO, EPI, FENCE)                       \
     extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {              \
         gemv<QT, KCAP, WAVES, RT, STEPS, true, true, PRO, EPI, true, FENCE>(a);             \
+    }
+#define ZLM_GEMVX_PFQ(NAME, QT, KCAP, WAVES, RT, STEPS, PRO, EPI, FENCE)                      \
+    extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {              \
+        gemv<QT, KCAP, WAVES, RT, STEPS, true, true, PRO, EPI, true, FENCE, true>(a);       \
     }
 #define ZLM_GEMVX_FORMS(QN, QT, KCAP, STEPS, EXACT, SFX)                                           \
     ZLM_GEMVX(zlm_gemv_##QN##_pair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_PLAIN, EPI_PAIR)           \

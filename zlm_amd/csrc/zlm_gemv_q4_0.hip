@@ -7,12 +7,16 @@ ZLM_GEMV_Q4(q4_0, Q4_0)
 ZLM_GEMVX_Q4(q4_0, Q4_0)
 ZLM_GEMVX_FORMS(q4_0, Q4_0, 16384, 6, true, s6)
 
-// Prefetching forms for the decode-step shapes (measured on gfx950 against
-// the forms above: gate_up 12288 x 4096 15.3 -> 13.1 us with 8-wave
-// workgroups; down 4096 x 12288 12.9 -> 10.4 us with a 12288-float x, so two
-// workgroups fit a CU's LDS).
-ZLM_GEMVX_PF(zlm_gemv_q4_0_pair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PAIR, false)
-ZLM_GEMVX_PF(zlm_gemv_q4_0_normpair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_NORM, EPI_PAIR, false)
-ZLM_GEMVX_PF(zlm_gemv_q4_0_resid_s6_pf, Q4_0, 12288, 4, 1, 6, PRO_PLAIN, EPI_RESID, true)
+// Prefetching forms for the decode-step shapes, x staged as int8 planes
+// (v_dot4 on the nibbles), measured on gfx950 against the forms above:
+// gate_up 12288 x 4096 with 8-wave workgroups at 8 waves per CU (16.3 ->
+// 13.5 us in the sweep harness), down 4096 x 12288 with 16-wave workgroups at
+// one per CU (10.4 -> 9.6 us), the normed q;k;v 6144 x 4096 with 8-wave
+// workgroups at 16 waves per CU (6.4 -> 6.0 us).  4096-row launches (o, C0)
+// stay plain: their workgroups have too few rows to repay the quantization.
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_pair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PAIR, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_normpair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_NORM, EPI_PAIR, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_resid_s6_pfw16, Q4_0, 12288, 16, 1, 6, PRO_PLAIN, EPI_RESID, true)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s2_pfw16, Q4_0, 4096, 8, 1, 2, PRO_NORM, EPI_PLAIN, false)
 
 ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)

@@ -576,8 +576,15 @@ const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint3
     const int rt = form_is_pair(form) ? 2 : 1;
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
-    snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d_pf", qn, kFormNames[form], steps);
-    if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 8, true)) return g;
+    // prefetching instances: the name suffix gives the grid's waves per CU
+    const struct {
+        const char* suffix;
+        int waves_per_cu;
+    } pf[] = {{"_pf", 8}, {"_pfw16", 16}};
+    for (const auto& v : pf) {
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d%s", qn, kFormNames[form], steps, v.suffix);
+        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, v.waves_per_cu, true)) return g;
+    }
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d", qn, kFormNames[form], steps);
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_g", qn, kFormNames[form]);
