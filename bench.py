@@ -35,6 +35,8 @@ from zlm_amd import synth  # noqa: E402
 
 PEAK_GBPS = 8000.0
 MALL_DEFEAT_BYTES = 512 * 1024 * 1024
+# The kernel the host picks for the 12288 x 4096 Q8_0 gate/up GEMV (the roofline kernel).
+ROOFLINE_KERNEL = "zlm_gemv_q8_0_r1_s4"
 METRIC = "quant GEMV HBM GB/s (% of 8 TB/s peak); decode tok/s, Qwen3-8B-shape Q4_0 bs=1"
 
 
@@ -177,7 +179,7 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             t = json.load(f)
-        traffic = t.get("zlm_gemv_q8_0_r1_s4", {}).get("bytes_per_launch")
+        traffic = t.get(ROOFLINE_KERNEL, {}).get("bytes_per_launch")
 
     cpu = None
     if not args.no_cpu:
@@ -282,7 +284,7 @@ def main():
         "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "zlm_gemv_q8_0_r1_s4 (gate/up 12288x4096)",
+            "kernel": f"{ROOFLINE_KERNEL} (gate/up 12288x4096)",
             "achieved": round(gu_gbps, 1),
             "peak": PEAK_GBPS,
             "unit": "GB/s",

@@ -399,22 +399,30 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
     return it->second.fn ? &it->second : nullptr;
 }
 
-// The GEMV kernel for a shape: for a 1-row tile and fewer than 65536 rows
-// the prefetching instance of the exact step count if the quant has one
-// (zlm_gemv_<quant>_r1_s<steps>_pf); else the instance whose step count
-// equals ceil(chunks per row / 64) with the requested row tile, else with a
-// 1-row tile, else the generic bounded instance.  Chunks per row:
-// k / chunk_elems (k/16 for q8_0, k/32 for q4_0, q4_1 and the K-quants, k/8
-// for f16 / bf16, k/4 for f32).  Tall launches (the lm_heads) keep the plain
-// instances at 8 workgroups per CU (gemv_grid).
+// The prefetching instances' name suffixes and the grid's waves per CU.
+struct PfSuffix {
+    const char* suffix;
+    int waves_per_cu;
+};
+constexpr PfSuffix kPfSuffixes[] = {{"_pf", 8}, {"_pfw16", 16}};
+
+// The GEMV kernel for a shape: for a 1-row tile the prefetching instance of
+// the exact step count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_pf
+// or _pfw16; q6_k's only below 65536 rows, where it was measured); else the
+// instance whose step count equals ceil(chunks per row / 64) with the
+// requested row tile, else with a 1-row tile, else the generic bounded
+// instance.  Chunks per row: k / chunk_elems (k/16 for q8_0, k/32 for q4_0,
+// q4_1 and the K-quants, k/8 for f16 / bf16, k/4 for f32).
 const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows) {
     const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
-    if (rt == 1 && rows < 65536) {
-        snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d_pf", qn, steps);
-        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps, 8, true)) return g;
+    if (rt == 1 && (rows < 65536 || qi->type != ZLM_GGML_Q6_K)) {
+        for (const PfSuffix& v : kPfSuffixes) {
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d%s", qn, steps, v.suffix);
+            if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps, v.waves_per_cu, true)) return g;
+        }
     }
     snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d", qn, rt, steps);
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
@@ -576,12 +584,7 @@ const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint3
     const int rt = form_is_pair(form) ? 2 : 1;
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
-    // prefetching instances: the name suffix gives the grid's waves per CU
-    const struct {
-        const char* suffix;
-        int waves_per_cu;
-    } pf[] = {{"_pf", 8}, {"_pfw16", 16}};
-    for (const auto& v : pf) {
+    for (const PfSuffix& v : kPfSuffixes) {
         snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d%s", qn, kFormNames[form], steps, v.suffix);
         if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, v.waves_per_cu, true)) return g;
     }
