@@ -208,3 +208,45 @@ def test_device_forms_match_oracle(dev, qt, rows, k):
         dev.dev_free(p)
     dev.free_resident(rw)
     dev.free_resident(ru)
+
+
+# Row counts around the split-K kernels' tile and grid sizes (2-row tiles for
+# q8_0, 4-row for q4_0, one workgroup per CU): fewer rows than a tile, a
+# ragged last tile, fewer tiles than CUs, one tile past a whole grid, and
+# several ring turns per workgroup.
+SPLIT_ROWS = [1, 3, 5, 255, 513, 1028, 2051, 3000]
+
+
+@pytest.mark.parametrize("qt", [synth.Q8_0, synth.Q4_0], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("rows", SPLIT_ROWS)
+def test_split_k_shapes_match_oracle(dev, qt, rows):
+    """The k = 12288 GEMVs run split-K: the plain form and the residual form
+    (also in place, res aliasing y) against the oracle, and two launches
+    agree bit for bit (the waves' partials meet in a fixed order)."""
+    k = 12288
+    _say(f"split-k {NAMES[qt]} rows={rows}")
+    w = synth.weights(qt, rows, k, seed=rows + 901)
+    x = synth.activation(rows + 902, k)
+    res = synth.activation(rows + 903, rows)
+    rw = dev.upload_resident(w)
+    xd, resd, yd = _dev_vec(dev, x), _dev_vec(dev, res), dev.dev_malloc(rows * 4)
+    q = zd.quant(qt)
+    want = oracle.matvec(qt, w, k, rows, x)
+    got = np.zeros(rows, np.float32)
+    again = np.zeros(rows, np.float32)
+    assert dev.gemv_op_enqueue(zd.FORM_PLAIN, q, rw, rows, k, xd, yd), dev.last_error()
+    dev.dev_download(got, yd)
+    assert rel_l2(got, want) <= REL_L2
+    assert dev.gemv_op_enqueue(zd.FORM_PLAIN, q, rw, rows, k, xd, yd), dev.last_error()
+    dev.dev_download(again, yd)
+    np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
+    assert dev.gemv_op_enqueue(zd.FORM_RESID, q, rw, rows, k, xd, yd, res=resd), dev.last_error()
+    dev.dev_download(got, yd)
+    assert rel_l2(got, res + want) <= REL_L2
+    dev.dev_upload(yd, res)
+    assert dev.gemv_op_enqueue(zd.FORM_RESID, q, rw, rows, k, xd, yd, res=yd), dev.last_error()
+    dev.dev_download(again, yd)
+    np.testing.assert_array_equal(again.view(np.uint32), got.view(np.uint32))
+    for p in (xd, resd, yd):
+        dev.dev_free(p)
+    dev.free_resident(rw)

@@ -128,10 +128,12 @@ def test_async_burst_batch_agree(dev):
         dev.free_resident(res)
 
 
-@pytest.mark.parametrize("qt,k", [(synth.Q8_0, 4096), (synth.Q4_K, 3840), (synth.F16, 1024), (synth.Q4_1, 12288)],
-                         ids=["q8_0", "q4_k", "f16", "q4_1"])
+@pytest.mark.parametrize("qt,k", [(synth.Q8_0, 4096), (synth.Q4_K, 3840), (synth.F16, 1024), (synth.Q4_1, 12288),
+                                  (synth.Q8_0, 12288), (synth.Q4_0, 12288)],
+                         ids=["q8_0", "q4_k", "f16", "q4_1", "q8_0_split", "q4_0_split"])
 def test_batch_one_launch_matches_single_ops(dev, qt, k):
-    """A same-quant batch runs as one launch of the batch kernel; every op's
+    """A same-quant batch runs as one launch of the batch kernel (op by op
+    where the single op runs split-K, k = 12288 for q8_0 / q4_0); every op's
     rows equal the single-op GEMV's bit for bit (same per-lane order and
     reduction), including eight ops of ragged row counts."""
     _say(f"batch {NAMES[qt]} k={k}")

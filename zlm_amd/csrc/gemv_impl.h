@@ -106,6 +106,28 @@ struct XQTile {
     static_assert(kDummy + 4 <= XTile<KCAP>::kFloats, "the int8 planes fit the fp32 tile");
 };
 
+// The block exponent e of a block whose largest magnitude is am.
+__device__ __forceinline__ int xq_exp(float am) {
+    const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, am) >> 23) & 0xffu);
+    return min(max(eb - 127, -122), 127);
+}
+
+// The three int8 planes of four x values at block scale s, one byte each.
+__device__ __forceinline__ void xq_planes(float4 v, float s, uint32_t& p0, uint32_t& p1, uint32_t& p2) {
+    const float t[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
+    p0 = p1 = p2 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float q0 = rintf(t[j]);
+        const float u = (t[j] - q0) * 128.0f;
+        const float q1 = rintf(u);
+        const float q2 = rintf((u - q1) * 128.0f);
+        p0 |= (static_cast<uint32_t>(static_cast<int>(q0)) & 0xffu) << (8 * j);
+        p1 |= (static_cast<uint32_t>(static_cast<int>(q1)) & 0xffu) << (8 * j);
+        p2 |= (static_cast<uint32_t>(static_cast<int>(q2)) & 0xffu) << (8 * j);
+    }
+}
+
 template <int KCAP, bool XQ>
 __device__ __forceinline__ void xput(float4 v, int i, bool valid, float* xl) {
     if constexpr (!XQ) {
@@ -115,21 +137,9 @@ __device__ __forceinline__ void xput(float4 v, int i, bool valid, float* xl) {
         am = fmaxf(am, __shfl_xor(am, 1, kWave));
         am = fmaxf(am, __shfl_xor(am, 2, kWave));
         am = fmaxf(am, __shfl_xor(am, 4, kWave));
-        const int eb = static_cast<int>((__builtin_bit_cast(uint32_t, am) >> 23) & 0xffu);
-        const int e = min(max(eb - 127, -122), 127);
-        const float s = ldexpf(1.0f, 5 - e);
-        const float t[4] = {v.x * s, v.y * s, v.z * s, v.w * s};
-        uint32_t p0 = 0, p1 = 0, p2 = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float q0 = rintf(t[j]);
-            const float u = (t[j] - q0) * 128.0f;
-            const float q1 = rintf(u);
-            const float q2 = rintf((u - q1) * 128.0f);
-            p0 |= (static_cast<uint32_t>(static_cast<int>(q0)) & 0xffu) << (8 * j);
-            p1 |= (static_cast<uint32_t>(static_cast<int>(q1)) & 0xffu) << (8 * j);
-            p2 |= (static_cast<uint32_t>(static_cast<int>(q2)) & 0xffu) << (8 * j);
-        }
+        const int e = xq_exp(am);
+        uint32_t p0, p1, p2;
+        xq_planes(v, ldexpf(1.0f, 5 - e), p0, p1, p2);
         uint32_t* w = reinterpret_cast<uint32_t*>(xl);
         const int slot = valid ? i : XQTile<KCAP>::kDummy;
         w[slot] = p0;
@@ -466,21 +476,13 @@ __device__ __forceinline__ void compute_float(const Frag<QT, RT>& f, const float
     }
 }
 
-// q4_0 against the int8 planes (XQ): per plane the 32 nibble-times-q products
-// by v_dot4_i32_i8 (nibbles 0..15 are valid int8), the planes combined in
-// fp32, the nibble bias -8 through the block's fp32 run sums.
-template <int RT, int KCAP>
-__device__ __forceinline__ void compute_q4_0_xq(const Frag<Q4_0, RT>& f, const float* xl, const float* xs, int c,
-                                                bool valid, float* acc) {
-    const int8_t* xq = reinterpret_cast<const int8_t*>(xl);
-    const float d1 = xl[XQTile<KCAP>::kScales + c];
-    const float xsum = xs[2 * c] + xs[2 * c + 1];
-    uint4 pl[3], ph[3];
-#pragma unroll
-    for (int p = 0; p < 3; p++) {
-        pl[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + 32 * c);
-        ph[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + 32 * c + 16);
-    }
+// q4_0 against the int8 planes (XQ) of one block position for RT rows: per
+// plane the 32 nibble-times-q products by v_dot4_i32_i8 (nibbles 0..15 are
+// valid int8), the planes combined in fp32, the nibble bias -8 through the
+// block's fp32 x sum.  pl / ph: planes of elements 0..15 / 16..31; d1 = 1/s.
+template <int RT>
+__device__ __forceinline__ void q4_0_xq_rows(const Frag<Q4_0, RT>& f, const uint4 (&pl)[3], const uint4 (&ph)[3],
+                                             float d1, float xsum, bool valid, float* acc) {
 #pragma unroll
     for (int r = 0; r < RT; r++) {
         int s0 = 0, s1 = 0, s2 = 0;
@@ -499,6 +501,22 @@ __device__ __forceinline__ void compute_q4_0_xq(const Frag<Q4_0, RT>& f, const f
             fmaf(static_cast<float>(s2), 1.0f / 16384.0f, fmaf(static_cast<float>(s1), 1.0f / 128.0f, static_cast<float>(s0)));
         acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, fmaf(v, d1, -8.0f * xsum), acc[r]);
     }
+}
+
+// q4_0 against the XQ planes of the LDS tile (block c).
+template <int RT, int KCAP>
+__device__ __forceinline__ void compute_q4_0_xq(const Frag<Q4_0, RT>& f, const float* xl, const float* xs, int c,
+                                                bool valid, float* acc) {
+    const int8_t* xq = reinterpret_cast<const int8_t*>(xl);
+    const float d1 = xl[XQTile<KCAP>::kScales + c];
+    const float xsum = xs[2 * c] + xs[2 * c + 1];
+    uint4 pl[3], ph[3];
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        pl[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + 32 * c);
+        ph[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + 32 * c + 16);
+    }
+    q4_0_xq_rows<RT>(f, pl, ph, d1, xsum, valid, acc);
 }
 
 template <int RT>
@@ -908,11 +926,11 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
     }
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-    compute_group<QT, RT, STEPS, EXACT, false, KCAP, XQ>(f, xl, xs, C, 0, lane, acc);
+    compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, 0, lane, acc);
     if constexpr (!EXACT) {
         for (int cb = GROUP; cb < C; cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute_group<QT, RT, STEPS, EXACT, false, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
+            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
         }
     }
     if (tile < ntiles) reduce_store<RT, EPI>(acc, a, tile, scale, lane);
@@ -922,7 +940,7 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
         for (int r = 0; r < RT; r++) acc[r] = 0.0f;
         for (int cb = 0; cb < (EXACT ? 1 : C); cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute_group<QT, RT, STEPS, EXACT, false, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
+            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
         }
         reduce_store<RT, EPI>(acc, a, tile, scale, lane);
     }
@@ -997,6 +1015,261 @@ __device__ __forceinline__ void gemv_multi(const GemvMultiArgs& a) {
     }
 }
 
+// ---- split-K GEMV (short, wide matrices) -------------------------------------
+// The FFN down projection (k = 12288 over 4096 rows) leaves the one-wave-per-
+// row kernel one wave per SIMD: a row's 12 chunk steps of fragments take ~300
+// registers, so few rows' loads are in flight.  Here the W waves of a
+// workgroup share each tile of RT rows: wave w covers chunk steps
+// [w*SPL, (w+1)*SPL) of every row (lane l: chunks (w*SPL + s)*64 + l, s <
+// SPL), holds x of exactly those chunks in registers for the whole launch --
+// x is read once per workgroup and never staged in LDS -- and the W partial
+// sums of a row meet in LDS, one barrier per tile, added in wave order.  A
+// wave loads its next tile while it computes the current one.  Every wave of
+// the workgroup stores the tile's rows (the same values), so the stores need
+// no branch.  Chunks past the row's end (W*SPL*64 > chunks) are clamped
+// loads with zero x and a zero scale.
+template <int QT, bool XQ>
+struct XChunk;
+template <>
+struct XChunk<Q8_0, false> {  // the chunk's 16 x values
+    float v[16];
+};
+template <>
+struct XChunk<Q4_0, true> {  // the block's 32 x values as int8 planes (XQTile's encoding)
+    uint4 pl[3];             // plane p of elements 0..15
+    uint4 ph[3];             // plane p of elements 16..31
+    float d1;                // 1/s
+    float sum;               // the fp32 sum of the 32 values
+};
+
+template <int QT>
+constexpr int sk_chunk_elems() {
+    static_assert(QT == Q8_0 || QT == Q4_0, "split-K is implemented for q8_0 and q4_0");
+    return QT == Q8_0 ? 16 : 32;
+}
+
+template <int QT>
+struct XRaw {
+    float4 v[sk_chunk_elems<QT>() / 4];
+};
+
+template <int QT>
+__device__ __forceinline__ void xraw_load(const float* __restrict__ x, int c, XRaw<QT>& r) {
+    constexpr int N = sk_chunk_elems<QT>() / 4;
+    const float4* p = reinterpret_cast<const float4*>(x) + static_cast<size_t>(c) * N;
+#pragma unroll
+    for (int i = 0; i < N; i++) r.v[i] = p[i];
+}
+
+__device__ __forceinline__ float4 zero_unless(float4 v, bool valid) {
+    return valid ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
+__device__ __forceinline__ XChunk<Q8_0, false> make_xchunk(const XRaw<Q8_0>& r, bool valid) {
+    XChunk<Q8_0, false> x;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 v = zero_unless(r.v[i], valid);
+        x.v[4 * i] = v.x;
+        x.v[4 * i + 1] = v.y;
+        x.v[4 * i + 2] = v.z;
+        x.v[4 * i + 3] = v.w;
+    }
+    return x;
+}
+
+// The block's planes exactly as xput forms them in LDS (same amax, exponent
+// and rounding), and its sum in xstore's order (float4 sums, then pairs).
+__device__ __forceinline__ XChunk<Q4_0, true> make_xchunk(const XRaw<Q4_0>& r, bool valid) {
+    XChunk<Q4_0, true> x;
+    float4 v[8];
+    float am = 0.0f, q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        v[i] = zero_unless(r.v[i], valid);
+        am = fmaxf(am, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        q[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    const int e = xq_exp(am);
+    const float s = ldexpf(1.0f, 5 - e);
+    x.d1 = ldexpf(1.0f, e - 5);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        xq_planes(v[i], s, (&x.pl[0].x)[i], (&x.pl[1].x)[i], (&x.pl[2].x)[i]);
+        xq_planes(v[4 + i], s, (&x.ph[0].x)[i], (&x.ph[1].x)[i], (&x.ph[2].x)[i]);
+    }
+    x.sum = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+    return x;
+}
+
+template <int RT>
+__device__ __forceinline__ void dot_xchunk(const Frag<Q8_0, RT>& f, const XChunk<Q8_0, false>& x, bool valid,
+                                           float* acc) {
+    float s[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) s[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const uint32_t wv = (&f.q[r].x)[i];
+            s[r] = fmaf(sb(wv, 0), x.v[4 * i], s[r]);
+            s[r] = fmaf(sb(wv, 1), x.v[4 * i + 1], s[r]);
+            s[r] = fmaf(sb(wv, 2), x.v[4 * i + 2], s[r]);
+            s[r] = fmaf(sb(wv, 3), x.v[4 * i + 3], s[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, s[r], acc[r]);
+}
+
+template <int RT>
+__device__ __forceinline__ void dot_xchunk(const Frag<Q4_0, RT>& f, const XChunk<Q4_0, true>& x, bool valid,
+                                           float* acc) {
+    q4_0_xq_rows<RT>(f, x.pl, x.ph, x.d1, x.sum, valid, acc);
+}
+
+// The loads of tile t (RT consecutive rows, clamped) at the lane's chunks.
+template <int QT, int RT, int SPL>
+__device__ __forceinline__ void sk_load(Frag<QT, RT> (&f)[SPL], const GemvArgs& a, uint32_t t, const int (&cs)[SPL]) {
+    TileRows<RT> tr;
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        tr.w[r] = a.w0;
+        tr.d[r] = a.d0;
+        tr.r[r] = min(t * RT + static_cast<uint32_t>(r), a.rows - 1);
+    }
+#pragma unroll
+    for (int s = 0; s < SPL; s++) load_frag<QT, RT, true>(f[s], tr, a.nb, cs[s]);
+}
+
+template <int RT>
+constexpr int sk_log() {
+    return (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
+}
+
+// The output row of this lane's fragment row after the butterfly (clamped).
+template <int RT>
+__device__ __forceinline__ uint32_t sk_row(const GemvArgs& a, uint32_t t, int lane) {
+    return min(t * RT + static_cast<uint32_t>(lane >> (6 - sk_log<RT>())), a.rows - 1);
+}
+
+// Reduce the wave's RT partials (the transposing butterfly of reduce_store,
+// selecting through bit masks so the compiler keeps v in registers), meet
+// the other waves' partials in red, store the tile.  EPI_RESID: the residual
+// rides in wave 0's partial, so every wave has its residual load back before
+// the barrier -- y may alias res, and the tile's stores follow the barrier.
+template <int W, int RT, int EPI>
+__device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvArgs& a, uint32_t t, int lane,
+                                          int wid, float rv) {
+    constexpr int LOG = sk_log<RT>();
+#pragma unroll
+    for (int st = 0; st < LOG; st++) {
+        const int half = (RT >> st) >> 1;
+        const int bit = 32 >> st;
+        const uint32_t m = (lane & bit) != 0 ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int i = 0; i < half; i++) {
+            const uint32_t lo = __builtin_bit_cast(uint32_t, v[i]);
+            const uint32_t hi = __builtin_bit_cast(uint32_t, v[half + i]);
+            const float keep = __builtin_bit_cast(float, (hi & m) | (lo & ~m));
+            const float send = __builtin_bit_cast(float, (lo & m) | (hi & ~m));
+            v[i] = keep + __shfl_xor(send, bit, kWave);
+        }
+    }
+    float s = v[0];
+#pragma unroll
+    for (int off = 32 >> LOG; off >= 1; off >>= 1) s += __shfl_xor(s, off, kWave);
+    if constexpr (EPI == EPI_RESID) s += wid == 0 ? rv : 0.0f;
+    const int fr = lane >> (6 - LOG);
+    red[fr][wid] = s;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; w++) tot += red[fr][w];
+    a.y[sk_row<RT>(a, t, lane)] = tot;
+}
+
+// y = W.x (EPI_PLAIN) or res + W.x (EPI_RESID).  The host launches at most
+// ceil(rows/RT) workgroups and W*SPL == ceil(chunks per row / 64); EXACT
+// instances require chunks per row == 64*W*SPL (no clamping).  A workgroup
+// walks tiles blockIdx + j*gridDim with NB fragment sets in a ring: while it
+// computes one tile the loads of the next NB-1 are in flight (tiles past the
+// end are clamped loads, dropped).  The exit is uniform over the workgroup,
+// so every wave meets every barrier; consecutive tiles use different red
+// buffers, so one barrier per tile suffices.  Scheduling barriers keep each
+// tile's loads ahead of its compute and the compute ahead of the reduction:
+// without them the compiler interleaved the three and reused a prefetch
+// destination register, which costs a wait for every load in flight
+// (measured on gfx950, q8_0 4096 x 12288: 12.0 vs 10.5 us).
+template <int QT, int W, int RT, int SPL, int EPI, bool XQ, int NB, bool EXACT>
+__device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
+    static_assert(EPI == EPI_PLAIN || EPI == EPI_RESID, "split-K forms: plain, resid");
+    static_assert(XQ == (QT == Q4_0), "q4_0 runs on the int8 planes, q8_0 on fp32 x");
+    static_assert(NB >= 2, "a ring of at least two fragment sets");
+    __shared__ float red[NB][RT][W];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wid = static_cast<int>(threadIdx.x / kWave);
+    const int C = chunks_per_row<QT>(a.nb);
+    const uint32_t ntiles = (a.rows + RT - 1) / RT;
+    const uint32_t G = gridDim.x;
+    int cs[SPL];
+    bool ok[SPL];
+    XRaw<QT> xr[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; s++) {
+        const int c = (wid * SPL + s) * kWave + lane;
+        ok[s] = EXACT || c < C;
+        cs[s] = EXACT ? c : min(c, C - 1);
+        xraw_load<QT>(a.x, cs[s], xr[s]);
+    }
+    uint32_t t = blockIdx.x;
+    Frag<QT, RT> f[NB][SPL];
+    float rv[NB];
+    auto issue = [&](int b, uint32_t ahead) {
+        const uint32_t tc =
+            static_cast<uint32_t>(min(static_cast<uint64_t>(t) + static_cast<uint64_t>(ahead) * G,
+                                      static_cast<uint64_t>(ntiles - 1)));
+        sk_load<QT, RT, SPL>(f[b], a, tc, cs);
+        rv[b] = EPI == EPI_RESID ? a.res[sk_row<RT>(a, tc, lane)] : 0.0f;
+    };
+#pragma unroll
+    for (int j = 0; j < NB - 1; j++) issue(j, static_cast<uint32_t>(j));
+    XChunk<QT, XQ> xc[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; s++) xc[s] = make_xchunk(xr[s], ok[s]);
+    float acc[RT];
+    // Whole turns of the ring (all NB tiles exist) in a loop with one exit, so
+    // the compiler's wait counts stay exact across the back edge; then the
+    // last fewer-than-NB tiles, whose loads are already in flight.
+    while (static_cast<uint64_t>(t) + static_cast<uint64_t>(NB - 1) * G < ntiles) {
+#pragma unroll
+        for (int p = 0; p < NB; p++) {
+            issue((p + NB - 1) % NB, NB - 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], ok[s], acc);
+            __builtin_amdgcn_sched_barrier(0);
+            sk_finish<W, RT, EPI>(acc, red[p], a, t, lane, wid, rv[p]);
+            t += G;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < NB - 1; p++) {
+        if (t >= ntiles) return;
+#pragma unroll
+        for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], ok[s], acc);
+        sk_finish<W, RT, EPI>(acc, red[p], a, t, lane, wid, rv[p]);
+        t += G;
+    }
+}
+
 }  // namespace
 
 // ---- GEMV entry points ---------------------------------------------------
@@ -1036,6 +1309,12 @@ __device__ __forceinline__ void gemv_multi(const GemvMultiArgs& a) {
 #define ZLM_GEMVX_PFQ(NAME, QT, KCAP, WAVES, RT, STEPS, PRO, EPI, FENCE)                      \
     extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {              \
         gemv<QT, KCAP, WAVES, RT, STEPS, true, true, PRO, EPI, true, FENCE, true>(a);       \
+    }
+// Split-K instances zlm_gemv_<quant>_r1_s<STEPS>_sk<RT> / _resid_s<STEPS>_sk<RT>:
+// W waves share a tile of RT rows (W*SPL == STEPS), one workgroup per CU.
+#define ZLM_GEMV_SK(NAME, QT, W, RT, SPL, EPI, XQ, NB, EXACT)                   \
+    extern "C" __global__ void __launch_bounds__(W * 64) NAME(GemvArgs a) {     \
+        gemv_sk<QT, W, RT, SPL, EPI, XQ, NB, EXACT>(a);                        \
     }
 #define ZLM_GEMVX_FORMS(QN, QT, KCAP, STEPS, EXACT, SFX)                                           \
     ZLM_GEMVX(zlm_gemv_##QN##_pair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_PLAIN, EPI_PAIR)           \

@@ -104,6 +104,7 @@ struct GemvKernel {
     int threads = 256;     // the kernel's launch bounds
     int waves_per_cu = 0;  // grid target of a prefetching instance; 0 = gemv_grid's rule
     bool struct_args = false;  // takes one GemvArgs (fused forms, prefetching instances)
+    bool split = false;        // split-K: the workgroup's waves share each tile of rt rows
 };
 
 struct Slot {
@@ -376,7 +377,7 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
 // Look up (and cache) a GEMV entry point by name in its quant's code object;
 // the block size is the kernel's launch bound.
 const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps, int waves_per_cu = 0,
-                            bool struct_args = false) {
+                            bool struct_args = false, bool split = false) {
     auto it = d->gemv.find(name);
     if (it == d->gemv.end()) {
         GemvKernel g;
@@ -385,6 +386,7 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
             g.steps = steps;
             g.waves_per_cu = waves_per_cu;
             g.struct_args = struct_args;
+            g.split = split;
             int mt = 0;
             if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g.fn) == hipSuccess && mt >= 64)
                 g.threads = mt;
@@ -406,8 +408,26 @@ struct PfSuffix {
 };
 constexpr PfSuffix kPfSuffixes[] = {{"_pf", 8}, {"_pfw16", 16}};
 
-// The GEMV kernel for a shape: for a 1-row tile the prefetching instance of
-// the exact step count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_pf
+// The split-K instances' name suffixes _sk<RT> (rows per tile); they exist
+// for exact shapes only (chunks per row == 64 * steps) and run one
+// workgroup per CU.
+constexpr int kSkRows[] = {2, 4};
+
+const GemvKernel* find_split(zlm_device* d, const QuantInfo* qi, size_t k, const char* form) {
+    const size_t chunks = k / qi->chunk_elems;
+    if (chunks % 64 != 0) return nullptr;
+    const int steps = static_cast<int>(chunks / 64);
+    char nm[96];
+    for (int rt : kSkRows) {
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d_sk%d", kQuantNames[qi->slot], form, steps, rt);
+        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 0, true, true)) return g;
+    }
+    return nullptr;
+}
+
+// The GEMV kernel for a shape: for a 1-row tile the split-K instance of the
+// shape if the quant has one, else the prefetching instance of the exact step
+// count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_pf
 // or _pfw16; q6_k's only below 65536 rows, where it was measured); else the
 // instance whose step count equals ceil(chunks per row / 64) with the
 // requested row tile, else with a 1-row tile, else the generic bounded
@@ -418,6 +438,9 @@ const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt
     const int steps = static_cast<int>((chunks + 63) / 64);
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
+    if (rt == 1) {
+        if (const GemvKernel* g = find_split(d, qi, k, "r1")) return g;
+    }
     if (rt == 1 && (rows < 65536 || qi->type != ZLM_GGML_Q6_K)) {
         for (const PfSuffix& v : kPfSuffixes) {
             snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d%s", qn, steps, v.suffix);
@@ -454,8 +477,10 @@ bool check_resident(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t 
 // tiles, the lm_heads) with a 4096-float x capacity (19 KB of LDS) run 8
 // workgroups per CU: 262144 x 3840 q6_k 222 -> 190 us.  steps 0 = the generic
 // instance (32768-float x capacity, one workgroup per CU).
-// A prefetching instance (waves_per_cu set) runs that many waves per CU.
+// A prefetching instance (waves_per_cu set) runs that many waves per CU; a
+// split-K instance one workgroup (one tile at a time) per CU.
 unsigned gemv_grid(const zlm_device* d, const QuantInfo* qi, uint64_t tiles, const GemvKernel* gk) {
+    if (gk->split) return static_cast<unsigned>(std::min<uint64_t>(tiles, static_cast<uint64_t>(d->cus)));
     const uint64_t waves = static_cast<uint64_t>(gk->threads / 64);
     const uint64_t wgs = (tiles + waves - 1) / waves;
     const int steps = gk->steps;
@@ -576,14 +601,26 @@ bool enqueue_multi(zlm_device* d, const QuantInfo* qi, size_t k, const float* x_
     return launch(d, gk->fn, gemv_grid(d, qi, total, gk), static_cast<unsigned>(gk->threads), args, "gemv batch");
 }
 
-// The fused-form kernel for a shape: the prefetching exact-steps instance if
-// the quant has one, else the exact-steps instance, else the generic one.
+// Whether a same-quant batch at this k runs as one launch of the batch
+// kernel: its rows equal the single-op kernel's bit for bit (same per-lane
+// order) unless the single op runs split-K.
+bool batch_one_launch(zlm_device* d, const QuantInfo* qi, size_t k) {
+    const GemvKernel* g = pick_gemv(d, qi, k, 1, 0);
+    return g && !g->split;
+}
+
+// The fused-form kernel for a shape: the split-K instance (resid form) or the
+// prefetching exact-steps instance if the quant has one, else the exact-steps
+// instance, else the generic one.
 const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form) {
     const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const int rt = form_is_pair(form) ? 2 : 1;
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
+    if (form == ZLM_FORM_RESID) {
+        if (const GemvKernel* g = find_split(d, qi, k, kFormNames[form])) return g;
+    }
     for (const PfSuffix& v : kPfSuffixes) {
         snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d%s", qn, kFormNames[form], steps, v.suffix);
         if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, v.waves_per_cu, true)) return g;
@@ -627,7 +664,8 @@ bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     a.eps = op.eps;
     a.act = op.act;
     void* args[] = {&a};
-    return launch(d, gk->fn, gemv_grid(d, qi, op.rows, gk), static_cast<unsigned>(gk->threads), args,
+    const uint64_t tiles = gk->split ? (op.rows + gk->rt - 1) / gk->rt : op.rows;
+    return launch(d, gk->fn, gemv_grid(d, qi, tiles, gk), static_cast<unsigned>(gk->threads), args,
                   kFormNames[op.form]);
 }
 
@@ -1102,9 +1140,10 @@ extern "C" bool zlm_gpu_mat_vec_resident_batch(zlm_device* d, size_t k, const fl
     }
     if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, total)) return false;
     if (!stage_x_sync(d, x, k)) return false;
-    // Ops of one quant go out as one launch of the batch kernel; a mixed batch
-    // runs op by op.
-    bool same = n > 1;
+    // Ops of one quant go out as one launch of the batch kernel; a mixed batch,
+    // or one whose shape has a split-K single-op kernel (another summation
+    // order), runs op by op.
+    bool same = n > 1 && batch_one_launch(d, quant_info(ops[0].quant), k);
     for (size_t i = 1; i < n; i++) same = same && (ops[i].quant & 0xffu) == (ops[0].quant & 0xffu);
     size_t off = 0;
     if (same) {
@@ -1505,8 +1544,10 @@ extern "C" bool zlm_gpu_mat_vec_batch_enqueue(zlm_device* d, zlm_resident* const
         if (!y_dev[i]) return fail(d, "null y");
         if (!check_resident(d, res[i], qi, rows[i], k)) return false;
     }
-    if (n == 1) return enqueue_gemv(d, res[0], quant, rows[0], k, x_dev, y_dev[0]);
-    return enqueue_multi(d, qi, k, x_dev, res, rows, y_dev, n);
+    if (n > 1 && batch_one_launch(d, qi, k)) return enqueue_multi(d, qi, k, x_dev, res, rows, y_dev, n);
+    for (size_t i = 0; i < n; i++)
+        if (!enqueue_gemv(d, res[i], quant, rows[i], k, x_dev, y_dev[i])) return false;
+    return true;
 }
 
 extern "C" bool zlm_gpu_mat_mul_enqueue(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
