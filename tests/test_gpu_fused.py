@@ -211,19 +211,21 @@ def test_device_forms_match_oracle(dev, qt, rows, k):
 
 
 # Row counts around the split-K kernels' tile and grid sizes (2-row tiles for
-# q8_0, 4-row for q4_0, one workgroup per CU): fewer rows than a tile, a
+# q8_0 and the K-quants, 4-row for q4_0, one workgroup per CU): fewer rows than a tile, a
 # ragged last tile, fewer tiles than CUs, one tile past a whole grid, and
 # several ring turns per workgroup.
 SPLIT_ROWS = [1, 3, 5, 255, 513, 1028, 2051, 3000]
 
 
-@pytest.mark.parametrize("qt", [synth.Q8_0, synth.Q4_0], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("qt,k", [(synth.Q8_0, 12288), (synth.Q4_0, 12288), (synth.Q4_K, 15360), (synth.Q6_K, 15360)],
+                         ids=["q8_0", "q4_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("rows", SPLIT_ROWS)
-def test_split_k_shapes_match_oracle(dev, qt, rows):
-    """The k = 12288 GEMVs run split-K: the plain form and the residual form
-    (also in place, res aliasing y) against the oracle, and two launches
-    agree bit for bit (the waves' partials meet in a fixed order)."""
-    k = 12288
+def test_split_k_shapes_match_oracle(dev, qt, k, rows):
+    """The down-projection shapes run split-K (q8_0 / q4_0 at k = 12288, the
+    K-quants at k = 15360, whose 480 chunks per row leave the last wave half
+    idle): the plain form and the residual form (also in place, res aliasing
+    y) against the oracle, and two launches agree bit for bit (the waves'
+    partials meet in a fixed order)."""
     _say(f"split-k {NAMES[qt]} rows={rows}")
     w = synth.weights(qt, rows, k, seed=rows + 901)
     x = synth.activation(rows + 902, k)

@@ -561,22 +561,32 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
 
 // q4_k piece p = c&7 of super-block c>>3 (16 qs bytes of group g = p/2): low
 // nibbles are elements 64g + 16(p%2) + j (scale 2g), high nibbles +32 (scale
-// 2g+1); value d*sc*nib - dmin*mn.
-template <int RT>
-__device__ __forceinline__ void compute_q4_k(const Frag<Q4_K, RT>& f, const float* xl, const float* xs, int c,
-                                             bool valid, float* acc) {
-    const int sbk = c >> 3, p = c & 7, g = p >> 1, h = p & 1;
-    const int elo = 256 * sbk + 64 * g + 16 * h, ehi = elo + 32;
-    const float* xa_p = xl + xpad(elo);
-    const float* xb_p = xl + xpad(ehi);
-    const float xs_lo = xs[elo >> 4], xs_hi = xs[ehi >> 4];
+// 2g+1); value d*sc*nib - dmin*mn.  The math takes x through accessors
+// (xa(i) / xb(i): float4 i of the low / high run, xs_lo / xs_hi: the runs'
+// sums), so the LDS-staged and the register-held x share it.
+template <int QT>
+__device__ __forceinline__ void kquant_runs(int c, int& e_lo, int& e_hi) {
+    const int sbk = c >> 3, p = c & 7;
+    if constexpr (QT == Q4_K) {
+        e_lo = 256 * sbk + 64 * (p >> 1) + 16 * (p & 1);
+        e_hi = e_lo + 32;
+    } else {
+        e_lo = 256 * sbk + 128 * (p >> 2) + 32 * (p & 1) + 16 * ((p >> 1) & 1);
+        e_hi = e_lo + 64;
+    }
+}
+
+template <int RT, class XA, class XB>
+__device__ __forceinline__ void q4_k_rows(const Frag<Q4_K, RT>& f, int c, XA xa_at, XB xb_at, float xs_lo,
+                                          float xs_hi, bool valid, float* acc) {
+    const int g = (c & 7) >> 1;
     float slo[RT], shi[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) slo[r] = shi[r] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 xa = lds4(xa_p + 4 * i);
-        const float4 xb = lds4(xb_p + 4 * i);
+        const float4 xa = xa_at(i);
+        const float4 xb = xb_at(i);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const uint32_t wv = (&f.q[r].x)[i];
@@ -606,25 +616,34 @@ __device__ __forceinline__ void compute_q4_k(const Frag<Q4_K, RT>& f, const floa
     }
 }
 
+template <int RT>
+__device__ __forceinline__ void compute_q4_k(const Frag<Q4_K, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    int elo, ehi;
+    kquant_runs<Q4_K>(c, elo, ehi);
+    const float* xa_p = xl + xpad(elo);
+    const float* xb_p = xl + xpad(ehi);
+    q4_k_rows<RT>(
+        f, c, [&](int i) { return lds4(xa_p + 4 * i); }, [&](int i) { return lds4(xb_p + 4 * i); }, xs[elo >> 4],
+        xs[ehi >> 4], valid, acc);
+}
+
 // q6_k part p = c&7 of super-block c>>3: half n = p/4, 16-run h, ql half ws;
 // low nibbles + qh bits 2ws are elements 128n + 32ws + 16h + j, high nibbles +
 // qh bits 4+2ws are those +64.  value d*sc*(q-32); Sum (q-32)*x = Sum q*x - 32*Sum x.
-template <int RT>
-__device__ __forceinline__ void compute_q6_k(const Frag<Q6_K, RT>& f, const float* xl, const float* xs, int c,
-                                             bool valid, float* acc) {
-    const int sbk = c >> 3, p = c & 7, n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
-    const int ea = 256 * sbk + 128 * n + 32 * ws + 16 * h, eb = ea + 64;
-    const float* xa_p = xl + xpad(ea);
-    const float* xb_p = xl + xpad(eb);
-    const float xs_a = xs[ea >> 4], xs_b = xs[eb >> 4];
+// x through accessors as for q4_k.
+template <int RT, class XA, class XB>
+__device__ __forceinline__ void q6_k_rows(const Frag<Q6_K, RT>& f, int c, XA xa_at, XB xb_at, float xs_a,
+                                          float xs_b, bool valid, float* acc) {
+    const int p = c & 7, h = (p >> 1) & 1, ws = p & 1;
     const int sh_lo = 2 * ws, sh_hi = 4 + 2 * ws, sci = 8 * (h + 2 * ws);
     float sa[RT], sbv[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) sa[r] = sbv[r] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 xa = lds4(xa_p + 4 * i);
-        const float4 xb = lds4(xb_p + 4 * i);
+        const float4 xa = xa_at(i);
+        const float4 xb = xb_at(i);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
@@ -649,6 +668,18 @@ __device__ __forceinline__ void compute_q6_k(const Frag<Q6_K, RT>& f, const floa
         t = fmaf(d * sc_b, fmaf(-32.0f, xs_b, sbv[r]), t);
         acc[r] += t;
     }
+}
+
+template <int RT>
+__device__ __forceinline__ void compute_q6_k(const Frag<Q6_K, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    int ea, eb;
+    kquant_runs<Q6_K>(c, ea, eb);
+    const float* xa_p = xl + xpad(ea);
+    const float* xb_p = xl + xpad(eb);
+    q6_k_rows<RT>(
+        f, c, [&](int i) { return lds4(xa_p + 4 * i); }, [&](int i) { return lds4(xb_p + 4 * i); }, xs[ea >> 4],
+        xs[eb >> 4], valid, acc);
 }
 
 template <int QT, int RT, int KCAP = 0, bool XQ = false>
@@ -1041,10 +1072,21 @@ struct XChunk<Q4_0, true> {  // the block's 32 x values as int8 planes (XQTile's
     float d1;                // 1/s
     float sum;               // the fp32 sum of the 32 values
 };
+struct XRuns {  // a K-quant piece's two 16-element runs of x and their sums
+    float4 a[4];
+    float4 b[4];
+    float sa;
+    float sb;
+};
+template <>
+struct XChunk<Q4_K, false> : XRuns {};
+template <>
+struct XChunk<Q6_K, false> : XRuns {};
 
 template <int QT>
 constexpr int sk_chunk_elems() {
-    static_assert(QT == Q8_0 || QT == Q4_0, "split-K is implemented for q8_0 and q4_0");
+    static_assert(QT == Q8_0 || QT == Q4_0 || QT == Q4_K || QT == Q6_K,
+                  "split-K is implemented for q8_0, q4_0, q4_k and q6_k");
     return QT == Q8_0 ? 16 : 32;
 }
 
@@ -1053,12 +1095,25 @@ struct XRaw {
     float4 v[sk_chunk_elems<QT>() / 4];
 };
 
+// x of chunk c: its consecutive elements (q8_0, q4_0) or its two runs
+// (K-quants: v[0..3] the low run, v[4..7] the high one).
 template <int QT>
 __device__ __forceinline__ void xraw_load(const float* __restrict__ x, int c, XRaw<QT>& r) {
-    constexpr int N = sk_chunk_elems<QT>() / 4;
-    const float4* p = reinterpret_cast<const float4*>(x) + static_cast<size_t>(c) * N;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    if constexpr (QT == Q4_K || QT == Q6_K) {
+        int e_lo, e_hi;
+        kquant_runs<QT>(c, e_lo, e_hi);
 #pragma unroll
-    for (int i = 0; i < N; i++) r.v[i] = p[i];
+        for (int i = 0; i < 4; i++) {
+            r.v[i] = x4[(e_lo >> 2) + i];
+            r.v[4 + i] = x4[(e_hi >> 2) + i];
+        }
+    } else {
+        constexpr int N = sk_chunk_elems<QT>() / 4;
+        const float4* p = x4 + static_cast<size_t>(c) * N;
+#pragma unroll
+        for (int i = 0; i < N; i++) r.v[i] = p[i];
+    }
 }
 
 __device__ __forceinline__ float4 zero_unless(float4 v, bool valid) {
@@ -1102,8 +1157,48 @@ __device__ __forceinline__ XChunk<Q4_0, true> make_xchunk(const XRaw<Q4_0>& r, b
     return x;
 }
 
+// The runs and their sums in xstore's order (float4 sums, then pairs).
+template <int QT>
+__device__ __forceinline__ XRuns make_xruns(const XRaw<QT>& r, bool valid) {
+    XRuns x;
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = zero_unless(r.v[i], valid);
+        if (i < 4) x.a[i & 3] = v;
+        else x.b[i & 3] = v;
+        q[i] = (v.x + v.y) + (v.z + v.w);
+    }
+    x.sa = (q[0] + q[1]) + (q[2] + q[3]);
+    x.sb = (q[4] + q[5]) + (q[6] + q[7]);
+    return x;
+}
+__device__ __forceinline__ XChunk<Q4_K, false> make_xchunk(const XRaw<Q4_K>& r, bool valid) {
+    XChunk<Q4_K, false> x;
+    static_cast<XRuns&>(x) = make_xruns<Q4_K>(r, valid);
+    return x;
+}
+__device__ __forceinline__ XChunk<Q6_K, false> make_xchunk(const XRaw<Q6_K>& r, bool valid) {
+    XChunk<Q6_K, false> x;
+    static_cast<XRuns&>(x) = make_xruns<Q6_K>(r, valid);
+    return x;
+}
+
 template <int RT>
-__device__ __forceinline__ void dot_xchunk(const Frag<Q8_0, RT>& f, const XChunk<Q8_0, false>& x, bool valid,
+__device__ __forceinline__ void dot_xchunk(const Frag<Q4_K, RT>& f, const XChunk<Q4_K, false>& x, int c, bool valid,
+                                           float* acc) {
+    q4_k_rows<RT>(
+        f, c, [&](int i) { return x.a[i]; }, [&](int i) { return x.b[i]; }, x.sa, x.sb, valid, acc);
+}
+template <int RT>
+__device__ __forceinline__ void dot_xchunk(const Frag<Q6_K, RT>& f, const XChunk<Q6_K, false>& x, int c, bool valid,
+                                           float* acc) {
+    q6_k_rows<RT>(
+        f, c, [&](int i) { return x.a[i]; }, [&](int i) { return x.b[i]; }, x.sa, x.sb, valid, acc);
+}
+
+template <int RT>
+__device__ __forceinline__ void dot_xchunk(const Frag<Q8_0, RT>& f, const XChunk<Q8_0, false>& x, int, bool valid,
                                            float* acc) {
     float s[RT];
 #pragma unroll
@@ -1124,7 +1219,7 @@ __device__ __forceinline__ void dot_xchunk(const Frag<Q8_0, RT>& f, const XChunk
 }
 
 template <int RT>
-__device__ __forceinline__ void dot_xchunk(const Frag<Q4_0, RT>& f, const XChunk<Q4_0, true>& x, bool valid,
+__device__ __forceinline__ void dot_xchunk(const Frag<Q4_0, RT>& f, const XChunk<Q4_0, true>& x, int, bool valid,
                                            float* acc) {
     q4_0_xq_rows<RT>(f, x.pl, x.ph, x.d1, x.sum, valid, acc);
 }
@@ -1207,7 +1302,7 @@ __device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvA
 template <int QT, int W, int RT, int SPL, int EPI, bool XQ, int NB, bool EXACT>
 __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     static_assert(EPI == EPI_PLAIN || EPI == EPI_RESID, "split-K forms: plain, resid");
-    static_assert(XQ == (QT == Q4_0), "q4_0 runs on the int8 planes, q8_0 on fp32 x");
+    static_assert(XQ == (QT == Q4_0), "q4_0 runs on the int8 planes, the others on fp32 x");
     static_assert(NB >= 2, "a ring of at least two fragment sets");
     __shared__ float red[NB][RT][W];
     const int lane = threadIdx.x & (kWave - 1);
@@ -1252,7 +1347,7 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 #pragma unroll
             for (int r = 0; r < RT; r++) acc[r] = 0.0f;
 #pragma unroll
-            for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], ok[s], acc);
+            for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], cs[s], ok[s], acc);
             __builtin_amdgcn_sched_barrier(0);
             sk_finish<W, RT, EPI>(acc, red[p], a, t, lane, wid, rv[p]);
             t += G;
@@ -1264,7 +1359,7 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 #pragma unroll
         for (int r = 0; r < RT; r++) acc[r] = 0.0f;
 #pragma unroll
-        for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], ok[s], acc);
+        for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], cs[s], ok[s], acc);
         sk_finish<W, RT, EPI>(acc, red[p], a, t, lane, wid, rv[p]);
         t += G;
     }
@@ -1310,7 +1405,8 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {              \
         gemv<QT, KCAP, WAVES, RT, STEPS, true, true, PRO, EPI, true, FENCE, true>(a);       \
     }
-// Split-K instances zlm_gemv_<quant>_r1_s<STEPS>_sk<RT> / _resid_s<STEPS>_sk<RT>:
+// Split-K instances zlm_gemv_<quant>_r1_s<STEPS>_sk<RT> / _resid_s<STEPS>_sk<RT>
+// (any row of STEPS chunk steps), ..._sk<RT>x (EXACT: chunks == 64*STEPS):
 // W waves share a tile of RT rows (W*SPL == STEPS), one workgroup per CU.
 #define ZLM_GEMV_SK(NAME, QT, W, RT, SPL, EPI, XQ, NB, EXACT)                   \
     extern "C" __global__ void __launch_bounds__(W * 64) NAME(GemvArgs a) {     \

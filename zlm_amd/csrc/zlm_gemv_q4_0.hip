@@ -22,7 +22,7 @@ ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s2_pfw16, Q4_0, 4096, 8, 1, 2, PRO_NORM, EPI_PL
 // Split-K forms of the down projection (k = 12288), x as int8 planes in
 // registers: 6-wave workgroups, one per CU, four rows per tile.  Measured on
 // gfx950 at 4096 x 12288 (resid): 9.6 us (resid_s6_pfw16) -> 9.1 us.
-ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s6_sk4, Q4_0, 6, 4, 1, EPI_PLAIN, true, 2, true)
-ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s6_sk4, Q4_0, 6, 4, 1, EPI_RESID, true, 2, true)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s6_sk4x, Q4_0, 6, 4, 1, EPI_PLAIN, true, 2, true)
+ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s6_sk4x, Q4_0, 6, 4, 1, EPI_RESID, true, 2, true)
 
 ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)

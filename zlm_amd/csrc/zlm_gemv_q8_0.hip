@@ -10,6 +10,6 @@ ZLM_GEMVX_Q8(q8_0, Q8_0)
 // one per CU, each wave one chunk step of two rows per tile.  Measured on
 // gfx950 at 4096 x 12288: 13.1 -> 10.5 us (the one-wave-per-row kernel takes
 // ~320 registers per wave and runs one wave per SIMD).
-ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s12_sk2, Q8_0, 12, 2, 1, EPI_PLAIN, false, 2, true)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s12_sk2x, Q8_0, 12, 2, 1, EPI_PLAIN, false, 2, true)
 
 ZLM_GEMV_MULTI_Q8(q8_0, Q8_0)

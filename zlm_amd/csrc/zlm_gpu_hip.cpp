@@ -408,17 +408,21 @@ struct PfSuffix {
 };
 constexpr PfSuffix kPfSuffixes[] = {{"_pf", 8}, {"_pfw16", 16}};
 
-// The split-K instances' name suffixes _sk<RT> (rows per tile); they exist
-// for exact shapes only (chunks per row == 64 * steps) and run one
-// workgroup per CU.
+// The split-K instances' name suffixes: _sk<RT> (RT rows per tile) for any
+// row of ceil(chunks / 64) == steps, _sk<RT>x for exact rows only (chunks ==
+// 64 * steps); one workgroup per CU.
 constexpr int kSkRows[] = {2, 4};
 
 const GemvKernel* find_split(zlm_device* d, const QuantInfo* qi, size_t k, const char* form) {
     const size_t chunks = k / qi->chunk_elems;
-    if (chunks % 64 != 0) return nullptr;
-    const int steps = static_cast<int>(chunks / 64);
+    const int steps = static_cast<int>((chunks + 63) / 64);
+    const bool exact = chunks % 64 == 0;
     char nm[96];
     for (int rt : kSkRows) {
+        if (exact) {
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d_sk%dx", kQuantNames[qi->slot], form, steps, rt);
+            if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 0, true, true)) return g;
+        }
         snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d_sk%d", kQuantNames[qi->slot], form, steps, rt);
         if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 0, true, true)) return g;
     }
