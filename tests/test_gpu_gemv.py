@@ -133,7 +133,8 @@ def test_async_burst_batch_agree(dev):
                          ids=["q8_0", "q4_k", "f16", "q4_1", "q8_0_split", "q4_0_split"])
 def test_batch_one_launch_matches_single_ops(dev, qt, k):
     """A same-quant batch runs as one launch of the batch kernel (op by op
-    where the single op runs split-K, k = 12288 for q8_0 / q4_0); every op's
+    where the single op sums in another order: split-K at k = 12288 for
+    q8_0 / q4_0, int8-plane x for q4_k at k = 3840); every op's
     rows equal the single-op GEMV's bit for bit (same per-lane order and
     reduction), including eight ops of ragged row counts."""
     _say(f"batch {NAMES[qt]} k={k}")
@@ -246,6 +247,7 @@ def test_quantizer_bit_exact(dev):
 
 CONFIG_SHAPES = [
     ("c0_q4_0", synth.Q4_0, 4096, 4096),
+    ("tall_q6_k", synth.Q6_K, 65536 + 37, 3840),  # the lm_head kernel (from 65536 rows)
     ("c1_gate_q8_0", synth.Q8_0, 12288, 4096),
     ("c1_down_q8_0", synth.Q8_0, 4096, 12288),
     ("c3_gate_q4_k", synth.Q4_K, 15360, 3840),

@@ -682,17 +682,116 @@ __device__ __forceinline__ void compute_q6_k(const Frag<Q6_K, RT>& f, const floa
         xs[eb >> 4], valid, acc);
 }
 
+// The K-quants against the int8 planes (XQ): a piece's two 16-element runs
+// each take three 16-byte plane slices and their block's 1/s; the 6-bit
+// (q6_k, 0..63) or 4-bit (q4_k) quants are valid int8, so each run's
+// sum q*x is three v_dot4_i32_i8 chains combined in fp32, the biases and
+// mins through the fp32 run sums as in the fp32 path.
+struct XqRuns {
+    uint4 pa[3];  // planes of the low run
+    uint4 pb[3];  // planes of the high run
+    float d1a;    // 1/s of the low run's block
+    float d1b;
+    float sa;     // fp32 sums of the runs
+    float sb;
+};
+
+__device__ __forceinline__ float xq_combine(int s0, int s1, int s2, float d1) {
+    return fmaf(static_cast<float>(s2), 1.0f / 16384.0f, fmaf(static_cast<float>(s1), 1.0f / 128.0f, static_cast<float>(s0))) *
+           d1;
+}
+
+template <int RT>
+__device__ __forceinline__ void q4_k_xq_rows(const Frag<Q4_K, RT>& f, int c, const XqRuns& x, bool valid, float* acc) {
+    const int g = (c & 7) >> 1;
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t wv = (&f.q[r].x)[i];
+            const int lo = static_cast<int>(wv & 0x0F0F0F0Fu), hi = static_cast<int>((wv >> 4) & 0x0F0F0F0Fu);
+            a0 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[0].x)[i]), a0, false);
+            a1 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[1].x)[i]), a1, false);
+            a2 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[2].x)[i]), a2, false);
+            b0 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[0].x)[i]), b0, false);
+            b1 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[1].x)[i]), b1, false);
+            b2 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[2].x)[i]), b2, false);
+        }
+        const uint32_t dd = valid ? f.hd[r].x : 0u;
+        const float d = h2f(dd), dmin = h2f(dd >> 16);
+        float sc1, mn1, sc2, mn2;
+        scale_min_k4(2 * g, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc1, mn1);
+        scale_min_k4(2 * g + 1, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc2, mn2);
+        float t = (d * sc1) * xq_combine(a0, a1, a2, x.d1a);
+        t = fmaf(d * sc2, xq_combine(b0, b1, b2, x.d1b), t);
+        t = fmaf(-(dmin * mn1), x.sa, t);
+        t = fmaf(-(dmin * mn2), x.sb, t);
+        acc[r] += t;
+    }
+}
+
+template <int RT>
+__device__ __forceinline__ void q6_k_xq_rows(const Frag<Q6_K, RT>& f, int c, const XqRuns& x, bool valid, float* acc) {
+    const int p = c & 7, h = (p >> 1) & 1, ws = p & 1;
+    const int sh_lo = 2 * ws, sh_hi = 4 + 2 * ws, sci = 8 * (h + 2 * ws);
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
+            const int lo = static_cast<int>((lw & 0x0F0F0F0Fu) | (((hw >> sh_lo) & 0x03030303u) << 4));
+            const int hi = static_cast<int>(((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> sh_hi) & 0x03030303u) << 4));
+            a0 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[0].x)[i]), a0, false);
+            a1 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[1].x)[i]), a1, false);
+            a2 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[2].x)[i]), a2, false);
+            b0 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[0].x)[i]), b0, false);
+            b1 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[1].x)[i]), b1, false);
+            b2 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[2].x)[i]), b2, false);
+        }
+        const float d = valid ? h2f(f.d[r]) : 0.0f;
+        const float sc_a = static_cast<float>(static_cast<int32_t>(f.sc[r].x << (24 - sci)) >> 24);
+        const float sc_b = static_cast<float>(static_cast<int32_t>(f.sc[r].y << (24 - sci)) >> 24);
+        float t = (d * sc_a) * fmaf(-32.0f, x.sa, xq_combine(a0, a1, a2, x.d1a));
+        t = fmaf(d * sc_b, fmaf(-32.0f, x.sb, xq_combine(b0, b1, b2, x.d1b)), t);
+        acc[r] += t;
+    }
+}
+
+// The XQ runs of K-quant piece c from the LDS tile.
+template <int QT, int KCAP>
+__device__ __forceinline__ XqRuns xq_runs_lds(const float* xl, const float* xs, int c) {
+    int ea, eb;
+    kquant_runs<QT>(c, ea, eb);
+    const int8_t* xq = reinterpret_cast<const int8_t*>(xl);
+    XqRuns x;
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        x.pa[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + ea);
+        x.pb[p] = *reinterpret_cast<const uint4*>(xq + p * KCAP + eb);
+    }
+    x.d1a = xl[XQTile<KCAP>::kScales + (ea >> 5)];
+    x.d1b = xl[XQTile<KCAP>::kScales + (eb >> 5)];
+    x.sa = xs[ea >> 4];
+    x.sb = xs[eb >> 4];
+    return x;
+}
+
 template <int QT, int RT, int KCAP = 0, bool XQ = false>
 __device__ __forceinline__ void compute_frag(const Frag<QT, RT>& f, const float* xl, const float* xs, int c,
                                              bool valid, float* acc) {
-    static_assert(!XQ || QT == Q4_0, "the int8-plane x is implemented for q4_0");
+    static_assert(!XQ || QT == Q4_0 || QT == Q4_K || QT == Q6_K,
+                  "the int8-plane x is implemented for q4_0, q4_k and q6_k");
     if constexpr (QT == Q4_0 && XQ) compute_q4_0_xq<RT, KCAP>(f, xl, xs, c, valid, acc);
     if constexpr (QT == Q4_0 && !XQ) compute_q4_0<RT>(f, xl, xs, c, valid, acc);
     if constexpr (QT == Q4_1) compute_q4_1<RT>(f, xl, xs, c, valid, acc);
     if constexpr (is_float_type(QT)) compute_float<QT, RT>(f, xl, c, valid, acc);
     if constexpr (QT == Q8_0) compute_q8_0<RT>(f, xl, xs, c, valid, acc);
-    if constexpr (QT == Q4_K) compute_q4_k<RT>(f, xl, xs, c, valid, acc);
-    if constexpr (QT == Q6_K) compute_q6_k<RT>(f, xl, xs, c, valid, acc);
+    if constexpr (QT == Q4_K && XQ) q4_k_xq_rows<RT>(f, c, xq_runs_lds<Q4_K, KCAP>(xl, xs, c), valid, acc);
+    if constexpr (QT == Q4_K && !XQ) compute_q4_k<RT>(f, xl, xs, c, valid, acc);
+    if constexpr (QT == Q6_K && XQ) q6_k_xq_rows<RT>(f, c, xq_runs_lds<Q6_K, KCAP>(xl, xs, c), valid, acc);
+    if constexpr (QT == Q6_K && !XQ) compute_q6_k<RT>(f, xl, xs, c, valid, acc);
 }
 
 // Prologue / epilogue forms of the GEMV (template parameters PRO and EPI).
@@ -1082,6 +1181,10 @@ template <>
 struct XChunk<Q4_K, false> : XRuns {};
 template <>
 struct XChunk<Q6_K, false> : XRuns {};
+template <>
+struct XChunk<Q4_K, true> : XqRuns {};  // the runs as int8 planes, one scale per run
+template <>
+struct XChunk<Q6_K, true> : XqRuns {};
 
 template <int QT>
 constexpr int sk_chunk_elems() {
@@ -1182,6 +1285,48 @@ __device__ __forceinline__ XChunk<Q6_K, false> make_xchunk(const XRaw<Q6_K>& r, 
     XChunk<Q6_K, false> x;
     static_cast<XRuns&>(x) = make_xruns<Q6_K>(r, valid);
     return x;
+}
+
+// A K-quant piece's runs as int8 planes in registers: the XQ encoding with one
+// power-of-two scale per 16-element run (the lane holds half of each
+// 32-element block, so it scales its runs on their own).
+template <int QT>
+__device__ __forceinline__ XChunk<QT, true> make_xq_runs(const XRaw<QT>& r, bool valid) {
+    XChunk<QT, true> x;
+    float q[8];
+    float4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        v[i] = zero_unless(r.v[i], valid);
+        q[i] = (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    auto encode = [](const float4* u, uint4 (&pl)[3], float& d1) {
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            am = fmaxf(am, fmaxf(fmaxf(fabsf(u[i].x), fabsf(u[i].y)), fmaxf(fabsf(u[i].z), fabsf(u[i].w))));
+        const int e = xq_exp(am);
+        const float sc = ldexpf(1.0f, 5 - e);
+#pragma unroll
+        for (int i = 0; i < 4; i++) xq_planes(u[i], sc, (&pl[0].x)[i], (&pl[1].x)[i], (&pl[2].x)[i]);
+        d1 = ldexpf(1.0f, e - 5);
+    };
+    encode(v, x.pa, x.d1a);
+    encode(v + 4, x.pb, x.d1b);
+    x.sa = (q[0] + q[1]) + (q[2] + q[3]);
+    x.sb = (q[4] + q[5]) + (q[6] + q[7]);
+    return x;
+}
+
+template <int RT>
+__device__ __forceinline__ void dot_xchunk(const Frag<Q4_K, RT>& f, const XChunk<Q4_K, true>& x, int c, bool valid,
+                                           float* acc) {
+    q4_k_xq_rows<RT>(f, c, x, valid, acc);
+}
+template <int RT>
+__device__ __forceinline__ void dot_xchunk(const Frag<Q6_K, RT>& f, const XChunk<Q6_K, true>& x, int c, bool valid,
+                                           float* acc) {
+    q6_k_xq_rows<RT>(f, c, x, valid, acc);
 }
 
 template <int RT>
@@ -1302,7 +1447,8 @@ __device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvA
 template <int QT, int W, int RT, int SPL, int EPI, bool XQ, int NB, bool EXACT>
 __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     static_assert(EPI == EPI_PLAIN || EPI == EPI_RESID, "split-K forms: plain, resid");
-    static_assert(XQ == (QT == Q4_0), "q4_0 runs on the int8 planes, the others on fp32 x");
+    static_assert(XQ == (QT == Q4_0) || QT == Q4_K || QT == Q6_K,
+                  "q4_0 runs on the int8 planes, q8_0 on fp32 x, the K-quants on either");
     static_assert(NB >= 2, "a ring of at least two fragment sets");
     __shared__ float red[NB][RT][W];
     const int lane = threadIdx.x & (kWave - 1);
@@ -1334,7 +1480,10 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     for (int j = 0; j < NB - 1; j++) issue(j, static_cast<uint32_t>(j));
     XChunk<QT, XQ> xc[SPL];
 #pragma unroll
-    for (int s = 0; s < SPL; s++) xc[s] = make_xchunk(xr[s], ok[s]);
+    for (int s = 0; s < SPL; s++) {
+        if constexpr (XQ && QT != Q4_0) xc[s] = make_xq_runs<QT>(xr[s], ok[s]);
+        else xc[s] = make_xchunk(xr[s], ok[s]);
+    }
     float acc[RT];
     // Whole turns of the ring (all NB tiles exist) in a loop with one exit, so
     // the compiler's wait counts stay exact across the back edge; then the
@@ -1395,8 +1544,10 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     }
 // Prefetching instances zlm_gemv_<quant>_<form>_s<STEPS>_pf (launched at 8
 // waves per CU) and ..._pfw16 (16 waves per CU): WAVES waves per workgroup
-// (the host reads the block size from the kernel's launch bounds); XQ stages
-// x as int8 planes (q4_0).
+// (the host reads the block size from the kernel's launch bounds).  The
+// ZLM_GEMVX_PFQ instances stage x as int8 planes (q4_0, q4_k, q6_k) and carry
+// a q in the suffix (_pfq, _pfqw16, _tallq: 16 waves per CU from 65536 rows),
+// which tells the host their summation differs from the batch kernel's.
 #define ZLM_GEMVX_PF(NAME, QT, KCAP, WAVES, RT, STEPS, PRO, EPI, FENCE)                       \
     extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {              \
         gemv<QT, KCAP, WAVES, RT, STEPS, true, true, PRO, EPI, true, FENCE>(a);             \

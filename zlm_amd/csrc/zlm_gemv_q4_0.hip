@@ -14,14 +14,14 @@ ZLM_GEMVX_FORMS(q4_0, Q4_0, 16384, 6, true, s6)
 // one per CU (10.4 -> 9.6 us), the normed q;k;v 6144 x 4096 with 8-wave
 // workgroups at 16 waves per CU (6.4 -> 6.0 us).  4096-row launches (o, C0)
 // stay plain: their workgroups have too few rows to repay the quantization.
-ZLM_GEMVX_PFQ(zlm_gemv_q4_0_pair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PAIR, false)
-ZLM_GEMVX_PFQ(zlm_gemv_q4_0_normpair_s2_pf, Q4_0, 4096, 8, 2, 2, PRO_NORM, EPI_PAIR, false)
-ZLM_GEMVX_PFQ(zlm_gemv_q4_0_resid_s6_pfw16, Q4_0, 12288, 16, 1, 6, PRO_PLAIN, EPI_RESID, true)
-ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s2_pfw16, Q4_0, 4096, 8, 1, 2, PRO_NORM, EPI_PLAIN, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_pair_s2_pfq, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PAIR, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_normpair_s2_pfq, Q4_0, 4096, 8, 2, 2, PRO_NORM, EPI_PAIR, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_resid_s6_pfqw16, Q4_0, 12288, 16, 1, 6, PRO_PLAIN, EPI_RESID, true)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s2_pfqw16, Q4_0, 4096, 8, 1, 2, PRO_NORM, EPI_PLAIN, false)
 
 // Split-K forms of the down projection (k = 12288), x as int8 planes in
 // registers: 6-wave workgroups, one per CU, four rows per tile.  Measured on
-// gfx950 at 4096 x 12288 (resid): 9.6 us (resid_s6_pfw16) -> 9.1 us.
+// gfx950 at 4096 x 12288 (resid): 9.6 us (resid_s6_pfqw16) -> 9.1 us.
 ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s6_sk4x, Q4_0, 6, 4, 1, EPI_PLAIN, true, 2, true)
 ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s6_sk4x, Q4_0, 6, 4, 1, EPI_RESID, true, 2, true)
 

@@ -105,6 +105,7 @@ struct GemvKernel {
     int waves_per_cu = 0;  // grid target of a prefetching instance; 0 = gemv_grid's rule
     bool struct_args = false;  // takes one GemvArgs (fused forms, prefetching instances)
     bool split = false;        // split-K: the workgroup's waves share each tile of rt rows
+    bool xq = false;           // sums in another order than the batch kernel (int8-plane x or split-K)
 };
 
 struct Slot {
@@ -377,7 +378,7 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
 // Look up (and cache) a GEMV entry point by name in its quant's code object;
 // the block size is the kernel's launch bound.
 const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps, int waves_per_cu = 0,
-                            bool struct_args = false, bool split = false) {
+                            bool struct_args = false, bool split = false, bool xq = false) {
     auto it = d->gemv.find(name);
     if (it == d->gemv.end()) {
         GemvKernel g;
@@ -387,6 +388,7 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
             g.waves_per_cu = waves_per_cu;
             g.struct_args = struct_args;
             g.split = split;
+            g.xq = xq || split;
             int mt = 0;
             if (hipFuncGetAttribute(&mt, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g.fn) == hipSuccess && mt >= 64)
                 g.threads = mt;
@@ -401,12 +403,17 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
     return it->second.fn ? &it->second : nullptr;
 }
 
-// The prefetching instances' name suffixes and the grid's waves per CU.
+// The prefetching instances' name suffixes, the grid's waves per CU, the
+// fewest rows a suffix is taken for (_tallq: the lm_heads) and whether x is
+// staged as int8 planes (a summation the batch kernel does not share).
 struct PfSuffix {
     const char* suffix;
     int waves_per_cu;
+    size_t min_rows;
+    bool xq;
 };
-constexpr PfSuffix kPfSuffixes[] = {{"_pf", 8}, {"_pfw16", 16}};
+constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true}, {"_pf", 8, 0, false},   {"_pfw16", 16, 0, false},
+                                    {"_pfq", 8, 0, true},        {"_pfqw16", 16, 0, true}};
 
 // The split-K instances' name suffixes: _sk<RT> (RT rows per tile) for any
 // row of ceil(chunks / 64) == steps, _sk<RT>x for exact rows only (chunks ==
@@ -431,8 +438,8 @@ const GemvKernel* find_split(zlm_device* d, const QuantInfo* qi, size_t k, const
 
 // The GEMV kernel for a shape: for a 1-row tile the split-K instance of the
 // shape if the quant has one, else the prefetching instance of the exact step
-// count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_pf
-// or _pfw16; q6_k's only below 65536 rows, where it was measured); else the
+// count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_tallq from 65536
+// rows, _pf, _pfw16, _pfq, _pfqw16); else the
 // instance whose step count equals ceil(chunks per row / 64) with the
 // requested row tile, else with a 1-row tile, else the generic bounded
 // instance.  Chunks per row: k / chunk_elems (k/16 for q8_0, k/32 for q4_0,
@@ -444,11 +451,11 @@ const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt
     char nm[96];
     if (rt == 1) {
         if (const GemvKernel* g = find_split(d, qi, k, "r1")) return g;
-    }
-    if (rt == 1 && (rows < 65536 || qi->type != ZLM_GGML_Q6_K)) {
         for (const PfSuffix& v : kPfSuffixes) {
+            if (rows < v.min_rows) continue;
             snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d%s", qn, steps, v.suffix);
-            if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps, v.waves_per_cu, true)) return g;
+            if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps, v.waves_per_cu, true, false, v.xq))
+                return g;
         }
     }
     snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d", qn, rt, steps);
@@ -607,10 +614,10 @@ bool enqueue_multi(zlm_device* d, const QuantInfo* qi, size_t k, const float* x_
 
 // Whether a same-quant batch at this k runs as one launch of the batch
 // kernel: its rows equal the single-op kernel's bit for bit (same per-lane
-// order) unless the single op runs split-K.
+// order) unless the single op runs split-K or on int8-plane x.
 bool batch_one_launch(zlm_device* d, const QuantInfo* qi, size_t k) {
     const GemvKernel* g = pick_gemv(d, qi, k, 1, 0);
-    return g && !g->split;
+    return g && !g->xq;
 }
 
 // The fused-form kernel for a shape: the split-K instance (resid form) or the
@@ -626,8 +633,9 @@ const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint3
         if (const GemvKernel* g = find_split(d, qi, k, kFormNames[form])) return g;
     }
     for (const PfSuffix& v : kPfSuffixes) {
+        if (v.min_rows > 0) continue;
         snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d%s", qn, kFormNames[form], steps, v.suffix);
-        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, v.waves_per_cu, true)) return g;
+        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, v.waves_per_cu, true, false, v.xq)) return g;
     }
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d", qn, kFormNames[form], steps);
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
