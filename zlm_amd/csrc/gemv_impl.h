@@ -361,19 +361,19 @@ __device__ __forceinline__ void load_frag(Frag<QT, RT>& f, const TileRows<RT>& t
 }
 
 // Byte j of a q4_0 block holds element j (low nibble) and j+16 (high);
-// value (nib-8)*d, and Sum (nib-8)*x = Sum nib*x - 8*Sum x.
-template <int RT>
-__device__ __forceinline__ void compute_q4_0(const Frag<Q4_0, RT>& f, const float* xl, const float* xs, int c,
-                                             bool valid, float* acc) {
-    const float* xb = xl + xpad(c << 5);
-    const float xsum = xs[2 * c] + xs[2 * c + 1];
+// value (nib-8)*d, and Sum (nib-8)*x = Sum nib*x - 8*Sum x.  x through
+// accessors (xa(i) / xh(i): float4 i of elements 0..15 / 16..31), so the
+// LDS-staged and the register-held x share the math.
+template <int RT, class XA, class XH>
+__device__ __forceinline__ void q4_0_rows(const Frag<Q4_0, RT>& f, XA xa_at, XH xh_at, float xsum, bool valid,
+                                          float* acc) {
     float s[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) s[r] = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float4 xa = lds4(xb + 4 * i);
-        const float4 xh = lds4(xb + 16 + 4 * i);
+        const float4 xa = xa_at(i);
+        const float4 xh = xh_at(i);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const uint32_t wv = (&f.q[r].x)[i];
@@ -390,6 +390,15 @@ __device__ __forceinline__ void compute_q4_0(const Frag<Q4_0, RT>& f, const floa
     }
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, fmaf(-8.0f, xsum, s[r]), acc[r]);
+}
+
+template <int RT>
+__device__ __forceinline__ void compute_q4_0(const Frag<Q4_0, RT>& f, const float* xl, const float* xs, int c,
+                                             bool valid, float* acc) {
+    const float* xb = xl + xpad(c << 5);
+    q4_0_rows<RT>(
+        f, [&](int i) { return lds4(xb + 4 * i); }, [&](int i) { return lds4(xb + 16 + 4 * i); },
+        xs[2 * c] + xs[2 * c + 1], valid, acc);
 }
 
 // Byte j of a q4_1 block holds element j (low nibble) and j+16 (high); value
@@ -1178,6 +1187,8 @@ struct XRuns {  // a K-quant piece's two 16-element runs of x and their sums
     float sb;
 };
 template <>
+struct XChunk<Q4_0, false> : XRuns {};  // the block's elements 0..15 (a) and 16..31 (b)
+template <>
 struct XChunk<Q4_K, false> : XRuns {};
 template <>
 struct XChunk<Q6_K, false> : XRuns {};
@@ -1223,22 +1234,27 @@ __device__ __forceinline__ float4 zero_unless(float4 v, bool valid) {
     return valid ? v : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
-__device__ __forceinline__ XChunk<Q8_0, false> make_xchunk(const XRaw<Q8_0>& r, bool valid) {
-    XChunk<Q8_0, false> x;
+// The runs of a chunk (K-quants: its two 16-element runs; q4_0: the block's
+// two halves) and their sums in xstore's order (float4 sums, then pairs).
+template <int QT>
+__device__ __forceinline__ XRuns make_xruns(const XRaw<QT>& r, bool valid) {
+    XRuns x;
+    float q[8];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 8; i++) {
         const float4 v = zero_unless(r.v[i], valid);
-        x.v[4 * i] = v.x;
-        x.v[4 * i + 1] = v.y;
-        x.v[4 * i + 2] = v.z;
-        x.v[4 * i + 3] = v.w;
+        if (i < 4) x.a[i & 3] = v;
+        else x.b[i & 3] = v;
+        q[i] = (v.x + v.y) + (v.z + v.w);
     }
+    x.sa = (q[0] + q[1]) + (q[2] + q[3]);
+    x.sb = (q[4] + q[5]) + (q[6] + q[7]);
     return x;
 }
 
 // The block's planes exactly as xput forms them in LDS (same amax, exponent
 // and rounding), and its sum in xstore's order (float4 sums, then pairs).
-__device__ __forceinline__ XChunk<Q4_0, true> make_xchunk(const XRaw<Q4_0>& r, bool valid) {
+__device__ __forceinline__ XChunk<Q4_0, true> make_xq_block(const XRaw<Q4_0>& r, bool valid) {
     XChunk<Q4_0, true> x;
     float4 v[8];
     float am = 0.0f, q[8];
@@ -1257,33 +1273,6 @@ __device__ __forceinline__ XChunk<Q4_0, true> make_xchunk(const XRaw<Q4_0>& r, b
         xq_planes(v[4 + i], s, (&x.ph[0].x)[i], (&x.ph[1].x)[i], (&x.ph[2].x)[i]);
     }
     x.sum = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
-    return x;
-}
-
-// The runs and their sums in xstore's order (float4 sums, then pairs).
-template <int QT>
-__device__ __forceinline__ XRuns make_xruns(const XRaw<QT>& r, bool valid) {
-    XRuns x;
-    float q[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float4 v = zero_unless(r.v[i], valid);
-        if (i < 4) x.a[i & 3] = v;
-        else x.b[i & 3] = v;
-        q[i] = (v.x + v.y) + (v.z + v.w);
-    }
-    x.sa = (q[0] + q[1]) + (q[2] + q[3]);
-    x.sb = (q[4] + q[5]) + (q[6] + q[7]);
-    return x;
-}
-__device__ __forceinline__ XChunk<Q4_K, false> make_xchunk(const XRaw<Q4_K>& r, bool valid) {
-    XChunk<Q4_K, false> x;
-    static_cast<XRuns&>(x) = make_xruns<Q4_K>(r, valid);
-    return x;
-}
-__device__ __forceinline__ XChunk<Q6_K, false> make_xchunk(const XRaw<Q6_K>& r, bool valid) {
-    XChunk<Q6_K, false> x;
-    static_cast<XRuns&>(x) = make_xruns<Q6_K>(r, valid);
     return x;
 }
 
@@ -1316,6 +1305,37 @@ __device__ __forceinline__ XChunk<QT, true> make_xq_runs(const XRaw<QT>& r, bool
     x.sa = (q[0] + q[1]) + (q[2] + q[3]);
     x.sb = (q[4] + q[5]) + (q[6] + q[7]);
     return x;
+}
+
+// The lane's register x of one chunk from its raw float4s (zero if the chunk
+// is past the row's end).
+template <int QT, bool XQ>
+__device__ __forceinline__ XChunk<QT, XQ> make_xchunk(const XRaw<QT>& r, bool valid) {
+    XChunk<QT, XQ> x;
+    if constexpr (QT == Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = zero_unless(r.v[i], valid);
+            x.v[4 * i] = v.x;
+            x.v[4 * i + 1] = v.y;
+            x.v[4 * i + 2] = v.z;
+            x.v[4 * i + 3] = v.w;
+        }
+    } else if constexpr (QT == Q4_0 && XQ) {
+        x = make_xq_block(r, valid);
+    } else if constexpr (XQ) {
+        x = make_xq_runs<QT>(r, valid);
+    } else {
+        static_cast<XRuns&>(x) = make_xruns<QT>(r, valid);
+    }
+    return x;
+}
+
+template <int RT>
+__device__ __forceinline__ void dot_xchunk(const Frag<Q4_0, RT>& f, const XChunk<Q4_0, false>& x, int, bool valid,
+                                           float* acc) {
+    q4_0_rows<RT>(
+        f, [&](int i) { return x.a[i]; }, [&](int i) { return x.b[i]; }, x.sa + x.sb, valid, acc);
 }
 
 template <int RT>
@@ -1447,8 +1467,7 @@ __device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvA
 template <int QT, int W, int RT, int SPL, int EPI, bool XQ, int NB, bool EXACT>
 __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     static_assert(EPI == EPI_PLAIN || EPI == EPI_RESID, "split-K forms: plain, resid");
-    static_assert(XQ == (QT == Q4_0) || QT == Q4_K || QT == Q6_K,
-                  "q4_0 runs on the int8 planes, q8_0 on fp32 x, the K-quants on either");
+    static_assert(!XQ || QT != Q8_0, "q8_0 runs on fp32 x");
     static_assert(NB >= 2, "a ring of at least two fragment sets");
     __shared__ float red[NB][RT][W];
     const int lane = threadIdx.x & (kWave - 1);
@@ -1480,10 +1499,7 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     for (int j = 0; j < NB - 1; j++) issue(j, static_cast<uint32_t>(j));
     XChunk<QT, XQ> xc[SPL];
 #pragma unroll
-    for (int s = 0; s < SPL; s++) {
-        if constexpr (XQ && QT != Q4_0) xc[s] = make_xq_runs<QT>(xr[s], ok[s]);
-        else xc[s] = make_xchunk(xr[s], ok[s]);
-    }
+    for (int s = 0; s < SPL; s++) xc[s] = make_xchunk<QT, XQ>(xr[s], ok[s]);
     float acc[RT];
     // Whole turns of the ring (all NB tiles exist) in a loop with one exit, so
     // the compiler's wait counts stay exact across the back edge; then the

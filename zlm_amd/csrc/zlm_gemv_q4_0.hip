@@ -7,6 +7,11 @@ ZLM_GEMV_Q4(q4_0, Q4_0)
 ZLM_GEMVX_Q4(q4_0, Q4_0)
 ZLM_GEMVX_FORMS(q4_0, Q4_0, 16384, 6, true, s6)
 
+// The residual form with two-row tiles, taken for launches of at most 8192
+// rows at k <= 4096 (the decode step's o projection: 4.91 -> 4.54 us in the
+// sweep harness, 1.619 -> 1.605 ms per decode token on gfx950).
+ZLM_GEMVX(zlm_gemv_q4_0_resid_s2_r2, Q4_0, 4096, 2, 2, true, PRO_PLAIN, EPI_RESID)
+
 // Prefetching forms for the decode-step shapes, x staged as int8 planes
 // (v_dot4 on the nibbles), measured on gfx950 against the forms above:
 // gate_up 12288 x 4096 with 8-wave workgroups at 8 waves per CU (16.3 ->
