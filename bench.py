@@ -124,6 +124,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--decode-replays", type=int, default=30, metavar="N",
+                    help="graph replays per timed decode run (warm-up run + 3 timed runs of N)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="also run the library copy kernel 5x over BYTES (for HBM traffic counter calibration)")
     args = ap.parse_args()
@@ -254,8 +256,8 @@ def main():
         model.step(x, cfg.max_seq - 1)  # eager: converts layouts, sizes scratch
         graph = model.capture()
         model.set_input(x, cfg.max_seq - 1)
-        reps = 30
-        dev.graph_launch(graph, reps)  # ~50 ms untimed: clocks up after the host-side synthesis
+        reps = max(1, args.decode_replays)
+        dev.graph_launch(graph, reps)  # ~50 ms untimed (30 replays): clocks up after the host-side synthesis
         ms = sorted(dev.graph_launch(graph, reps) / reps for _ in range(3))[1]
         tok_bytes = zdec.weight_bytes(cfg) + zdec.kv_bytes(cfg, cfg.max_seq)
         gbps = tok_bytes / (ms * 1e-3) / 1e9
