@@ -252,3 +252,31 @@ def test_split_k_shapes_match_oracle(dev, qt, k, rows):
     for p in (xd, resd, yd):
         dev.dev_free(p)
     dev.free_resident(rw)
+
+
+# Row lengths just below the split-K shapes: q4_k / q6_k at 58 super-blocks
+# (464 chunks: the split-K instance's last wave holds 16 valid chunks and
+# clamps the rest), q8_0 / q4_0 one block short of 12288 (no exact split-K
+# instance: the one-wave-per-row kernels run).
+@pytest.mark.parametrize("qt,k", [(synth.Q4_K, 14848), (synth.Q6_K, 14848), (synth.Q8_0, 12256), (synth.Q4_0, 12256)],
+                         ids=["q4_k", "q6_k", "q8_0", "q4_0"])
+@pytest.mark.parametrize("rows", [3, 515])
+def test_split_k_ragged_rows_match_oracle(dev, qt, k, rows):
+    _say(f"split-k ragged {NAMES[qt]} rows={rows} k={k}")
+    w = synth.weights(qt, rows, k, seed=rows + k)
+    x = synth.activation(rows + 7, k)
+    res = synth.activation(rows + 8, rows)
+    rw = dev.upload_resident(w)
+    xd, resd, yd = _dev_vec(dev, x), _dev_vec(dev, res), dev.dev_malloc(rows * 4)
+    q = zd.quant(qt)
+    want = oracle.matvec(qt, w, k, rows, x)
+    got = np.zeros(rows, np.float32)
+    assert dev.gemv_op_enqueue(zd.FORM_PLAIN, q, rw, rows, k, xd, yd), dev.last_error()
+    dev.dev_download(got, yd)
+    assert rel_l2(got, want) <= REL_L2
+    assert dev.gemv_op_enqueue(zd.FORM_RESID, q, rw, rows, k, xd, yd, res=resd), dev.last_error()
+    dev.dev_download(got, yd)
+    assert rel_l2(got, res + want) <= REL_L2
+    for p in (xd, resd, yd):
+        dev.dev_free(p)
+    dev.free_resident(rw)
