@@ -29,6 +29,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <unordered_map>
 #include <string>
 #include <vector>
 
@@ -150,6 +151,7 @@ struct zlm_device {
     hipModule_t mod = nullptr;          // zlm_kernels_gfx950.hsaco
     hipModule_t gemv_mod[kNumQuants] = {};  // zlm_gemv_<quant>_gfx950.hsaco, by QuantInfo::slot
     std::map<std::string, GemvKernel> gemv;  // by entry-point name; null fn = absent
+    std::unordered_map<uint64_t, const GemvKernel*> picks;  // kernel picked per shape class (pick_key)
     hipFunction_t repack = nullptr;
     hipFunction_t dequant[kNumQuants] = {};
     hipFunction_t quantize_q8 = nullptr;
@@ -245,6 +247,7 @@ void unload_modules(zlm_device* d) {
         if (m) hipModuleUnload(m);
         m = nullptr;
     }
+    d->picks.clear();
     d->gemv.clear();
 }
 
@@ -454,7 +457,28 @@ bool resid_two_rows(const QuantInfo* qi, int steps, size_t rows) {
     return qi->type == ZLM_GGML_Q4_0 && steps == 2 && rows <= 8192;
 }
 
+// The pick functions below depend on the shape only through (quant, k, row
+// tile or form, rows >= 65536, rows <= 8192); the device caches their result
+// per class so an op's host path is one hash lookup (the name lookups cost
+// ~1 us per launch, most of a small GEMV's enqueue).
+uint64_t pick_key(const QuantInfo* qi, size_t k, int rt_or_form, size_t rows) {
+    const uint64_t rows_class = rows >= 65536 ? 2 : rows <= 8192 ? 1 : 0;
+    return (static_cast<uint64_t>(k) << 16) | (static_cast<uint64_t>(qi->slot) << 8) |
+           (static_cast<uint64_t>(rt_or_form & 0x3f) << 2) | rows_class;
+}
+
+const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows);
+
 const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows) {
+    const uint64_t key = pick_key(qi, k, rt, rows);
+    auto it = d->picks.find(key);
+    if (it != d->picks.end()) return it->second;
+    const GemvKernel* g = pick_gemv_named(d, qi, k, rt, rows);
+    d->picks.emplace(key, g);
+    return g;
+}
+
+const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows) {
     const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const char* qn = kQuantNames[qi->slot];
@@ -633,7 +657,18 @@ bool batch_one_launch(zlm_device* d, const QuantInfo* qi, size_t k) {
 // The fused-form kernel for a shape: the split-K or two-row-tile instance
 // (resid form) or the prefetching exact-steps instance if the quant has one,
 // else the exact-steps instance, else the generic one.
+const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form, size_t rows);
+
 const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form, size_t rows) {
+    const uint64_t key = pick_key(qi, k, 32 + static_cast<int>(form), rows);  // forms apart from row tiles
+    auto it = d->picks.find(key);
+    if (it != d->picks.end()) return it->second;
+    const GemvKernel* g = pick_gemvx_named(d, qi, k, form, rows);
+    d->picks.emplace(key, g);
+    return g;
+}
+
+const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form, size_t rows) {
     const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const int rt = form_is_pair(form) ? 2 : 1;
