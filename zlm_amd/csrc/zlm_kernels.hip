@@ -195,14 +195,18 @@ extern "C" __global__ void __launch_bounds__(256)
 // mt*32: qx [mt][nb][32 tokens][32 B], dx [mt][nb][32 tokens] and, when `ds`
 // is not null, ds = dx * f32(sum of the block's q) in the same order (the
 // min-term factor of q4_1 / q4_k); padding tokens are zeros.  One thread per
-// (token, block).
+// (token, block), numbered in output order (thread i writes slot i), so a
+// wave's qx / dx / ds stores are contiguous (32 consecutive threads are the
+// 32 tokens of one token tile and block): 6.8 -> 6.2 us at 512 x 4096.
 extern "C" __global__ void __launch_bounds__(256)
     zlm_quantize_q8_tiled(const float* __restrict__ x, int8_t* __restrict__ qx, float* __restrict__ dx,
                           uint32_t m, uint32_t nb, uint32_t mt, float* __restrict__ ds) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<uint64_t>(mt) * 32 * nb) return;
-    const uint32_t t = static_cast<uint32_t>(i / nb), b = static_cast<uint32_t>(i % nb);
-    const uint64_t slot = (static_cast<uint64_t>(t / 32) * nb + b) * 32 + (t % 32);
+    const uint64_t tb = i / 32;  // token tile * nb + block
+    const uint32_t b = static_cast<uint32_t>(tb % nb);
+    const uint32_t t = static_cast<uint32_t>(tb / nb) * 32 + static_cast<uint32_t>(i % 32);
+    const uint64_t slot = i;
     float d;
     int32_t sum;
     quantize_block(t < m ? x + (static_cast<uint64_t>(t) * nb + b) * 32 : nullptr,
