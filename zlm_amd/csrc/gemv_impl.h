@@ -7,7 +7,10 @@
 //   q4_1  payload [rows][nb][16 B nibbles]        + scales [rows][nb] (f16 d, f16 m)
 //   q8_0  payload [rows][nb][32 B int8]           + scales [rows][nb] f16
 //   q6_k  payload [rows][nb][208 B ql|qh|sc]      + scales [rows][nb] f16
-//   q4_k  raw     [rows][nb][144 B]  (already a multiple of 16 B per block)
+//   q4_k  payload [rows][nb][128 B qs]            + records [rows][nb][20 B]:
+//         dword 0 = f16 d | f16 dmin << 16, dword 1+g (g = 0..3) = the 6-bit
+//         scales and mins of sub-blocks 2g, 2g+1 decoded to bytes
+//         (sc[2g], sc[2g+1], mn[2g], mn[2g+1]); see zlm_repack_q4_k
 //   f32 / f16 / bf16  raw [rows][k] (k a multiple of 32, so rows stay 16-byte
 //         aligned; the kernels count nb = k/32 "blocks" of 32 elements)
 // Every payload block is a whole number of 16-byte chunks, so the GEMV
@@ -296,7 +299,8 @@ struct Frag<BF16, RT> {
 };
 template <int RT>
 struct Frag<Q4_K, RT> {
-    uint4 hd[RT];
+    uint32_t dm[RT];  // f16 d | f16 dmin << 16
+    uint32_t sm[RT];  // bytes sc[2g], sc[2g+1], mn[2g], mn[2g+1] of the chunk's group g
     uint4 q[RT];
 };
 template <int RT>
@@ -345,9 +349,11 @@ __device__ __forceinline__ void load_frag(Frag<QT, RT>& f, const TileRows<RT>& t
             f.q[r] = ld16<NT>(w + (row * (2 * nb) + c) * 16);
             f.d[r] = ld2<NT>(dsc + row * nb + (c >> 1));
         } else if constexpr (QT == Q4_K) {
-            const uint8_t* blk = w + (row * nb + (c >> 3)) * 144;
-            f.hd[r] = ld16<false>(blk);
-            f.q[r] = ld16<NT>(blk + 16 + 16 * (c & 7));
+            const size_t bi = row * nb + (c >> 3);
+            const uint32_t* rec = reinterpret_cast<const uint32_t*>(dsc) + bi * 5;
+            f.dm[r] = ld4<false>(rec);
+            f.sm[r] = ld4<false>(rec + 1 + ((c & 7) >> 1));
+            f.q[r] = ld16<NT>(w + bi * 128 + 16 * (c & 7));
         } else {
             const int p = c & 7, n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
             const size_t bi = row * nb + (c >> 3);
@@ -551,26 +557,10 @@ __device__ __forceinline__ void compute_q8_0(const Frag<Q8_0, RT>& f, const floa
     for (int r = 0; r < RT; r++) acc[r] = fmaf(valid ? h2f(f.d[r]) : 0.0f, s[r], acc[r]);
 }
 
-// getScaleMinK4 (reference quant/k_quants.zig:24-32) on the 12 packed bytes
-// held as three dwords; j in 0..7, any lane-varying j.
-__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, float& sc, float& mn) {
-    const int t = (j & 3) * 8;
-    const uint32_t b0 = (s0 >> t) & 0xffu, b1 = (s1 >> t) & 0xffu, b2 = (s2 >> t) & 0xffu;
-    uint32_t d, m;
-    if (j < 4) {
-        d = b0 & 63u;
-        m = b1 & 63u;
-    } else {
-        d = (b2 & 15u) | ((b0 >> 6) << 4);
-        m = (b2 >> 4) | ((b1 >> 6) << 4);
-    }
-    sc = static_cast<float>(d);
-    mn = static_cast<float>(m);
-}
-
 // q4_k piece p = c&7 of super-block c>>3 (16 qs bytes of group g = p/2): low
 // nibbles are elements 64g + 16(p%2) + j (scale 2g), high nibbles +32 (scale
-// 2g+1); value d*sc*nib - dmin*mn.  The math takes x through accessors
+// 2g+1); value d*sc*nib - dmin*mn, the four 6-bit factors bytes of the
+// fragment's sm dword.  The math takes x through accessors
 // (xa(i) / xb(i): float4 i of the low / high run, xs_lo / xs_hi: the runs'
 // sums), so the LDS-staged and the register-held x share it.
 template <int QT>
@@ -588,7 +578,6 @@ __device__ __forceinline__ void kquant_runs(int c, int& e_lo, int& e_hi) {
 template <int RT, class XA, class XB>
 __device__ __forceinline__ void q4_k_rows(const Frag<Q4_K, RT>& f, int c, XA xa_at, XB xb_at, float xs_lo,
                                           float xs_hi, bool valid, float* acc) {
-    const int g = (c & 7) >> 1;
     float slo[RT], shi[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) slo[r] = shi[r] = 0.0f;
@@ -612,11 +601,9 @@ __device__ __forceinline__ void q4_k_rows(const Frag<Q4_K, RT>& f, int c, XA xa_
     }
 #pragma unroll
     for (int r = 0; r < RT; r++) {
-        const uint32_t dd = valid ? f.hd[r].x : 0u;
+        const uint32_t dd = valid ? f.dm[r] : 0u;
         const float d = h2f(dd), dmin = h2f(dd >> 16);
-        float sc1, mn1, sc2, mn2;
-        scale_min_k4(2 * g, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc1, mn1);
-        scale_min_k4(2 * g + 1, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc2, mn2);
+        const float sc1 = ub(f.sm[r], 0), sc2 = ub(f.sm[r], 1), mn1 = ub(f.sm[r], 2), mn2 = ub(f.sm[r], 3);
         float t = (d * sc1) * slo[r];
         t = fmaf(d * sc2, shi[r], t);
         t = fmaf(-(dmin * mn1), xs_lo, t);
@@ -712,7 +699,6 @@ __device__ __forceinline__ float xq_combine(int s0, int s1, int s2, float d1) {
 
 template <int RT>
 __device__ __forceinline__ void q4_k_xq_rows(const Frag<Q4_K, RT>& f, int c, const XqRuns& x, bool valid, float* acc) {
-    const int g = (c & 7) >> 1;
 #pragma unroll
     for (int r = 0; r < RT; r++) {
         int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
@@ -727,11 +713,9 @@ __device__ __forceinline__ void q4_k_xq_rows(const Frag<Q4_K, RT>& f, int c, con
             b1 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[1].x)[i]), b1, false);
             b2 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[2].x)[i]), b2, false);
         }
-        const uint32_t dd = valid ? f.hd[r].x : 0u;
+        const uint32_t dd = valid ? f.dm[r] : 0u;
         const float d = h2f(dd), dmin = h2f(dd >> 16);
-        float sc1, mn1, sc2, mn2;
-        scale_min_k4(2 * g, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc1, mn1);
-        scale_min_k4(2 * g + 1, f.hd[r].y, f.hd[r].z, f.hd[r].w, sc2, mn2);
+        const float sc1 = ub(f.sm[r], 0), sc2 = ub(f.sm[r], 1), mn1 = ub(f.sm[r], 2), mn2 = ub(f.sm[r], 3);
         float t = (d * sc1) * xq_combine(a0, a1, a2, x.d1a);
         t = fmaf(d * sc2, xq_combine(b0, b1, b2, x.d1b), t);
         t = fmaf(-(dmin * mn1), x.sa, t);
@@ -816,7 +800,7 @@ enum : int { EPI_PLAIN = 0, EPI_RESID = 1, EPI_PAIR = 2 };
 // Kernel arguments of every GEMV form, passed by value.
 struct GemvArgs {
     const uint8_t* w0;   // payload (the gate matrix for EPI_PAIR)
-    const uint16_t* d0;  // split f16 scales (unused for q4_k)
+    const uint16_t* d0;  // split f16 scales (q4_k: the 20-byte records)
     const uint8_t* w1;   // EPI_PAIR: the up matrix
     const uint16_t* d1;
     const float* x;

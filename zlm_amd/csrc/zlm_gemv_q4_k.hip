@@ -13,12 +13,14 @@ ZLM_GEMVX_PF(zlm_gemv_q4_k_r1_s8_pf, Q4_K, 16384, 8, 1, 8, PRO_PLAIN, EPI_PLAIN,
 // Split-K form for 7 < chunks/64 <= 8 (the C3 down projection 3840 x 15360):
 // 8-wave workgroups, one per CU, four rows per tile, x as int8 planes in
 // registers; measured on gfx950 16.7 -> 12.2 us against the prefetching
-// instance above (13.0 us with fp32 x and two rows per tile).
+// instance above (13.0 us with fp32 x and two rows per tile), 10.7 us on the
+// qs + record layout.
 ZLM_GEMV_SK(zlm_gemv_q4_k_r1_s8_sk4, Q4_K, 8, 4, 1, EPI_PLAIN, true, 2, false)
 
 // k <= 4096 (the C3 gate/up 15360 x 3840): x as int8 planes, prefetching
-// 8-wave workgroups at 16 waves per CU; 11.6 -> 10.9 us against the 4-wave
-// exact-steps instance at 4 workgroups per CU.
-ZLM_GEMVX_PFQ(zlm_gemv_q4_k_r1_s2_pfqw16, Q4_K, 4096, 8, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
+// 16-wave workgroups, one per CU (the x planes are built once per 16 waves);
+// 11.6 -> 10.9 us (8-wave groups on the raw blocks) -> 9.1 us on the qs +
+// record layout, against the 4-wave exact-steps instance at 4 workgroups per CU.
+ZLM_GEMVX_PFQ(zlm_gemv_q4_k_r1_s2_pfqw16, Q4_K, 4096, 16, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
 
 ZLM_GEMV_MULTI_Q4(q4_k, Q4_K)

@@ -37,6 +37,7 @@ namespace {
 
 constexpr int kRing = ZLM_RING_SIZE;
 constexpr uint32_t kNoLayout = 0xffffffffu;
+constexpr uint32_t kQ4kRecords = 0xfffffffeu;
 
 // Supported GEMV quants and their GGUF block geometry (the contract's
 // blockElems/blockBytes, reference gpu/backend/root.zig:198-220: the float
@@ -46,9 +47,11 @@ struct QuantInfo {
     uint32_t block_elems;
     uint32_t block_bytes;
     uint32_t payload_bytes;  // bytes per block in the device layout (scales split out)
-    uint32_t scale_offset;   // offset of the f16 scales inside the raw block, or kNoLayout (raw layout)
+    uint32_t scale_offset;   // offset of the f16 scales inside the raw block, kNoLayout (raw layout)
+                             // or kQ4kRecords (zlm_repack_q4_k)
     int slot;                // index into the kernel tables
-    uint32_t scale_count;    // f16 scales per block in the split layout (q4_1: d and m)
+    uint32_t scale_count;    // 16-bit words per block in the scale area (q4_1: d and m; q4_k: its
+                             // 20-byte record)
     uint32_t chunk_elems;    // elements per 16-byte payload chunk of a row (the GEMV's unit)
     uint32_t kblock;         // elements per kernel block: the kernels take nb = k / kblock
 };
@@ -56,7 +59,7 @@ struct QuantInfo {
 const QuantInfo kQuants[] = {
     {ZLM_GGML_Q4_0, 32, 18, 16, 0, 0, 1, 32, 32},
     {ZLM_GGML_Q8_0, 32, 34, 32, 0, 1, 1, 16, 32},
-    {ZLM_GGML_Q4_K, 256, 144, 144, kNoLayout, 2, 0, 32, 256},
+    {ZLM_GGML_Q4_K, 256, 144, 128, kQ4kRecords, 2, 10, 32, 256},
     {ZLM_GGML_Q6_K, 256, 210, 208, 208, 3, 1, 32, 256},
     {ZLM_GGML_Q4_1, 32, 20, 16, 0, 4, 2, 32, 32},
     {ZLM_GGML_F32, 1, 4, 4, kNoLayout, 5, 0, 4, 32},
@@ -153,6 +156,7 @@ struct zlm_device {
     std::map<std::string, GemvKernel> gemv;  // by entry-point name; null fn = absent
     std::unordered_map<uint64_t, const GemvKernel*> picks;  // kernel picked per shape class (pick_key)
     hipFunction_t repack = nullptr;
+    hipFunction_t repack_q4_k = nullptr;
     hipFunction_t dequant[kNumQuants] = {};
     hipFunction_t quantize_q8 = nullptr;
     hipFunction_t quantize_q8_tiled = nullptr;
@@ -266,6 +270,7 @@ bool load_kernels(zlm_device* d) {
         if (!ok(d, hipModuleGetFunction(&d->dequant[q], d->mod, nm), nm)) return false;
     }
     if (!ok(d, hipModuleGetFunction(&d->repack, d->mod, "zlm_repack_split"), "zlm_repack_split")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->repack_q4_k, d->mod, "zlm_repack_q4_k"), "zlm_repack_q4_k")) return false;
     if (!ok(d, hipModuleGetFunction(&d->quantize_q8, d->mod, "zlm_quantize_q8"), "zlm_quantize_q8")) return false;
     if (!ok(d, hipModuleGetFunction(&d->quantize_q8_tiled, d->mod, "zlm_quantize_q8_tiled"), "quantize tiled"))
         return false;
@@ -341,10 +346,15 @@ bool convert_blocks(zlm_device* d, const uint8_t* raw, uint64_t nblk, const Quan
     uint16_t* scales = reinterpret_cast<uint16_t*>(dst + p);
     *scales_out = scales;
     if (nblk == 0) return true;
-    uint32_t bb = qi->block_bytes, so = qi->scale_offset, ns = qi->scale_count;
     uint64_t n = nblk;
+    const unsigned grid = static_cast<unsigned>((nblk + 255) / 256);
+    if (qi->scale_offset == kQ4kRecords) {
+        void* args[] = {&raw, &dst, &scales, &n};
+        return launch(d, d->repack_q4_k, grid, 256, args, "repack q4_k");
+    }
+    uint32_t bb = qi->block_bytes, so = qi->scale_offset, ns = qi->scale_count;
     void* args[] = {&raw, &dst, &scales, &n, &bb, &so, &ns};
-    return launch(d, d->repack, static_cast<unsigned>((nblk + 255) / 256), 256, args, "repack");
+    return launch(d, d->repack, grid, 256, args, "repack");
 }
 
 // Convert a resident's raw blocks into the device layout of `qi` (once; the
@@ -354,7 +364,7 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
     if (r->layout != kNoLayout) return fail(d, "resident already holds a type-%u layout", r->layout);
     if (!r->raw) return fail(d, "resident has no raw bytes");
     const uint64_t nblk = r->bytes / qi->block_bytes;
-    if (qi->scale_offset == kNoLayout) {  // q4_k: the raw blocks are the layout
+    if (qi->scale_offset == kNoLayout) {  // f32 / f16 / bf16: the raw rows are the layout
         r->payload = r->raw;
         r->raw = nullptr;
         r->scales = nullptr;
@@ -827,8 +837,8 @@ bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_G
 //   q4_0 / q8_0  payload [rt][nb][32 rows][16 / 32 B] + f16 scales [rt][nb][32]
 //                (from the split layout);
 //   q4_1 / q4_k  payload [rt][nb][32 rows][16 B nibbles] + (scale, min) float2
-//                [rt][nb][32] (q4_1 from its split layout, q4_k from its raw
-//                super-blocks).
+//                [rt][nb][32] (q4_1 from its split layout, q4_k from its
+//                qs payload and records).
 // The resident's layout type never changes, so nb keys the copy.
 bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint64_t nb) {
     if (r->gemm_payload && r->gemm_nb == nb) return true;
@@ -855,13 +865,11 @@ bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint
     const uint64_t n = rt * 32 * nb;
     const unsigned grid = static_cast<unsigned>((n + 255) / 256);
     bool good;
-    if (qi->type == ZLM_GGML_Q4_K) {
-        void* args[] = {&payload, &tp, &ts, &rows32, &nb32, &rt32};
-        good = launch(d, d->tile_q4_k, grid, 256, args, "tile weights");
-    } else {
+    {
         void* args[] = {&payload, &scales, &tp, &ts, &rows32, &nb32, &rt32};
         hipFunction_t tile = qi->type == ZLM_GGML_Q8_0   ? d->tile_q8_0
                              : qi->type == ZLM_GGML_Q4_1 ? d->tile_q4_1
+                             : qi->type == ZLM_GGML_Q4_K ? d->tile_q4_k
                                                          : d->tile_q4_0;
         good = launch(d, tile, grid, 256, args, "tile weights");
     }

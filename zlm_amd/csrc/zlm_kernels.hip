@@ -28,6 +28,42 @@ extern "C" __global__ void __launch_bounds__(256)
     }
 }
 
+// getScaleMinK4 (reference quant/k_quants.zig:24-32): the 6-bit scale and min
+// of sub-block j (0..7) from the 12 packed bytes.
+__device__ __forceinline__ void scale_min_k4_u8(int j, const uint8_t* q, uint32_t& sc, uint32_t& mn) {
+    if (j < 4) {
+        sc = q[j] & 63u;
+        mn = q[j + 4] & 63u;
+    } else {
+        sc = (q[j + 4] & 15u) | ((q[j - 4] >> 6) << 4);
+        mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// q4_k raw super-block (reference quant/k_quants.zig:34-72: f16 d, f16 dmin,
+// 12 packed scale bytes, 128 qs bytes) -> payload [nb][128 B qs] and a 20-byte
+// record per block: dword 0 = d | dmin << 16 (the raw bytes 0..3), dword 1+g =
+// sc[2g] | sc[2g+1] << 8 | mn[2g] << 16 | mn[2g+1] << 24.  A GEMV lane reads
+// the one dword its 32-element group needs and converts the bytes directly.
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_repack_q4_k(const uint8_t* __restrict__ raw, uint8_t* __restrict__ payload, uint32_t* __restrict__ rec,
+                    uint64_t nblocks) {
+    const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint8_t* src = raw + b * 144;
+    const uint4* qs = reinterpret_cast<const uint4*>(src + 16);
+    uint4* dst = reinterpret_cast<uint4*>(payload + b * 128);
+    for (int i = 0; i < 8; i++) dst[i] = qs[i];
+    uint32_t* o = rec + b * 5;
+    o[0] = *reinterpret_cast<const uint32_t*>(src);
+    for (int g = 0; g < 4; g++) {
+        uint32_t s0, m0, s1, m1;
+        scale_min_k4_u8(2 * g, src + 4, s0, m0);
+        scale_min_k4_u8(2 * g + 1, src + 4, s1, m1);
+        o[1 + g] = s0 | (s1 << 8) | (m0 << 16) | (m1 << 24);
+    }
+}
+
 // ---- dequant from the device layout (bit-exact vs the CPU codecs) ---------
 // One thread per block; `out` receives block_elems floats per block.
 
@@ -98,20 +134,17 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 extern "C" __global__ void __launch_bounds__(256)
-    zlm_dequant_q4_k(const uint8_t* __restrict__ w, const uint16_t* __restrict__, float* __restrict__ out,
+    zlm_dequant_q4_k(const uint8_t* __restrict__ w, const uint16_t* __restrict__ dsc, float* __restrict__ out,
                      uint64_t nblocks) {
     const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
-    const uint8_t* blk = w + b * 144;
-    const uint32_t* hd = reinterpret_cast<const uint32_t*>(blk);
-    const float d = h2f(hd[0]), dmin = h2f(hd[0] >> 16);
+    const uint32_t* rec = reinterpret_cast<const uint32_t*>(dsc) + b * 5;
+    const float d = h2f(rec[0]), dmin = h2f(rec[0] >> 16);
     float* o = out + b * 256;
     for (int g = 0; g < 4; g++) {
-        float sc1, mn1, sc2, mn2;
-        scale_min_k4(2 * g, hd[1], hd[2], hd[3], sc1, mn1);
-        scale_min_k4(2 * g + 1, hd[1], hd[2], hd[3], sc2, mn2);
-        const float d1 = d * sc1, m1 = dmin * mn1, d2 = d * sc2, m2 = dmin * mn2;
-        const uint8_t* q = blk + 16 + 32 * g;
+        const uint32_t sm = rec[1 + g];
+        const float d1 = d * ub(sm, 0), m1 = dmin * ub(sm, 2), d2 = d * ub(sm, 1), m2 = dmin * ub(sm, 3);
+        const uint8_t* q = w + b * 128 + 32 * g;
         for (int l = 0; l < 32; l++) {
             o[64 * g + l] = __builtin_fmaf(static_cast<float>(q[l] & 15), d1, -m1);
             o[64 * g + 32 + l] = __builtin_fmaf(static_cast<float>(q[l] >> 4), d2, -m2);
@@ -279,14 +312,14 @@ extern "C" __global__ void __launch_bounds__(256)
     tsm[slot] = sm;
 }
 
-// q4_k (raw 144-byte super-blocks, reference quant/k_quants.zig:34-72):
-// 32-element block b of a row is sub-block j = b%8 of super-block b/8, the low
-// (j even) or high (j odd) nibbles of qs[32*(j/2) .. +32]; scale = d*sc_j,
-// min = -(dmin*mn_j) (getScaleMinK4, the products of the reference's int path,
-// quantized.zig:111-123).
+// q4_k (the zlm_repack_q4_k layout of the 144-byte super-blocks, reference
+// quant/k_quants.zig:34-72): 32-element block b of a row is sub-block j = b%8
+// of super-block b/8, the low (j even) or high (j odd) nibbles of
+// qs[32*(j/2) .. +32]; scale = d*sc_j, min = -(dmin*mn_j) (getScaleMinK4, the
+// products of the reference's int path, quantized.zig:111-123).
 extern "C" __global__ void __launch_bounds__(256)
-    zlm_tile_q4_k(const uint8_t* __restrict__ raw, uint8_t* __restrict__ tpayload, float2* __restrict__ tsm,
-                  uint32_t rows, uint32_t nb, uint32_t rt) {
+    zlm_tile_q4_k(const uint8_t* __restrict__ payload, const uint16_t* __restrict__ records,
+                  uint8_t* __restrict__ tpayload, float2* __restrict__ tsm, uint32_t rows, uint32_t nb, uint32_t rt) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<uint64_t>(rt) * 32 * nb) return;
     const uint32_t r = static_cast<uint32_t>(i / nb), b = static_cast<uint32_t>(i % nb);
@@ -294,13 +327,13 @@ extern "C" __global__ void __launch_bounds__(256)
     uint32_t packed[4] = {0u, 0u, 0u, 0u};
     float2 sm = make_float2(0.0f, 0.0f);
     if (r < rows) {
-        const uint8_t* blk = raw + (static_cast<uint64_t>(r) * (nb / 8) + b / 8) * 144;
+        const uint64_t sb = static_cast<uint64_t>(r) * (nb / 8) + b / 8;
         const uint32_t j = b % 8, sh = 4 * (j & 1);
-        const uint32_t* hd = reinterpret_cast<const uint32_t*>(blk);
-        float sc, mn;
-        scale_min_k4(static_cast<int>(j), hd[1], hd[2], hd[3], sc, mn);
-        sm = make_float2(h2f(hd[0]) * sc, -(h2f(hd[0] >> 16) * mn));
-        const uint8_t* qs = blk + 16 + 32 * (j / 2);
+        const uint32_t* rec = reinterpret_cast<const uint32_t*>(records) + sb * 5;
+        const uint32_t sms = rec[1 + j / 2];
+        const float sc = ub(sms, j & 1), mn = ub(sms, 2 + (j & 1));
+        sm = make_float2(h2f(rec[0]) * sc, -(h2f(rec[0] >> 16) * mn));
+        const uint8_t* qs = payload + sb * 128 + 32 * (j / 2);
         for (int e = 0; e < 16; e++) {
             const uint32_t lo = (qs[e] >> sh) & 15u, hi = (qs[e + 16] >> sh) & 15u;
             packed[e / 4] |= (lo | (hi << 4)) << (8 * (e % 4));
