@@ -627,12 +627,14 @@ __device__ __forceinline__ void compute_q4_k(const Frag<Q4_K, RT>& f, const floa
 // q6_k part p = c&7 of super-block c>>3: half n = p/4, 16-run h, ql half ws;
 // low nibbles + qh bits 2ws are elements 128n + 32ws + 16h + j, high nibbles +
 // qh bits 4+2ws are those +64.  value d*sc*(q-32); Sum (q-32)*x = Sum q*x - 32*Sum x.
-// x through accessors as for q4_k.
+// The two qh bits land at bits 4-5 of each byte with one shift and one mask
+// ((qh << (4-2ws)) or (qh >> 2ws), & 0x30303030): bits shifted in from the
+// neighbouring bytes fall outside the mask.  x through accessors as for q4_k.
 template <int RT, class XA, class XB>
 __device__ __forceinline__ void q6_k_rows(const Frag<Q6_K, RT>& f, int c, XA xa_at, XB xb_at, float xs_a,
                                           float xs_b, bool valid, float* acc) {
     const int p = c & 7, h = (p >> 1) & 1, ws = p & 1;
-    const int sh_lo = 2 * ws, sh_hi = 4 + 2 * ws, sci = 8 * (h + 2 * ws);
+    const int sh_lo = 4 - 2 * ws, sh_hi = 2 * ws, sci = 8 * (h + 2 * ws);
     float sa[RT], sbv[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) sa[r] = sbv[r] = 0.0f;
@@ -643,8 +645,8 @@ __device__ __forceinline__ void q6_k_rows(const Frag<Q6_K, RT>& f, int c, XA xa_
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
-            const uint32_t lo = (lw & 0x0F0F0F0Fu) | (((hw >> sh_lo) & 0x03030303u) << 4);
-            const uint32_t hi = ((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> sh_hi) & 0x03030303u) << 4);
+            const uint32_t lo = (lw & 0x0F0F0F0Fu) | ((hw << sh_lo) & 0x30303030u);
+            const uint32_t hi = ((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> sh_hi) & 0x30303030u);
             sa[r] = fmaf(ub(lo, 0), xa.x, sa[r]);
             sa[r] = fmaf(ub(lo, 1), xa.y, sa[r]);
             sa[r] = fmaf(ub(lo, 2), xa.z, sa[r]);
@@ -727,15 +729,15 @@ __device__ __forceinline__ void q4_k_xq_rows(const Frag<Q4_K, RT>& f, int c, con
 template <int RT>
 __device__ __forceinline__ void q6_k_xq_rows(const Frag<Q6_K, RT>& f, int c, const XqRuns& x, bool valid, float* acc) {
     const int p = c & 7, h = (p >> 1) & 1, ws = p & 1;
-    const int sh_lo = 2 * ws, sh_hi = 4 + 2 * ws, sci = 8 * (h + 2 * ws);
+    const int sh_lo = 4 - 2 * ws, sh_hi = 2 * ws, sci = 8 * (h + 2 * ws);
 #pragma unroll
     for (int r = 0; r < RT; r++) {
         int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
-            const int lo = static_cast<int>((lw & 0x0F0F0F0Fu) | (((hw >> sh_lo) & 0x03030303u) << 4));
-            const int hi = static_cast<int>(((lw >> 4) & 0x0F0F0F0Fu) | (((hw >> sh_hi) & 0x03030303u) << 4));
+            const int lo = static_cast<int>((lw & 0x0F0F0F0Fu) | ((hw << sh_lo) & 0x30303030u));
+            const int hi = static_cast<int>(((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> sh_hi) & 0x30303030u));
             a0 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[0].x)[i]), a0, false);
             a1 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[1].x)[i]), a1, false);
             a2 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[2].x)[i]), a2, false);
