@@ -6,7 +6,10 @@
 //   q4_0  payload [rows][nb][16 B nibbles]        + scales [rows][nb] f16
 //   q4_1  payload [rows][nb][16 B nibbles]        + scales [rows][nb] (f16 d, f16 m)
 //   q8_0  payload [rows][nb][32 B int8]           + scales [rows][nb] f16
-//   q6_k  payload [rows][nb][208 B ql|qh|sc]      + scales [rows][nb] f16
+//   q6_k  payload [rows][nb][128 B ql]            + records [rows][nb][84 B]:
+//         bytes 8p..8p+7 = the qh bits of chunk p (see q6_k_rows), 64..65 =
+//         f16 d, 68+2p / 69+2p = the chunk's two int8 scales; see
+//         zlm_repack_q6_k
 //   q4_k  payload [rows][nb][128 B qs]            + records [rows][nb][20 B]:
 //         dword 0 = f16 d | f16 dmin << 16, dword 1+g (g = 0..3) = the 6-bit
 //         scales and mins of sub-blocks 2g, 2g+1 decoded to bytes
@@ -306,9 +309,9 @@ struct Frag<Q4_K, RT> {
 template <int RT>
 struct Frag<Q6_K, RT> {
     uint4 ql[RT];
-    uint4 qh[RT];
-    uint2 sc[RT];
-    uint32_t d[RT];
+    uint2 qh[RT];     // the chunk's 32 2-bit high parts, two per byte pair (see q6_k_rows)
+    uint32_t sc[RT];  // bytes 2(p&1), 2(p&1)+1: the chunk's two int8 scales
+    uint32_t d[RT];   // f16 d in the low half
 };
 
 // q4_0 / q4_1: chunk c = block c (16 nibble bytes).  q8_0: chunk c = half
@@ -357,11 +360,11 @@ __device__ __forceinline__ void load_frag(Frag<QT, RT>& f, const TileRows<RT>& t
         } else {
             const int p = c & 7, n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
             const size_t bi = row * nb + (c >> 3);
-            const uint8_t* blk = w + bi * 208;
-            f.ql[r] = ld16<NT>(blk + 64 * n + 32 * ws + 16 * h);
-            f.qh[r] = ld16<false>(blk + 128 + 32 * n + 16 * h);
-            f.sc[r] = ld8<false>(blk + 192 + 8 * n);
-            f.d[r] = ld2<false>(dsc + bi);
+            f.ql[r] = ld16<NT>(w + bi * 128 + (64 * n + 32 * ws + 16 * h));
+            const uint8_t* rec = reinterpret_cast<const uint8_t*>(dsc) + bi * 84;
+            f.qh[r] = ld8<NT>(rec + 8 * p);
+            f.d[r] = ld4<false>(reinterpret_cast<const uint32_t*>(rec + 64));
+            f.sc[r] = ld4<false>(reinterpret_cast<const uint32_t*>(rec + 68 + 4 * (p >> 1)));
         }
     }
 }
@@ -625,16 +628,18 @@ __device__ __forceinline__ void compute_q4_k(const Frag<Q4_K, RT>& f, const floa
 }
 
 // q6_k part p = c&7 of super-block c>>3: half n = p/4, 16-run h, ql half ws;
-// low nibbles + qh bits 2ws are elements 128n + 32ws + 16h + j, high nibbles +
-// qh bits 4+2ws are those +64.  value d*sc*(q-32); Sum (q-32)*x = Sum q*x - 32*Sum x.
-// The two qh bits land at bits 4-5 of each byte with one shift and one mask
-// ((qh << (4-2ws)) or (qh >> 2ws), & 0x30303030): bits shifted in from the
-// neighbouring bytes fall outside the mask.  x through accessors as for q4_k.
+// low nibbles of the 16 ql bytes are elements 128n + 32ws + 16h + j (scale
+// byte 0 of the pair), high nibbles are those +64 (scale byte 1).  The high
+// two bits of ql dword i sit in qh dword i/2 (zlm_repack_q6_k): byte b holds
+// the low-nibble element's bits at 0-1 and the high-nibble element's at 2-3
+// for even i, at 4-5 and 6-7 for odd i, so one shift and one mask put them at
+// bits 4-5 of each byte (bits shifted in from neighbouring bytes fall outside
+// the mask).  value d*sc*(q-32); Sum (q-32)*x = Sum q*x - 32*Sum x.  x through
+// accessors as for q4_k.
 template <int RT, class XA, class XB>
 __device__ __forceinline__ void q6_k_rows(const Frag<Q6_K, RT>& f, int c, XA xa_at, XB xb_at, float xs_a,
                                           float xs_b, bool valid, float* acc) {
-    const int p = c & 7, h = (p >> 1) & 1, ws = p & 1;
-    const int sh_lo = 4 - 2 * ws, sh_hi = 2 * ws, sci = 8 * (h + 2 * ws);
+    const int sh = 16 * (c & 1);  // the scale pair's bit offset in f.sc
     float sa[RT], sbv[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) sa[r] = sbv[r] = 0.0f;
@@ -644,9 +649,9 @@ __device__ __forceinline__ void q6_k_rows(const Frag<Q6_K, RT>& f, int c, XA xa_
         const float4 xb = xb_at(i);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
-            const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
-            const uint32_t lo = (lw & 0x0F0F0F0Fu) | ((hw << sh_lo) & 0x30303030u);
-            const uint32_t hi = ((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> sh_hi) & 0x30303030u);
+            const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i >> 1];
+            const uint32_t lo = (lw & 0x0F0F0F0Fu) | (((i & 1) ? hw : (hw << 4)) & 0x30303030u);
+            const uint32_t hi = ((lw >> 4) & 0x0F0F0F0Fu) | (((i & 1) ? (hw >> 2) : (hw << 2)) & 0x30303030u);
             sa[r] = fmaf(ub(lo, 0), xa.x, sa[r]);
             sa[r] = fmaf(ub(lo, 1), xa.y, sa[r]);
             sa[r] = fmaf(ub(lo, 2), xa.z, sa[r]);
@@ -660,8 +665,8 @@ __device__ __forceinline__ void q6_k_rows(const Frag<Q6_K, RT>& f, int c, XA xa_
 #pragma unroll
     for (int r = 0; r < RT; r++) {
         const float d = valid ? h2f(f.d[r]) : 0.0f;
-        const float sc_a = static_cast<float>(static_cast<int32_t>(f.sc[r].x << (24 - sci)) >> 24);
-        const float sc_b = static_cast<float>(static_cast<int32_t>(f.sc[r].y << (24 - sci)) >> 24);
+        const float sc_a = static_cast<float>(static_cast<int32_t>(f.sc[r] << (24 - sh)) >> 24);
+        const float sc_b = static_cast<float>(static_cast<int32_t>(f.sc[r] << (16 - sh)) >> 24);
         float t = (d * sc_a) * fmaf(-32.0f, xs_a, sa[r]);
         t = fmaf(d * sc_b, fmaf(-32.0f, xs_b, sbv[r]), t);
         acc[r] += t;
@@ -728,16 +733,15 @@ __device__ __forceinline__ void q4_k_xq_rows(const Frag<Q4_K, RT>& f, int c, con
 
 template <int RT>
 __device__ __forceinline__ void q6_k_xq_rows(const Frag<Q6_K, RT>& f, int c, const XqRuns& x, bool valid, float* acc) {
-    const int p = c & 7, h = (p >> 1) & 1, ws = p & 1;
-    const int sh_lo = 4 - 2 * ws, sh_hi = 2 * ws, sci = 8 * (h + 2 * ws);
+    const int sh = 16 * (c & 1);
 #pragma unroll
     for (int r = 0; r < RT; r++) {
         int a0 = 0, a1 = 0, a2 = 0, b0 = 0, b1 = 0, b2 = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i];
-            const int lo = static_cast<int>((lw & 0x0F0F0F0Fu) | ((hw << sh_lo) & 0x30303030u));
-            const int hi = static_cast<int>(((lw >> 4) & 0x0F0F0F0Fu) | ((hw >> sh_hi) & 0x30303030u));
+            const uint32_t lw = (&f.ql[r].x)[i], hw = (&f.qh[r].x)[i >> 1];
+            const int lo = static_cast<int>((lw & 0x0F0F0F0Fu) | (((i & 1) ? hw : (hw << 4)) & 0x30303030u));
+            const int hi = static_cast<int>(((lw >> 4) & 0x0F0F0F0Fu) | (((i & 1) ? (hw >> 2) : (hw << 2)) & 0x30303030u));
             a0 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[0].x)[i]), a0, false);
             a1 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[1].x)[i]), a1, false);
             a2 = __builtin_amdgcn_sdot4(lo, static_cast<int>((&x.pa[2].x)[i]), a2, false);
@@ -746,8 +750,8 @@ __device__ __forceinline__ void q6_k_xq_rows(const Frag<Q6_K, RT>& f, int c, con
             b2 = __builtin_amdgcn_sdot4(hi, static_cast<int>((&x.pb[2].x)[i]), b2, false);
         }
         const float d = valid ? h2f(f.d[r]) : 0.0f;
-        const float sc_a = static_cast<float>(static_cast<int32_t>(f.sc[r].x << (24 - sci)) >> 24);
-        const float sc_b = static_cast<float>(static_cast<int32_t>(f.sc[r].y << (24 - sci)) >> 24);
+        const float sc_a = static_cast<float>(static_cast<int32_t>(f.sc[r] << (24 - sh)) >> 24);
+        const float sc_b = static_cast<float>(static_cast<int32_t>(f.sc[r] << (16 - sh)) >> 24);
         float t = (d * sc_a) * fmaf(-32.0f, x.sa, xq_combine(a0, a1, a2, x.d1a));
         t = fmaf(d * sc_b, fmaf(-32.0f, x.sb, xq_combine(b0, b1, b2, x.d1b)), t);
         acc[r] += t;

@@ -38,6 +38,7 @@ namespace {
 constexpr int kRing = ZLM_RING_SIZE;
 constexpr uint32_t kNoLayout = 0xffffffffu;
 constexpr uint32_t kQ4kRecords = 0xfffffffeu;
+constexpr uint32_t kQ6kRecords = 0xfffffffdu;
 
 // Supported GEMV quants and their GGUF block geometry (the contract's
 // blockElems/blockBytes, reference gpu/backend/root.zig:198-220: the float
@@ -47,11 +48,11 @@ struct QuantInfo {
     uint32_t block_elems;
     uint32_t block_bytes;
     uint32_t payload_bytes;  // bytes per block in the device layout (scales split out)
-    uint32_t scale_offset;   // offset of the f16 scales inside the raw block, kNoLayout (raw layout)
-                             // or kQ4kRecords (zlm_repack_q4_k)
+    uint32_t scale_offset;   // offset of the f16 scales inside the raw block, kNoLayout (raw layout),
+                             // kQ4kRecords (zlm_repack_q4_k) or kQ6kRecords (zlm_repack_q6_k)
     int slot;                // index into the kernel tables
-    uint32_t scale_count;    // 16-bit words per block in the scale area (q4_1: d and m; q4_k: its
-                             // 20-byte record)
+    uint32_t scale_count;    // 16-bit words per block in the scale area (q4_1: d and m; q4_k / q6_k:
+                             // their 20- / 84-byte records)
     uint32_t chunk_elems;    // elements per 16-byte payload chunk of a row (the GEMV's unit)
     uint32_t kblock;         // elements per kernel block: the kernels take nb = k / kblock
 };
@@ -60,7 +61,7 @@ const QuantInfo kQuants[] = {
     {ZLM_GGML_Q4_0, 32, 18, 16, 0, 0, 1, 32, 32},
     {ZLM_GGML_Q8_0, 32, 34, 32, 0, 1, 1, 16, 32},
     {ZLM_GGML_Q4_K, 256, 144, 128, kQ4kRecords, 2, 10, 32, 256},
-    {ZLM_GGML_Q6_K, 256, 210, 208, 208, 3, 1, 32, 256},
+    {ZLM_GGML_Q6_K, 256, 210, 128, kQ6kRecords, 3, 42, 32, 256},
     {ZLM_GGML_Q4_1, 32, 20, 16, 0, 4, 2, 32, 32},
     {ZLM_GGML_F32, 1, 4, 4, kNoLayout, 5, 0, 4, 32},
     {ZLM_GGML_F16, 1, 2, 2, kNoLayout, 6, 0, 8, 32},
@@ -157,6 +158,7 @@ struct zlm_device {
     std::unordered_map<uint64_t, const GemvKernel*> picks;  // kernel picked per shape class (pick_key)
     hipFunction_t repack = nullptr;
     hipFunction_t repack_q4_k = nullptr;
+    hipFunction_t repack_q6_k = nullptr;
     hipFunction_t dequant[kNumQuants] = {};
     hipFunction_t quantize_q8 = nullptr;
     hipFunction_t quantize_q8_tiled = nullptr;
@@ -271,6 +273,7 @@ bool load_kernels(zlm_device* d) {
     }
     if (!ok(d, hipModuleGetFunction(&d->repack, d->mod, "zlm_repack_split"), "zlm_repack_split")) return false;
     if (!ok(d, hipModuleGetFunction(&d->repack_q4_k, d->mod, "zlm_repack_q4_k"), "zlm_repack_q4_k")) return false;
+    if (!ok(d, hipModuleGetFunction(&d->repack_q6_k, d->mod, "zlm_repack_q6_k"), "zlm_repack_q6_k")) return false;
     if (!ok(d, hipModuleGetFunction(&d->quantize_q8, d->mod, "zlm_quantize_q8"), "zlm_quantize_q8")) return false;
     if (!ok(d, hipModuleGetFunction(&d->quantize_q8_tiled, d->mod, "zlm_quantize_q8_tiled"), "quantize tiled"))
         return false;
@@ -348,9 +351,10 @@ bool convert_blocks(zlm_device* d, const uint8_t* raw, uint64_t nblk, const Quan
     if (nblk == 0) return true;
     uint64_t n = nblk;
     const unsigned grid = static_cast<unsigned>((nblk + 255) / 256);
-    if (qi->scale_offset == kQ4kRecords) {
+    if (qi->scale_offset == kQ4kRecords || qi->scale_offset == kQ6kRecords) {
         void* args[] = {&raw, &dst, &scales, &n};
-        return launch(d, d->repack_q4_k, grid, 256, args, "repack q4_k");
+        return launch(d, qi->scale_offset == kQ4kRecords ? d->repack_q4_k : d->repack_q6_k, grid, 256, args,
+                      "repack records");
     }
     uint32_t bb = qi->block_bytes, so = qi->scale_offset, ns = qi->scale_count;
     void* args[] = {&raw, &dst, &scales, &n, &bb, &so, &ns};

@@ -64,6 +64,44 @@ extern "C" __global__ void __launch_bounds__(256)
     }
 }
 
+// q6_k raw super-block (reference quant/k_quants.zig: ql[128], qh[64], int8
+// scales[16], f16 d; 210 bytes) -> payload [nb][128 B ql] (as is) and an
+// 84-byte record per block.  GEMV chunk p (n = p/4, h = (p/2)&1, ws = p&1)
+// reads ql[64n + 32ws + 16h ..+16]; its byte j = 4i + b (ql dword i) holds
+// element 128n + 32ws + 16h + j in the low nibble (qh[32n + 16h + j] bits 2ws)
+// and that element + 64 in the high nibble (bits 4 + 2ws).  Record bytes
+// 8p + 4(i/2) + b carry those two 2-bit parts (low-nibble element at bits 0-1,
+// high at 2-3 for even i; at 4-5 and 6-7 for odd i), bytes 64..65 d, bytes
+// 68 + 2p and 69 + 2p the scales of the chunk's two 16-element runs,
+// scales[8n + h + 2ws] and scales[8n + 4 + h + 2ws].
+extern "C" __global__ void __launch_bounds__(256)
+    zlm_repack_q6_k(const uint8_t* __restrict__ raw, uint8_t* __restrict__ payload, uint8_t* __restrict__ rec,
+                    uint64_t nblocks) {
+    const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (b >= nblocks) return;
+    const uint8_t* src = raw + b * 210;
+    const uint8_t *ql = src, *qh = src + 128, *sc = src + 192;
+    uint8_t* dst = payload + b * 128;
+    for (int i = 0; i < 128; i++) dst[i] = ql[i];
+    uint8_t* o = rec + b * 84;
+    for (int p = 0; p < 8; p++) {
+        const int n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
+        for (int k = 0; k < 8; k++) o[8 * p + k] = 0;
+        for (int j = 0; j < 16; j++) {
+            const int i = j >> 2, bb = j & 3;
+            const uint32_t q = qh[32 * n + 16 * h + j];
+            const uint32_t lo2 = (q >> (2 * ws)) & 3u, hi2 = (q >> (4 + 2 * ws)) & 3u;
+            o[8 * p + 4 * (i >> 1) + bb] |= static_cast<uint8_t>((lo2 | (hi2 << 2)) << (4 * (i & 1)));
+        }
+        o[68 + 2 * p] = sc[8 * n + h + 2 * ws];
+        o[69 + 2 * p] = sc[8 * n + 4 + h + 2 * ws];
+    }
+    o[64] = src[208];
+    o[65] = src[209];
+    o[66] = 0;
+    o[67] = 0;
+}
+
 // ---- dequant from the device layout (bit-exact vs the CPU codecs) ---------
 // One thread per block; `out` receives block_elems floats per block.
 
@@ -157,23 +195,23 @@ extern "C" __global__ void __launch_bounds__(256)
                      uint64_t nblocks) {
     const uint64_t b = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
-    const uint8_t* blk = w + b * 208;
-    const uint8_t *ql = blk, *qh = blk + 128;
-    const int8_t* sc = reinterpret_cast<const int8_t*>(blk + 192);
-    const float d = h2f(dsc[b]);
+    const uint8_t* ql = w + b * 128;
+    const uint8_t* rec = reinterpret_cast<const uint8_t*>(dsc) + b * 84;
+    const float d = h2f(static_cast<uint32_t>(rec[64]) | (static_cast<uint32_t>(rec[65]) << 8));
     float* o = out + b * 256;
-    for (int n = 0; n < 2; n++) {
-        for (int l = 0; l < 32; l++) {
-            const int is = l / 16;
-            const uint8_t a = ql[64 * n + l], a2 = ql[64 * n + l + 32], hb = qh[32 * n + l];
-            const int q1 = (a & 15) | (((hb >> 0) & 3) << 4);
-            const int q2 = (a2 & 15) | (((hb >> 2) & 3) << 4);
-            const int q3 = (a >> 4) | (((hb >> 4) & 3) << 4);
-            const int q4 = (a2 >> 4) | (((hb >> 6) & 3) << 4);
-            o[128 * n + l] = static_cast<float>(q1 - 32) * (d * static_cast<float>(sc[8 * n + is + 0]));
-            o[128 * n + l + 32] = static_cast<float>(q2 - 32) * (d * static_cast<float>(sc[8 * n + is + 2]));
-            o[128 * n + l + 64] = static_cast<float>(q3 - 32) * (d * static_cast<float>(sc[8 * n + is + 4]));
-            o[128 * n + l + 96] = static_cast<float>(q4 - 32) * (d * static_cast<float>(sc[8 * n + is + 6]));
+    for (int p = 0; p < 8; p++) {  // the GEMV's chunks (zlm_repack_q6_k)
+        const int n = p >> 2, h = (p >> 1) & 1, ws = p & 1;
+        const uint8_t* q = ql + 64 * n + 32 * ws + 16 * h;
+        const float sa = static_cast<float>(static_cast<int8_t>(rec[68 + 2 * p]));
+        const float sb = static_cast<float>(static_cast<int8_t>(rec[69 + 2 * p]));
+        const int e = 128 * n + 32 * ws + 16 * h;
+        for (int j = 0; j < 16; j++) {
+            const int i = j >> 2;
+            const uint32_t t = rec[8 * p + 4 * (i >> 1) + (j & 3)] >> (4 * (i & 1));
+            const int qa = (q[j] & 15) | static_cast<int>((t & 3u) << 4);
+            const int qb = (q[j] >> 4) | static_cast<int>(((t >> 2) & 3u) << 4);
+            o[e + j] = static_cast<float>(qa - 32) * (d * sa);
+            o[e + j + 64] = static_cast<float>(qb - 32) * (d * sb);
         }
     }
 }
