@@ -19,8 +19,11 @@ ZLM_GEMVX(zlm_gemv_q4_0_resid_s2_r2, Q4_0, 4096, 2, 2, true, PRO_PLAIN, EPI_RESI
 // one per CU (10.4 -> 9.6 us), the normed q;k;v 6144 x 4096 with 8-wave
 // workgroups at 16 waves per CU (6.4 -> 6.0 us).  4096-row launches (o, C0)
 // stay plain: their workgroups have too few rows to repay the quantization.
+// The normed gate_up runs 16-wave workgroups at one per CU (the RMSNorm and
+// the planes are built once per 16 waves): decode step 1.6028 -> 1.5964 ms
+// per token against 8-wave workgroups at 8 waves per CU.
 ZLM_GEMVX_PFQ(zlm_gemv_q4_0_pair_s2_pfq, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PAIR, false)
-ZLM_GEMVX_PFQ(zlm_gemv_q4_0_normpair_s2_pfq, Q4_0, 4096, 8, 2, 2, PRO_NORM, EPI_PAIR, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_normpair_s2_pfqw16, Q4_0, 4096, 16, 2, 2, PRO_NORM, EPI_PAIR, false)
 ZLM_GEMVX_PFQ(zlm_gemv_q4_0_resid_s6_pfqw16, Q4_0, 12288, 16, 1, 6, PRO_PLAIN, EPI_RESID, true)
 ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s2_pfqw16, Q4_0, 4096, 8, 1, 2, PRO_NORM, EPI_PLAIN, false)
 
