@@ -1409,9 +1409,11 @@ __device__ __forceinline__ uint32_t sk_row(const GemvArgs& a, uint32_t t, int la
 // the other waves' partials in red, store the tile.  EPI_RESID: the residual
 // rides in wave 0's partial, so every wave has its residual load back before
 // the barrier -- y may alias res, and the tile's stores follow the barrier.
+// The in-wave part of a tile's reduction: after the transposing butterfly
+// lane group fr holds row fr's partial of this wave (plus the residual in
+// wave 0), written to red[fr][wid].
 template <int W, int RT, int EPI>
-__device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvArgs& a, uint32_t t, int lane,
-                                          int wid, float rv) {
+__device__ __forceinline__ void sk_park(float* v, float (*red)[W], int lane, int wid, float rv) {
     constexpr int LOG = sk_log<RT>();
 #pragma unroll
     for (int st = 0; st < LOG; st++) {
@@ -1431,15 +1433,32 @@ __device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvA
 #pragma unroll
     for (int off = 32 >> LOG; off >= 1; off >>= 1) s += __shfl_xor(s, off, kWave);
     if constexpr (EPI == EPI_RESID) s += wid == 0 ? rv : 0.0f;
-    const int fr = lane >> (6 - LOG);
-    red[fr][wid] = s;
+    red[lane >> (6 - LOG)][wid] = s;
+}
+
+__device__ __forceinline__ void sk_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Sum a parked tile over the waves in wave order and store its rows (every
+// wave stores the same values; no branch before the store).
+template <int W, int RT>
+__device__ __forceinline__ void sk_store(const float (*red)[W], const GemvArgs& a, uint32_t t, int lane) {
+    const int fr = lane >> (6 - sk_log<RT>());
     float tot = 0.0f;
 #pragma unroll
     for (int w = 0; w < W; w++) tot += red[fr][w];
     a.y[sk_row<RT>(a, t, lane)] = tot;
+}
+
+template <int W, int RT, int EPI>
+__device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvArgs& a, uint32_t t, int lane,
+                                          int wid, float rv) {
+    sk_park<W, RT, EPI>(v, red, lane, wid, rv);
+    sk_barrier();
+    sk_store<W, RT>(red, a, t, lane);
 }
 
 // y = W.x (EPI_PLAIN) or res + W.x (EPI_RESID).  The host launches at most
@@ -1449,17 +1468,20 @@ __device__ __forceinline__ void sk_finish(float* v, float (*red)[W], const GemvA
 // computes one tile the loads of the next NB-1 are in flight (tiles past the
 // end are clamped loads, dropped).  The exit is uniform over the workgroup,
 // so every wave meets every barrier; consecutive tiles use different red
-// buffers, so one barrier per tile suffices.  Scheduling barriers keep each
+// buffers, so one barrier per tile suffices.  With PARK > 0 the tiles' wave
+// partials wait in PARK LDS slots and are summed and stored after one barrier
+// per PARK tiles (fewer waits for the slowest wave; the stores come later).  Scheduling barriers keep each
 // tile's loads ahead of its compute and the compute ahead of the reduction:
 // without them the compiler interleaved the three and reused a prefetch
 // destination register, which costs a wait for every load in flight
 // (measured on gfx950, q8_0 4096 x 12288: 12.0 vs 10.5 us).
-template <int QT, int W, int RT, int SPL, int EPI, bool XQ, int NB, bool EXACT>
+template <int QT, int W, int RT, int SPL, int EPI, bool XQ, int NB, bool EXACT, int PARK = 0>
 __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     static_assert(EPI == EPI_PLAIN || EPI == EPI_RESID, "split-K forms: plain, resid");
     static_assert(!XQ || QT != Q8_0, "q8_0 runs on fp32 x");
     static_assert(NB >= 2, "a ring of at least two fragment sets");
-    __shared__ float red[NB][RT][W];
+    static_assert(PARK % NB == 0, "parked tiles come in whole ring turns");
+    __shared__ float red[PARK > 0 ? PARK : NB][RT][W];
     const int lane = threadIdx.x & (kWave - 1);
     const int wid = static_cast<int>(threadIdx.x / kWave);
     const int C = chunks_per_row<QT>(a.nb);
@@ -1491,6 +1513,52 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 #pragma unroll
     for (int s = 0; s < SPL; s++) xc[s] = make_xchunk<QT, XQ>(xr[s], ok[s]);
     float acc[RT];
+    if constexpr (PARK > 0) {
+        // Parked reduction: each tile's partials wait in LDS slot n; one
+        // barrier per PARK tiles (and one at the end), then every wave sums
+        // and stores the parked tiles.  Same sums in the same order as below.
+        int n = 0;
+        uint32_t t0 = t;
+        auto flush = [&]() {
+            sk_barrier();
+            for (int j = 0; j < n; j++) sk_store<W, RT>(red[j], a, t0 + static_cast<uint32_t>(j) * G, lane);
+            sk_barrier();
+        };
+        while (static_cast<uint64_t>(t) + static_cast<uint64_t>(NB - 1) * G < ntiles) {
+#pragma unroll
+            for (int p = 0; p < NB; p++) {
+                issue((p + NB - 1) % NB, NB - 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+#pragma unroll
+                for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], cs[s], ok[s], acc);
+                __builtin_amdgcn_sched_barrier(0);
+                sk_park<W, RT, EPI>(acc, red[n + p], lane, wid, rv[p]);
+                t += G;
+            }
+            n += NB;
+            if (n == PARK) {
+                flush();
+                n = 0;
+                t0 = t;
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < NB - 1; p++) {
+            if (t < ntiles) {
+#pragma unroll
+                for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+#pragma unroll
+                for (int s = 0; s < SPL; s++) dot_xchunk<RT>(f[p][s], xc[s], cs[s], ok[s], acc);
+                sk_park<W, RT, EPI>(acc, red[n], lane, wid, rv[p]);
+                n++;
+                t += G;
+            }
+        }
+        flush();
+        return;
+    }
     // Whole turns of the ring (all NB tiles exist) in a loop with one exit, so
     // the compiler's wait counts stay exact across the back edge; then the
     // last fewer-than-NB tiles, whose loads are already in flight.
@@ -1568,6 +1636,11 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 #define ZLM_GEMV_SK(NAME, QT, W, RT, SPL, EPI, XQ, NB, EXACT)                   \
     extern "C" __global__ void __launch_bounds__(W * 64) NAME(GemvArgs a) {     \
         gemv_sk<QT, W, RT, SPL, EPI, XQ, NB, EXACT>(a);                        \
+    }
+// The same with the parked reduction: one barrier per PARK tiles.
+#define ZLM_GEMV_SKP(NAME, QT, W, RT, SPL, EPI, XQ, NB, EXACT, PARK)           \
+    extern "C" __global__ void __launch_bounds__(W * 64) NAME(GemvArgs a) {     \
+        gemv_sk<QT, W, RT, SPL, EPI, XQ, NB, EXACT, PARK>(a);                  \
     }
 #define ZLM_GEMVX_FORMS(QN, QT, KCAP, STEPS, EXACT, SFX)                                           \
     ZLM_GEMVX(zlm_gemv_##QN##_pair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_PLAIN, EPI_PAIR)           \

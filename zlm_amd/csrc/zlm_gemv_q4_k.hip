@@ -14,8 +14,9 @@ ZLM_GEMVX_PF(zlm_gemv_q4_k_r1_s8_pf, Q4_K, 16384, 8, 1, 8, PRO_PLAIN, EPI_PLAIN,
 // 8-wave workgroups, one per CU, four rows per tile, x as int8 planes in
 // registers; measured on gfx950 16.7 -> 12.2 us against the prefetching
 // instance above (13.0 us with fp32 x and two rows per tile), 10.7 us on the
-// qs + record layout.
-ZLM_GEMV_SK(zlm_gemv_q4_k_r1_s8_sk4, Q4_K, 8, 4, 1, EPI_PLAIN, true, 2, false)
+// qs + record layout, 10.4 us with the parked reduction (one barrier per 16
+// tiles instead of one per tile).
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s8_sk4, Q4_K, 8, 4, 1, EPI_PLAIN, true, 2, false, 16)
 
 // k <= 4096 (the C3 gate/up 15360 x 3840): x as int8 planes, prefetching
 // 16-wave workgroups, one per CU (the x planes are built once per 16 waves);

@@ -22,7 +22,9 @@ ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r1_s2_tallq, Q6_K, 4096, 8, 1, 2, PRO_PLAIN, EPI_PLA
 // Split-K form for 7 < chunks/64 <= 8 (the C3 down projection 3840 x 15360):
 // 8-wave workgroups, one per CU, two rows per tile; measured on gfx950 19.5 ->
 // 14.8 us against the 4-wave exact-steps instance, 13.1 us on the ql + record
-// layout.
-ZLM_GEMV_SK(zlm_gemv_q6_k_r1_s8_sk2, Q6_K, 8, 2, 1, EPI_PLAIN, false, 2, false)
+// layout, 12.5 us with the parked reduction (one barrier per 16 tiles).  The
+// q8_0 / q4_0 split-K downs measured slower parked (10.6 -> 11.4, 9.1 -> 9.5
+// us) and keep one barrier per tile.
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s8_sk2, Q6_K, 8, 2, 1, EPI_PLAIN, false, 2, false, 16)
 
 ZLM_GEMV_MULTI_Q4(q6_k, Q6_K)
