@@ -237,6 +237,7 @@ __device__ __forceinline__ float wave_sum_all(float v) {
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef unsigned int v2u_a4 __attribute__((ext_vector_type(2), aligned(4)));  // 8 bytes at a 4-byte boundary
 
 template <bool NT>
 __device__ __forceinline__ uint4 ld16(const uint8_t* p) {
@@ -256,6 +257,14 @@ __device__ __forceinline__ uint2 ld8(const uint8_t* p) {
     } else {
         return *reinterpret_cast<const uint2*>(p);
     }
+}
+
+// 8 bytes from a 4-byte aligned address (the q6_k records have an 84-byte stride).
+template <bool NT>
+__device__ __forceinline__ uint2 ld8_a4(const uint8_t* p) {
+    const v2u_a4 t = NT ? __builtin_nontemporal_load(reinterpret_cast<const v2u_a4*>(p))
+                        : *reinterpret_cast<const v2u_a4*>(p);
+    return make_uint2(t.x, t.y);
 }
 
 template <bool NT>
@@ -362,7 +371,7 @@ __device__ __forceinline__ void load_frag(Frag<QT, RT>& f, const TileRows<RT>& t
             const size_t bi = row * nb + (c >> 3);
             f.ql[r] = ld16<NT>(w + bi * 128 + (64 * n + 32 * ws + 16 * h));
             const uint8_t* rec = reinterpret_cast<const uint8_t*>(dsc) + bi * 84;
-            f.qh[r] = ld8<NT>(rec + 8 * p);
+            f.qh[r] = ld8_a4<NT>(rec + 8 * p);
             f.d[r] = ld4<false>(reinterpret_cast<const uint32_t*>(rec + 64));
             f.sc[r] = ld4<false>(reinterpret_cast<const uint32_t*>(rec + 68 + 4 * (p >> 1)));
         }
