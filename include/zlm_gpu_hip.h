@@ -214,8 +214,8 @@ bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant,
  * one x_dev (k floats), res[i] (rows[i] x k, all of one quant type) into
  * y_dev[i], enqueued as one launch (no wait) -- or as n launches of the
  * single-op kernel where that kernel sums in another order (split-K: the
- * down-projection shapes; int8-plane x: Q4_K at k <= 4096), so every row
- * always equals the single op's bit for bit. */
+ * down-projection shapes; int8-plane x: Q4_K and Q6_K at k <= 4096, the
+ * q4_0 fused forms), so every row always equals the single op's bit for bit. */
 bool zlm_gpu_mat_vec_batch_enqueue(zlm_device *dev, zlm_resident *const *res, uint32_t quant, const size_t *rows,
                                    size_t n, size_t k, const float *x_dev, float *const *y_dev);
 /* Enqueue the prefill GEMM out_dev[t*rows + r] (x_dev: m x k fp32, token-major):
