@@ -12,4 +12,11 @@ ZLM_GEMVX_Q8(q8_0, Q8_0)
 // ~320 registers per wave and runs one wave per SIMD).
 ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s12_sk2x, Q8_0, 12, 2, 1, EPI_PLAIN, false, 2, true)
 
+// The lm_heads (from 65536 rows, k = 4096): prefetching 8-wave workgroups at
+// 16 waves per CU, plain and RMSNorm-fused; measured on gfx950 at 151936 x
+// 4096: 98.6 -> 94.8 us against the 4-wave exact-steps instance at 8
+// workgroups per CU.
+ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s4_tall, Q8_0, 4096, 8, 1, 4, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q8_0_norm_s4_tall, Q8_0, 4096, 8, 1, 4, PRO_NORM, EPI_PLAIN, false)
+
 ZLM_GEMV_MULTI_Q8(q8_0, Q8_0)

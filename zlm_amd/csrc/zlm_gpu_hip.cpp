@@ -421,16 +421,17 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
 }
 
 // The prefetching instances' name suffixes, the grid's waves per CU, the
-// fewest rows a suffix is taken for (_tallq: the lm_heads) and whether x is
-// staged as int8 planes (a summation the batch kernel does not share).
+// fewest rows a suffix is taken for (_tallq / _tall: the lm_heads, with and
+// without int8-plane x) and whether x is staged as int8 planes (a summation
+// the batch kernel does not share).
 struct PfSuffix {
     const char* suffix;
     int waves_per_cu;
     size_t min_rows;
     bool xq;
 };
-constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true}, {"_pf", 8, 0, false},   {"_pfw16", 16, 0, false},
-                                    {"_pfq", 8, 0, true},        {"_pfqw16", 16, 0, true}};
+constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true}, {"_tall", 16, 65536, false}, {"_pf", 8, 0, false},
+                                    {"_pfw16", 16, 0, false},    {"_pfq", 8, 0, true},          {"_pfqw16", 16, 0, true}};
 
 // The split-K instances' name suffixes: _sk<RT> (RT rows per tile) for any
 // row of ceil(chunks / 64) == steps, _sk<RT>x for exact rows only (chunks ==
@@ -455,8 +456,8 @@ const GemvKernel* find_split(zlm_device* d, const QuantInfo* qi, size_t k, const
 
 // The GEMV kernel for a shape: for a 1-row tile the split-K instance of the
 // shape if the quant has one, else the prefetching instance of the exact step
-// count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_tallq from 65536
-// rows, _pf, _pfw16, _pfq, _pfqw16); else the
+// count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_tallq or _tall
+// from 65536 rows, _pf, _pfw16, _pfq, _pfqw16); else the
 // instance whose step count equals ceil(chunks per row / 64) with the
 // requested row tile, else with a 1-row tile, else the generic bounded
 // instance.  Chunks per row: k / chunk_elems (k/16 for q8_0, k/32 for q4_0,
@@ -696,7 +697,7 @@ const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k,
         }
     }
     for (const PfSuffix& v : kPfSuffixes) {
-        if (v.min_rows > 0) continue;
+        if (rows < v.min_rows) continue;
         snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d%s", qn, kFormNames[form], steps, v.suffix);
         if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, v.waves_per_cu, true, false, v.xq)) return g;
     }
