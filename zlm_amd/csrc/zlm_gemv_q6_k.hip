@@ -14,10 +14,10 @@ ZLM_GEMVX_Q4(q6_k, Q6_K)
 ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r1_s2_pfqw16, Q6_K, 4096, 16, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
 
 // The lm_head (from 65536 rows, k <= 4096): x as int8 planes, prefetching
-// 8-wave workgroups at 16 waves per CU; measured on gfx950 at 262144 x 3840:
-// 190.7 -> 156.5 us against the 4-wave exact-steps instance, 147.7 us on the
-// ql + record layout.
-ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r1_s2_tallq, Q6_K, 4096, 8, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
+// 8-wave workgroups at 16 waves per CU, two rows per wave tile; measured on
+// gfx950 at 262144 x 3840: 190.7 -> 156.5 us against the 4-wave exact-steps
+// instance, 147.7 us on the ql + record layout, 140.8 us with two-row tiles.
+ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r2_s2_tallq, Q6_K, 4096, 8, 2, 2, PRO_PLAIN, EPI_PLAIN, false)
 
 // Split-K form for 7 < chunks/64 <= 8 (the C3 down projection 3840 x 15360):
 // 8-wave workgroups, one per CU, two rows per tile; measured on gfx950 19.5 ->

@@ -429,9 +429,11 @@ struct PfSuffix {
     int waves_per_cu;
     size_t min_rows;
     bool xq;
+    int rt;  // rows per wave tile of the plain (r<rt>) instance
 };
-constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true}, {"_tall", 16, 65536, false}, {"_pf", 8, 0, false},
-                                    {"_pfw16", 16, 0, false},    {"_pfq", 8, 0, true},          {"_pfqw16", 16, 0, true}};
+constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true, 2}, {"_tall", 16, 65536, false, 1},
+                                    {"_pf", 8, 0, false, 1},         {"_pfw16", 16, 0, false, 1},
+                                    {"_pfq", 8, 0, true, 1},         {"_pfqw16", 16, 0, true, 1}};
 
 // The split-K instances' name suffixes: _sk<RT> (RT rows per tile) for any
 // row of ceil(chunks / 64) == steps, _sk<RT>x for exact rows only (chunks ==
@@ -456,8 +458,9 @@ const GemvKernel* find_split(zlm_device* d, const QuantInfo* qi, size_t k, const
 
 // The GEMV kernel for a shape: for a 1-row tile the split-K instance of the
 // shape if the quant has one, else the prefetching instance of the exact step
-// count if the quant has one (zlm_gemv_<quant>_r1_s<steps>_tallq or _tall
-// from 65536 rows, _pf, _pfw16, _pfq, _pfqw16); else the
+// count if the quant has one (zlm_gemv_<quant>_r2_s<steps>_tallq or
+// _r1_s<steps>_tall from 65536 rows, then _r1_s<steps> with _pf, _pfw16, _pfq,
+// _pfqw16); else the
 // instance whose step count equals ceil(chunks per row / 64) with the
 // requested row tile, else with a 1-row tile, else the generic bounded
 // instance.  Chunks per row: k / chunk_elems (k/16 for q8_0, k/32 for q4_0,
@@ -502,8 +505,8 @@ const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, 
         if (const GemvKernel* g = find_split(d, qi, k, "r1")) return g;
         for (const PfSuffix& v : kPfSuffixes) {
             if (rows < v.min_rows) continue;
-            snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_s%d%s", qn, steps, v.suffix);
-            if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps, v.waves_per_cu, true, false, v.xq))
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d%s", qn, v.rt, steps, v.suffix);
+            if (const GemvKernel* g = find_gemv(d, qi->slot, nm, v.rt, steps, v.waves_per_cu, true, false, v.xq))
                 return g;
         }
     }
