@@ -247,7 +247,8 @@ def test_quantizer_bit_exact(dev):
 
 CONFIG_SHAPES = [
     ("c0_q4_0", synth.Q4_0, 4096, 4096),
-    ("tall_q6_k", synth.Q6_K, 65536 + 37, 3840),  # the lm_head kernel (from 65536 rows)
+    ("tall_q6_k", synth.Q6_K, 65536 + 37, 3840),  # the lm_head kernels (from 65536 rows)
+    ("tall_q8_0", synth.Q8_0, 65536 + 37, 4096),
     ("c1_gate_q8_0", synth.Q8_0, 12288, 4096),
     ("c1_down_q8_0", synth.Q8_0, 4096, 12288),
     ("c3_gate_q4_k", synth.Q4_K, 15360, 3840),

@@ -94,7 +94,9 @@ class DecodeModel:
 
     ``host`` (optional) gives the weights as raw GGUF bytes and f32 norm
     vectors, per layer: 'qkv', 'o', 'gate', 'up', 'down', 'attn_norm',
-    'ffn_norm', 'q_norm', 'k_norm'; plus 'lm_head' and 'out_norm'.  Without it
+    'ffn_norm', 'q_norm', 'k_norm', and optionally the f16 caches 'k_cache' /
+    'v_cache' ([n_kv_heads][max_seq][head_dim], zeros when absent); plus
+    'lm_head' and 'out_norm'.  Without it
     the projections are synthesised in HBM (q4_0 scales |N(0,1)|*0.02, q8_0
     |N(0,1)|*0.01) and the norm weights are 1 + 0.1 N(0,1)."""
 
@@ -146,8 +148,13 @@ class DecodeModel:
                 dev.synth_f16(kc, cache_elems, seed + s + 7, 1.0)
                 dev.synth_f16(vc, cache_elems, seed + s + 8, 1.0)
             else:
-                dev.dev_upload(kc, np.zeros(cache_elems, np.float16))
-                dev.dev_upload(vc, np.zeros(cache_elems, np.float16))
+                for cache, name in ((kc, "k_cache"), (vc, "v_cache")):
+                    hist = L.get(name)
+                    if hist is None:
+                        hist = np.zeros(cache_elems, np.float16)
+                    elif hist.dtype != np.float16 or hist.size != cache_elems:
+                        raise ValueError(f"layer {i} {name}: {cache_elems} f16 values expected")
+                    dev.dev_upload(cache, np.ascontiguousarray(hist).reshape(-1))
             self.layers.append(_Layer(
                 qkv=res("qkv", c.qkv_rows, c.hidden, c.proj_type, L, s + 1),
                 o=res("o", c.hidden, c.n_heads * c.head_dim, c.proj_type, L, s + 2),

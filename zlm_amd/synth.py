@@ -22,6 +22,8 @@ The raw byte layout is GGUF's (block formats as in the reference's
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 GAMMA = np.uint64(0x9E3779B97F4A7C15)
@@ -93,40 +95,82 @@ def _bf16_bytes(v: np.ndarray) -> np.ndarray:
     return r.view(np.uint8).reshape(-1, 2)
 
 
+def _bytes_at(seed: int, stream: int, byte0: int, n: int) -> np.ndarray:
+    """Bytes [byte0, byte0 + n) of stream ``stream`` (what ``random_bytes``
+    returns for the whole stream, sliced)."""
+    w0 = byte0 // 8
+    words = u64(seed, stream, (byte0 + n + 7) // 8 - w0, offset=w0)
+    lo = byte0 - 8 * w0
+    return words.view(np.uint8)[lo:lo + n]
+
+
+def _normal_at(seed: int, stream: int, i0: int, n: int) -> np.ndarray:
+    """Values [i0, i0 + n) of ``normal(seed, stream, ...)``."""
+    w = u64(seed, stream, 2 * n, offset=2 * i0)
+    a = (w[0::2] >> np.uint64(11)).astype(np.float64)
+    b = (w[1::2] >> np.uint64(11)).astype(np.float64)
+    u1 = (a + 1.0) * (1.0 / 9007199254740992.0)
+    u2 = b * (1.0 / 9007199254740992.0)
+    return np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+
+
+def _fill_blocks(out: np.ndarray, qtype: int, seed: int, b0: int) -> None:
+    """Blocks [b0, b0 + len(out)) of a weight stream into ``out`` (n x block bytes)."""
+    n = out.shape[0]
+    if qtype == Q4_0:
+        out[:, 0:2] = _f16_bytes(np.abs(_normal_at(seed, 1, b0, n)) * 0.02)
+        out[:, 2:18] = _bytes_at(seed, 2, 16 * b0, 16 * n).reshape(n, 16)
+    elif qtype == Q8_0:
+        out[:, 0:2] = _f16_bytes(np.abs(_normal_at(seed, 1, b0, n)) * 0.01)
+        r = _bytes_at(seed, 2, 64 * b0, 64 * n).view(np.uint16).astype(np.uint32)
+        q = ((r * 255) >> 16).astype(np.int32) - 127
+        out[:, 2:34] = q.astype(np.int8).view(np.uint8).reshape(n, 32)
+    elif qtype == Q4_1:
+        out[:, 0:2] = _f16_bytes(np.abs(_normal_at(seed, 1, b0, n)) * 0.02)
+        out[:, 2:4] = _f16_bytes(-np.abs(_normal_at(seed, 3, b0, n)) * 0.1)
+        out[:, 4:20] = _bytes_at(seed, 2, 16 * b0, 16 * n).reshape(n, 16)
+    elif qtype == Q4_K:
+        out[:, 0:2] = _f16_bytes(np.abs(_normal_at(seed, 1, b0, n)) * 0.02)
+        out[:, 2:4] = _f16_bytes(np.abs(_normal_at(seed, 3, b0, n)) * 0.02)
+        out[:, 4:144] = _bytes_at(seed, 2, 140 * b0, 140 * n).reshape(n, 140)
+    elif qtype == Q6_K:
+        out[:, 0:208] = _bytes_at(seed, 2, 208 * b0, 208 * n).reshape(n, 208)
+        out[:, 208:210] = _f16_bytes(np.abs(_normal_at(seed, 1, b0, n)) * 0.02)
+    elif qtype == F32:
+        out[:] = np.ascontiguousarray((_normal_at(seed, 1, b0, n) * 0.02).astype(np.float32)).view(
+            np.uint8).reshape(n, 4)
+    elif qtype == F16:
+        out[:] = _f16_bytes(_normal_at(seed, 1, b0, n) * 0.02)
+    elif qtype == BF16:
+        out[:] = _bf16_bytes(_normal_at(seed, 1, b0, n) * 0.02)
+    else:
+        raise ValueError(f"unsupported type {qtype}")
+
+
+_CHUNK_BYTES = 16 << 20
+
+
 def weights(qtype: int, rows: int, k: int, seed: int) -> np.ndarray:
-    """Raw GGUF bytes of a ``rows x k`` weight (row-major blocks), uint8."""
+    """Raw GGUF bytes of a ``rows x k`` weight (row-major blocks), uint8.
+    Large tensors are generated in chunks on a few threads (numpy releases
+    the GIL); the bytes do not depend on the chunking."""
+    if qtype not in BLOCK_ELEMS:
+        raise ValueError(f"unsupported type {qtype}")
     be, bb = BLOCK_ELEMS[qtype], BLOCK_BYTES[qtype]
     if k % be:
         raise ValueError(f"k={k} is not a multiple of the {TYPE_NAMES[qtype]} block ({be})")
     nblk = rows * (k // be)
     out = np.empty((nblk, bb), dtype=np.uint8)
-    if qtype == Q4_0:
-        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
-        out[:, 2:18] = random_bytes(seed, 2, nblk * 16).reshape(nblk, 16)
-    elif qtype == Q8_0:
-        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.01)
-        r = random_bytes(seed, 2, nblk * 64).view(np.uint16).astype(np.uint32)
-        q = ((r * 255) >> 16).astype(np.int32) - 127
-        out[:, 2:34] = q.astype(np.int8).view(np.uint8).reshape(nblk, 32)
-    elif qtype == Q4_1:
-        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
-        out[:, 2:4] = _f16_bytes(-np.abs(normal(seed, 3, nblk)) * 0.1)
-        out[:, 4:20] = random_bytes(seed, 2, nblk * 16).reshape(nblk, 16)
-    elif qtype == Q4_K:
-        out[:, 0:2] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
-        out[:, 2:4] = _f16_bytes(np.abs(normal(seed, 3, nblk)) * 0.02)
-        out[:, 4:144] = random_bytes(seed, 2, nblk * 140).reshape(nblk, 140)
-    elif qtype == Q6_K:
-        out[:, 0:208] = random_bytes(seed, 2, nblk * 208).reshape(nblk, 208)
-        out[:, 208:210] = _f16_bytes(np.abs(normal(seed, 1, nblk)) * 0.02)
-    elif qtype == F32:
-        out[:] = np.ascontiguousarray((normal(seed, 1, nblk) * 0.02).astype(np.float32)).view(np.uint8).reshape(nblk, 4)
-    elif qtype == F16:
-        out[:] = _f16_bytes(normal(seed, 1, nblk) * 0.02)
-    elif qtype == BF16:
-        out[:] = _bf16_bytes(normal(seed, 1, nblk) * 0.02)
+    per = max(1, _CHUNK_BYTES // bb)
+    starts = list(range(0, nblk, per))
+    if len(starts) <= 1:
+        _fill_blocks(out, qtype, seed, 0)
     else:
-        raise ValueError(f"unsupported type {qtype}")
+        from concurrent.futures import ThreadPoolExecutor
+
+        workers = max(1, min(8, len(os.sched_getaffinity(0)), len(starts)))
+        with ThreadPoolExecutor(workers) as pool:
+            list(pool.map(lambda b0: _fill_blocks(out[b0:b0 + per], qtype, seed, b0), starts))
     return out.reshape(-1)
 
 
