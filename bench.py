@@ -7,14 +7,17 @@ weights already resident in HBM and activations already on the device.  Every
 step reads a different copy of the three weights (>= 512 MiB in rotation), so
 the 256 MiB Infinity Cache cannot serve them and the rate is an HBM rate.
 
-Timing: W warm-up steps, then K steps between two HIP events on the backend's
-stream (the stream every launch goes to).  `value` = algorithmic bytes of a
-step (weights + x + y) / (elapsed / K).  The defaults (W = K = 2000, ~65 ms
-each) let the GPU's clocks settle after the host-side weight synthesis: with
-W = 40 the same run measured ~4.5% lower.  The roofline object reports the
-dominant kernel (the k=4096 Q8_0 GEMV of gate/up), timed on its own after
-~50 ms of untimed launches, median of three runs; the other configs likewise.  The CPU baseline is the oracle's restatement of zlm's production sweep
-on the same gate weight, on the host cores.
+Timing: W warm-up steps, then untimed steps until at least 50 ms of GPU work
+has run (the clocks ramp over the first milliseconds after the host-side weight
+synthesis; a short warm-up alone read ~4.5% low), then exactly K steps between
+two HIP events on the backend's stream (the stream every launch goes to).
+`value` = algorithmic bytes of a step (weights + x + y) / (elapsed / K).  The
+roofline object reports the dominant kernel (the k=4096 Q8_0 GEMV of gate/up),
+timed on its own after ~50 ms of untimed launches, median of three runs; the
+other configs likewise.  The CPU baseline is the oracle's restatement of zlm's
+production sweep on the same gate weight, on one thread per physical core (at
+most 16, the CPU share of one GPU) and on one thread; configs[4] and [2] get
+CPU figures of their own in `extra`.
 
 Prints one JSON line.  --gpus N with N > 1 is refused: this backend runs on one
 GPU.
@@ -40,6 +43,8 @@ MALL_DEFEAT_BYTES = 512 * 1024 * 1024
 # The kernel the host picks for the 12288 x 4096 Q8_0 gate/up GEMV (the roofline kernel).
 ROOFLINE_KERNEL = "zlm_gemv_q8_0_r1_s4"
 METRIC = "quant GEMV HBM GB/s (% of 8 TB/s peak); decode tok/s, Qwen3-8B-shape Q4_0 bs=1"
+# Untimed GPU work before the headline's timed steps, whatever --warmup is.
+CLOCK_WARM_MS = 50.0
 
 
 def log(msg: str) -> None:
@@ -95,14 +100,43 @@ def time_launches(dev, descs, launches_target, warmup_ms=50.0):
     return runs[1]
 
 
+def cpu_threads() -> int:
+    """One thread per physical core among the cores this process may run on
+    (the reference pins one worker per physical core), at most 16: the CPU
+    share of one GPU on the benchmark box."""
+    cpus = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology"
+        try:
+            with open(f"{base}/physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(f"{base}/core_id") as f:
+                core = f.read().strip()
+            cores.add((pkg, core))
+        except OSError:
+            cores.add(("?", str(c)))
+    return max(1, min(16, len(cores)))
+
+
+def _min_time(fn, budget_s: float, max_reps: int = 50000) -> tuple:
+    """(best seconds, reps) of fn(reps) -> min-of-reps seconds, sized to ~budget_s."""
+    t1 = fn(2)
+    reps = max(3, min(max_reps, int(budget_s / max(t1, 1e-6))))
+    return min(t1, fn(reps)), reps + 2
+
+
 def cpu_baseline(g: Gemv, budget_s: float):
+    """The oracle's restatement of zlm's production sweep on the headline gate
+    weight: all physical cores (<= 16) split by rangeOf, and one thread."""
     import oracle
 
-    threads = min(16, len(os.sched_getaffinity(0)))
-    t1 = oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=threads, reps=3)  # warm, min of 3
-    reps = max(3, min(50000, int(budget_s / max(t1, 1e-6))))
+    threads = cpu_threads()
     t0 = time.perf_counter()
-    best = oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=threads, reps=reps)
+    best, reps = _min_time(lambda r: oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=threads, reps=r),
+                           0.6 * budget_s)
+    best1, reps1 = _min_time(lambda r: oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=1, reps=r),
+                             0.4 * budget_s, max_reps=200)
     spent = time.perf_counter() - t0
     return {
         "value": round(g.algo_bytes / best / 1e9, 3),
@@ -110,20 +144,67 @@ def cpu_baseline(g: Gemv, budget_s: float):
         "cores": threads,
         "kind": "port",
         "sample": f"oracle restatement of zlm's production sweep (-O3, x86-64-v3, lanes=8), "
-                  f"{g.name} {g.rows}x{g.k} Q8_0 GEMV, {threads} threads split by rangeOf, "
-                  f"min of {reps} reps ({spent:.1f} s)",
+                  f"{g.name} {g.rows}x{g.k} Q8_0 GEMV, {threads} threads (one per physical core, at most 16) "
+                  f"split by rangeOf, min of {reps} reps; 1 thread: min of {reps1} reps ({spent:.1f} s in all)",
         "ms_per_gemv": round(best * 1e3, 4),
+        "one_thread": {"value": round(g.algo_bytes / best1 / 1e9, 3), "unit": "GB/s",
+                       "ms_per_gemv": round(best1 * 1e3, 4)},
     }
+
+
+def cpu_prefill_sample(w: np.ndarray, rows: int, k: int, budget_s: float):
+    """configs[4] on the CPU: the oracle's int path (q8 activations, zlm's
+    Q4_0 intBlock) over a 64-token sample of the 512-token workload, all
+    physical cores; rates scale per token."""
+    import oracle
+
+    threads = cpu_threads()
+    m = 64
+    x = synth.activation(0x5A4C4D0D, m * k)
+    best, reps = _min_time(
+        lambda r: oracle.time_matmul_int(synth.Q4_0, w, k, rows, m, x, threads=threads, reps=r), budget_s, 20)
+    ops = 2.0 * rows * k * m
+    return {"tok_per_s": round(m / best, 1), "TOPS_int8": round(ops / best / 1e12, 4), "cores": threads,
+            "kind": "port", "sample": f"orc_matmul_int Q4_0 {rows}x{k}, {m} of the 512 tokens, {threads} threads "
+                                      f"split by rangeOf, min of {reps} reps"}
+
+
+def cpu_decode_sample(cfg, budget_s: float):
+    """configs[2] on the CPU: one token's projection GEMVs (q;k;v, o, gate, up,
+    down per layer, times the layer count, plus the Q8_0 lm_head) with the
+    oracle's production sweep on all physical cores.  Attention and the
+    elementwise glue are not included (on the GPU they are ~20% of a token)."""
+    import oracle
+
+    threads = cpu_threads()
+    per = max(0.5, budget_s / 6.0)
+    h, f = cfg.hidden, cfg.ffn
+    shapes = [("qkv", cfg.qkv_rows, h, synth.Q4_0), ("o", h, cfg.n_heads * cfg.head_dim, synth.Q4_0),
+              ("gate", f, h, synth.Q4_0), ("up", f, h, synth.Q4_0), ("down", h, f, synth.Q4_0)]
+    layer_s = 0.0
+    for i, (name, rows, k, qt) in enumerate(shapes):
+        w = synth.weights(qt, rows, k, 0x5A4C4D70 + i)
+        x = synth.activation(0x5A4C4D78 + i, k)
+        layer_s += _min_time(lambda r: oracle.time_matvec(qt, w, k, rows, x, threads=threads, reps=r), per, 200)[0]
+    w = synth.weights(cfg.lm_type, cfg.vocab, h, 0x5A4C4D7F)
+    x = synth.activation(0x5A4C4D7E, h)
+    lm_s = _min_time(lambda r: oracle.time_matvec(cfg.lm_type, w, h, cfg.vocab, x, threads=threads, reps=r), per,
+                     50)[0]
+    tok_s = cfg.n_layers * layer_s + lm_s
+    return {"tok_per_s": round(1.0 / tok_s, 2), "ms_per_token": round(tok_s * 1e3, 2), "cores": threads,
+            "kind": "port", "sample": f"production-sweep GEMVs of one layer (x{cfg.n_layers}) and the lm_head, "
+                                      f"{threads} threads, min of reps each; attention and glue not timed"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=16.0,
+                    help="CPU-baseline budget: half on the headline GEMV, a quarter each on configs[4] and [2]")
     ap.add_argument("--decode-replays", type=int, default=30, metavar="N",
                     help="graph replays per timed decode run (warm-up run + 3 timed runs of N)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -159,14 +240,26 @@ def main():
         step_descs += [gate.desc(c), up.desc(c), down.desc(c)]
     step_bytes = gate.algo_bytes + up.algo_bytes + down.algo_bytes
 
-    passes_w = max(1, args.warmup // copies)
-    passes = max(1, args.steps // copies)
-    dev.time_gemv_sequence(step_descs, passes_w)
-    ms_total = dev.time_gemv_sequence(step_descs, passes)
-    steps = passes * copies
+    def steps_of(n):  # n consecutive steps, step i on weight copy i % copies
+        out = []
+        for i in range(n):
+            out += [gate.desc(i), up.desc(i), down.desc(i)]
+        return out
+
+    # W warm-up steps, then untimed steps until >= 50 ms of GPU time have run
+    # since the host-side synthesis (the clocks ramp over the first
+    # milliseconds; a short warm-up alone reads several percent low), then
+    # exactly K timed steps.
+    steps = max(1, args.steps)
+    warmup = max(0, args.warmup)
+    clock_ms = dev.time_gemv_sequence(steps_of(warmup), 1) if warmup else 0.0
+    while clock_ms < CLOCK_WARM_MS:
+        clock_ms += dev.time_gemv_sequence(step_descs, max(1, 200 // copies))
+    ms_total = dev.time_gemv_sequence(steps_of(steps), 1)
     ms_step = ms_total / steps
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"C1 step: {ms_step * 1e3:.2f} us -> {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak)")
+    log(f"C1 step: {ms_step * 1e3:.2f} us -> {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak) over "
+        f"{steps} steps after {warmup} warm-up steps ({clock_ms:.1f} ms of untimed GPU work)")
 
     # dominant kernel: the k=4096 gate/up GEMV, alone, same rotation
     gu_descs = []
@@ -192,9 +285,9 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(gate, args.cpu_seconds)
-        log(f"CPU: {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"CPU baseline (~{0.5 * args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(gate, 0.5 * args.cpu_seconds)
+        log(f"CPU: {cpu['value']} GB/s on {cpu['cores']} threads, {cpu['one_thread']['value']} GB/s on 1")
     for g in (gate, up, down):
         g.free()
 
@@ -243,6 +336,10 @@ def main():
             "tok_per_s": round(m / (ms * 1e-3), 1),
             "note": "activation quantizer + int8-MFMA GEMM per iteration; dense int8 peak taken as 5.0 POP/s"}
         log(f"c4 prefill GEMM: {ms * 1e3:.1f} us, {ops / (ms * 1e-3) / 1e12:.1f} TOP/s")
+        if not args.no_cpu:
+            c4cpu = cpu_prefill_sample(w, rows, k, 0.25 * args.cpu_seconds)
+            extra["c4_prefill_q4_0_12288x4096_m512"]["cpu_baseline"] = c4cpu
+            log(f"c4 CPU: {c4cpu['tok_per_s']} tok/s on {c4cpu['cores']} threads")
         for r in ress:
             dev.free_resident(r)
         dev.dev_free(x_dev)
@@ -273,6 +370,10 @@ def main():
         log(f"c2 decode: {ms:.3f} ms/token = {1e3 / ms:.1f} tok/s, {gbps:.1f} GB/s ({100 * gbps / PEAK_GBPS:.1f}%)")
         dev.graph_destroy(graph)
         model.free()
+        if not args.no_cpu:
+            c2cpu = cpu_decode_sample(cfg, 0.25 * args.cpu_seconds)
+            extra["c2_decode_qwen3_8b_q4_0"]["cpu_baseline"] = c2cpu
+            log(f"c2 CPU: {c2cpu['tok_per_s']} tok/s (projection GEMVs) on {c2cpu['cores']} threads")
 
     line = {
         "metric": METRIC,
@@ -280,7 +381,8 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": passes_w * copies,
+        "warmup": warmup,
+        "warmup_gpu_ms": round(clock_ms, 2),
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",

@@ -1769,19 +1769,24 @@ bool ensure_attn_scratch(zlm_device* d, size_t need) {
 
 }  // namespace
 
-extern "C" bool zlm_gpu_attention_decode_enqueue(zlm_device* d, const float* qkv, const float* q_norm_w,
-                                                 const float* k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
-                                                 uint32_t head_dim, float eps, float freq_base, const int32_t* pos,
-                                                 uint16_t* k_cache, uint16_t* v_cache, uint32_t max_seq, float scale,
-                                                 float* out) {
-    if (!d || !d->avail) return false;
+namespace {
+
+bool check_attn_decode(zlm_device* d, const float* qkv, const float* q_norm_w, const float* k_norm_w,
+                       uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, const int32_t* pos,
+                       const uint16_t* k_cache, const uint16_t* v_cache, uint32_t max_seq, const float* out) {
     if (!qkv || !q_norm_w || !k_norm_w || !pos || !k_cache || !v_cache || !out) return fail(d, "null buffer");
     if (head_dim != 128) return fail(d, "attention supports head_dim 128 (got %u)", head_dim);
     if (n_kv_heads == 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 4 || max_seq == 0)
         return fail(d, "attention supports 1-4 q heads per kv head");
-    uint32_t nsplit = (max_seq + 63) / 64;
-    if (!ensure_attn_scratch(d, static_cast<size_t>(n_heads) * nsplit * 130)) return false;
-    float* part = d->attn_part;
+    return true;
+}
+
+// The fused attention launch and the merge, with the partials in `part`
+// (n_heads * nsplit * 130 floats).
+bool enqueue_attn_decode(zlm_device* d, const float* qkv, const float* q_norm_w, const float* k_norm_w,
+                         uint32_t n_heads, uint32_t n_kv_heads, float eps, float freq_base, const int32_t* pos,
+                         uint16_t* k_cache, uint16_t* v_cache, uint32_t max_seq, float scale, float* out,
+                         float* part, uint32_t nsplit) {
     {
         void* args[] = {&qkv, &q_norm_w, &k_norm_w, &n_heads, &n_kv_heads, &eps, &freq_base, &pos, &k_cache,
                         &v_cache, &max_seq, &scale, &part, &nsplit};
@@ -1792,6 +1797,23 @@ extern "C" bool zlm_gpu_attention_decode_enqueue(zlm_device* d, const float* qkv
     }
     void* args[] = {&part, &nsplit, &out};
     return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
+}
+
+}  // namespace
+
+extern "C" bool zlm_gpu_attention_decode_enqueue(zlm_device* d, const float* qkv, const float* q_norm_w,
+                                                 const float* k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                                 uint32_t head_dim, float eps, float freq_base, const int32_t* pos,
+                                                 uint16_t* k_cache, uint16_t* v_cache, uint32_t max_seq, float scale,
+                                                 float* out) {
+    if (!d || !d->avail) return false;
+    if (!check_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, head_dim, pos, k_cache, v_cache, max_seq,
+                           out))
+        return false;
+    const uint32_t nsplit = static_cast<uint32_t>((static_cast<uint64_t>(max_seq) + 63) / 64);
+    if (!ensure_attn_scratch(d, static_cast<size_t>(n_heads) * nsplit * 130)) return false;
+    return enqueue_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, eps, freq_base, pos, k_cache, v_cache,
+                               max_seq, scale, out, d->attn_part, nsplit);
 }
 
 extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const uint16_t* k_cache,
@@ -1850,24 +1872,39 @@ extern "C" zlm_graph* zlm_gpu_capture_end(zlm_device* d) {
     return g;
 }
 
+// Graph launches queued ahead of the GPU by one zlm_gpu_graph_launch call:
+// before launch i the host waits for launch i - kGraphsInFlight to finish, so
+// a long run of replays never holds more than this many graphs' dispatches
+// (a decode step is ~220 kernels) in the stream's queue at once.
+constexpr int kGraphsInFlight = 4;
+
 extern "C" bool zlm_gpu_graph_launch(zlm_device* d, zlm_graph* g, int iters, double* ms) {
     if (!d || !d->avail || !g || iters < 1) return false;
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (ms) {
-        if (!ok(d, hipEventCreate(&e0), "event") || !ok(d, hipEventCreate(&e1), "event")) return false;
-        hipEventRecord(e0, d->stream);
-    }
+    hipEvent_t done[kGraphsInFlight] = {};
     bool good = true;
-    for (int i = 0; i < iters && good; i++) good = ok(d, hipGraphLaunch(g->exec, d->stream), "graph launch");
-    if (ms) hipEventRecord(e1, d->stream);
-    good = ok(d, hipStreamSynchronize(d->stream), "sync") && good;
-    if (ms) {
-        float t = 0.0f;
-        hipEventElapsedTime(&t, e0, e1);
-        *ms = t;
-        hipEventDestroy(e0);
-        hipEventDestroy(e1);
+    for (hipEvent_t& e : done) good = good && ok(d, hipEventCreateWithFlags(&e, hipEventDisableTiming), "event");
+    if (good && ms) {
+        good = ok(d, hipEventCreate(&e0), "event") && ok(d, hipEventCreate(&e1), "event") &&
+               ok(d, hipEventRecord(e0, d->stream), "record");
     }
+    for (int i = 0; i < iters && good; i++) {
+        hipEvent_t e = done[i % kGraphsInFlight];
+        if (i >= kGraphsInFlight) good = ok(d, hipEventSynchronize(e), "graph wait");
+        good = good && ok(d, hipGraphLaunch(g->exec, d->stream), "graph launch") &&
+               ok(d, hipEventRecord(e, d->stream), "record");
+    }
+    if (good && ms) good = ok(d, hipEventRecord(e1, d->stream), "record");
+    good = ok(d, hipStreamSynchronize(d->stream), "sync") && good;
+    if (good && ms) {
+        float t = 0.0f;
+        good = ok(d, hipEventElapsedTime(&t, e0, e1), "elapsed");
+        *ms = t;
+    }
+    for (hipEvent_t e : {e0, e1})
+        if (e) hipEventDestroy(e);
+    for (hipEvent_t e : done)
+        if (e) hipEventDestroy(e);
     return good;
 }
 
