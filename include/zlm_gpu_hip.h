@@ -300,6 +300,25 @@ bool zlm_gpu_attention_decode_enqueue(zlm_device *dev, const float *qkv, const f
                                       uint16_t *k_cache, uint16_t *v_cache, uint32_t max_seq, float scale,
                                       float *out);
 
+/* zlm_gpu_attention_decode_enqueue without any allocation: no counterpart in
+ * the reference.  For callers that cannot allocate device memory at call time
+ * (code under HIP graph capture before any eager call, serving loops that
+ * forbid hipMalloc).  Same arguments, kernels and results (bit for bit) as
+ * zlm_gpu_attention_decode_enqueue; the split partials live in a fixed
+ * library array of ZLM_NOALLOC_ATTN_HEAD_SPLITS head-splits (8,519,680 bytes)
+ * that each GPU the library runs on holds until the process ends.  Limit:
+ * n_heads * ceil(max_seq / 64) <= ZLM_NOALLOC_ATTN_HEAD_SPLITS (e.g. 32 q
+ * heads up to max_seq 32768); larger shapes return false with a reason in
+ * zlm_gpu_last_error.  Every call on one GPU shares that GPU's array, which
+ * keeps the last call's contents: calls that overlap on one GPU (two devices
+ * or streams driving the same GPU concurrently) race. */
+#define ZLM_NOALLOC_ATTN_HEAD_SPLITS 16384u
+bool zlm_gpu_attention_decode_enqueue_noalloc(zlm_device *dev, const float *qkv, const float *q_norm_w,
+                                              const float *k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                              uint32_t head_dim, float eps, float freq_base, const int32_t *pos,
+                                              uint16_t *k_cache, uint16_t *v_cache, uint32_t max_seq, float scale,
+                                              float *out);
+
 /* ---- HIP graphs over the device stream ----
  * Everything enqueued between capture_begin and capture_end is recorded, not
  * run.  Ops that allocate or convert layouts on first use must have run once

@@ -19,6 +19,8 @@
 //     first submit (reference pipeline.zig:264-276 only documents it).
 #include "zlm_gpu_hip.h"
 
+#include "zlm_static_scratch.h"
+
 #include <dlfcn.h>
 #include <hip/hip_runtime_api.h>
 #include <time.h>
@@ -182,6 +184,10 @@ struct zlm_device {
     float* attn_part = nullptr;
     size_t attn_part_cap = 0;
     bool capturing = false;
+    // this device's address of the fixed static scratch (the no-alloc entry
+    // point's partials); null if the lookup at init failed
+    float* static_scratch = nullptr;
+    std::string static_scratch_err;
 
     // prefill scratch: quantized activations (qx, dx, sums) and staged x/out
     uint8_t* q_scratch = nullptr;
@@ -629,6 +635,7 @@ struct GemvMultiArgsHost {
 };
 static_assert(sizeof(GemvMultiArgsHost) == 248, "GemvMultiArgs layout");
 static_assert(kMultiMax == kRing, "a batch holds at most RingSize ops");
+static_assert(ZLM_NOALLOC_ATTN_HEAD_SPLITS == ZLM_STATIC_SCRATCH_HEAD_SPLITS, "no-alloc scratch size");
 
 // Enqueue up to kMultiMax GEMVs that share quant `qi`, k and x_dev as one
 // launch of the batch kernel, op i's rows into ys[i].  The residents are
@@ -980,6 +987,13 @@ extern "C" zlm_device* zlm_gpu_init(void) {
         snprintf(d->name, sizeof d->name, "off");
         d->err = why;
         return d;
+    }
+    // The fixed scratch of the no-alloc entry point: this device's address of
+    // the array, looked up once with the device current.
+    const hipError_t se = zlm_static_scratch_address(&d->static_scratch);
+    if (se != hipSuccess) {
+        d->static_scratch = nullptr;
+        d->static_scratch_err = hipGetErrorString(se);
     }
     d->avail = true;
     d->err.clear();
@@ -1814,6 +1828,26 @@ extern "C" bool zlm_gpu_attention_decode_enqueue(zlm_device* d, const float* qkv
     if (!ensure_attn_scratch(d, static_cast<size_t>(n_heads) * nsplit * 130)) return false;
     return enqueue_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, eps, freq_base, pos, k_cache, v_cache,
                                max_seq, scale, out, d->attn_part, nsplit);
+}
+
+extern "C" bool zlm_gpu_attention_decode_enqueue_noalloc(zlm_device* d, const float* qkv, const float* q_norm_w,
+                                                         const float* k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                                         uint32_t head_dim, float eps, float freq_base,
+                                                         const int32_t* pos, uint16_t* k_cache, uint16_t* v_cache,
+                                                         uint32_t max_seq, float scale, float* out) {
+    if (!d || !d->avail) return false;
+    if (!d->static_scratch)
+        return fail(d, "static scratch unavailable (lookup at init failed: %s)", d->static_scratch_err.c_str());
+    if (!check_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, head_dim, pos, k_cache, v_cache, max_seq,
+                           out))
+        return false;
+    const uint32_t nsplit = static_cast<uint32_t>((static_cast<uint64_t>(max_seq) + 63) / 64);
+    const uint64_t head_splits = static_cast<uint64_t>(n_heads) * nsplit;
+    if (head_splits > ZLM_STATIC_SCRATCH_HEAD_SPLITS)
+        return fail(d, "no-alloc attention holds at most %u head-splits (n_heads * ceil(max_seq / 64)); got %u * %u",
+                    ZLM_STATIC_SCRATCH_HEAD_SPLITS, n_heads, nsplit);
+    return enqueue_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, eps, freq_base, pos, k_cache, v_cache,
+                               max_seq, scale, out, d->static_scratch, nsplit);
 }
 
 extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const uint16_t* k_cache,

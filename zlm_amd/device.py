@@ -172,6 +172,8 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_attention_enqueue": (B, [P, P, P, P, U, U, U, P, U, ctypes.c_float, P]),
         "zlm_gpu_attention_decode_enqueue": (B, [P, P, P, P, U, U, U, ctypes.c_float, ctypes.c_float, P, P, P, U,
                                                  ctypes.c_float, P]),
+        "zlm_gpu_attention_decode_enqueue_noalloc": (B, [P, P, P, P, U, U, U, ctypes.c_float, ctypes.c_float, P, P,
+                                                         P, U, ctypes.c_float, P]),
         "zlm_gpu_capture_begin": (B, [P]),
         "zlm_gpu_capture_end": (P, [P]),
         "zlm_gpu_graph_launch": (B, [P, P, ctypes.c_int, P]),
@@ -484,6 +486,15 @@ class Device:
         return bool(self._L.zlm_gpu_attention_decode_enqueue(self._h, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads,
                                                              head_dim, eps, freq_base, pos, k_cache, v_cache,
                                                              max_seq, scale, out))
+
+    def attention_decode_enqueue_noalloc(self, qkv: int, q_norm_w: int, k_norm_w: int, n_heads: int,
+                                         n_kv_heads: int, head_dim: int, eps: float, freq_base: float, pos: int,
+                                         k_cache: int, v_cache: int, max_seq: int, scale: float, out: int) -> bool:
+        """attention_decode_enqueue with its partials in the library's fixed
+        static scratch: allocates nothing (see the C header for the limit)."""
+        return bool(self._L.zlm_gpu_attention_decode_enqueue_noalloc(self._h, qkv, q_norm_w, k_norm_w, n_heads,
+                                                                     n_kv_heads, head_dim, eps, freq_base, pos,
+                                                                     k_cache, v_cache, max_seq, scale, out))
 
     def capture_begin(self) -> bool:
         return bool(self._L.zlm_gpu_capture_begin(self._h))
