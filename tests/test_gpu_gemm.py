@@ -1,11 +1,14 @@
-"""GPU parity of the prefill GEMM (q8 activations, int8 MFMA) through the C ABI.
+"""GPU parity of the matrix products (matMulBatch / matMulResident) through the C ABI.
 
-The oracle is zlm's int path (reference matvec/kernels/quantized.zig:49-55 for
-Q4_0, :79-87 for Q4_1, :111-123 for Q4_K, :149-156 for Q8_0, over the
-activation quantizer of matvec/layout.zig:458-476) applied per token:
-relative L2 <= 1e-3 (the block dots are exact integers; only fp32 scaling and
-summation order differ).  Against the fp32 GEMM the reference's own int-vs-fp
-bound applies, |int - fp| <= 0.02 * sum|w*x| (kernels/quantized_test.zig:61).
+From 3 tokens on the device runs zlm's int path (q8 activations, int8 MFMA);
+its oracle is the int path of the reference (matvec/kernels/quantized.zig:49-55
+for Q4_0, :79-87 for Q4_1, :111-123 for Q4_K, :149-156 for Q8_0, over the
+activation quantizer of matvec/layout.zig:458-476) applied per token: relative
+L2 <= 1e-3 (the block dots are exact integers; only fp32 scaling and summation
+order differ).  Against the fp32 GEMM the reference's own int-vs-fp bound
+applies, |int - fp| <= 0.02 * sum|w*x| (kernels/quantized_test.zig:61).  One
+or two tokens run one fp GEMV per token, checked against the oracle's fp
+matMulRows (form/single.zig:213-292), relative L2 <= 1e-3.
 """
 import sys
 
@@ -30,13 +33,24 @@ SHAPES = [(64, 256, 4), (100, 512, 37), (64, 1024, 64), (130, 4096, 70), (48, 16
 GEMM_QUANTS = [(synth.Q4_0, zd.Q4_0), (synth.Q8_0, zd.Q8_0), (synth.Q4_1, zd.Q4_1), (synth.Q4_K, zd.Q4_K)]
 
 
+# Token counts up to this run one fp GEMV per token (the host's kGemmGemvM).
+GEMV_M = 2
+
+
+def _oracle(qt, w, k, rows, m, x):
+    """The arithmetic the device runs for m tokens: fp GEMVs or the int path."""
+    if m <= GEMV_M:
+        return oracle.matmul_rows(qt, w, k, rows, m, x)
+    return oracle.matmul_int(qt, w, k, rows, m, x)
+
+
 @pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0", "q4_1", "q4_k"])
 @pytest.mark.parametrize("rows,k,m", SHAPES)
 def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     _say(f"gemm type={qt} rows={rows} k={k} m={m}")
     w = synth.weights(qt, rows, k, seed=rows + k + m)
     x = synth.activation(m + 5, m * k)
-    want = oracle.matmul_int(qt, w, k, rows, m, x)
+    want = _oracle(qt, w, k, rows, m, x)
     out = np.full(m * rows, np.nan, np.float32)
     assert dev.mat_mul_batch(zd.quant(zq), w, rows, k, m, x, out), dev.last_error()
     got = out.reshape(m, rows)
@@ -50,6 +64,34 @@ def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     dq = np.abs(oracle.dequant(qt, w, rows * k).reshape(rows, k).astype(np.float64))
     mag = np.abs(x.reshape(m, k).astype(np.float64)) @ dq.T
     assert np.all(np.abs(got - fp) <= 0.02 * mag + 1e-6)
+    dev.free_resident(res)
+
+
+# The small-M path (m <= 32: one 32-token tile, the workgroup's 8 waves split
+# the row's blocks in pairs): odd block counts (a pair's second block past the
+# end), block counts not a multiple of the 16 blocks a split step covers,
+# ragged row tiles, one token, a full tile, and the first m past it (the
+# tiled kernel).
+SMALL_M = [(33, 4096, 2), (64, 4096, 9), (96, 3840, 32), (40, 12288, 31), (37, 288, 5), (64, 256, 33),
+           (32, 512, 1), (4096 + 17, 4096, 8), (50, 4096, 3)]
+
+
+@pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0", "q4_1", "q4_k"])
+@pytest.mark.parametrize("rows,k,m", SMALL_M)
+def test_small_m_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
+    if k % synth.BLOCK_ELEMS[qt]:
+        pytest.skip("k not a multiple of the block")
+    _say(f"small-m gemm type={qt} rows={rows} k={k} m={m}")
+    w = synth.weights(qt, rows, k, seed=rows * 3 + k + m)
+    x = synth.activation(m + 11, m * k)
+    want = _oracle(qt, w, k, rows, m, x)
+    res = dev.upload_resident(w)
+    out = np.full(m * rows, np.nan, np.float32)
+    assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, out), dev.last_error()
+    assert rel_l2(out.reshape(m, rows), want) <= 1e-3
+    again = np.full(m * rows, np.nan, np.float32)
+    assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, again), dev.last_error()
+    np.testing.assert_array_equal(again.view(np.uint32), out.view(np.uint32))  # fixed summation order
     dev.free_resident(res)
 
 

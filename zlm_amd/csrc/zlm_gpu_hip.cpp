@@ -172,6 +172,10 @@ struct zlm_device {
     hipFunction_t gemm_q4_k = nullptr;
     hipFunction_t copy16 = nullptr;
     hipFunction_t gemm_q4_0 = nullptr;
+    hipFunction_t gemm_small_q4_0 = nullptr;  // m <= kGemmSmallM: split-K, one 32-token tile
+    hipFunction_t gemm_small_q8_0 = nullptr;
+    hipFunction_t gemm_small_q4_1 = nullptr;
+    hipFunction_t gemm_small_q4_k = nullptr;
     hipFunction_t gemm_q8_0 = nullptr;
     hipFunction_t qk_norm_rope_kv = nullptr;
     hipFunction_t attn_partial = nullptr;
@@ -295,7 +299,11 @@ bool load_kernels(zlm_device* d) {
     const struct {
         hipFunction_t* f;
         const char* name;
-    } more[] = {{&d->qk_norm_rope_kv, "zlm_qk_norm_rope_kv"},
+    } more[] = {{&d->gemm_small_q4_0, "zlm_gemm_small_q4_0_q8"},
+                {&d->gemm_small_q8_0, "zlm_gemm_small_q8_0_q8"},
+                {&d->gemm_small_q4_1, "zlm_gemm_small_q4_1_q8"},
+                {&d->gemm_small_q4_k, "zlm_gemm_small_q4_k_q8"},
+                {&d->qk_norm_rope_kv, "zlm_qk_norm_rope_kv"},
                 {&d->attn_partial, "zlm_attn_partial"},
                 {&d->attn_combine, "zlm_attn_combine"},
                 {&d->attn_decode, "zlm_attn_decode"},
@@ -842,6 +850,15 @@ double now_ns() {
 }
 
 // The quants with a prefill GEMM and whether their tiles carry a min term.
+// Matrix products by token count m: up to kGemmGemvM tokens one fp GEMV per
+// token (the production GEMV's arithmetic, as zlm's CPU runs small batches
+// through its fp batched GEMV, reference form/single.zig:258-292; m GEMVs cost
+// less than the int path's quantizer + GEMM there); up to one 32-token tile
+// the split-K small-M int GEMM (zlm_gemm_small_*: 16 waves per workgroup for
+// q4_0 / q8_0, 8 for q4_1 / q4_k); beyond it the 128 x 64 tiled int GEMM.
+constexpr size_t kGemmGemvM = 2;
+constexpr size_t kGemmSmallM = 32;
+
 bool gemm_supported(uint32_t type) {
     return type == ZLM_GGML_Q4_0 || type == ZLM_GGML_Q8_0 || type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K;
 }
@@ -915,6 +932,11 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     if (r->bytes < rows * wblocks * qi->block_bytes) return fail(d, "resident too short");
     if (!ensure_layout(d, r, qi)) return false;
     if (r->blocks < rows * wblocks) return fail(d, "resident layout too short");
+    if (m <= kGemmGemvM) {  // one fp GEMV per token (no activation quantizer, no tiled weight copy)
+        for (size_t t = 0; t < m; t++)
+            if (!enqueue_gemv(d, r, quant, rows, k, x_dev + t * k, out_dev + t * rows)) return false;
+        return true;
+    }
     if (!ensure_gemm_tiles(d, r, qi, nb)) return false;
     if (r->gemm_rt * 32 < rows) return fail(d, "GEMM tiles too short");
     const bool with_min = gemm_has_min(qi->type);
@@ -936,6 +958,18 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     }
     const uint8_t* wq = r->gemm_payload;
     const void* ws = r->gemm_scales;
+    if (m <= kGemmSmallM) {  // one token tile: the split-K kernel, a workgroup per 32-row tile
+        const float* dsa = ds ? ds : dx;
+        void* args[] = {&wq, &ws, &qx, &dx, &dsa, &out_dev, &rows32, &m32, &nb32};
+        hipFunction_t f = qi->type == ZLM_GGML_Q4_0   ? d->gemm_small_q4_0
+                          : qi->type == ZLM_GGML_Q8_0 ? d->gemm_small_q8_0
+                          : qi->type == ZLM_GGML_Q4_1 ? d->gemm_small_q4_1
+                                                      : d->gemm_small_q4_k;
+        const unsigned threads = with_min ? 8 * 64 : 16 * 64;
+        return ok(d, hipModuleLaunchKernel(f, static_cast<unsigned>((rows + 31) / 32), 1, 1, threads, 1, 1, 0,
+                                           d->stream, args, nullptr),
+                  "gemm small");
+    }
     const unsigned gx = static_cast<unsigned>((rows + 63) / 64), gy = static_cast<unsigned>((m + 127) / 128);
     if (with_min) {
         void* args[] = {&wq, &ws, &qx, &dx, &ds, &out_dev, &rows32, &m32, &nb32, &mt32};

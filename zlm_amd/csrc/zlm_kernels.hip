@@ -406,111 +406,145 @@ extern "C" __global__ void __launch_bounds__(256)
 // low nibbles of the row's 16 block bytes for lanes 0-31, the high nibbles for
 // 32-63), D[t = 8*(i/4) + 4*(l/32) + i%4][r = l%32].  A nibble n enters as the
 // int8 16*(n-8) (n^8 in the high nibble), so each block dot is exact in int32.
-// The block's scale matrix dx[t]*dw[r]/16 is the outer product of two vectors;
-// v_mfma_f32_32x32x2f32 with the vectors in k = 0 and zeros in k = 1 produces
-// it in the same D layout on the matrix pipe, leaving one convert and one fma
-// per output on the VALU.  A wave owns 64 tokens x 32 rows (two MFMA tiles
-// share the unpacked weights) and keeps the next four blocks' loads in flight
-// while it computes the current four.  A workgroup of 4 waves owns 128 tokens
-// x 64 rows; padding tokens and rows of the tiled layouts are zeros and their
-// outputs are not stored, blocks past the end get a zero scale.
+// A wave owns 64 tokens (two 32-token tiles) x 32 rows.  The block's two scale
+// matrices dx[t]*dw[r] (one per token tile) are outer products of vectors:
+// one v_mfma_f32_32x32x1_2b_f32 (block 0 from lanes 0-31: token tile 0's dx
+// by dw, block 1 from lanes 32-63: token tile 1's dx by dw) yields both, in
+// the D layout of the int8 results (block 0 in result registers 0-15, block 1
+// in 16-31), on the matrix pipe; the VALU does one convert and one fma per
+// output.  Operand addresses are a wave-uniform base (per block, in SGPRs)
+// plus a per-lane offset fixed for the whole loop, so the loads need no
+// per-block address arithmetic on the VALU.  A workgroup of 4 waves owns 128
+// tokens x 64 rows; padding tokens and rows of the tiled layouts are zeros and
+// their outputs are not stored, blocks past the end get a zero scale.
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 struct GemmBlk {
     uint4 a0, a1, w;
     uint32_t d;      // q4_0 / q8_0: the f16 weight scale
-    float x0, x1;    // dx of the two token tiles
+    float x;         // dx of this lane's token tile (lanes 0-31: tile 0, 32-63: tile 1)
     float2 sm;       // q4_1 / q4_k: (scale, min)
-    float s0, s1;    // q4_1 / q4_k: dx * sum(q) of the two token tiles
+    float s;         // q4_1 / q4_k: dx * sum(q) of this lane's token tile
 };
 
 constexpr bool gemm_has_min(int qt) { return qt == Q4_1 || qt == Q4_K; }
 
-// Per-wave operand pointers of the GEMM (lane offsets applied).
+// Per-wave operand buffers (raw buffer resources at the wave's tile bases,
+// wave-uniform) with per-lane byte offsets fixed for the whole loop; a block's
+// loads add its wave-uniform byte offset in an SGPR.
 struct GemmPtrs {
-    const int8_t *a0, *a1;
-    const uint8_t* wr;
-    const uint16_t* dr;  // q4_0 / q8_0 scales
-    const float2* smr;   // q4_1 / q4_k (scale, min)
-    const float *x0, *x1, *s0, *s1;
+    __amdgpu_buffer_rsrc_t a, w, sc, x, s;  // qx, weights, scales, dx, dx*sum(q)
+    uint32_t a1;                            // token tile 1's byte offset in `a`
+    uint32_t oa, ow, osc, ox;               // lane byte offsets
 };
 
-// Depth 1 keeps the kernel at 129 VGPRs, so the 3 waves per SIMD that the
-// 12288 x 512 launch places are all resident at once (depths 2-4 measured no
-// faster and need 193-250 VGPRs).
-#ifndef ZLM_GEMM_DEPTH
-#define ZLM_GEMM_DEPTH 1
-#endif
+// 119 VGPRs (q4_0), so the 3 waves per SIMD that the 12288 x 512 launch
+// places are all resident at once.
 #ifndef ZLM_GEMM_WAVES_PER_EU
 #define ZLM_GEMM_WAVES_PER_EU 3
 #endif
-constexpr int kGemmDepth = ZLM_GEMM_DEPTH;  // blocks per register set
 
-template <int QT>
-__device__ __forceinline__ void gemm_load(GemmBlk& g, const GemmPtrs& p, uint32_t b) {
-    constexpr size_t kWStride = QT == Q8_0 ? 1024 : 512;  // tiled weight bytes per block
-    g.a0 = *reinterpret_cast<const uint4*>(p.a0 + static_cast<size_t>(b) * 1024);
-    g.a1 = *reinterpret_cast<const uint4*>(p.a1 + static_cast<size_t>(b) * 1024);
-    g.w = *reinterpret_cast<const uint4*>(p.wr + static_cast<size_t>(b) * kWStride);
-    if constexpr (gemm_has_min(QT)) {
-        g.sm = p.smr[static_cast<size_t>(b) * 32];
-        g.s0 = p.s0[static_cast<size_t>(b) * 32];
-        g.s1 = p.s1[static_cast<size_t>(b) * 32];
-    } else {
-        g.d = p.dr[static_cast<size_t>(b) * 32];
-    }
-    g.x0 = p.x0[static_cast<size_t>(b) * 32];
-    g.x1 = p.x1[static_cast<size_t>(b) * 32];
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ uint4 gemm_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 template <int QT>
-__device__ __forceinline__ void gemm_block(const GemmBlk& g, bool valid, bool lo_half, int sh, v16f& acc0,
-                                           v16f& acc1, v16f& accm0, v16f& accm1) {
+__device__ __forceinline__ void gemm_load(GemmBlk& g, const GemmPtrs& p, uint32_t b) {
+    constexpr uint32_t kWStride = QT == Q8_0 ? 1024 : 512;  // tiled weight bytes per block
+    g.a0 = gemm_ld16(p.a, p.oa, b * 1024);
+    g.a1 = gemm_ld16(p.a, p.oa, p.a1 + b * 1024);
+    g.w = gemm_ld16(p.w, p.ow, b * kWStride);
+    if constexpr (gemm_has_min(QT)) {
+        // two dword loads (the compiler merges them into one dwordx2; the
+        // 64-bit buffer-load builtin compiled to a single dword load here)
+        const uint32_t sx = __builtin_amdgcn_raw_buffer_load_b32(p.sc, static_cast<int>(p.osc), static_cast<int>(b * 256), 0);
+        const uint32_t sy =
+            __builtin_amdgcn_raw_buffer_load_b32(p.sc, static_cast<int>(p.osc + 4), static_cast<int>(b * 256), 0);
+        g.sm = make_float2(__builtin_bit_cast(float, sx), __builtin_bit_cast(float, sy));
+        g.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(p.s, static_cast<int>(p.ox),
+                                                                             static_cast<int>(b * 128), 0));
+    } else {
+        g.d = __builtin_amdgcn_raw_buffer_load_b16(p.sc, static_cast<int>(p.osc), static_cast<int>(b * 64), 0);
+    }
+    g.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(p.x, static_cast<int>(p.ox),
+                                                                         static_cast<int>(b * 128), 0));
+}
+
+struct GemmI {
+    v16i i0, i1;  // the block's exact int32 dots, token tiles 0 and 1
+};
+
+// A block's two int8 MFMAs (both token tiles share the unpacked weights).
+// The B operand of a block's int8 MFMA from this lane's 16 weight bytes: q8_0
+// as they are; q4_0 nibbles as the int8 16*(n-8) (lanes 0-31 the low
+// nibbles, 32-63 the high); q4_1 / q4_k nibbles unsigned.
+template <int QT>
+__device__ __forceinline__ v4i gemm_unpack(const uint4 w, bool lo_half, int sh) {
     v4i bv;
     if constexpr (QT == Q8_0) {
-        bv = v4i{static_cast<int>(g.w.x), static_cast<int>(g.w.y), static_cast<int>(g.w.z), static_cast<int>(g.w.w)};
-    } else if constexpr (gemm_has_min(QT)) {  // unsigned nibbles 0..15 as int8: lanes 0-31 low, 32-63 high
+        bv = v4i{static_cast<int>(w.x), static_cast<int>(w.y), static_cast<int>(w.z), static_cast<int>(w.w)};
+    } else if constexpr (gemm_has_min(QT)) {
         const int rs = lo_half ? 0 : 4;
-        bv.x = static_cast<int>((g.w.x >> rs) & 0x0F0F0F0Fu);
-        bv.y = static_cast<int>((g.w.y >> rs) & 0x0F0F0F0Fu);
-        bv.z = static_cast<int>((g.w.z >> rs) & 0x0F0F0F0Fu);
-        bv.w = static_cast<int>((g.w.w >> rs) & 0x0F0F0F0Fu);
+        bv.x = static_cast<int>((w.x >> rs) & 0x0F0F0F0Fu);
+        bv.y = static_cast<int>((w.y >> rs) & 0x0F0F0F0Fu);
+        bv.z = static_cast<int>((w.z >> rs) & 0x0F0F0F0Fu);
+        bv.w = static_cast<int>((w.w >> rs) & 0x0F0F0F0Fu);
     } else {
-        bv.x = static_cast<int>(((g.w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
-        bv.y = static_cast<int>(((g.w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
-        bv.z = static_cast<int>(((g.w.z << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
-        bv.w = static_cast<int>(((g.w.w << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+        bv.x = static_cast<int>(((w.x << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+        bv.y = static_cast<int>(((w.y << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+        bv.z = static_cast<int>(((w.z << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
+        bv.w = static_cast<int>(((w.w << sh) & 0xF0F0F0F0u) ^ 0x80808080u);
     }
+    return bv;
+}
+
+// A block's two int8 MFMAs (both token tiles share the unpacked weights).
+template <int QT>
+__device__ __forceinline__ GemmI gemm_int(const GemmBlk& g, bool lo_half, int sh) {
+    const v4i bv = gemm_unpack<QT>(g.w, lo_half, sh);
     const v4i a0 = {static_cast<int>(g.a0.x), static_cast<int>(g.a0.y), static_cast<int>(g.a0.z),
                     static_cast<int>(g.a0.w)};
     const v4i a1 = {static_cast<int>(g.a1.x), static_cast<int>(g.a1.y), static_cast<int>(g.a1.z),
                     static_cast<int>(g.a1.w)};
     const v16i zi = {};
-    const v16i i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bv, zi, 0, 0, 0);
-    const v16i i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv, zi, 0, 0, 0);
-    const bool use = valid && lo_half;
+    GemmI r;
+    r.i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bv, zi, 0, 0, 0);
+    r.i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv, zi, 0, 0, 0);
+    return r;
+}
+
+// A block's scale matrices (and, with a min term, its accumulated min
+// outer products); a block past the end gets zero scales.
+template <int QT>
+__device__ __forceinline__ v32f gemm_scale(const GemmBlk& g, bool valid, v32f& accm) {
     float bw;
     if constexpr (gemm_has_min(QT)) {
-        bw = use ? g.sm.x : 0.0f;
-        // the min term sum_t' (dx*sum q)[t] * min[r]: an outer product the matrix
-        // pipe accumulates by itself
-        const float bm = use ? g.sm.y : 0.0f;
-        accm0 = __builtin_amdgcn_mfma_f32_32x32x2f32(use ? g.s0 : 0.0f, bm, accm0, 0, 0, 0);
-        accm1 = __builtin_amdgcn_mfma_f32_32x32x2f32(use ? g.s1 : 0.0f, bm, accm1, 0, 0, 0);
+        bw = g.sm.x;
+        // the min term sum_b (dx*sum q)[t] * min[r]: outer products the matrix
+        // pipe accumulates by itself (both token tiles in one instruction)
+        accm = __builtin_amdgcn_mfma_f32_32x32x1f32(valid ? g.s : 0.0f, g.sm.y, accm, 0, 0, 0);
     } else {
-        bw = use ? h2f(g.d) : 0.0f;
+        bw = h2f(g.d);
     }
-    const float s0 = use ? g.x0 : 0.0f;  // q4_0: the 16 of the nibble encoding is divided out at the store
-    const float s1 = use ? g.x1 : 0.0f;
-    const v16f zf = {};
-    const v16f c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(s0, bw, zf, 0, 0, 0);
-    const v16f c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(s1, bw, zf, 0, 0, 0);
+    // q4_0: the 16 of the nibble encoding is divided out at the store
+    const v32f zf = {};
+    return __builtin_amdgcn_mfma_f32_32x32x1f32(valid ? g.x : 0.0f, bw, zf, 0, 0, 0);
+}
+
+// The VALU epilogue of a block: one convert and one fma per output.
+__device__ __forceinline__ void gemm_acc(const v32f& c, const GemmI& I, v16f& acc0, v16f& acc1) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        acc0[i] = fmaf(c0[i], static_cast<float>(i0[i]), acc0[i]);
-        acc1[i] = fmaf(c1[i], static_cast<float>(i1[i]), acc1[i]);
+        acc0[i] = fmaf(c[i], static_cast<float>(I.i0[i]), acc0[i]);
+        acc1[i] = fmaf(c[16 + i], static_cast<float>(I.i1[i]), acc1[i]);
     }
 }
 
@@ -526,52 +560,58 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
                                            const float* __restrict__ ds, float* __restrict__ out, uint32_t rows,
                                            uint32_t m, uint32_t nb, uint32_t mt) {
     const int lane = threadIdx.x & 63;
-    const int wid = threadIdx.x >> 6;
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const uint32_t tok0 = blockIdx.y * 128 + 64 * (wid & 1);  // multiple of 32
     const uint32_t row0 = blockIdx.x * 64 + 32 * (wid >> 1);  // multiple of 32
     const int half = lane >> 5;
     const int l32 = lane & 31;
     const uint32_t tt0 = min(tok0 / 32, mt - 1), tt1 = min(tok0 / 32 + 1, mt - 1);
     const uint32_t rt = min(row0 / 32, (rows + 31) / 32 - 1);  // a wave past the last tile re-reads it, stores nothing
+    // the wave's buffers start at its first token tile / its row tile
+    constexpr uint32_t kWStride = QT == Q8_0 ? 1024 : 512;
+    constexpr uint32_t kScBytes = gemm_has_min(QT) ? 8 : 2;
     GemmPtrs ptr;
-    ptr.a0 = qx + static_cast<size_t>(tt0) * nb * 1024 + l32 * 32 + 16 * half;
-    ptr.a1 = qx + static_cast<size_t>(tt1) * nb * 1024 + l32 * 32 + 16 * half;
-    ptr.wr = QT == Q8_0 ? wq + static_cast<size_t>(rt) * nb * 1024 + l32 * 32 + 16 * half
-                      : wq + static_cast<size_t>(rt) * nb * 512 + l32 * 16;
-    ptr.dr = static_cast<const uint16_t*>(wsc) + static_cast<size_t>(rt) * nb * 32 + l32;
-    ptr.smr = static_cast<const float2*>(wsc) + static_cast<size_t>(rt) * nb * 32 + l32;
-    ptr.x0 = dx + static_cast<size_t>(tt0) * nb * 32 + l32;
-    ptr.x1 = dx + static_cast<size_t>(tt1) * nb * 32 + l32;
-    ptr.s0 = gemm_has_min(QT) ? ds + static_cast<size_t>(tt0) * nb * 32 + l32 : nullptr;
-    ptr.s1 = gemm_has_min(QT) ? ds + static_cast<size_t>(tt1) * nb * 32 + l32 : nullptr;
+    ptr.a = gemm_rsrc(qx + static_cast<size_t>(tt0) * nb * 1024, (mt - tt0) * nb * 1024);
+    ptr.a1 = (tt1 - tt0) * nb * 1024;
+    ptr.oa = l32 * 32 + 16 * half;
+    ptr.w = gemm_rsrc(wq + static_cast<size_t>(rt) * nb * kWStride, nb * kWStride);
+    ptr.ow = QT == Q8_0 ? l32 * 32 + 16 * half : l32 * 16;
+    ptr.sc = gemm_rsrc(static_cast<const uint8_t*>(wsc) + static_cast<size_t>(rt) * nb * 32 * kScBytes,
+                       nb * 32 * kScBytes);
+    ptr.osc = l32 * kScBytes;
+    // lanes 0-31 read token tile 0's dx, lanes 32-63 tile 1's (the A operand
+    // of the two-block outer product)
+    ptr.x = gemm_rsrc(dx + static_cast<size_t>(tt0) * nb * 32, (mt - tt0) * nb * 128);
+    ptr.s = gemm_rsrc(gemm_has_min(QT) ? ds + static_cast<size_t>(tt0) * nb * 32 : dx, (mt - tt0) * nb * 128);
+    ptr.ox = ((half ? (tt1 - tt0) * nb * 32 : 0u) + l32) * 4;
     const int sh = half ? 0 : 4;  // q4_0: lanes 0-31 take the low nibbles, 32-63 the high
     const bool lo_half = half == 0;
 
-    v16f acc0 = {}, acc1 = {}, accm0 = {}, accm1 = {};
-    // Two register sets, A and B, alternate: one set's loads are in flight
-    // while the other's blocks are computed.  The scheduling barriers keep each
+    v16f acc0 = {}, acc1 = {};
+    v32f accm = {};
+    // Two operand sets, A and B, alternate: one set's loads are in flight
+    // while the other's block is computed.  The scheduling barriers keep each
     // set's loads ahead of the compute (the scheduler would otherwise sink them
     // next to their uses), and the ping-pong needs no register copies.
-    GemmBlk A[kGemmDepth], B[kGemmDepth];
-#pragma unroll
-    for (int p = 0; p < kGemmDepth; p++)
-        gemm_load<QT>(A[p], ptr, min(static_cast<uint32_t>(p), nb - 1));
-    for (uint32_t b = 0; b < nb; b += 2 * kGemmDepth) {
-#pragma unroll
-        for (int p = 0; p < kGemmDepth; p++)
-            gemm_load<QT>(B[p], ptr, min(b + kGemmDepth + p, nb - 1));
+    // (Issuing block b+1's MFMAs ahead of block b's epilogue -- a software
+    // pipeline at 164 VGPRs -- measured the same; VALU and MFMA of different
+    // waves co-issue only in part on gfx950, so the kernel stays VALU-bound.)
+    GemmBlk A, B;
+    gemm_load<QT>(A, ptr, 0);
+    for (uint32_t b = 0; b < nb; b += 2) {
+        gemm_load<QT>(B, ptr, min(b + 1, nb - 1));
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int p = 0; p < kGemmDepth; p++)
-            gemm_block<QT>(A[p], b + p < nb, lo_half, sh, acc0, acc1, accm0, accm1);
+        {
+            const GemmI I = gemm_int<QT>(A, lo_half, sh);
+            gemm_acc(gemm_scale<QT>(A, b < nb, accm), I, acc0, acc1);
+        }
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int p = 0; p < kGemmDepth; p++)
-            gemm_load<QT>(A[p], ptr, min(b + 2 * kGemmDepth + p, nb - 1));
+        gemm_load<QT>(A, ptr, min(b + 2, nb - 1));
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int p = 0; p < kGemmDepth; p++)
-            gemm_block<QT>(B[p], b + kGemmDepth + p < nb, lo_half, sh, acc0, acc1, accm0, accm1);
+        {
+            const GemmI I = gemm_int<QT>(B, lo_half, sh);
+            gemm_acc(gemm_scale<QT>(B, b + 1 < nb, accm), I, acc0, acc1);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
     constexpr float kOut = QT == Q4_0 ? 0.0625f : 1.0f;
@@ -582,8 +622,8 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
             const uint32_t t = tok0 + 8 * (i / 4) + 4 * half + (i % 4);
             float v0 = acc0[i] * kOut, v1 = acc1[i] * kOut;
             if constexpr (gemm_has_min(QT)) {
-                v0 += accm0[i];
-                v1 += accm1[i];
+                v0 += accm[i];
+                v1 += accm[16 + i];
             }
             if (t < m) out[static_cast<size_t>(t) * rows + r] = v0;
             if (t + 32 < m) out[static_cast<size_t>(t + 32) * rows + r] = v1;
@@ -620,6 +660,162 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
     gemm_tiles<Q4_K>(wq, wsm, qx, dx, ds, out, rows, m, nb, mt);
 }
 
+
+// ---- small-M prefill GEMM (m <= 32: verify and microbatch batches) ----------
+// The same int path and tiled operands as gemm_tiles, for one 32-token tile.
+// A 32-row tile is too little work for one wave over the whole row (the
+// 128-token GEMM would leave most CUs idle and run a 4096-long K loop per
+// wave), so the kGemmSmallWaves waves of a workgroup split the row's blocks:
+// wave w takes block pairs (2w + 2*W*j, +1), the next pair's loads in flight
+// while a pair computes (at these sizes the loop is bound by memory latency,
+// so more waves -- shorter chains per wave -- pay).  Per pair: two int8 MFMAs (one per
+// block) and one v_mfma_f32_32x32x1_2b_f32 for both blocks' scale matrices
+// (lanes 0-31: the first block's dx by dw, lanes 32-63 the second's; each
+// lane loads its own half's block scales).  The waves' partial sums meet in
+// LDS and are added in wave order (deterministic), two output registers per
+// wave.
+// Waves per workgroup: 16 (128 VGPRs each at most) for q4_0 / q8_0, 8 for
+// the min-carrying types (their min term holds 32 more accumulators).
+template <int QT>
+constexpr int gemm_small_waves() {
+    return gemm_has_min(QT) ? 8 : 16;
+}
+
+template <int QT>
+__device__ __forceinline__ void gemm_small(const uint8_t* __restrict__ wq, const void* __restrict__ wsc,
+                                           const int8_t* __restrict__ qx, const float* __restrict__ dx,
+                                           const float* __restrict__ ds, float* __restrict__ out, uint32_t rows,
+                                           uint32_t m, uint32_t nb) {
+    constexpr int W = gemm_small_waves<QT>();
+    constexpr bool MIN = gemm_has_min(QT);
+    __shared__ float red[W][MIN ? 32 : 16][kWave];
+    const int lane = threadIdx.x & 63;
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+    const uint32_t rt = blockIdx.x;  // the grid is exactly the row tiles
+    constexpr uint32_t kWStride = QT == Q8_0 ? 1024 : 512;
+    constexpr uint32_t kScBytes = MIN ? 8 : 2;
+    GemmPtrs ptr;
+    ptr.a = gemm_rsrc(qx, nb * 1024);
+    ptr.a1 = 0;
+    ptr.oa = l32 * 32 + 16 * half;
+    ptr.w = gemm_rsrc(wq + static_cast<size_t>(rt) * nb * kWStride, nb * kWStride);
+    ptr.ow = QT == Q8_0 ? l32 * 32 + 16 * half : l32 * 16;
+    ptr.sc = gemm_rsrc(static_cast<const uint8_t*>(wsc) + static_cast<size_t>(rt) * nb * 32 * kScBytes,
+                       nb * 32 * kScBytes);
+    ptr.osc = l32 * kScBytes;
+    ptr.x = gemm_rsrc(dx, nb * 128);
+    ptr.s = gemm_rsrc(MIN ? ds : dx, nb * 128);
+    ptr.ox = l32 * 4;
+    const int sh = half ? 0 : 4;
+    const bool lo_half = half == 0;
+
+    // a block pair's operands: both blocks' qx and weights, this lane's half's scales
+    struct Pair {
+        uint4 a0, a1, w0, w1;
+        uint32_t d;
+        float x, s;
+        float2 sm;
+    };
+    auto load_pair = [&](Pair& p, uint32_t b) {
+        const uint32_t b0 = min(b, nb - 1), b1 = min(b + 1, nb - 1), bh = half ? b1 : b0;
+        p.a0 = gemm_ld16(ptr.a, ptr.oa, b0 * 1024);
+        p.a1 = gemm_ld16(ptr.a, ptr.oa, b1 * 1024);
+        p.w0 = gemm_ld16(ptr.w, ptr.ow, b0 * kWStride);
+        p.w1 = gemm_ld16(ptr.w, ptr.ow, b1 * kWStride);
+        if constexpr (MIN) {
+            const uint32_t sx = __builtin_amdgcn_raw_buffer_load_b32(ptr.sc, static_cast<int>(ptr.osc),
+                                                                     static_cast<int>(bh * 256), 0);
+            const uint32_t sy = __builtin_amdgcn_raw_buffer_load_b32(ptr.sc, static_cast<int>(ptr.osc + 4),
+                                                                     static_cast<int>(bh * 256), 0);
+            p.sm = make_float2(__builtin_bit_cast(float, sx), __builtin_bit_cast(float, sy));
+            p.s = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ptr.s, static_cast<int>(ptr.ox),
+                                                                                 static_cast<int>(bh * 128), 0));
+        } else {
+            p.d = __builtin_amdgcn_raw_buffer_load_b16(ptr.sc, static_cast<int>(ptr.osc), static_cast<int>(bh * 64), 0);
+        }
+        p.x = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ptr.x, static_cast<int>(ptr.ox),
+                                                                             static_cast<int>(bh * 128), 0));
+    };
+    v16f acc = {};
+    v32f accm = {};
+    auto compute_pair = [&](const Pair& p, uint32_t b) {
+        const v4i bv0 = gemm_unpack<QT>(p.w0, lo_half, sh), bv1 = gemm_unpack<QT>(p.w1, lo_half, sh);
+        const v4i a0 = {static_cast<int>(p.a0.x), static_cast<int>(p.a0.y), static_cast<int>(p.a0.z),
+                        static_cast<int>(p.a0.w)};
+        const v4i a1 = {static_cast<int>(p.a1.x), static_cast<int>(p.a1.y), static_cast<int>(p.a1.z),
+                        static_cast<int>(p.a1.w)};
+        const v16i zi = {};
+        const v16i i0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bv0, zi, 0, 0, 0);
+        const v16i i1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bv1, zi, 0, 0, 0);
+        const bool valid = b + half < nb;  // this lane's half's block exists
+        float bw;
+        if constexpr (MIN) {
+            bw = p.sm.x;
+            accm = __builtin_amdgcn_mfma_f32_32x32x1f32(valid ? p.s : 0.0f, p.sm.y, accm, 0, 0, 0);
+        } else {
+            bw = h2f(p.d);
+        }
+        const v32f zf = {};
+        const v32f c = __builtin_amdgcn_mfma_f32_32x32x1f32(valid ? p.x : 0.0f, bw, zf, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            acc[i] = fmaf(c[i], static_cast<float>(i0[i]), acc[i]);
+            acc[i] = fmaf(c[16 + i], static_cast<float>(i1[i]), acc[i]);
+        }
+    };
+    constexpr uint32_t kStep = 2 * W;  // blocks between a wave's consecutive pairs
+    Pair A, B;
+    uint32_t b = 2 * wid;
+    load_pair(A, b);
+    while (b < nb) {
+        load_pair(B, b + kStep);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_pair(A, b);
+        __builtin_amdgcn_sched_barrier(0);
+        b += kStep;
+        if (b >= nb) break;
+        load_pair(A, b + kStep);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_pair(B, b);
+        __builtin_amdgcn_sched_barrier(0);
+        b += kStep;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) red[wid][i][lane] = acc[i];
+    if constexpr (MIN) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) red[wid][16 + i][lane] = accm[i] + accm[16 + i];
+    }
+    __syncthreads();
+    constexpr float kOut = QT == Q4_0 ? 0.0625f : 1.0f;
+    const uint32_t r = rt * 32 + l32;
+#pragma unroll
+    for (int j = 0; j < 16 / W; j++) {
+        const int i = static_cast<int>(wid) * (16 / W) + j;  // this wave's output register
+        float v = 0.0f, vm = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            v += red[w][i][lane];
+            if constexpr (MIN) vm += red[w][16 + i][lane];
+        }
+        const uint32_t t = 8 * (i / 4) + 4 * half + (i % 4);
+        if (r < rows && t < m) out[static_cast<size_t>(t) * rows + r] = v * kOut + vm;
+    }
+}
+
+#define ZLM_GEMM_SMALL(NAME, QT, WT)                                                                          \
+    extern "C" __global__ void __launch_bounds__(gemm_small_waves<QT>() * 64)                                 \
+        NAME(const uint8_t* __restrict__ wq, const WT* __restrict__ ws, const int8_t* __restrict__ qx,      \
+             const float* __restrict__ dx, const float* __restrict__ ds, float* __restrict__ out,           \
+             uint32_t rows, uint32_t m, uint32_t nb) {                                                      \
+        gemm_small<QT>(wq, ws, qx, dx, ds, out, rows, m, nb);                                              \
+    }
+ZLM_GEMM_SMALL(zlm_gemm_small_q4_0_q8, Q4_0, uint16_t)
+ZLM_GEMM_SMALL(zlm_gemm_small_q8_0_q8, Q8_0, uint16_t)
+ZLM_GEMM_SMALL(zlm_gemm_small_q4_1_q8, Q4_1, float2)
+ZLM_GEMM_SMALL(zlm_gemm_small_q4_k_q8, Q4_K, float2)
 
 // ---- decode-step glue -------------------------------------------------------
 // The non-GEMV ops of one Qwen3 decode layer (reference
