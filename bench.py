@@ -43,8 +43,11 @@ MALL_DEFEAT_BYTES = 512 * 1024 * 1024
 # The kernel the host picks for the 12288 x 4096 Q8_0 gate/up GEMV (the roofline kernel).
 ROOFLINE_KERNEL = "zlm_gemv_q8_0_r1_s4"
 METRIC = "quant GEMV HBM GB/s (% of 8 TB/s peak); decode tok/s, Qwen3-8B-shape Q4_0 bs=1"
-# Untimed GPU work before the headline's timed steps, whatever --warmup is.
-CLOCK_WARM_MS = 50.0
+# Untimed GPU work before each timed measurement (the headline's whatever
+# --warmup is), and a scale on the launches per measurement; --counters sets
+# both low so a rocprofv3 counter pass (which serialises every dispatch) stays
+# short.  Figures from a --counters run are not timings.
+WARM = {"ms": 50.0, "launch_scale": 1.0}
 
 
 def log(msg: str) -> None:
@@ -87,14 +90,14 @@ class Gemv:
         self.res = []
 
 
-def time_launches(dev, descs, launches_target, warmup_ms=50.0):
+def time_launches(dev, descs, launches_target):
     """Average ms per pass over `descs` (a pass = every desc once): untimed
-    passes until ~warmup_ms of GPU work has run (the clocks ramp over the first
+    passes until ~50 ms of GPU work has run (the clocks ramp over the first
     milliseconds after an idle host phase), then the median of three timed
     runs of launches_target launches."""
-    passes = max(1, launches_target // len(descs))
+    passes = max(1, int(launches_target * WARM["launch_scale"]) // len(descs))
     spent = 0.0
-    while spent < warmup_ms:
+    while spent < WARM["ms"]:
         spent += dev.time_gemv_sequence(descs, passes)
     runs = sorted(dev.time_gemv_sequence(descs, passes) / passes for _ in range(3))
     return runs[1]
@@ -205,11 +208,17 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--cpu-seconds", type=float, default=16.0,
                     help="CPU-baseline budget: half on the headline GEMV, a quarter each on configs[4] and [2]")
+    ap.add_argument("--decode-eager", type=int, default=0, metavar="N",
+                    help="run N eager decode steps instead of timing graph replays (for kernel-trace profiling)")
     ap.add_argument("--decode-replays", type=int, default=30, metavar="N",
                     help="graph replays per timed decode run (warm-up run + 3 timed runs of N)")
+    ap.add_argument("--counters", action="store_true",
+                    help="short warm-ups and few launches per shape, for rocprofv3 --pmc passes (not a timing run)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="also run the library copy kernel 5x over BYTES (for HBM traffic counter calibration)")
     args = ap.parse_args()
+    if args.counters:
+        WARM["ms"], WARM["launch_scale"] = 0.0, 0.05
     if args.gpus != 1:
         print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
               "(the multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
@@ -253,7 +262,7 @@ def main():
     steps = max(1, args.steps)
     warmup = max(0, args.warmup)
     clock_ms = dev.time_gemv_sequence(steps_of(warmup), 1) if warmup else 0.0
-    while clock_ms < CLOCK_WARM_MS:
+    while clock_ms < WARM["ms"]:
         clock_ms += dev.time_gemv_sequence(step_descs, max(1, 200 // copies))
     ms_total = dev.time_gemv_sequence(steps_of(steps), 1)
     ms_step = ms_total / steps
@@ -275,6 +284,17 @@ def main():
         "c1_gate_up_q8_0_12288x4096": {"us": round(ms_gu * 1e3, 3), "GBps": round(gu_gbps, 1)},
         "c1_down_q8_0_4096x12288": {"us": round(ms_dn * 1e3, 3), "GBps": round(dn_gbps, 1)},
     }
+
+    # the same GEMVs through the contract ops zlm's executor calls: a burst of
+    # one (host x staged) + waitResident (host y read back), host wall time
+    cit = max(20, int(400 * WARM["launch_scale"]))
+    for g_, key in ((gate, "c1_gate_up_q8_0_12288x4096"), (down, "c1_down_q8_0_4096x12288")):
+        dev.time_contract_gemv(g_.res, zd.quant(g_.qt), g_.rows, g_.k, cit)
+        us = sorted(dev.time_contract_gemv(g_.res, zd.quant(g_.qt), g_.rows, g_.k, cit) for _ in range(3))[1]
+        extra[key]["contract_us"] = round(us, 2)
+        extra[key]["contract_GBps"] = round(g_.algo_bytes / (us * 1e-6) / 1e9, 1)
+    log(f"contract path (burst + waitResident, host x/y): gate/up {extra['c1_gate_up_q8_0_12288x4096']['contract_us']}"
+        f" us, down {extra['c1_down_q8_0_4096x12288']['contract_us']} us")
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -323,9 +343,9 @@ def main():
         x_dev = dev.dev_malloc(xg.nbytes)
         dev.dev_upload(x_dev, xg)
         o_dev = dev.dev_malloc(m * rows * 4)
-        iters = 4 * ncopy
+        iters = max(2, int(4 * ncopy * WARM["launch_scale"]))
         spent = 0.0
-        while spent < 50.0:  # untimed: clocks up, as for the GEMVs
+        while spent < WARM["ms"]:  # untimed: clocks up, as for the GEMVs
             spent += dev.time_mat_mul(ress, zd.quant(zd.Q4_0), rows, k, m, x_dev, o_dev, iters)
         ms = sorted(dev.time_mat_mul(ress, zd.quant(zd.Q4_0), rows, k, m, x_dev, o_dev, iters) / iters
                     for _ in range(3))[1]
@@ -345,7 +365,44 @@ def main():
         dev.dev_free(x_dev)
         dev.dev_free(o_dev)
 
+    # ---- small token counts (verify / microbatch), as reference gpu/root_test.zig:651-696 ----
+    if not args.quick:
+        sweep = {}
+        for sname, qt, rows, k in (("q4_0_4096x4096", synth.Q4_0, 4096, 4096),
+                                   ("q4_k_4096x4096", synth.Q4_K, 4096, 4096),
+                                   ("q4_k_lm_head_262144x3840", synth.Q4_K, 262144, 3840)):
+            w = synth.weights(qt, rows, k, 0x5A4C4D05)
+            ncopy = max(1, math.ceil(MALL_DEFEAT_BYTES / w.size))
+            ress = [dev.upload_resident(w) for _ in range(ncopy)]
+            xs = synth.activation(0x5A4C4D0E, 9 * k)
+            x_dev = dev.dev_malloc(xs.nbytes)
+            dev.dev_upload(x_dev, xs)
+            o_dev = dev.dev_malloc(9 * rows * 4)
+            it = max(2, int(4 * ncopy * WARM["launch_scale"]))
+            spent = 0.0
+            while spent < WARM["ms"]:
+                spent += dev.time_mat_vec(ress, zd.quant(qt), rows, k, x_dev, o_dev, it)
+            gemv_us = sorted(dev.time_mat_vec(ress, zd.quant(qt), rows, k, x_dev, o_dev, it) / it
+                             for _ in range(3))[1] * 1e3
+            row = {"gemv_us": round(gemv_us, 2)}
+            for m in (1, 2, 3, 4, 5, 8, 9):
+                dev.time_mat_mul(ress, zd.quant(qt), rows, k, m, x_dev, o_dev, ncopy)
+                us = sorted(dev.time_mat_mul(ress, zd.quant(qt), rows, k, m, x_dev, o_dev, it) / it
+                            for _ in range(3))[1] * 1e3
+                row[f"m{m}_us"] = round(us, 2)
+            sweep[sname] = row
+            log(f"small-m {sname}: GEMV {gemv_us:.1f} us; " +
+                ", ".join(f"M{m} {row[f'm{m}_us']:.1f}" for m in (1, 2, 3, 4, 5, 8, 9)))
+            for r in ress:
+                dev.free_resident(r)
+            dev.dev_free(x_dev)
+            dev.dev_free(o_dev)
+        sweep["note"] = ("device-level matMul at m tokens vs one GEMV (weights rotated over >= 512 MiB): m <= 2 one "
+                         "fp GEMV per token, 3..32 the split-K int8-MFMA GEMM (activation quantizer included)")
+        extra["small_m_matmul"] = sweep
+
     # ---- decode step of a Qwen3-8B-shaped Q4_0 model, batch 1 ----------
+    cfg = None
     if not args.quick:
         from zlm_amd import decode as zdec
 
@@ -354,12 +411,26 @@ def main():
         model = zdec.DecodeModel(dev, cfg)
         x = synth.activation(0x5A4C4D02, cfg.hidden)
         model.step(x, cfg.max_seq - 1)  # eager: converts layouts, sizes scratch
+        tok_bytes = zdec.weight_bytes(cfg) + zdec.kv_bytes(cfg, cfg.max_seq)
+        if args.decode_eager:
+            # profiled runs: the step's kernels launched eagerly, no graph (a
+            # graph replayed under rocprofv3's kernel trace aborted the queue)
+            model.set_input(x, cfg.max_seq - 1)
+            for _ in range(args.decode_eager):
+                model.enqueue_step()
+            dev.sync()
+            extra["c2_decode_qwen3_8b_q4_0"] = {
+                "eager_steps": args.decode_eager, "bytes_per_token": tok_bytes,
+                "note": "--decode-eager: kernels launched eagerly for a profiler; no tok/s measured"}
+            log(f"c2 decode: {args.decode_eager} eager steps (profiling run, not timed)")
+            model.free()
+            cfg = None
+    if not args.quick and cfg is not None:
         graph = model.capture()
         model.set_input(x, cfg.max_seq - 1)
         reps = max(1, args.decode_replays)
         dev.graph_launch(graph, reps)  # ~50 ms untimed (30 replays): clocks up after the host-side synthesis
         ms = sorted(dev.graph_launch(graph, reps) / reps for _ in range(3))[1]
-        tok_bytes = zdec.weight_bytes(cfg) + zdec.kv_bytes(cfg, cfg.max_seq)
         gbps = tok_bytes / (ms * 1e-3) / 1e9
         extra["c2_decode_qwen3_8b_q4_0"] = {
             "tok_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4), "bytes_per_token": tok_bytes,
@@ -370,6 +441,35 @@ def main():
         log(f"c2 decode: {ms:.3f} ms/token = {1e3 / ms:.1f} tok/s, {gbps:.1f} GB/s ({100 * gbps / PEAK_GBPS:.1f}%)")
         dev.graph_destroy(graph)
         model.free()
+        # the same token's projections through the contract ops only, as zlm's
+        # executor submits them (separate q/k/v residents, bursts and drains,
+        # host activations); the CPU glue between them is not run
+        log("c2 decode via the contract ops: synthesising separate q/k/v/o/gate/up/down residents")
+        h_, f_ = cfg.hidden, cfg.ffn
+        qr, kvr = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        shapes = [(qr, h_), (kvr, h_), (kvr, h_), (h_, qr), (f_, h_), (f_, h_), (h_, f_)]
+        layers, allres = [], []
+        for li in range(cfg.n_layers):
+            layer = []
+            for j, (rr, kk) in enumerate(shapes):
+                r_ = dev.synth_resident(zd.Q4_0, rr * kk // 32, 0x5A4C4D90 + 16 * li + j, 0.02)
+                if r_ is None:
+                    raise RuntimeError(dev.last_error())
+                layer.append(r_)
+            layers.append(layer)
+            allres += layer
+        lm = dev.synth_resident(zd.Q8_0, cfg.vocab * h_ // 32, 0x5A4C4D9F, 0.01)
+        allres.append(lm)
+        ms_c = sorted(dev.time_contract_decode(layers, zd.quant(zd.Q4_0), h_, qr, kvr, f_, lm, zd.quant(zd.Q8_0),
+                                               cfg.vocab, 3) for _ in range(3))[1]
+        extra["c2_decode_qwen3_8b_q4_0"]["contract_path"] = {
+            "ms_per_token": round(ms_c, 3), "tok_per_s": round(1e3 / ms_c, 1),
+            "note": "projections only, through matVecResidentBurstAsync / matVecMlpPairResidentBurstAsync / "
+                    "waitResident / matVecResident with host activations, in the executor's burst pattern; "
+                    "CPU attention and glue not included"}
+        log(f"c2 decode via the contract ops: {ms_c:.3f} ms/token (GPU ops only)")
+        for r_ in allres:
+            dev.free_resident(r_)
         if not args.no_cpu:
             c2cpu = cpu_decode_sample(cfg, 0.25 * args.cpu_seconds)
             extra["c2_decode_qwen3_8b_q4_0"]["cpu_baseline"] = c2cpu

@@ -179,7 +179,15 @@ void zlm_gpu_sync(zlm_device *dev);
 /* Device.probeGpu (vulkan/root.zig:237-242, generic probe gpu/backend/root.zig:357-498). */
 void zlm_gpu_probe(zlm_device *dev, size_t rows, size_t k, size_t m, zlm_probe *out);
 
-/* Resident.bytes (reference gpu/backend/root.zig:241-244). */
+/* The per-variant rate table behind one quant's probe entry (no reference
+ * counterpart; for tests and tuning logs): rates[v] = GB/s of GpuVariant v,
+ * measured as zlm_gpu_probe measures it (interleaved min-of-5 contract ops on
+ * fillWeights-style inputs, rows <= 12288, k <= 4096), of the resident GEMV or,
+ * with gate_up, of the fused gate_up.  False, with rates zeroed, when the quant
+ * is unsupported or a variant did not run. */
+bool zlm_gpu_probe_rates(zlm_device *dev, uint32_t ggml_type, bool gate_up, size_t rows, size_t k, double *rates);
+
+/* Resident.bytes (reference gpu/backend/root.zig:241-244): the raw GGUF bytes uploaded. */
 uint64_t zlm_gpu_resident_bytes(const zlm_resident *res);
 
 /* ---- device-level entry points (no reference counterpart) ----
@@ -198,6 +206,19 @@ int zlm_gpu_cu_count(const zlm_device *dev);
  * first op names its quant; the conversion to the device layout briefly holds
  * both copies. */
 bool zlm_gpu_vram_info(zlm_device *dev, uint64_t *free_bytes, uint64_t *total_bytes);
+/* HBM a resident holds now: its raw bytes until the first op converts them,
+ * then the device layout, plus the prefill GEMM's tiled copy once a GEMM of
+ * 3 or more tokens has run on it. */
+uint64_t zlm_gpu_resident_device_bytes(const zlm_resident *res);
+/* HBM a rows x k weight of `quant` will hold once converted (its device
+ * layout), plus its GEMM tiled copy when `with_gemm` (tensors the plan also
+ * runs prefill GEMMs on); 0 for an unsupported quant or shape.  For the
+ * plan's --vram budget before anything is uploaded; the conversion itself
+ * briefly holds the raw bytes too. */
+uint64_t zlm_gpu_layout_bytes(uint32_t quant, size_t rows, size_t k, bool with_gemm);
+/* Free a resident's GEMM tiled copy (a later GEMM rebuilds it); false only
+ * for a null or inert device or resident. */
+bool zlm_gpu_release_gemm_tiles(zlm_device *dev, zlm_resident *res);
 void *zlm_gpu_dev_malloc(zlm_device *dev, size_t bytes);
 void zlm_gpu_dev_free(zlm_device *dev, void *ptr);
 bool zlm_gpu_dev_upload(zlm_device *dev, void *dst, const void *src, size_t bytes);
@@ -246,6 +267,28 @@ typedef struct {
 /* Enqueue descs[0..n) in order, `iters` times, between two HIP events on the
  * device stream; *ms = elapsed GPU milliseconds between the events. */
 bool zlm_gpu_time_gemv_sequence(zlm_device *dev, const zlm_gemv_desc *descs, size_t n, int iters, double *ms);
+/* ---- the contract path, timed as zlm's executor drives it (no reference
+ * counterpart; the rates zlm would see through this ABI) ----
+ * One contract GEMV per iteration: matVecResidentBurstAsync (first, host x
+ * staged) + waitResident (host y), rotating over n_res residents; *us = host
+ * wall microseconds per op. */
+bool zlm_gpu_time_contract_gemv(zlm_device *dev, zlm_resident *const *res, size_t n_res, uint32_t quant, size_t rows,
+                                size_t k, int iters, double *us);
+/* One layer's projections as separate residents (the GGUF tensors zlm uploads). */
+typedef struct {
+    zlm_resident *q, *k, *v, *o, *gate, *up, *down;
+} zlm_contract_layer;
+/* `iters` decode tokens through the contract ops only, in the executor's
+ * burst/drain pattern for a discrete device (reference
+ * runtime/executor.zig:236-258): per layer a burst of q, k, v over one host x
+ * and their drain; o as a burst of its own and its drain; the fused
+ * matVecMlpPairResidentBurstAsync and its drain; then the lm_head through
+ * matVecResident.  The CPU-side glue (norms, RoPE, attention, residual adds)
+ * is not run, so this is the GPU part of a token; *ms per token, host wall. */
+bool zlm_gpu_time_contract_decode(zlm_device *dev, const zlm_contract_layer *layers, size_t n_layers, uint32_t quant,
+                                  size_t hidden, size_t q_rows, size_t kv_rows, size_t ffn, zlm_resident *lm_head,
+                                  uint32_t lm_quant, size_t vocab, int iters, double *ms);
+
 /* GEMV forms of zlm_gemv_op; every form reads x from device memory:
  *   PLAIN     y = W x
  *   PAIR      y[r] = act(W x, W_up x)[r]             (the fused gate_up)

@@ -105,3 +105,25 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(zd, "_lib", None)
     with pytest.raises(ImportError):
         zd.Device()
+
+
+def test_layout_bytes_for_the_residency_budget():
+    """zlm_gpu_layout_bytes (host arithmetic, no GPU): the device layout of a
+    weight (payload rounded to 256 bytes, then the split scales or records,
+    then 256 bytes of slack) and the prefill GEMM's tiled copy."""
+    nblk = 4096 * 4096 // 32
+    q4 = 16 * nblk + 2 * nblk + 256
+    assert zd.layout_bytes(zd.quant(zd.Q4_0), 4096, 4096, False) == q4
+    tiles = 128 * 128 * 32 * 16 + 128 * 128 * 32 * 2  # 32-row tiles x blocks x (16 nibble bytes + f16 scale)
+    assert zd.layout_bytes(zd.quant(zd.Q4_0), 4096, 4096, True) == q4 + tiles
+    # q4_k: 128-byte qs blocks + 20-byte records; its tiles carry a (scale, min) float pair per 32 elements
+    kb = 15360 * 3840 // 256
+    q4k = 128 * kb + 20 * kb + 256
+    assert zd.layout_bytes(zd.quant(zd.Q4_K), 15360, 3840, False) == q4k
+    assert zd.layout_bytes(zd.quant(zd.Q4_K), 15360, 3840, True) == q4k + 480 * 120 * 32 * (16 + 8)
+    # q6_k has no GEMM: with_gemm adds nothing; the float types keep their raw rows
+    q6 = zd.layout_bytes(zd.quant(zd.Q6_K), 3840, 15360, False)
+    assert q6 == zd.layout_bytes(zd.quant(zd.Q6_K), 3840, 15360, True) == 128 * 230400 + 84 * 230400 + 256
+    assert zd.layout_bytes(zd.quant(zd.F16), 64, 256, True) == 64 * 256 * 2
+    assert zd.layout_bytes(zd.quant(zd.Q4_0), 64, 100, False) == 0  # k not whole blocks
+    assert zd.layout_bytes(77, 64, 256, False) == 0  # unknown type

@@ -280,3 +280,25 @@ def test_split_k_ragged_rows_match_oracle(dev, qt, k, rows):
     for p in (xd, resd, yd):
         dev.dev_free(p)
     dev.free_resident(rw)
+
+
+def test_contract_timing_helpers_run_the_contract_ops(dev):
+    """The contract-path timers (burst + waitResident per GEMV; a decode token
+    in the executor's burst pattern) run on small shapes and report positive
+    times; a layer whose weights are too short for the shapes is refused."""
+    hidden, qr, kvr, ffn, vocab = 256, 256, 128, 512, 1000
+    shapes = [(qr, hidden), (kvr, hidden), (kvr, hidden), (hidden, qr), (ffn, hidden), (ffn, hidden), (hidden, ffn)]
+    layers = []
+    for i in range(2):
+        layers.append([dev.upload_resident(synth.weights(synth.Q4_0, r, k, seed=10 * i + j))
+                       for j, (r, k) in enumerate(shapes)])
+    lm = dev.upload_resident(synth.weights(synth.Q8_0, vocab, hidden, seed=99))
+    assert dev.time_contract_gemv(layers[0][:1], zd.quant(zd.Q4_0), qr, hidden, 5) > 0.0
+    assert dev.time_contract_decode(layers, zd.quant(zd.Q4_0), hidden, qr, kvr, ffn, lm, zd.quant(zd.Q8_0), vocab,
+                                    2) > 0.0
+    with pytest.raises(RuntimeError):
+        dev.time_contract_decode(layers, zd.quant(zd.Q4_0), hidden, qr, kvr, 2 * ffn, lm, zd.quant(zd.Q8_0), vocab, 1)
+    for layer in layers:
+        for r in layer:
+            dev.free_resident(r)
+    dev.free_resident(lm)

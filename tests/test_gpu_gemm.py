@@ -143,3 +143,29 @@ def test_gemm_q4_k_c3_shape_rows_subset(dev):
         want = oracle.matmul_int(synth.Q4_K, w[r0 * rb:r1 * rb], k, r1 - r0, m, x)
         assert rel_l2(got[:, r0:r1], want) <= 1e-3, (r0, r1)
     dev.free_resident(res)
+
+
+def test_resident_device_bytes_follow_the_conversions(dev):
+    """The HBM a resident holds: its raw bytes after upload, the device layout
+    after the first op, plus the GEMM tiled copy after a GEMM of more than
+    two tokens (zlm_gpu_layout_bytes' estimate), and the layout again after
+    zlm_gpu_release_gemm_tiles (a later GEMM rebuilds the copy)."""
+    rows, k, m = 96, 4096, 8
+    for qt, zq in GEMM_QUANTS:
+        w = synth.weights(qt, rows, k, seed=77)
+        x = synth.activation(78, m * k)
+        res = dev.upload_resident(w)
+        assert dev.resident_device_bytes(res) == w.size
+        out = np.zeros(rows, np.float32)
+        assert dev.mat_vec_resident(res, zd.quant(zq), rows, k, x[:k], out), dev.last_error()
+        layout = zd.layout_bytes(zd.quant(zq), rows, k, False)
+        assert dev.resident_device_bytes(res) == layout
+        outm = np.zeros(m * rows, np.float32)
+        assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, outm), dev.last_error()
+        assert dev.resident_device_bytes(res) == zd.layout_bytes(zd.quant(zq), rows, k, True) > layout
+        assert dev.release_gemm_tiles(res)
+        assert dev.resident_device_bytes(res) == layout
+        again = np.zeros(m * rows, np.float32)
+        assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, again), dev.last_error()
+        np.testing.assert_array_equal(again, outm)
+        dev.free_resident(res)

@@ -118,10 +118,12 @@ struct GemvKernel {
 struct Slot {
     hipEvent_t done = nullptr;
     float* d_y = nullptr;
-    float* h_y = nullptr;
+    float* h_y = nullptr;  // pinned; the result kernel writes it through h_y_dev
+    float* h_y_dev = nullptr;
     size_t y_cap = 0;
     float* d_x = nullptr;
     float* h_x = nullptr;
+    float* h_x_dev = nullptr;
     size_t x_cap = 0;
     bool pending = false;
     uint32_t gen = 0;
@@ -144,6 +146,8 @@ struct zlm_resident {
     void* gemm_scales = nullptr;  // f16 (q4_0, q8_0) or float2 (scale, min) (q4_1, q4_k)
     uint64_t gemm_nb = 0;
     uint64_t gemm_rt = 0;  // 32-row tiles
+    uint64_t layout_alloc = 0;  // device bytes of the layout allocation
+    uint64_t gemm_alloc = 0;    // device bytes of the GEMM tile allocation
     zlm_device* owner = nullptr;
 };
 
@@ -201,12 +205,15 @@ struct zlm_device {
     Slot slots[kRing];
     int next_slot = 0;
 
-    // synchronous-op staging
+    // synchronous-op staging (pinned host halves mapped for the device: x is
+    // copied in by the copy kernel, y written by the GEMV itself)
     float* d_x = nullptr;
     float* h_x = nullptr;
+    float* h_x_dev = nullptr;
     size_t x_cap = 0;
     float* d_y = nullptr;
     float* h_y = nullptr;
+    float* h_y_dev = nullptr;
     size_t y_cap = 0;
     uint8_t* s_raw = nullptr;  // streamed-weight staging (raw blocks)
     uint64_t s_raw_cap = 0;
@@ -216,11 +223,13 @@ struct zlm_device {
     // the fused MLP's ffn_mid (device side; the host half is unused)
     float* d_mid = nullptr;
     float* h_mid = nullptr;
+    float* h_mid_dev = nullptr;
     size_t mid_cap = 0;
 
     // burst-shared activation
     float* d_bx = nullptr;
     float* h_bx = nullptr;
+    float* h_bx_dev = nullptr;
     size_t bx_cap = 0;
     hipEvent_t bx_copied = nullptr;
     const float* burst_src = nullptr;
@@ -315,12 +324,16 @@ bool load_kernels(zlm_device* d) {
 }
 
 // A device buffer and a pinned host buffer of `n` floats sharing one capacity.
-bool ensure_pair(zlm_device* d, float*& dev, float*& host, size_t& cap, size_t n) {
-    if (cap >= n && dev && host) return true;
+// A device buffer and a pinned host buffer of n floats, and the host
+// buffer's device-side address (kernels read or write it directly); all three
+// are replaced together when the buffer grows.
+bool ensure_pair(zlm_device* d, float*& dev, float*& host, size_t& cap, size_t n, float*& host_dev) {
+    if (cap >= n && dev && host && host_dev) return true;
     if (dev) hipFree(dev);
     if (host) hipHostFree(host);
     dev = nullptr;
     host = nullptr;
+    host_dev = nullptr;
     cap = 0;
     if (!ok(d, hipMalloc(reinterpret_cast<void**>(&dev), n * sizeof(float)), "hipMalloc")) return false;
     if (!ok(d, hipHostMalloc(reinterpret_cast<void**>(&host), n * sizeof(float), hipHostMallocDefault),
@@ -329,6 +342,15 @@ bool ensure_pair(zlm_device* d, float*& dev, float*& host, size_t& cap, size_t n
         dev = nullptr;
         return false;
     }
+    void* p = nullptr;
+    if (!ok(d, hipHostGetDevicePointer(&p, host, 0), "host buffer device address")) {
+        hipFree(dev);
+        hipHostFree(host);
+        dev = nullptr;
+        host = nullptr;
+        return false;
+    }
+    host_dev = static_cast<float*>(p);
     cap = n;
     return true;
 }
@@ -386,10 +408,12 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
         r->payload = r->raw;
         r->raw = nullptr;
         r->scales = nullptr;
+        r->layout_alloc = r->bytes;
     } else {
         uint8_t* dst = nullptr;
         if (!ok(d, hipMalloc(reinterpret_cast<void**>(&dst), layout_bytes(qi, nblk)), "hipMalloc layout"))
             return false;
+        r->layout_alloc = layout_bytes(qi, nblk);
         uint16_t* scales = nullptr;
         if (!convert_blocks(d, r->raw, nblk, qi, dst, &scales)) {
             hipFree(dst);
@@ -790,6 +814,8 @@ void release_resident_memory(zlm_resident* r) {
     r->scales = nullptr;
     r->layout = kNoLayout;
     r->blocks = 0;
+    r->layout_alloc = 0;
+    r->gemm_alloc = 0;
     r->gemm_payload = nullptr;
     r->gemm_scales = nullptr;
     r->gemm_nb = 0;
@@ -797,15 +823,31 @@ void release_resident_memory(zlm_resident* r) {
 }
 
 // Stage host x into the synchronous-op device buffer.
-bool stage_x_sync(zlm_device* d, const float* x, size_t n) {
-    if (!ensure_pair(d, d->d_x, d->h_x, d->x_cap, n)) return false;
-    memcpy(d->h_x, x, n * sizeof(float));
-    return ok(d, hipMemcpyAsync(d->d_x, d->h_x, n * sizeof(float), hipMemcpyHostToDevice, d->stream), "stage x");
+// Copy n floats from a pinned host buffer (its device address `src`) into
+// device memory on the stream: the library's copy kernel reading the host
+// memory directly (one dependent launch; cheaper than a DMA copy at these
+// sizes), or a DMA copy when n is not whole 16-byte units.
+bool stage_in(zlm_device* d, float* dst, const float* src, const float* src_host, size_t n) {
+    if (n % 4 == 0) {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+        uint4* d4 = reinterpret_cast<uint4*>(dst);
+        uint64_t n16 = n / 4;
+        void* args[] = {&s4, &d4, &n16};
+        return launch(d, d->copy16, static_cast<unsigned>(std::min<uint64_t>((n16 + 255) / 256, 1024)), 256, args,
+                      "stage x");
+    }
+    return ok(d, hipMemcpyAsync(dst, src_host, n * sizeof(float), hipMemcpyHostToDevice, d->stream), "stage x");
 }
 
+bool stage_x_sync(zlm_device* d, const float* x, size_t n) {
+    if (!ensure_pair(d, d->d_x, d->h_x, d->x_cap, n, d->h_x_dev)) return false;
+    memcpy(d->h_x, x, n * sizeof(float));
+    return stage_in(d, d->d_x, d->h_x_dev, d->h_x, n);
+}
+
+// Wait for the synchronous op whose result kernel wrote d->h_y (through its
+// device address), then copy it out.
 bool finish_sync(zlm_device* d, float* out, size_t n) {
-    if (!ok(d, hipMemcpyAsync(d->h_y, d->d_y, n * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y"))
-        return false;
     if (!ok(d, hipStreamSynchronize(d->stream), "sync")) return false;
     memcpy(out, d->h_y, n * sizeof(float));
     return true;
@@ -832,12 +874,11 @@ bool submit_into_slot(zlm_device* d, int s, zlm_resident* r, uint32_t quant, siz
                       const float* x_dev) {
     Slot& sl = d->slots[s];
     size_t ycap = sl.y_cap;
-    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows)) return false;
+    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows, sl.h_y_dev)) return false;
     sl.y_cap = ycap;
     if (!sl.done && !ok(d, hipEventCreateWithFlags(&sl.done, hipEventDisableTiming), "event")) return false;
-    if (!enqueue_gemv(d, r, quant, rows, k, x_dev, sl.d_y)) return false;
-    if (!ok(d, hipMemcpyAsync(sl.h_y, sl.d_y, rows * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y"))
-        return false;
+    // the GEMV writes the slot's pinned host buffer directly (no read-back copy)
+    if (!enqueue_gemv(d, r, quant, rows, k, x_dev, sl.h_y_dev)) return false;
     if (!ok(d, hipEventRecord(sl.done, d->stream), "record")) return false;
     sl.rows = rows;
     return true;
@@ -872,22 +913,36 @@ bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_G
 //                [rt][nb][32] (q4_1 from its split layout, q4_k from its
 //                qs payload and records).
 // The resident's layout type never changes, so nb keys the copy.
-bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint64_t nb) {
-    if (r->gemm_payload && r->gemm_nb == nb) return true;
+// Bytes of the GEMM's tiled copy of a weight of `rows` rows and nb 32-element
+// blocks per row: per 32-row tile and block, 16 (nibbles) or 32 (q8_0) bytes a
+// row plus the row's scale (f16) or (scale, min) float pair.
+uint64_t gemm_tile_bytes(uint32_t type, uint64_t rows, uint64_t nb) {
+    const uint64_t rt = (rows + 31) / 32;
+    return rt * nb * 32 * (type == ZLM_GGML_Q8_0 ? 32 : 16) + rt * nb * 32 * (gemm_has_min(type) ? 8 : 2);
+}
+
+void free_gemm_tiles(zlm_resident* r) {
     if (r->gemm_payload) hipFree(r->gemm_payload);
     r->gemm_payload = nullptr;
     r->gemm_scales = nullptr;
     r->gemm_nb = 0;
     r->gemm_rt = 0;
+    r->gemm_alloc = 0;
+}
+
+bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint64_t nb) {
+    if (r->gemm_payload && r->gemm_nb == nb) return true;
+    if (r->gemm_payload) hipStreamSynchronize(d->stream);
+    free_gemm_tiles(r);
     const uint64_t wblocks = nb * 32 / qi->block_elems;  // layout blocks per row
     const uint64_t rows_total = r->blocks / wblocks;
     const uint64_t rt = (rows_total + 31) / 32;
     if (rt == 0 || rt * 32 > 0xffffffffu) return fail(d, "GEMM weight shape out of range");
-    const bool with_min = gemm_has_min(qi->type);
     const uint64_t pbytes = rt * nb * 32 * (qi->type == ZLM_GGML_Q8_0 ? 32 : 16);
-    const uint64_t sbytes = rt * nb * 32 * (with_min ? 8 : 2);
+    const uint64_t sbytes = gemm_tile_bytes(qi->type, rows_total, nb) - pbytes;
     uint8_t* p = nullptr;
     if (!ok(d, hipMalloc(reinterpret_cast<void**>(&p), pbytes + sbytes), "hipMalloc gemm tiles")) return false;
+    r->gemm_alloc = pbytes + sbytes;
     uint8_t* payload = r->payload;
     uint16_t* scales = r->scales;
     uint8_t* tp = p;
@@ -1087,6 +1142,27 @@ extern "C" void zlm_gpu_free_resident(zlm_device* d, zlm_resident* r) {
 
 extern "C" uint64_t zlm_gpu_resident_bytes(const zlm_resident* r) { return r ? r->bytes : 0; }
 
+extern "C" uint64_t zlm_gpu_resident_device_bytes(const zlm_resident* r) {
+    if (!r) return 0;
+    return (r->raw ? r->bytes : 0) + r->layout_alloc + r->gemm_alloc;
+}
+
+extern "C" uint64_t zlm_gpu_layout_bytes(uint32_t quant, size_t rows, size_t k, bool with_gemm) {
+    const QuantInfo* qi = quant_info(quant);
+    if (!qi || rows == 0 || k == 0 || k % qi->block_elems) return 0;
+    const uint64_t nblk = static_cast<uint64_t>(rows) * (k / qi->block_elems);
+    uint64_t b = qi->scale_offset == kNoLayout ? nblk * qi->block_bytes : layout_bytes(qi, nblk);
+    if (with_gemm && gemm_supported(qi->type) && k % 32 == 0) b += gemm_tile_bytes(qi->type, rows, k / 32);
+    return b;
+}
+
+extern "C" bool zlm_gpu_release_gemm_tiles(zlm_device* d, zlm_resident* r) {
+    if (!d || !d->avail || !r) return false;
+    if (r->gemm_payload) hipStreamSynchronize(d->stream);
+    free_gemm_tiles(r);
+    return true;
+}
+
 extern "C" bool zlm_gpu_mat_vec_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
                                          const float* x, size_t x_len, float* out, size_t out_len) {
     if (!d || !d->avail) return false;
@@ -1094,9 +1170,9 @@ extern "C" bool zlm_gpu_mat_vec_resident(zlm_device* d, zlm_resident* r, uint32_
     hipFunction_t f;
     unsigned g, b;
     if (!prepare_gemv(d, r, quant, rows, k, &f, &g, &b)) return false;
-    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, rows)) return false;
+    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, rows, d->h_y_dev)) return false;
     if (!stage_x_sync(d, x, k)) return false;
-    if (!enqueue_gemv(d, r, quant, rows, k, d->d_x, d->d_y)) return false;
+    if (!enqueue_gemv(d, r, quant, rows, k, d->d_x, d->h_y_dev)) return false;
     return finish_sync(d, out, rows);
 }
 
@@ -1143,11 +1219,10 @@ extern "C" int32_t zlm_gpu_mat_vec_resident_async(zlm_device* d, zlm_resident* r
     if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
     Slot& sl = d->slots[s];
     size_t xcap = sl.x_cap;
-    if (!ensure_pair(d, sl.d_x, sl.h_x, xcap, k)) return ZLM_NULL_HANDLE;
+    if (!ensure_pair(d, sl.d_x, sl.h_x, xcap, k, sl.h_x_dev)) return ZLM_NULL_HANDLE;
     sl.x_cap = xcap;
     memcpy(sl.h_x, x, k * sizeof(float));
-    if (!ok(d, hipMemcpyAsync(sl.d_x, sl.h_x, k * sizeof(float), hipMemcpyHostToDevice, d->stream), "stage x"))
-        return ZLM_NULL_HANDLE;
+    if (!stage_in(d, sl.d_x, sl.h_x_dev, sl.h_x, k)) return ZLM_NULL_HANDLE;
     if (!submit_into_slot(d, s, r, quant, rows, k, sl.d_x)) return ZLM_NULL_HANDLE;
     return make_handle(d, s);
 }
@@ -1162,12 +1237,11 @@ const float* stage_burst(zlm_device* d, const float* x, size_t x_len, bool first
         // The previous burst's host->device copy must have consumed the pinned
         // buffer before it is overwritten.
         if (d->bx_copied && !ok(d, hipEventSynchronize(d->bx_copied), "burst wait")) return nullptr;
-        if (!ensure_pair(d, d->d_bx, d->h_bx, d->bx_cap, x_len)) return nullptr;
+        if (!ensure_pair(d, d->d_bx, d->h_bx, d->bx_cap, x_len, d->h_bx_dev)) return nullptr;
         if (!d->bx_copied && !ok(d, hipEventCreateWithFlags(&d->bx_copied, hipEventDisableTiming), "event"))
             return nullptr;
         memcpy(d->h_bx, x, x_len * sizeof(float));
-        if (!ok(d, hipMemcpyAsync(d->d_bx, d->h_bx, x_len * sizeof(float), hipMemcpyHostToDevice, d->stream),
-                "stage burst x") ||
+        if (!stage_in(d, d->d_bx, d->h_bx_dev, d->h_bx, x_len) ||
             !ok(d, hipEventRecord(d->bx_copied, d->stream), "record")) {
             d->burst_open = false;
             return nullptr;
@@ -1182,21 +1256,21 @@ const float* stage_burst(zlm_device* d, const float* x, size_t x_len, bool first
     return d->d_bx;
 }
 
-// Make slot `s` ready to receive `rows` floats.
+// Make slot `s` ready to receive `rows` floats (its result kernel writes the
+// pinned host buffer through sl.h_y_dev).
 bool prepare_slot(zlm_device* d, int s, size_t rows) {
     Slot& sl = d->slots[s];
     size_t ycap = sl.y_cap;
-    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows)) return false;
+    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows, sl.h_y_dev)) return false;
     sl.y_cap = ycap;
     if (!sl.done && !ok(d, hipEventCreateWithFlags(&sl.done, hipEventDisableTiming), "event")) return false;
     return true;
 }
 
-// Queue slot `s`'s read-back of `rows` floats and its completion event.
+// Queue slot `s`'s completion event (its result is already in host memory
+// when the event completes).
 bool finish_slot(zlm_device* d, int s, size_t rows) {
     Slot& sl = d->slots[s];
-    if (!ok(d, hipMemcpyAsync(sl.h_y, sl.d_y, rows * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y"))
-        return false;
     if (!ok(d, hipEventRecord(sl.done, d->stream), "record")) return false;
     sl.rows = rows;
     return true;
@@ -1206,7 +1280,7 @@ bool finish_slot(zlm_device* d, int s, size_t rows) {
 // device-side ffn_mid, then the down GEMV into slot `s`.
 bool enqueue_mlp(zlm_device* d, int s, zlm_resident* rg, zlm_resident* ru, zlm_resident* rd, uint32_t gu_quant,
                  uint32_t down_quant, size_t rows, size_t k, size_t ffn, const float* x_dev, uint32_t act) {
-    if (!ensure_pair(d, d->d_mid, d->h_mid, d->mid_cap, ffn)) return false;
+    if (!ensure_pair(d, d->d_mid, d->h_mid, d->mid_cap, ffn, d->h_mid_dev)) return false;
     zlm_gemv_op gu = {};
     gu.form = ZLM_FORM_PAIR;
     gu.quant = gu_quant;
@@ -1218,7 +1292,7 @@ bool enqueue_mlp(zlm_device* d, int s, zlm_resident* rg, zlm_resident* ru, zlm_r
     gu.act = act;
     gu.y = d->d_mid;
     if (!enqueue_op(d, gu)) return false;
-    return enqueue_gemv(d, rd, down_quant, rows, ffn, d->d_mid, d->slots[s].d_y);
+    return enqueue_gemv(d, rd, down_quant, rows, ffn, d->d_mid, d->slots[s].h_y_dev);
 }
 
 }  // namespace
@@ -1264,7 +1338,7 @@ extern "C" bool zlm_gpu_mat_vec_resident_batch(zlm_device* d, size_t k, const fl
         if (!prepare_gemv(d, ops[i].res, ops[i].quant, ops[i].rows, k, &f, &g, &b)) return false;
         total += ops[i].rows;
     }
-    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, total)) return false;
+    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, total, d->h_y_dev)) return false;
     if (!stage_x_sync(d, x, k)) return false;
     // Ops of one quant go out as one launch of the batch kernel; a mixed batch,
     // or one whose shape has a split-K single-op kernel (another summation
@@ -1310,8 +1384,8 @@ extern "C" bool zlm_gpu_mat_mul_resident(zlm_device* d, zlm_resident* r, uint32_
                                          size_t m, const float* x, size_t x_len, float* out, size_t out_len) {
     if (!d || !d->avail) return false;
     if (!x || !out || m == 0 || x_len != m * k || out_len < m * rows) return fail(d, "bad buffers");
-    if (!ensure_pair(d, d->d_x, d->h_x, d->x_cap, m * k)) return false;
-    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, m * rows)) return false;
+    if (!ensure_pair(d, d->d_x, d->h_x, d->x_cap, m * k, d->h_x_dev)) return false;
+    if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, m * rows, d->h_y_dev)) return false;
     memcpy(d->h_x, x, m * k * sizeof(float));
     if (!ok(d, hipMemcpyAsync(d->d_x, d->h_x, m * k * sizeof(float), hipMemcpyHostToDevice, d->stream), "stage x"))
         return false;
@@ -1319,6 +1393,9 @@ extern "C" bool zlm_gpu_mat_mul_resident(zlm_device* d, zlm_resident* r, uint32_
         hipStreamSynchronize(d->stream);
         return false;
     }
+    // the m x rows result (megabytes at prefill sizes) comes back by DMA
+    if (!ok(d, hipMemcpyAsync(d->h_y, d->d_y, m * rows * sizeof(float), hipMemcpyDeviceToHost, d->stream), "read y"))
+        return false;
     return finish_sync(d, out, m * rows);
 }
 
@@ -1376,7 +1453,7 @@ extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, z
     op.k = k;
     op.x = xd;
     op.act = act;
-    op.y = d->slots[s].d_y;
+    op.y = d->slots[s].h_y_dev;
     if (!enqueue_op(d, op) || !finish_slot(d, s, rows)) return ZLM_NULL_HANDLE;
     return make_handle(d, s);
 }
@@ -1427,8 +1504,10 @@ extern "C" void zlm_gpu_sync(zlm_device* d) {
 // measures it: staging, dispatch and read-back included), in GB/s over the
 // weight bytes.  Variants are measured interleaved and the fastest recorded;
 // every GpuVariant maps to one of this backend's row tiles (rt_for_variant).
-// Quants this backend does not run (q4_1, f32, f16, bf16) keep rate 0 and
-// variant `plain`, the contract's "unmeasured".
+// Every quant the backend runs is probed (q4_0, q4_1, q8_0, q4_k, q6_k, f32,
+// f16, bf16) and the fused gate_up over q4_0, q8_0 and q4_1, as the
+// reference's probe does; the fused gate_up has one kernel per shape, so its
+// variants all measure that kernel.
 
 namespace {
 
@@ -1438,13 +1517,53 @@ constexpr size_t kProbeMaxK = 4 * 1024;
 constexpr uint32_t kAllVariants[] = {ZLM_VARIANT_PLAIN, ZLM_VARIANT_U4, ZLM_VARIANT_U8, ZLM_VARIANT_SUB,
                                      ZLM_VARIANT_UN2,   ZLM_VARIANT_UN4, ZLM_VARIANT_W32, ZLM_VARIANT_W128};
 
+// IEEE binary16 bits of a binary32 value (round to nearest even; subnormal
+// results rounded the same way, overflow to infinity, NaN kept quiet).
+uint16_t f32_to_f16_bits(uint32_t f) {
+    const uint32_t sign = (f >> 16) & 0x8000u;
+    const uint32_t exp = (f >> 23) & 0xffu;
+    uint32_t man = f & 0x7fffffu;
+    if (exp == 0xffu) return static_cast<uint16_t>(sign | 0x7c00u | (man ? 0x200u : 0u));
+    const int e = static_cast<int>(exp) - 127 + 15;
+    if (e >= 31) return static_cast<uint16_t>(sign | 0x7c00u);
+    if (e <= 0) {  // subnormal (or zero) half
+        if (e < -10) return static_cast<uint16_t>(sign);
+        man |= 0x800000u;
+        const int shift = 14 - e;  // 24-bit significand down to the subnormal's 10 bits
+        const uint32_t q = man >> shift, rem = man & ((1u << shift) - 1), halfway = 1u << (shift - 1);
+        const uint32_t r = q + ((rem > halfway || (rem == halfway && (q & 1u))) ? 1u : 0u);
+        return static_cast<uint16_t>(sign | r);
+    }
+    const uint32_t q = man >> 13, rem = man & 0x1fffu;
+    uint32_t h = (static_cast<uint32_t>(e) << 10) | q;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) h++;  // may carry into the exponent (and to inf)
+    return static_cast<uint16_t>(sign | h);
+}
+
 // fillWeights (gpu/backend/root.zig:734-786): random bytes with the scale
-// fields overwritten (q4_0/q8_0 d = 0.05, q4_k d = 0.05 and dmin = 0.02, q6_k
-// d = 0.02).  The bytes come from a splitmix64 stream, not Zig's PRNG.
+// fields overwritten (q4_0/q8_0 d = 0.05, q4_1 d = 0.05 and m = 0.02, q4_k
+// d = 0.05 and dmin = 0.02, q6_k d = 0.02); the float types the ramp
+// f32(i % 13) * 0.05 - 0.3 (f16 rounded, bf16 truncated).  The bytes come from
+// a splitmix64 stream, not Zig's PRNG.
 std::vector<uint8_t> probe_weights(uint32_t type, size_t rows, size_t k) {
     const QuantInfo* qi = quant_info(type);
     const size_t nblk = rows * (k / qi->block_elems);
     std::vector<uint8_t> w(nblk * qi->block_bytes);
+    if (qi->scale_offset == kNoLayout) {
+        for (size_t i = 0; i < nblk; i++) {
+            const float v = static_cast<float>(i % 13) * 0.05f - 0.3f;
+            if (type == ZLM_GGML_F32) {
+                memcpy(w.data() + 4 * i, &v, 4);
+            } else {
+                uint32_t bits;
+                memcpy(&bits, &v, 4);
+                uint16_t h;
+                h = type == ZLM_GGML_BF16 ? static_cast<uint16_t>(bits >> 16) : f32_to_f16_bits(bits);
+                memcpy(w.data() + 2 * i, &h, 2);
+            }
+        }
+        return w;
+    }
     uint64_t z = 0x9e3779b97f4a7c15ull;
     for (size_t i = 0; i < w.size(); i += 8) {
         z += 0x9E3779B97F4A7C15ull;
@@ -1462,7 +1581,7 @@ std::vector<uint8_t> probe_weights(uint32_t type, size_t rows, size_t k) {
             blk[off + 1] = static_cast<uint8_t>(v >> 8);
         };
         if (type == ZLM_GGML_Q4_0 || type == ZLM_GGML_Q8_0) put(0, h005);
-        if (type == ZLM_GGML_Q4_K) {
+        if (type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K) {
             put(0, h005);
             put(2, h002);
         }
@@ -1595,7 +1714,37 @@ extern "C" void zlm_gpu_probe(zlm_device* d, size_t rows_in, size_t k_in, size_t
     }
     probe_resident_variants(d, ZLM_GGML_Q8_0, rows, k, x.data(), y.data(), rates);
     out->q8_0_variant = fastest(rates);
+    probe_resident_variants(d, ZLM_GGML_Q4_1, rows, k, x.data(), y.data(), rates);
+    out->q4_1_variant = fastest(rates);
+    probe_gate_up(d, ZLM_GGML_Q4_1, rows, k, x.data(), y.data(), rates);
+    out->gate_up_q4_1_variant = fastest(rates);
+    probe_resident_variants(d, ZLM_GGML_F32, rows, k, x.data(), y.data(), rates);
+    out->f32_variant = fastest(rates);
+    probe_resident_variants(d, ZLM_GGML_F16, rows, k, x.data(), y.data(), rates);
+    out->f16_variant = fastest(rates);
+    probe_resident_variants(d, ZLM_GGML_BF16, rows, k, x.data(), y.data(), rates);
+    out->bf16_variant = fastest(rates);
     zlm_gpu_sync(d);
+}
+
+extern "C" bool zlm_gpu_probe_rates(zlm_device* d, uint32_t ggml_type, bool gate_up, size_t rows_in, size_t k_in,
+                                    double* rates) {
+    if (!rates) return false;
+    for (int v = 0; v < 8; v++) rates[v] = 0.0;
+    if (!d || !d->avail) return false;
+    const QuantInfo* qi = quant_info(ggml_type);
+    if (!qi || variant_of(ggml_type) != 0) return fail(d, "unsupported quant %u", ggml_type);
+    const size_t rows = std::min(rows_in, kProbeMaxRows);
+    size_t k = std::min(k_in, kProbeMaxK);
+    k -= k % std::max<size_t>(32, qi->block_elems);
+    if (rows == 0 || k == 0) return fail(d, "probe shape out of range");
+    std::vector<float> x(k), y(rows);
+    for (size_t i = 0; i < k; i++) x[i] = static_cast<float>(static_cast<int>((i * 7 + 3) % 17) - 8) * 0.125f;
+    if (gate_up) probe_gate_up(d, qi->type, rows, k, x.data(), y.data(), rates);
+    else probe_resident_variants(d, qi->type, rows, k, x.data(), y.data(), rates);
+    for (int v = 0; v < 8; v++)
+        if (!(rates[v] > 0.0)) return fail(d, "variant %d of quant %u was not measured", v, qi->type);
+    return true;
 }
 
 // ======================= device-level entry points =======================
@@ -1770,6 +1919,68 @@ extern "C" bool zlm_gpu_time_gemv_sequence(zlm_device* d, const zlm_gemv_desc* d
     hipEventDestroy(e1);
     *ms = t;
     return good;
+}
+
+// ---- the contract path as zlm's executor drives it (timing) ----
+
+extern "C" bool zlm_gpu_time_contract_gemv(zlm_device* d, zlm_resident* const* res, size_t n_res, uint32_t quant,
+                                           size_t rows, size_t k, int iters, double* us) {
+    if (!d || !d->avail || !res || n_res == 0 || iters < 1 || !us) return false;
+    std::vector<float> x(k), y(rows);
+    for (size_t i = 0; i < k; i++) x[i] = static_cast<float>(static_cast<int>((i * 7 + 3) % 17) - 8) * 0.125f;
+    for (size_t i = 0; i < n_res; i++)  // layouts converted outside the timed region
+        if (!zlm_gpu_mat_vec_resident(d, res[i], quant, rows, k, x.data(), k, y.data(), rows)) return false;
+    const double t0 = now_ns();
+    for (int it = 0; it < iters; it++) {
+        const int32_t h =
+            zlm_gpu_mat_vec_resident_burst_async(d, res[it % n_res], quant, rows, k, x.data(), k, true);
+        if (h == ZLM_NULL_HANDLE || !zlm_gpu_wait_resident(d, h, y.data(), rows, rows)) return false;
+    }
+    *us = (now_ns() - t0) / 1e3 / iters;
+    return true;
+}
+
+extern "C" bool zlm_gpu_time_contract_decode(zlm_device* d, const zlm_contract_layer* layers, size_t n_layers,
+                                             uint32_t quant, size_t hidden, size_t q_rows, size_t kv_rows,
+                                             size_t ffn, zlm_resident* lm_head, uint32_t lm_quant, size_t vocab,
+                                             int iters, double* ms) {
+    if (!d || !d->avail || !layers || n_layers == 0 || !lm_head || iters < 1 || !ms) return false;
+    std::vector<float> x(hidden), qo(q_rows), ko(kv_rows), vo(kv_rows), ho(hidden), mo(hidden), logits(vocab);
+    for (size_t i = 0; i < hidden; i++) x[i] = static_cast<float>(static_cast<int>((i * 7 + 3) % 17) - 8) * 0.125f;
+    for (size_t i = 0; i < q_rows; i++) qo[i] = x[i % hidden];
+    auto step = [&]() -> bool {
+        for (size_t l = 0; l < n_layers; l++) {
+            const zlm_contract_layer& L = layers[l];
+            // q, k, v share the normed hidden state: one burst, then the drain
+            const int32_t hq = zlm_gpu_mat_vec_resident_burst_async(d, L.q, quant, q_rows, hidden, x.data(), hidden,
+                                                                    true);
+            const int32_t hk = zlm_gpu_mat_vec_resident_burst_async(d, L.k, quant, kv_rows, hidden, x.data(),
+                                                                    hidden, false);
+            const int32_t hv = zlm_gpu_mat_vec_resident_burst_async(d, L.v, quant, kv_rows, hidden, x.data(),
+                                                                    hidden, false);
+            if (hq == ZLM_NULL_HANDLE || hk == ZLM_NULL_HANDLE || hv == ZLM_NULL_HANDLE) return false;
+            if (!zlm_gpu_wait_resident(d, hq, qo.data(), q_rows, q_rows) ||
+                !zlm_gpu_wait_resident(d, hk, ko.data(), kv_rows, kv_rows) ||
+                !zlm_gpu_wait_resident(d, hv, vo.data(), kv_rows, kv_rows))
+                return false;
+            // (the CPU's attention would run here; its output stands in as q's rows)
+            const int32_t ho_h = zlm_gpu_mat_vec_resident_burst_async(d, L.o, quant, hidden, q_rows, qo.data(),
+                                                                      q_rows, true);
+            if (ho_h == ZLM_NULL_HANDLE || !zlm_gpu_wait_resident(d, ho_h, ho.data(), hidden, hidden)) return false;
+            // (residual add and the FFN RMSNorm on the CPU) then the fused MLP pair
+            const int32_t hm = zlm_gpu_mat_vec_mlp_pair_resident_burst_async(
+                d, L.gate, L.up, L.down, quant, quant, hidden, hidden, ffn, x.data(), hidden, ZLM_ACT_SILU,
+                ZLM_VARIANT_PLAIN, true);
+            if (hm == ZLM_NULL_HANDLE || !zlm_gpu_wait_resident(d, hm, mo.data(), hidden, hidden)) return false;
+        }
+        return zlm_gpu_mat_vec_resident(d, lm_head, lm_quant, vocab, hidden, x.data(), hidden, logits.data(), vocab);
+    };
+    if (!step()) return false;  // layouts converted outside the timed region
+    const double t0 = now_ns();
+    for (int it = 0; it < iters; it++)
+        if (!step()) return false;
+    *ms = (now_ns() - t0) / 1e6 / iters;
+    return true;
 }
 
 extern "C" bool zlm_gpu_gemv_op_enqueue(zlm_device* d, const zlm_gemv_op* op) {

@@ -42,6 +42,11 @@ SILU, GELU = 0, 1
 FORM_PLAIN, FORM_PAIR, FORM_NORM, FORM_NORMPAIR, FORM_RESID = range(5)
 
 
+def layout_bytes(quant_code: int, rows: int, k: int, with_gemm: bool) -> int:
+    """HBM of a rows x k weight once converted (+ its GEMM tiled copy); no GPU needed."""
+    return int(lib().zlm_gpu_layout_bytes(quant_code, rows, k, with_gemm))
+
+
 def quant(ggml_type: int, variant: int = PLAIN) -> int:
     """The C ABI's quant code: GGML type in bits 0..7, GpuVariant in 8..15."""
     return (ggml_type & 0xFF) | ((variant & 0xFF) << 8)
@@ -174,6 +179,12 @@ def lib() -> ctypes.CDLL:
                                                  ctypes.c_float, P]),
         "zlm_gpu_attention_decode_enqueue_noalloc": (B, [P, P, P, P, U, U, U, ctypes.c_float, ctypes.c_float, P, P,
                                                          P, U, ctypes.c_float, P]),
+        "zlm_gpu_resident_device_bytes": (ctypes.c_uint64, [P]),
+        "zlm_gpu_layout_bytes": (ctypes.c_uint64, [U, S, S, ctypes.c_bool]),
+        "zlm_gpu_release_gemm_tiles": (B, [P, P]),
+        "zlm_gpu_probe_rates": (B, [P, U, ctypes.c_bool, S, S, P]),
+        "zlm_gpu_time_contract_gemv": (B, [P, P, S, U, S, S, ctypes.c_int, P]),
+        "zlm_gpu_time_contract_decode": (B, [P, P, S, U, S, S, S, S, P, U, S, ctypes.c_int, P]),
         "zlm_gpu_capture_begin": (B, [P]),
         "zlm_gpu_capture_end": (P, [P]),
         "zlm_gpu_graph_launch": (B, [P, P, ctypes.c_int, P]),
@@ -495,6 +506,41 @@ class Device:
         return bool(self._L.zlm_gpu_attention_decode_enqueue_noalloc(self._h, qkv, q_norm_w, k_norm_w, n_heads,
                                                                      n_kv_heads, head_dim, eps, freq_base, pos,
                                                                      k_cache, v_cache, max_seq, scale, out))
+
+    def probe_rates(self, ggml_type: int, gate_up: bool, rows: int, k: int) -> Optional[np.ndarray]:
+        """GB/s of each GpuVariant for one quant (resident GEMV or fused gate_up); None if one did not run."""
+        r = np.zeros(8, np.float64)
+        if not self._L.zlm_gpu_probe_rates(self._h, ggml_type, gate_up, rows, k, _p(r)):
+            return None
+        return r
+
+    def time_contract_gemv(self, residents: Sequence[Resident], quant: int, rows: int, k: int, iters: int) -> float:
+        """Host-wall us per contract GEMV (burst of one + waitResident, host x and y)."""
+        arr = (ctypes.c_void_p * len(residents))(*[r.ptr for r in residents])
+        us = ctypes.c_double(0.0)
+        if not self._L.zlm_gpu_time_contract_gemv(self._h, arr, len(residents), quant, rows, k, iters,
+                                                  ctypes.addressof(us)):
+            raise RuntimeError(self.last_error())
+        return us.value
+
+    def time_contract_decode(self, layers: Sequence[Sequence[Resident]], quant: int, hidden: int, q_rows: int,
+                             kv_rows: int, ffn: int, lm_head: Resident, lm_quant: int, vocab: int, iters: int) -> float:
+        """Host-wall ms per token of the projections driven through the contract ops
+        (layers[i] = (q, k, v, o, gate, up, down) residents)."""
+        Arr = ctypes.c_void_p * (7 * len(layers))
+        arr = Arr(*[r.ptr for layer in layers for r in layer])
+        ms = ctypes.c_double(0.0)
+        if not self._L.zlm_gpu_time_contract_decode(self._h, arr, len(layers), quant, hidden, q_rows, kv_rows, ffn,
+                                                    lm_head.ptr, lm_quant, vocab, iters, ctypes.addressof(ms)):
+            raise RuntimeError(self.last_error())
+        return ms.value
+
+    def resident_device_bytes(self, res: Resident) -> int:
+        """HBM the resident holds now (raw bytes, device layout, GEMM tiles)."""
+        return int(self._L.zlm_gpu_resident_device_bytes(res.ptr))
+
+    def release_gemm_tiles(self, res: Resident) -> bool:
+        return bool(self._L.zlm_gpu_release_gemm_tiles(self._h, res.ptr))
 
     def capture_begin(self) -> bool:
         return bool(self._L.zlm_gpu_capture_begin(self._h))
