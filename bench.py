@@ -212,6 +212,8 @@ def main():
                     help="run N eager decode steps instead of timing graph replays (for kernel-trace profiling)")
     ap.add_argument("--decode-replays", type=int, default=30, metavar="N",
                     help="graph replays per timed decode run (warm-up run + 3 timed runs of N)")
+    ap.add_argument("--no-small-m", action="store_true",
+                    help="skip the small-token-count matMul sweep (its GEMVs share kernels with configs[0]/[3])")
     ap.add_argument("--counters", action="store_true",
                     help="short warm-ups and few launches per shape, for rocprofv3 --pmc passes (not a timing run)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
@@ -366,7 +368,7 @@ def main():
         dev.dev_free(o_dev)
 
     # ---- small token counts (verify / microbatch), as reference gpu/root_test.zig:651-696 ----
-    if not args.quick:
+    if not args.quick and not args.no_small_m:
         sweep = {}
         for sname, qt, rows, k in (("q4_0_4096x4096", synth.Q4_0, 4096, 4096),
                                    ("q4_k_4096x4096", synth.Q4_K, 4096, 4096),
