@@ -94,18 +94,26 @@ def test_attention_matches_oracle(dev, nh, nkv, L):
         dev.dev_free(p)
 
 
-@pytest.mark.parametrize("nh,nkv,pos", [(32, 8, 0), (32, 8, 63), (32, 8, 64), (32, 8, 700), (32, 8, 2047),
-                                        (8, 4, 129), (16, 16, 5)])
-def test_fused_attention_decode_matches_oracle(dev, nh, nkv, pos):
+FUSED_CASES = [(32, 8, 0, 2048), (32, 8, 63, 2048), (32, 8, 64, 2048), (32, 8, 700, 2048), (32, 8, 2047, 2048),
+               (8, 4, 129, 2048), (16, 16, 5, 2048),
+               # 94 splits: the merge takes two passes of 64 splits, the
+               # later positions holding the larger scores
+               (32, 8, 5999, 6000), (8, 2, 4100, 6000)]
+
+
+@pytest.mark.parametrize("nh,nkv,pos,max_seq", FUSED_CASES)
+def test_fused_attention_decode_matches_oracle(dev, nh, nkv, pos, max_seq):
     """q/k head norm + RoPE, K/V append at pos and attention in one launch, then the merge."""
-    hd, max_seq, eps, base = 128, 2048, 1e-6, 1e6
-    _say(f"attention_decode nh={nh} nkv={nkv} pos={pos}")
+    hd, eps, base = 128, 1e-6, 1e6
+    _say(f"attention_decode nh={nh} nkv={nkv} pos={pos} max_seq={max_seq}")
     rng = np.random.default_rng(pos + nh)
     qkv = (rng.standard_normal((nh + 2 * nkv) * hd) * 2).astype(np.float32)
     qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
     kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
     kc0 = rng.standard_normal((nkv, max_seq, hd)).astype(np.float16)
     vc0 = rng.standard_normal((nkv, max_seq, hd)).astype(np.float16)
+    if max_seq > 2048:
+        kc0[:, 2048:] *= np.float16(1.5)
     scale = 1.0 / math.sqrt(hd)
     d_qkv, d_qn, d_kn, d_kc, d_vc = (_vec(dev, a) for a in (qkv, qn, kn, kc0, vc0))
     d_pos = _vec(dev, np.array([pos, 0, 0, 0], np.int32))
@@ -114,7 +122,7 @@ def test_fused_attention_decode_matches_oracle(dev, nh, nkv, pos):
     kref, vref = kc0.copy(), vc0.copy()
     od.write_kv(k, v, kref, vref, pos)
     want = od.attend(q, kref, vref, nh, pos, scale)
-    for rep in range(2):  # a second call over the appended caches gives the same result
+    for rep in range(3):  # later calls over the appended caches give the same result
         assert dev.attention_decode_enqueue(d_qkv, d_qn, d_kn, nh, nkv, hd, eps, base, d_pos, d_kc, d_vc, max_seq,
                                             scale, d_out), dev.last_error()
         out = np.zeros(nh * hd, np.float32)

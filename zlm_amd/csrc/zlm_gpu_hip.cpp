@@ -741,7 +741,9 @@ const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k,
     for (const PfSuffix& v : kPfSuffixes) {
         if (rows < v.min_rows) continue;
         snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d%s", qn, kFormNames[form], steps, v.suffix);
-        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, v.waves_per_cu, true, false, v.xq)) return g;
+        // the suffix's rows per tile, times the gate and up rows of a pair form
+        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, v.rt * rt, steps, v.waves_per_cu, true, false, v.xq))
+            return g;
     }
     snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_s%d", qn, kFormNames[form], steps);
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps)) return g;
