@@ -286,6 +286,16 @@ def main():
         "c1_gate_up_q8_0_12288x4096": {"us": round(ms_gu * 1e3, 3), "GBps": round(gu_gbps, 1)},
         "c1_down_q8_0_4096x12288": {"us": round(ms_dn * 1e3, 3), "GBps": round(dn_gbps, 1)},
     }
+    # gate and up over the same x as one matVecResidentBatch launch
+    pair = []
+    for c in range(copies):
+        pair += [gate.desc(c)[:4] + (gate.x_dev, gate.y_dev, 1), up.desc(c)[:4] + (gate.x_dev, up.y_dev, 0)]
+    ms_pair = time_launches(dev, pair, 4 * len(pair) * 25) / len(pair)
+    extra["c1_gate_up_batched"] = {
+        "us_per_gemv": round(ms_pair * 1e3, 3), "GBps": round(gate.algo_bytes / (ms_pair * 1e-3) / 1e9, 1),
+        "note": "gate and up over one x as one matVecResidentBatch launch (the batch kernel, both ops' rows)"}
+    log(f"gate + up as one batch launch: {ms_pair * 1e3:.2f} us per GEMV "
+        f"({extra['c1_gate_up_batched']['GBps']} GB/s)")
 
     # the same GEMVs through the contract ops zlm's executor calls: a burst of
     # one (host x staged) + waitResident (host y read back), host wall time
@@ -333,6 +343,17 @@ def main():
             extra[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1),
                            "copies": g.copies}
             log(f"{name}: {ms * 1e3:.2f} us, {gbps:.1f} GB/s ({100 * gbps / PEAK_GBPS:.1f}%)")
+            if name.startswith("c0_"):
+                # n GEMVs of this shape over one x in one matVecResidentBatch launch
+                batched = {}
+                for nb in (2, 4, 8):
+                    bd = [g.desc(c)[:6] + (1 if c % nb != nb - 1 else 0,) for c in range(g.copies - g.copies % nb)]
+                    msb = time_launches(dev, bd, max(len(bd), 400)) / len(bd)
+                    batched[f"x{nb}"] = {"us_per_gemv": round(msb * 1e3, 3),
+                                         "GBps": round(g.algo_bytes / (msb * 1e-3) / 1e9, 1)}
+                extra[name]["batched"] = batched
+                log(f"{name} batched: " + ", ".join(f"{key} {v['us_per_gemv']} us/GEMV ({v['GBps']} GB/s)"
+                                                    for key, v in batched.items()))
             g.free()
 
     # ---- prefill GEMM, Q4_0 12288x4096 x 512 tokens, int8 MFMA ---------

@@ -1135,6 +1135,33 @@ __device__ __forceinline__ void gemv_multi(const GemvMultiArgs& a) {
     load_group<QT, 1, STEPS, EXACT, true>(f, tr, a.nb, C, 0, lane);
     xstore<KCAP>(xr, k, xl, xs);
     float acc[1];
+    if constexpr (EXACT) {
+        // The wave's next row is loaded while the current one is computed
+        // (two fragment sets). Every lane stores the row's sum, so no branch
+        // guards the store (a guarded store makes the wait before the next
+        // compute include the prefetched loads); a prefetch past the end is
+        // clamped to the last row and never computed.
+        Frag<QT, 1> g[STEPS];
+        uint32_t op1;
+        TileRows<1> tr1;
+        uint32_t t = tile;
+        while (t < ntiles) {
+            const uint32_t t1 = t + tstride;
+            tr1 = multi_row(a, min(t1, ntiles - 1), op1);
+            load_group<QT, 1, STEPS, true, true>(g, tr1, a.nb, C, 0, lane);
+            acc[0] = 0.0f;
+            compute_group<QT, 1, STEPS, true, true>(f, xl, xs, C, 0, lane, acc);
+            a.y[op][tr.r[0]] = wave_sum_all(acc[0]);
+            if (t1 >= ntiles) break;
+            t = t1 + tstride;
+            tr = multi_row(a, min(t, ntiles - 1), op);
+            load_group<QT, 1, STEPS, true, true>(f, tr, a.nb, C, 0, lane);
+            acc[0] = 0.0f;
+            compute_group<QT, 1, STEPS, true, true>(g, xl, xs, C, 0, lane, acc);
+            a.y[op1][tr1.r[0]] = wave_sum_all(acc[0]);
+        }
+        return;
+    }
     for (;;) {
         acc[0] = 0.0f;
         compute_group<QT, 1, STEPS, EXACT>(f, xl, xs, C, 0, lane, acc);
