@@ -55,6 +55,11 @@ def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     assert dev.mat_mul_batch(zd.quant(zq), w, rows, k, m, x, out), dev.last_error()
     got = out.reshape(m, rows)
     assert rel_l2(got, want) <= 1e-3
+    if m > GEMV_M:
+        # the block dots are exact integers, so only the fp32 scaling and
+        # summation order may differ (~1e-7); one quantized activation off by
+        # one unit moves its token's outputs by ~1e-4
+        assert rel_l2(got, want) <= 1e-5
     res = dev.upload_resident(w)
     out2 = np.zeros(m * rows, np.float32)
     assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, out2), dev.last_error()

@@ -1008,7 +1008,7 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     uint32_t rows32 = static_cast<uint32_t>(rows), m32 = static_cast<uint32_t>(m), nb32 = static_cast<uint32_t>(nb),
              mt32 = static_cast<uint32_t>(mt);
     {
-        const uint64_t n = mt * 32 * nb;
+        const uint64_t n = mt * 32 * nb * 8;  // eight threads per (token, block)
         void* args[] = {const_cast<float**>(&x_dev), &qx, &dx, &m32, &nb32, &mt32, &ds};
         if (!launch(d, d->quantize_q8_tiled, static_cast<unsigned>((n + 255) / 256), 256, args, "quantize tiled"))
             return false;

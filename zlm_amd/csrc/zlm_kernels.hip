@@ -265,25 +265,57 @@ extern "C" __global__ void __launch_bounds__(256)
 // The prefill GEMM's tiled output for m tokens of nb blocks, tokens padded to
 // mt*32: qx [mt][nb][32 tokens][32 B], dx [mt][nb][32 tokens] and, when `ds`
 // is not null, ds = dx * f32(sum of the block's q) in the same order (the
-// min-term factor of q4_1 / q4_k); padding tokens are zeros.  One thread per
-// (token, block), numbered in output order (thread i writes slot i), so a
-// wave's qx / dx / ds stores are contiguous (32 consecutive threads are the
-// 32 tokens of one token tile and block): 6.8 -> 6.2 us at 512 x 4096.
+// min-term factor of q4_1 / q4_k); padding tokens are zeros.  Eight threads
+// per (token, block) slot, numbered in output order (slot i is threads 8i ..
+// 8i+7), each loading one float4 of the block and writing its 4 quantized
+// bytes: a wave reads 8 blocks as 128-byte runs and writes 256 contiguous
+// bytes of qx; the block's amax and sum meet across the 8 lanes (max and
+// integer sum: the same values in any order), so every output is bit for bit
+// the one-thread-per-block quantizer's.  At 512 x 4096: 6.3 -> 5.5 us (one
+// thread per slot before; numbering the threads in input order instead, so a
+// wave reads 1 KiB of one token's row, measured 5.9 us).
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1, kWave));
+    v = fmaxf(v, __shfl_xor(v, 2, kWave));
+    return fmaxf(v, __shfl_xor(v, 4, kWave));
+}
+__device__ __forceinline__ int32_t sum8(int32_t v) {
+    v += __shfl_xor(v, 1, kWave);
+    v += __shfl_xor(v, 2, kWave);
+    return v + __shfl_xor(v, 4, kWave);
+}
 extern "C" __global__ void __launch_bounds__(256)
     zlm_quantize_q8_tiled(const float* __restrict__ x, int8_t* __restrict__ qx, float* __restrict__ dx,
                           uint32_t m, uint32_t nb, uint32_t mt, float* __restrict__ ds) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (i >= static_cast<uint64_t>(mt) * 32 * nb) return;
-    const uint64_t tb = i / 32;  // token tile * nb + block
+    const uint64_t nslot = static_cast<uint64_t>(mt) * 32 * nb;
+    const uint64_t slot = min(i / 8, nslot - 1);  // whole waves stay in the shuffles
+    const uint32_t part = static_cast<uint32_t>(i % 8);
+    const uint64_t tb = slot / 32;  // token tile * nb + block
     const uint32_t b = static_cast<uint32_t>(tb % nb);
-    const uint32_t t = static_cast<uint32_t>(tb / nb) * 32 + static_cast<uint32_t>(i % 32);
-    const uint64_t slot = i;
-    float d;
-    int32_t sum;
-    quantize_block(t < m ? x + (static_cast<uint64_t>(t) * nb + b) * 32 : nullptr,
-                   reinterpret_cast<uint4*>(qx + slot * 32), &d, &sum);
-    dx[slot] = d;
-    if (ds) ds[slot] = d * static_cast<float>(sum);
+    const uint32_t t = static_cast<uint32_t>(tb / nb) * 32 + static_cast<uint32_t>(slot % 32);
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (t < m) v = reinterpret_cast<const float4*>(x + (static_cast<uint64_t>(t) * nb + b) * 32)[part];
+    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    const float d = __fdiv_rn(amax, 127.0f);
+    const float inv = (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    int32_t s = 0;
+    uint32_t wv = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int32_t q = static_cast<int32_t>(roundf(e[j] * inv));
+        q = q > 127 ? 127 : (q < -127 ? -127 : q);
+        s += q;
+        wv |= (static_cast<uint32_t>(q) & 0xffu) << (8 * j);
+    }
+    s = sum8(s);
+    if (i / 8 >= nslot) return;
+    reinterpret_cast<uint32_t*>(qx + slot * 32)[part] = wv;
+    if (part == 0) {
+        dx[slot] = d;
+        if (ds) ds[slot] = d * static_cast<float>(s);
+    }
 }
 
 // The prefill GEMM's tiled weight layout, rows padded to rt*32: payload
