@@ -23,13 +23,16 @@ def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
 def rope_half(head: np.ndarray, pos: int, freq_base: float) -> np.ndarray:
     """Rotate-half RoPE (rope.zig:4-33; frequencies as RopeTable, :46-104):
     inv_i = base^(-2i/hd), angle = pos*inv_i, (x_i, x_{i+hd/2}) ->
-    (x_i c - x_{i+hd/2} s, x_i s + x_{i+hd/2} c).  Computed in float64."""
+    (x_i c - x_{i+hd/2} s, x_i s + x_{i+hd/2} c).  The angle is formed as the
+    reference forms it, in f32 (RopeTable.init's f32 pow, RopeTable.ensure's
+    f32 product t * inv_freq[i]): at position 32767 that differs from the exact
+    angle by up to ~2e-3 rad.  Its cos / sin and the rotation are float64."""
     head = np.asarray(head, np.float64)
     hd = head.size
     half = hd // 2
-    i = np.arange(half, dtype=np.float64)
-    inv = np.power(np.float64(np.float32(freq_base)), -2.0 * i / hd)
-    ang = float(pos) * inv
+    fi = np.arange(half, dtype=np.float32)
+    inv = np.power(np.float32(freq_base), np.float32(-2.0) * fi / np.float32(hd)).astype(np.float32)
+    ang = (np.float32(pos) * inv).astype(np.float32).astype(np.float64)
     c, s = np.cos(ang), np.sin(ang)
     x0, x1 = head[:half], head[half:]
     return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c])

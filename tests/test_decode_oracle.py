@@ -21,13 +21,35 @@ def test_rope_is_a_rotation_that_composes():
     # each pair keeps its length, and rotating by p then q is rotating by p+q
     half = 64
     np.testing.assert_allclose(np.hypot(a[:half], a[half:]), np.hypot(x[:half], x[half:]), rtol=1e-12)
-    np.testing.assert_allclose(od.rope_half(od.rope_half(x, 5, 1e6), 7, 1e6), od.rope_half(x, 12, 1e6), atol=1e-9)
+    # (angles are f32 products, so composing positions holds to f32 rounding)
+    np.testing.assert_allclose(od.rope_half(od.rope_half(x, 5, 1e6), 7, 1e6), od.rope_half(x, 12, 1e6), atol=2e-6)
     # the frequencies: pair i turns by pos * base^(-2i/hd)
     e = np.zeros(128)
     e[3] = 1.0
     r = od.rope_half(e, 10, 1e4)
     ang = 10 * 1e4 ** (-2 * 3 / 128)
-    assert abs(r[3] - math.cos(ang)) < 1e-9 and abs(r[3 + half] - math.sin(ang)) < 1e-9
+    assert abs(r[3] - math.cos(ang)) < 1e-6 and abs(r[3 + half] - math.sin(ang)) < 1e-6
+
+
+def test_rope_angle_is_the_f32_product_at_long_positions():
+    # RopeTable (rope.zig:46-104) stores inv_freq as f32 and forms t * inv_freq
+    # in f32; at position 32767 that angle is far (up to ~2e-3 rad) from the
+    # exact one, and the oracle must rotate by the f32 angle
+    half, pos = 64, 32767
+    for i in (0, 1, 7, 40):
+        e = np.zeros(2 * half)
+        e[i] = 1.0
+        r = od.rope_half(e, pos, 1e6)
+        got = math.atan2(r[i + half], r[i])
+        inv32 = np.float32(np.power(np.float32(1e6), np.float32(-2.0 * i / (2 * half))))
+        want = float(np.float32(np.float32(pos) * inv32))
+        exact = pos * 1e6 ** (-2.0 * i / (2 * half))
+        d = (got - want + math.pi) % (2 * math.pi) - math.pi
+        assert abs(d) < 1e-9, (i, d)
+        if i == 0:  # pos * 1 is exact in f32 ...
+            assert want == exact
+        if i == 1:  # ... but pos * base^(-1/64) is not
+            assert abs(want - exact) > 1e-5
 
 
 def test_rms_norm_closed_form():

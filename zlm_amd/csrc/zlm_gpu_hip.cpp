@@ -184,6 +184,7 @@ struct zlm_device {
     hipFunction_t qk_norm_rope_kv = nullptr;
     hipFunction_t attn_partial = nullptr;
     hipFunction_t attn_combine = nullptr;
+    hipFunction_t attn_combine_wide = nullptr;
     hipFunction_t attn_decode = nullptr;
     hipFunction_t synth_blocks = nullptr;
     hipFunction_t synth_f16 = nullptr;
@@ -315,6 +316,7 @@ bool load_kernels(zlm_device* d) {
                 {&d->qk_norm_rope_kv, "zlm_qk_norm_rope_kv"},
                 {&d->attn_partial, "zlm_attn_partial"},
                 {&d->attn_combine, "zlm_attn_combine"},
+                {&d->attn_combine_wide, "zlm_attn_combine_wide"},
                 {&d->attn_decode, "zlm_attn_decode"},
                 {&d->synth_blocks, "zlm_synth_blocks"},
                 {&d->synth_f16, "zlm_synth_f16"}};
@@ -2032,6 +2034,18 @@ bool ensure_attn_scratch(zlm_device* d, size_t need) {
 
 namespace {
 
+// The split merge: one 256-thread workgroup per q head up to 64 splits
+// (4096 positions), beyond that the wide merge with one wave per 32 splits
+// (at most 16 waves).
+bool enqueue_attn_merge(zlm_device* d, float* part, uint32_t nsplit, uint32_t n_heads, float* out) {
+    void* args[] = {&part, &nsplit, &out};
+    if (nsplit > 64) {
+        const unsigned waves = std::min<unsigned>(16u, (nsplit + 31) / 32);
+        return launch(d, d->attn_combine_wide, n_heads, 64 * waves, args, "attention combine");
+    }
+    return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
+}
+
 bool check_attn_decode(zlm_device* d, const float* qkv, const float* q_norm_w, const float* k_norm_w,
                        uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, const int32_t* pos,
                        const uint16_t* k_cache, const uint16_t* v_cache, uint32_t max_seq, const float* out) {
@@ -2056,8 +2070,7 @@ bool enqueue_attn_decode(zlm_device* d, const float* qkv, const float* q_norm_w,
                 "attention decode"))
             return false;
     }
-    void* args[] = {&part, &nsplit, &out};
-    return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
+    return enqueue_attn_merge(d, part, nsplit, n_heads, out);
 }
 
 }  // namespace
@@ -2116,8 +2129,7 @@ extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const u
                 "attention"))
             return false;
     }
-    void* args[] = {&part, &nsplit, &out};
-    return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
+    return enqueue_attn_merge(d, part, nsplit, n_heads, out);
 }
 
 struct zlm_graph {
