@@ -212,6 +212,8 @@ def main():
                     help="run N eager decode steps instead of timing graph replays (for kernel-trace profiling)")
     ap.add_argument("--decode-replays", type=int, default=30, metavar="N",
                     help="graph replays per timed decode run (warm-up run + 3 timed runs of N)")
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip the decode step at 8192 and 32768 cached positions")
     ap.add_argument("--no-small-m", action="store_true",
                     help="skip the small-token-count matMul sweep (its GEMVs share kernels with configs[0]/[3])")
     ap.add_argument("--counters", action="store_true",
@@ -464,6 +466,28 @@ def main():
         log(f"c2 decode: {ms:.3f} ms/token = {1e3 / ms:.1f} tok/s, {gbps:.1f} GB/s ({100 * gbps / PEAK_GBPS:.1f}%)")
         dev.graph_destroy(graph)
         model.free()
+        # the same step at longer caches (the last position of each): attention's
+        # share grows with the KV bytes
+        if not args.no_long_context:
+            import dataclasses
+
+            longer = {}
+            for ctx in (8192, 32768):
+                lcfg = dataclasses.replace(cfg, max_seq=ctx)
+                lmodel = zdec.DecodeModel(dev, lcfg)
+                lmodel.step(x, ctx - 1)
+                lgraph = lmodel.capture()
+                lmodel.set_input(x, ctx - 1)
+                dev.graph_launch(lgraph, reps)
+                lms = sorted(dev.graph_launch(lgraph, reps) / reps for _ in range(3))[1]
+                lbytes = zdec.weight_bytes(lcfg) + zdec.kv_bytes(lcfg, ctx)
+                longer[str(ctx)] = {"tok_per_s": round(1e3 / lms, 1), "ms_per_token": round(lms, 4),
+                                    "bytes_per_token": lbytes, "GBps": round(lbytes / (lms * 1e-3) / 1e9, 1)}
+                log(f"c2 decode at context {ctx}: {lms:.3f} ms/token = {1e3 / lms:.1f} tok/s, "
+                    f"{longer[str(ctx)]['GBps']} GB/s")
+                dev.graph_destroy(lgraph)
+                lmodel.free()
+            extra["c2_decode_qwen3_8b_q4_0"]["longer_contexts"] = longer
         # the same token's projections through the contract ops only, as zlm's
         # executor submits them (separate q/k/v residents, bursts and drains,
         # host activations); the CPU glue between them is not run
