@@ -2035,13 +2035,15 @@ bool ensure_attn_scratch(zlm_device* d, size_t need) {
 namespace {
 
 // The split merge: one 256-thread workgroup per q head up to 64 splits
-// (4096 positions), beyond that the wide merge with one wave per 32 splits
-// (at most 16 waves).
+// (4096 positions), beyond that the wide merge: two workgroups per head (64
+// dims each) of one wave per 32 splits (at most 16 waves).
 bool enqueue_attn_merge(zlm_device* d, float* part, uint32_t nsplit, uint32_t n_heads, float* out) {
     void* args[] = {&part, &nsplit, &out};
     if (nsplit > 64) {
         const unsigned waves = std::min<unsigned>(16u, (nsplit + 31) / 32);
-        return launch(d, d->attn_combine_wide, n_heads, 64 * waves, args, "attention combine");
+        return ok(d, hipModuleLaunchKernel(d->attn_combine_wide, n_heads, 2, 1, 64 * waves, 1, 1, 0, d->stream, args,
+                                           nullptr),
+                  "attention combine");
     }
     return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
 }

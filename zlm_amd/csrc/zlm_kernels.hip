@@ -1199,68 +1199,62 @@ extern "C" __global__ void __launch_bounds__(256)
 }
 
 // The merge for many splits (long caches: nsplit > 64, i.e. more than 4096
-// positions).  One workgroup of nw = min(16, ceil(nsplit / 32)) waves per q
-// head; wave w takes splits [w*S, (w+1)*S), S = ceil(nsplit / nw), in chunks
-// of 32 whose loads are all issued before their first use (lane j holds split
-// j's m and l; every lane the chunk's 32 accumulator pairs of its dims 2l,
-// 2l+1), keeping a running maximum and rescaling its sums when a chunk raises
-// it; the waves' (M, den, acc) then merge in LDS, in wave order.  One memory
-// round trip per chunk instead of one per 64 splits in sequence.
+// positions).  Two workgroups per q head (grid.y picks dims [64y, 64y+64),
+// lane l dim 64y + l), each of nw = min(16, ceil(nsplit / 32)) waves; wave w
+// takes splits [w*S, (w+1)*S), S = ceil(nsplit / nw), in chunks of 32 whose
+// loads are all issued before their first use (lane j holds split j's m and
+// l; every lane the chunk's 32 accumulator values of its dim), keeping a
+// running maximum and rescaling its sums when a chunk raises it; the waves'
+// (M, den, acc) then merge in LDS, in wave order.  One memory round trip per
+// chunk instead of one per 64 splits in sequence, and each workgroup reads
+// half of a head's partials.
 extern "C" __global__ void __launch_bounds__(1024)
     zlm_attn_combine_wide(const float* __restrict__ part, uint32_t nsplit, float* __restrict__ out) {
     constexpr uint32_t W = 16, B = 32;
-    __shared__ float rm[W], rd[W];
-    __shared__ float2 ra[W][kWave];
+    __shared__ float rm[W], rd[W], ra[W][kWave];
     const uint32_t qh = blockIdx.x, tid = threadIdx.x, wid = tid / kWave, lane = tid & (kWave - 1);
+    const uint32_t dim = kWave * blockIdx.y + lane;
     const uint32_t nw = blockDim.x / kWave;  // <= W
     const float* base = part + static_cast<size_t>(qh) * nsplit * kAttnPart;
     const uint32_t S = (nsplit + nw - 1) / nw;
     const uint32_t s_begin = min(wid * S, nsplit), s_end = min(s_begin + S, nsplit);
-    float M = -INFINITY, den = 0.0f, a0 = 0.0f, a1 = 0.0f;
+    float M = -INFINITY, den = 0.0f, acc_d = 0.0f;
     for (uint32_t s0 = s_begin; s0 < s_end; s0 += B) {
         const uint32_t n = min(B, s_end - s0);
         const uint32_t sl = s0 + min(lane, n - 1);
         const float ms_raw = base[static_cast<size_t>(sl) * kAttnPart + kAttnHd];
         const float ls_raw = base[static_cast<size_t>(sl) * kAttnPart + kAttnHd + 1];
-        float2 acc[B];
+        float acc[B];
 #pragma unroll
-        for (uint32_t j = 0; j < B; j++)
-            acc[j] = *reinterpret_cast<const float2*>(base + static_cast<size_t>(s0 + min(j, n - 1)) * kAttnPart +
-                                                      2 * lane);
+        for (uint32_t j = 0; j < B; j++) acc[j] = base[static_cast<size_t>(s0 + min(j, n - 1)) * kAttnPart + dim];
         const float ms = lane < n ? ms_raw : -INFINITY;
         const float Mn = fmaxf(M, wave_max(ms));
         const float r = (M == -INFINITY) ? 0.0f : expf(M - Mn);
         const float w = (ms == -INFINITY) ? 0.0f : expf(ms - Mn);
         den = fmaf(den, r, wave_sum(lane < n ? w * ls_raw : 0.0f));
-        a0 *= r;
-        a1 *= r;
+        acc_d *= r;
         const int wb = __builtin_bit_cast(int, w);
 #pragma unroll
-        for (uint32_t j = 0; j < B; j++) {
-            const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(wb, j));  // 0 past n
-            a0 = fmaf(wj, acc[j].x, a0);
-            a1 = fmaf(wj, acc[j].y, a1);
-        }
+        for (uint32_t j = 0; j < B; j++)
+            acc_d = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(wb, j)), acc[j], acc_d);  // 0 past n
         M = Mn;
     }
     if (lane == 0) {
         rm[wid] = M;
         rd[wid] = den;
     }
-    ra[wid][lane] = make_float2(a0, a1);
+    ra[wid][lane] = acc_d;
     __syncthreads();
     if (wid == 0) {
         float Mt = -INFINITY;
         for (uint32_t g = 0; g < nw; g++) Mt = fmaxf(Mt, rm[g]);
-        float d = 0.0f, t0 = 0.0f, t1 = 0.0f;
+        float d = 0.0f, t = 0.0f;
         for (uint32_t g = 0; g < nw; g++) {
             const float e = (rm[g] == -INFINITY) ? 0.0f : expf(rm[g] - Mt);
             d = fmaf(e, rd[g], d);
-            t0 = fmaf(e, ra[g][lane].x, t0);
-            t1 = fmaf(e, ra[g][lane].y, t1);
+            t = fmaf(e, ra[g][lane], t);
         }
-        const float inv = 1.0f / d;
-        *reinterpret_cast<float2*>(out + static_cast<size_t>(qh) * kAttnHd + 2 * lane) = make_float2(t0 * inv, t1 * inv);
+        out[static_cast<size_t>(qh) * kAttnHd + dim] = t / d;
     }
 }
 
