@@ -100,7 +100,9 @@ FUSED_CASES = [(32, 8, 0, 2048), (32, 8, 63, 2048), (32, 8, 64, 2048), (32, 8, 7
                # for most waves), 512 (one chunk of 32 per wave) and 625 (two
                # chunks, the running rescale); the later positions hold the
                # larger scores
-               (32, 8, 5999, 6000), (8, 2, 4100, 6000), (32, 8, 32767, 32768), (8, 2, 39999, 40000)]
+               (32, 8, 5999, 6000), (8, 2, 4100, 6000), (32, 8, 32767, 32768), (8, 2, 39999, 40000),
+               # 65 splits (the first wide case), the new row alone in the last
+               (32, 8, 4096, 4100)]
 
 
 @pytest.mark.parametrize("nh,nkv,pos,max_seq", FUSED_CASES)
