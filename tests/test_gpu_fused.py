@@ -302,3 +302,44 @@ def test_contract_timing_helpers_run_the_contract_ops(dev):
         for r in layer:
             dev.free_resident(r)
     dev.free_resident(lm)
+
+
+# Shapes on the kernel pickers' boundaries: the row classes (<= 8192 rows
+# takes the residual form's two-row q4_0 tiles, >= 65536 the tall instances --
+# here quants without one), chunk-step counts that are not a whole number of
+# 64-chunk steps (k = 4352, 2304, 8448, 12544), the widest generic x and k at
+# its maximum.  (A wider sweep of these boundaries -- 8 quants x 20 k x the row
+# classes x all forms, 4000 checks -- passed the same bar.)
+BOUNDARY_SHAPES = [
+    (synth.Q4_0, 8192, 4096), (synth.Q4_0, 8193, 4096), (synth.Q8_0, 8193, 4352), (synth.F16, 65537, 2048),
+    (synth.Q4_1, 65537, 2048), (synth.Q4_K, 255, 2304), (synth.Q6_K, 3, 8448), (synth.Q4_0, 255, 12544),
+    (synth.F32, 8193, 4352), (synth.BF16, 3, 24576), (synth.Q8_0, 3, 32768),
+]
+
+
+@pytest.mark.parametrize("qt,rows,k", BOUNDARY_SHAPES,
+                         ids=[f"{NAMES[q]}-{r}x{k}" for q, r, k in BOUNDARY_SHAPES])
+def test_picker_boundary_shapes_match_oracle(dev, qt, rows, k):
+    _say(f"boundary shape {NAMES[qt]} rows={rows} k={k}")
+    eps = 1e-6
+    w = synth.weights(qt, rows, k, seed=rows + 3 * k + qt)
+    x = synth.activation(k + 1, k) * np.float32(2.0)
+    nw = (1.0 + 0.1 * synth.activation(k + 7, k)).astype(np.float32)
+    res = synth.activation(k + 5, rows)
+    rw = dev.upload_resident(w)
+    assert rw is not None, dev.last_error()
+    xd, nwd, resd, yd = _dev_vec(dev, x), _dev_vec(dev, nw), _dev_vec(dev, res), dev.dev_malloc(rows * 4)
+    base = oracle.matvec(qt, w, k, rows, x)
+    cases = [(zd.FORM_PLAIN, dict(), base), (zd.FORM_RESID, dict(res=resd), res + base),
+             (zd.FORM_NORM, dict(norm_w=nwd, eps=eps), oracle.matvec(qt, w, k, rows, _rmsnorm(x, nw, eps)))]
+    for form, kw, want in cases:
+        assert dev.gemv_op_enqueue(form, zd.quant(qt), rw, rows, k, xd, yd, **kw), dev.last_error()
+        got = np.zeros(rows, np.float32)
+        dev.dev_download(got, yd)
+        assert np.isfinite(got).all() and rel_l2(got, want) <= REL_L2, form
+    out = np.full(rows, np.nan, np.float32)
+    assert dev.mat_vec_resident(rw, zd.quant(qt), rows, k, x, out), dev.last_error()
+    assert rel_l2(out, base) <= REL_L2
+    for p in (xd, nwd, resd, yd):
+        dev.dev_free(p)
+    dev.free_resident(rw)
