@@ -1002,39 +1002,9 @@ __device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], co
 // the current one (two fragment sets used in turn, the last tile's prefetch
 // clamped to a valid tile and dropped), stores with reduce_store_all.
 // FENCE: see compute_group.
-// Per-wave timeline (TL instances only, zlm_gemv_timeline.hip): the 100 MHz
-// s_memrealtime at the wave's start, after the x staging and after each of
-// its first six tiles, written by lane 0 to tl[wave * 8 + 0..7] (0 = no such
-// point).  A plain launch (TL false) compiles none of it.
-template <bool TL>
-struct Timeline {
-    uint64_t t[8] = {};  // filled by selects on the point count, so it stays in registers
-    int n = 1;
-    __device__ __forceinline__ void start() {
-        if constexpr (TL) t[0] = __builtin_amdgcn_s_memrealtime();
-    }
-    __device__ __forceinline__ void mark() {
-        if constexpr (TL) {
-            const uint64_t now = __builtin_amdgcn_s_memrealtime();
-#pragma unroll
-            for (int i = 1; i < 8; i++) t[i] = n == i ? now : t[i];
-            n = min(n + 1, 8);
-        }
-    }
-    __device__ __forceinline__ void write(uint64_t* tl, uint32_t wave, int lane) {
-        if constexpr (TL) {
-            if (tl && lane == 0)
-#pragma unroll
-                for (int i = 0; i < 8; i++) tl[static_cast<size_t>(wave) * 8 + i] = t[i];
-        }
-    }
-};
-
 template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT, int PRO, int EPI, bool PF = false,
-          bool FENCE = false, bool XQ = false, bool TL = false>
-__device__ __forceinline__ void gemv(const GemvArgs& a, uint64_t* tl = nullptr) {
-    Timeline<TL> tml;
-    tml.start();
+          bool FENCE = false, bool XQ = false>
+__device__ __forceinline__ void gemv(const GemvArgs& a) {
     __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
     __shared__ float xs[XTile<KCAP>::kRuns + 1];
     __shared__ float red[WAVES];
@@ -1059,7 +1029,6 @@ __device__ __forceinline__ void gemv(const GemvArgs& a, uint64_t* tl = nullptr) 
     float scale = 1.0f;
     if constexpr (PRO == PRO_NORM) scale = xstore_norm<KCAP, NX, WAVES, XQ>(xr, gr, k, a.eps, xl, xs, red);
     else xstore<KCAP, NX, XQ>(xr, k, xl, xs);
-    tml.mark();
 
     float acc[RT];
     if constexpr (PF) {
@@ -1091,8 +1060,6 @@ __device__ __forceinline__ void gemv(const GemvArgs& a, uint64_t* tl = nullptr) 
             compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(g, xl, xs, C, 0, lane, acc);
             reduce_store_all<RT, EPI>(acc, a, t1, scale, lane, rg);
         }
-        tml.mark();
-        tml.write(tl, blockIdx.x * WAVES + wid, lane);
         return;
     }
 #pragma unroll
@@ -1105,8 +1072,6 @@ __device__ __forceinline__ void gemv(const GemvArgs& a, uint64_t* tl = nullptr) 
         }
     }
     if (tile < ntiles) reduce_store<RT, EPI>(acc, a, tile, scale, lane);
-    tml.mark();
-    const uint32_t wave = blockIdx.x * WAVES + wid;
     for (tile += tstride; tile < ntiles; tile += tstride) {
         tr = tile_rows<RT, PAIR>(a, tile);
 #pragma unroll
@@ -1117,8 +1082,6 @@ __device__ __forceinline__ void gemv(const GemvArgs& a, uint64_t* tl = nullptr) 
         }
         reduce_store<RT, EPI>(acc, a, tile, scale, lane);
     }
-    tml.mark();
-    tml.write(tl, wave, lane);
 }
 // ---- several matrices over one x in one launch -------------------------------
 // The contract's matVecResidentBatch (reference gpu/backend/root.zig:249-254,
