@@ -103,23 +103,27 @@ def time_launches(dev, descs, launches_target):
     return runs[1]
 
 
-def cpu_threads() -> int:
-    """One thread per physical core among the cores this process may run on
-    (the reference pins one worker per physical core), at most 16: the CPU
-    share of one GPU on the benchmark box."""
-    cpus = sorted(os.sched_getaffinity(0))
-    cores = set()
-    for c in cpus:
-        base = f"/sys/devices/system/cpu/cpu{c}/topology"
-        try:
-            with open(f"{base}/physical_package_id") as f:
-                pkg = f.read().strip()
-            with open(f"{base}/core_id") as f:
-                core = f.read().strip()
-            cores.add((pkg, core))
-        except OSError:
-            cores.add(("?", str(c)))
-    return max(1, min(16, len(cores)))
+def cpu_threads() -> tuple:
+    """(threads, physical cores): one thread per physical core among the cores
+    this process may run on (the reference pins one worker per physical core),
+    capped at the process's CPU share when OMP_NUM_THREADS states one (the
+    benchmark box gives each GPU 16 CPUs and sets OMP_NUM_THREADS=16 for it)."""
+    import oracle
+
+    cores = len(oracle.physical_cores()) or len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return max(1, min(cores, share) if share > 0 else cores), cores
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def _min_time(fn, budget_s: float, max_reps: int = 50000) -> tuple:
@@ -130,56 +134,74 @@ def _min_time(fn, budget_s: float, max_reps: int = 50000) -> tuple:
 
 
 def cpu_baseline(g: Gemv, budget_s: float):
-    """The oracle's restatement of zlm's production sweep on the headline gate
-    weight: all physical cores (<= 16) split by rangeOf, and one thread."""
+    """zlm's production sweep on the headline gate weight, on the CPU: the
+    speed-faithful restatement (oracle/zlm_cpu_sweep.c: compile-time lanes at
+    zlm's native width, per-type row loops, vector dequant; bit-identical to
+    the oracle) over the persistent pinned pool split by rangeOf, plus one
+    thread, plus the single-thread [4096, 8192] q8_0 / q4_0 GEMVs zlm publishes."""
     import oracle
 
-    threads = cpu_threads()
+    threads, cores = cpu_threads()
+    lanes = oracle.fast_native_lanes()
     t0 = time.perf_counter()
-    best, reps = _min_time(lambda r: oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=threads, reps=r),
-                           0.6 * budget_s)
-    best1, reps1 = _min_time(lambda r: oracle.time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads=1, reps=r),
-                             0.4 * budget_s, max_reps=200)
+    best, reps = _min_time(lambda r: oracle.fast_time_matvec(g.qt, g.w, g.k, g.rows, g.x, threads, r),
+                           0.5 * budget_s)
+    best1, reps1 = _min_time(lambda r: oracle.fast_time_matvec(g.qt, g.w, g.k, g.rows, g.x, 1, r),
+                             0.2 * budget_s, max_reps=200)
+    published = {}
+    # zlm's own single-thread figures: [4096, 8192] (8192 rows of 4096) on a
+    # Ryzen 7 5700X (sdd/tasks/kernels/12-instruction-audit.md:81-82)
+    for qt, name, ref in ((synth.Q8_0, "q8_0", 17.93), (synth.Q4_0, "q4_0", 7.23)):
+        w = synth.weights(qt, 8192, 4096, 0x5A4C4DA0 + qt)
+        x = synth.activation(0x5A4C4DA8 + qt, 4096)
+        t1 = _min_time(lambda r: oracle.fast_time_matvec(qt, w, 4096, 8192, x, 1, r), 0.15 * budget_s, 100)[0]
+        published[name] = {"GBps_1_thread": round(w.nbytes / t1 / 1e9, 2), "ms": round(t1 * 1e3, 3),
+                           "zlm_published_GBps_1_thread": ref, "zlm_host": "Ryzen 7 5700X (AVX2, 8 lanes)"}
     spent = time.perf_counter() - t0
     return {
         "value": round(g.algo_bytes / best / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"oracle restatement of zlm's production sweep (-O3, x86-64-v3, lanes=8), "
-                  f"{g.name} {g.rows}x{g.k} Q8_0 GEMV, {threads} threads (one per physical core, at most 16) "
-                  f"split by rangeOf, min of {reps} reps; 1 thread: min of {reps1} reps ({spent:.1f} s in all)",
+        "sample": f"zlm's production sweep restated at zlm's speed (oracle/zlm_cpu_sweep.c, {lanes} lanes as "
+                  f"simd.native on this host; bit-identical to the oracle), {g.name} {g.rows}x{g.k} Q8_0 GEMV, "
+                  f"{threads} threads pinned one per physical core ({cores} in the affinity mask) split by "
+                  f"rangeOf, min of {reps} reps; 1 thread: min of {reps1} reps ({spent:.1f} s in all)",
         "ms_per_gemv": round(best * 1e3, 4),
+        "cpu": cpu_model(),
+        "lanes": lanes,
         "one_thread": {"value": round(g.algo_bytes / best1 / 1e9, 3), "unit": "GB/s",
                        "ms_per_gemv": round(best1 * 1e3, 4)},
+        "published_shapes_1_thread": published,
     }
 
 
 def cpu_prefill_sample(w: np.ndarray, rows: int, k: int, budget_s: float):
-    """configs[4] on the CPU: the oracle's int path (q8 activations, zlm's
-    Q4_0 intBlock) over a 64-token sample of the 512-token workload, all
-    physical cores; rates scale per token."""
+    """configs[4] on the CPU: zlm's int path (q8 activations, Q4_0 intBlock)
+    at zlm's speed over a 64-token sample of the 512-token workload, all
+    threads of the pool; rates scale per token."""
     import oracle
 
-    threads = cpu_threads()
+    threads, _ = cpu_threads()
     m = 64
     x = synth.activation(0x5A4C4D0D, m * k)
-    best, reps = _min_time(
-        lambda r: oracle.time_matmul_int(synth.Q4_0, w, k, rows, m, x, threads=threads, reps=r), budget_s, 20)
+    best, reps = _min_time(lambda r: oracle.fast_time_matmul_int(synth.Q4_0, w, k, rows, m, x, threads, r),
+                           budget_s, 20)
     ops = 2.0 * rows * k * m
     return {"tok_per_s": round(m / best, 1), "TOPS_int8": round(ops / best / 1e12, 4), "cores": threads,
-            "kind": "port", "sample": f"orc_matmul_int Q4_0 {rows}x{k}, {m} of the 512 tokens, {threads} threads "
-                                      f"split by rangeOf, min of {reps} reps"}
+            "kind": "port", "sample": f"zlm's int sweep (Q4_0 intBlock, {oracle.fast_native_lanes()} lanes) "
+                                      f"{rows}x{k}, {m} of the 512 tokens, {threads} pinned threads split by "
+                                      f"rangeOf, min of {reps} reps"}
 
 
 def cpu_decode_sample(cfg, budget_s: float):
     """configs[2] on the CPU: one token's projection GEMVs (q;k;v, o, gate, up,
-    down per layer, times the layer count, plus the Q8_0 lm_head) with the
-    oracle's production sweep on all physical cores.  Attention and the
+    down per layer, times the layer count, plus the Q8_0 lm_head) with zlm's
+    production sweep at zlm's speed on the pool's threads.  Attention and the
     elementwise glue are not included (on the GPU they are ~20% of a token)."""
     import oracle
 
-    threads = cpu_threads()
+    threads, _ = cpu_threads()
     per = max(0.5, budget_s / 6.0)
     h, f = cfg.hidden, cfg.ffn
     shapes = [("qkv", cfg.qkv_rows, h, synth.Q4_0), ("o", h, cfg.n_heads * cfg.head_dim, synth.Q4_0),
@@ -188,11 +210,10 @@ def cpu_decode_sample(cfg, budget_s: float):
     for i, (name, rows, k, qt) in enumerate(shapes):
         w = synth.weights(qt, rows, k, 0x5A4C4D70 + i)
         x = synth.activation(0x5A4C4D78 + i, k)
-        layer_s += _min_time(lambda r: oracle.time_matvec(qt, w, k, rows, x, threads=threads, reps=r), per, 200)[0]
+        layer_s += _min_time(lambda r: oracle.fast_time_matvec(qt, w, k, rows, x, threads, r), per, 200)[0]
     w = synth.weights(cfg.lm_type, cfg.vocab, h, 0x5A4C4D7F)
     x = synth.activation(0x5A4C4D7E, h)
-    lm_s = _min_time(lambda r: oracle.time_matvec(cfg.lm_type, w, h, cfg.vocab, x, threads=threads, reps=r), per,
-                     50)[0]
+    lm_s = _min_time(lambda r: oracle.fast_time_matvec(cfg.lm_type, w, h, cfg.vocab, x, threads, r), per, 50)[0]
     tok_s = cfg.n_layers * layer_s + lm_s
     return {"tok_per_s": round(1.0 / tok_s, 2), "ms_per_token": round(tok_s * 1e3, 2), "cores": threads,
             "kind": "port", "sample": f"production-sweep GEMVs of one layer (x{cfg.n_layers}) and the lm_head, "
@@ -321,7 +342,10 @@ def main():
     if not args.no_cpu:
         log(f"CPU baseline (~{0.5 * args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(gate, 0.5 * args.cpu_seconds)
-        log(f"CPU: {cpu['value']} GB/s on {cpu['cores']} threads, {cpu['one_thread']['value']} GB/s on 1")
+        log(f"CPU ({cpu['cpu']}, {cpu['lanes']} lanes): {cpu['value']} GB/s on {cpu['cores']} threads, "
+            f"{cpu['one_thread']['value']} GB/s on 1; [4096, 8192] on 1 thread: " +
+            ", ".join(f"{n} {v['GBps_1_thread']} GB/s (zlm {v['zlm_published_GBps_1_thread']})"
+                      for n, v in cpu["published_shapes_1_thread"].items()))
     for g in (gate, up, down):
         g.free()
 
@@ -451,6 +475,12 @@ def main():
             model.free()
             cfg = None
     if not args.quick and cfg is not None:
+        if zd.profiler_loaded():
+            # the library refuses graph replays under a profiler (replays of
+            # this step under rocprofv3's kernel trace aborted the process)
+            raise SystemExit("bench.py: a rocprofiler library is loaded in this process, and the decode step is "
+                             "timed from graph replays, which the library refuses under a profiler; profile the "
+                             "decode kernels with --decode-eager N instead")
         graph = model.capture()
         model.set_input(x, cfg.max_seq - 1)
         reps = max(1, args.decode_replays)

@@ -364,15 +364,36 @@ bool zlm_gpu_attention_decode_enqueue_noalloc(zlm_device *dev, const float *qkv,
 
 /* ---- HIP graphs over the device stream ----
  * Everything enqueued between capture_begin and capture_end is recorded, not
- * run.  Ops that allocate or convert layouts on first use must have run once
- * eagerly before their capture. */
+ * run.  Only the *_enqueue entry points can be captured: the host-buffer
+ * contract ops (matVec*, matMul*, waitResident, uploadResident, the probe and
+ * timers) fail while a capture is open.  Ops that allocate or convert layouts
+ * on first use (a resident's first op, a resident's first matMul, the
+ * attention and GEMM scratch) must have run once eagerly before their
+ * capture; under capture they fail instead.  The library never frees or
+ * replaces scratch that a captured graph references while that graph exists:
+ * after capturing an attention call, an eager attention call that needs more
+ * partials fails with the reason; after capturing a matMul, an eager matMul
+ * that needs more activation scratch, a rebuild of a resident's GEMM tiles
+ * (a matMul at another k) and zlm_gpu_release_gemm_tiles fail -- until those
+ * graphs are destroyed (zlm_gpu_graph_destroy with the device that captured
+ * them).  Freeing a resident (or any caller buffer) a live graph reads is the
+ * caller's error. */
 typedef struct zlm_graph zlm_graph;
 bool zlm_gpu_capture_begin(zlm_device *dev);
 zlm_graph *zlm_gpu_capture_end(zlm_device *dev);
 /* Launch the graph `iters` times back to back and wait; *ms (optional) = GPU
- * milliseconds between events around the launches. */
+ * milliseconds between events around the launches.  Refused (false, reason in
+ * zlm_gpu_last_error) while a rocprofiler library is loaded in the process:
+ * replays of the decode step under rocprofv3's kernel trace aborted inside
+ * hipGraphLaunch; profile eager launches instead. */
 bool zlm_gpu_graph_launch(zlm_device *dev, zlm_graph *graph, int iters, double *ms);
 void zlm_gpu_graph_destroy(zlm_device *dev, zlm_graph *graph);
+/* Whether a rocprofiler library appears in a /proc/<pid>/maps-format file
+ * (null: this process's own map): the check behind the replay refusal. */
+bool zlm_gpu_profiler_loaded(const char *maps_path);
+/* Device bytes the library itself holds on `dev` (staging, attention and GEMM
+ * scratch; not residents, not the fixed no-alloc array). */
+uint64_t zlm_gpu_scratch_device_bytes(const zlm_device *dev);
 
 /* ---- synthetic data generated in HBM (benchmark, large-shape tests) ----
  * A resident of `n_blocks` raw GGUF blocks (q4_0: f16 d + 16 random bytes;

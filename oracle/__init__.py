@@ -78,6 +78,24 @@ def lib() -> ctypes.CDLL:
         L.orc_time_matvec.argtypes = [U, P, S, S, S, P, P, I, I, I]
         L.orc_time_matmul_int.restype = ctypes.c_double
         L.orc_time_matmul_int.argtypes = [U, P, S, S, S, S, P, P, I, I, I]
+        L.orc_fast_native_lanes.restype = I
+        L.orc_fast_native_lanes.argtypes = []
+        for name in ("orc_fast_matvec", "orc_fast_matvec_int"):
+            fn = getattr(L, name)
+            fn.restype = I
+            fn.argtypes = [U, P, S, S, S, P, P, S, S, I]
+        L.orc_physical_cores.restype = I
+        L.orc_physical_cores.argtypes = [P, I]
+        L.orc_pool_start.restype = I
+        L.orc_pool_start.argtypes = [I]
+        L.orc_pool_stop.restype = None
+        L.orc_pool_stop.argtypes = []
+        L.orc_pool_threads.restype = I
+        L.orc_pool_threads.argtypes = []
+        L.orc_fast_time_matvec.restype = ctypes.c_double
+        L.orc_fast_time_matvec.argtypes = [U, P, S, S, S, P, P, I, I, I]
+        L.orc_fast_time_matmul_int.restype = ctypes.c_double
+        L.orc_fast_time_matmul_int.argtypes = [U, P, S, S, S, S, P, P, I, I, I]
         _lib = L
     return _lib
 
@@ -229,3 +247,59 @@ def time_matmul_int(t: int, w, k: int, rows: int, m: int, x, threads: int, reps:
     out = np.zeros(m * rows, np.float32)
     return lib().orc_time_matmul_int(t, _ptr(wb), wb.size, k, rows, m, _ptr(xf), _ptr(out), threads,
                                      reps, lanes)
+
+
+# ---- the speed-faithful sweep (zlm_cpu_sweep.c / zlm_cpu_pool.c) -------------
+
+def fast_native_lanes() -> int:
+    """The width zlm's simd.native picks on this host: 16 (AVX-512), 8 (AVX2) or 0."""
+    return int(lib().orc_fast_native_lanes())
+
+
+def fast_matvec(t: int, w, k: int, rows: int, x, lanes: int = 0, begin: int = 0, end: int = -1) -> np.ndarray:
+    """The production sweep at zlm's speed; bit-identical to matvec(..., lanes)."""
+    wb, xf = _u8(w), _f32(x)
+    out = np.zeros(rows, np.float32)
+    _check(lib().orc_fast_matvec(t, _ptr(wb), wb.size, k, rows, _ptr(xf), _ptr(out), begin,
+                                 rows if end < 0 else end, lanes))
+    return out
+
+
+def fast_matvec_int(t: int, w, k: int, rows: int, x, lanes: int = 0) -> np.ndarray:
+    """The int sweep (q8 activations) at zlm's speed; bit-identical to matvec_int."""
+    wb, xf = _u8(w), _f32(x)
+    out = np.zeros(rows, np.float32)
+    _check(lib().orc_fast_matvec_int(t, _ptr(wb), wb.size, k, rows, _ptr(xf), _ptr(out), 0, rows, lanes))
+    return out
+
+
+def physical_cores() -> list[int]:
+    """One logical CPU per physical core of this process's affinity mask."""
+    buf = (ctypes.c_int * 1024)()
+    n = lib().orc_physical_cores(ctypes.addressof(buf), 1024)
+    return list(buf[:n])
+
+
+def fast_time_matvec(t: int, w, k: int, rows: int, x, threads: int, reps: int, lanes: int = 0,
+                     out: np.ndarray | None = None) -> float:
+    """Min-of-reps wall seconds of one GEMV over the pinned persistent pool
+    (the results land in `out` when given)."""
+    wb, xf = _u8(w), _f32(x)
+    if out is None:
+        out = np.zeros(rows, np.float32)
+    assert out.dtype == np.float32 and out.size >= rows
+    return lib().orc_fast_time_matvec(t, _ptr(wb), wb.size, k, rows, _ptr(xf), _ptr(out), threads, reps, lanes)
+
+
+def fast_time_matmul_int(t: int, w, k: int, rows: int, m: int, x, threads: int, reps: int,
+                         lanes: int = 0, out: np.ndarray | None = None) -> float:
+    wb, xf = _u8(w), _f32(x)
+    if out is None:
+        out = np.zeros(m * rows, np.float32)
+    assert out.dtype == np.float32 and out.size >= m * rows
+    return lib().orc_fast_time_matmul_int(t, _ptr(wb), wb.size, k, rows, m, _ptr(xf), _ptr(out), threads, reps,
+                                          lanes)
+
+
+def pool_threads() -> int:
+    return int(lib().orc_pool_threads())

@@ -81,6 +81,29 @@ double orc_time_matmul_int(uint32_t type, const uint8_t *w, size_t w_len, size_t
                            size_t rows, size_t m, const float *x, float *out, int threads,
                            int reps, int lanes);
 
+/* ---- the speed-faithful sweep (zlm_cpu_sweep.c, zlm_cpu_pool.c) ----------
+ * Bit-identical to orc_matvec / orc_matvec_int at the same lanes, written as
+ * zlm's ReleaseFast build runs it; lanes 8 (AVX2) or 16 (AVX-512), 0 = the
+ * width zlm's simd.native picks on this host.  ORC_E_UNSUPPORTED when the
+ * host lacks the width. */
+int orc_fast_native_lanes(void);
+int orc_fast_matvec(uint32_t type, const uint8_t *w, size_t w_len, size_t k, size_t rows,
+                    const float *x, float *out, size_t begin, size_t end, int lanes);
+int orc_fast_matvec_int(uint32_t type, const uint8_t *w, size_t w_len, size_t k, size_t rows,
+                        const float *x, float *out, size_t begin, size_t end, int lanes);
+/* One logical CPU per physical core of the process's affinity mask. */
+int orc_physical_cores(int *cpus, int max);
+/* The persistent pool (runtime/pool.zig): workers pinned one per physical
+ * core, the caller running part 0. */
+int orc_pool_start(int threads);
+void orc_pool_stop(void);
+int orc_pool_threads(void);
+double orc_fast_time_matvec(uint32_t type, const uint8_t *w, size_t w_len, size_t k, size_t rows,
+                            const float *x, float *out, int threads, int reps, int lanes);
+double orc_fast_time_matmul_int(uint32_t type, const uint8_t *w, size_t w_len, size_t k,
+                                size_t rows, size_t m, const float *x, float *out, int threads,
+                                int reps, int lanes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -127,3 +127,25 @@ def test_layout_bytes_for_the_residency_budget():
     assert zd.layout_bytes(zd.quant(zd.F16), 64, 256, True) == 64 * 256 * 2
     assert zd.layout_bytes(zd.quant(zd.Q4_0), 64, 100, False) == 0  # k not whole blocks
     assert zd.layout_bytes(77, 64, 256, False) == 0  # unknown type
+
+
+def test_profiler_check_reads_the_process_map(tmp_path):
+    """Graph replays are refused while a profiler library is mapped: the check
+    matches rocprofiler-sdk (what rocprofv3 preloads) and the older
+    librocprofiler64, not the HIP runtime's own librocprofiler-register or
+    torch's roctracer / roctx, which every process maps."""
+    base = ("7f0000000000-7f0000001000 r-xp 00000000 08:01 1 /opt/rocm/lib/libamdhip64.so.7\n"
+            "7f0000001000-7f0000002000 r-xp 00000000 08:01 2 /opt/rocm/lib/librocprofiler-register.so.0.6.0\n"
+            "7f0000002000-7f0000003000 r-xp 00000000 08:01 3 /usr/lib/torch/lib/libroctracer64.so\n"
+            "7f0000003000-7f0000004000 r-xp 00000000 08:01 4 /usr/lib/torch/lib/libroctx64.so\n")
+    plain = tmp_path / "plain"
+    plain.write_text(base)
+    assert not zd.profiler_loaded(str(plain))
+    for lib_name in ("/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so.1",
+                     "/opt/rocm/lib/librocprofiler-sdk.so.1.1.0", "/opt/rocm/lib/librocprofiler64.so.2"):
+        traced = tmp_path / "traced"
+        traced.write_text(base + f"7f0000005000-7f0000006000 r-xp 00000000 08:01 5 {lib_name}\n")
+        assert zd.profiler_loaded(str(traced)), lib_name
+    assert not zd.profiler_loaded(str(tmp_path / "missing"))
+    # this test process runs without a profiler
+    assert not zd.profiler_loaded()

@@ -72,11 +72,13 @@ def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     dev.free_resident(res)
 
 
-# The small-M path (m <= 32: one 32-token tile, the workgroup's 8 waves split
-# the row's blocks in pairs): odd block counts (a pair's second block past the
-# end), block counts not a multiple of the 16 blocks a split step covers,
-# ragged row tiles, one token, a full tile, and the first m past it (the
-# tiled kernel).
+# The small-M path (3 <= m <= 32: one 32-token tile; the workgroup's waves
+# split the row's blocks in pairs -- 16 waves and 32-block split steps for
+# q4_0 / q8_0, 8 waves and 16-block steps for q4_1 / q4_k): odd block counts
+# (a pair's second block past the end), block counts not a multiple of a split
+# step (k = 3840 and 288), ragged row tiles, one token, a full tile, and the
+# first m past it (the tiled kernel).  A k that is not whole super-blocks for
+# q4_k is rounded up to the next one.
 SMALL_M = [(33, 4096, 2), (64, 4096, 9), (96, 3840, 32), (40, 12288, 31), (37, 288, 5), (64, 256, 33),
            (32, 512, 1), (4096 + 17, 4096, 8), (50, 4096, 3)]
 
@@ -84,8 +86,8 @@ SMALL_M = [(33, 4096, 2), (64, 4096, 9), (96, 3840, 32), (40, 12288, 31), (37, 2
 @pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0", "q4_1", "q4_k"])
 @pytest.mark.parametrize("rows,k,m", SMALL_M)
 def test_small_m_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
-    if k % synth.BLOCK_ELEMS[qt]:
-        pytest.skip("k not a multiple of the block")
+    be = synth.BLOCK_ELEMS[qt]
+    k = (k + be - 1) // be * be
     _say(f"small-m gemm type={qt} rows={rows} k={k} m={m}")
     w = synth.weights(qt, rows, k, seed=rows * 3 + k + m)
     x = synth.activation(m + 11, m * k)
@@ -97,6 +99,13 @@ def test_small_m_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     again = np.full(m * rows, np.nan, np.float32)
     assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, again), dev.last_error()
     np.testing.assert_array_equal(again.view(np.uint32), out.view(np.uint32))  # fixed summation order
+    # From 3 tokens the device runs the int path, where the reference's
+    # matMulResident is fp32: the reference's own int-vs-fp bound
+    # (kernels/quantized_test.zig:61) holds against the oracle's fp matMulRows
+    fp = oracle.matmul_rows(qt, w, k, rows, m, x)
+    dq = np.abs(oracle.dequant(qt, w, rows * k).reshape(rows, k).astype(np.float64))
+    mag = np.abs(x.reshape(m, k).astype(np.float64)) @ dq.T
+    assert np.all(np.abs(out.reshape(m, rows) - fp) <= 0.02 * mag + 1e-6)
     dev.free_resident(res)
 
 

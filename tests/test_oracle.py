@@ -354,3 +354,94 @@ def test_threaded_timer_runs():
     w = synth.weights(qt, rows, k, seed=1)
     x = synth.activation(1, k)
     assert oracle.time_matvec(qt, w, k, rows, x, threads=4, reps=2) > 0
+
+
+# ---- the speed-faithful sweep (oracle/zlm_cpu_sweep.c) -------------------------------
+# The CPU baseline runs zlm's production sweep the way zlm's ReleaseFast build
+# does (compile-time lanes, per-type row loops, vector dequant).  It must be
+# the oracle's arithmetic exactly: bit for bit at the same lane count, for
+# every type, on odd row ranges and the boundary cases the sweeps share.
+
+FAST_LANES = [L for L in (8, 16) if oracle.fast_native_lanes() >= L]
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).reshape(-1).view(np.uint32)
+
+
+@pytest.mark.skipif(not FAST_LANES, reason="host has neither AVX2 nor AVX-512")
+@pytest.mark.parametrize("lanes", FAST_LANES)
+@pytest.mark.parametrize("qt", TYPES)
+@pytest.mark.parametrize("rows,k", [(37, 256), (130, 4096), (9, 12288), (5, 3840)])
+def test_fast_sweep_is_the_oracle_bit_for_bit(qt, lanes, rows, k):
+    if k % synth.BLOCK_ELEMS[qt]:
+        pytest.skip("k not whole blocks")
+    w = synth.weights(qt, rows, k, seed=rows * 7 + k + qt)
+    x = synth.activation(rows + qt, k)
+    want = oracle.matvec(qt, w, k, rows, x, lanes=lanes)
+    np.testing.assert_array_equal(_bits(oracle.fast_matvec(qt, w, k, rows, x, lanes=lanes)), _bits(want))
+    # a row range leaves the other rows alone
+    part = oracle.fast_matvec(qt, w, k, rows, x, lanes=lanes, begin=rows // 3, end=rows - 1)
+    np.testing.assert_array_equal(_bits(part[rows // 3:rows - 1]), _bits(want[rows // 3:rows - 1]))
+    assert not part[:rows // 3].any() and part[rows - 1] == 0
+
+
+@pytest.mark.skipif(not FAST_LANES, reason="host has neither AVX2 nor AVX-512")
+@pytest.mark.parametrize("lanes", FAST_LANES)
+def test_fast_sweep_special_values(lanes):
+    """Zero, signed-zero, extreme and subnormal scales and activations: the
+    paths where a reordered or contracted operation would show."""
+    rows, k = 16, 512
+    for qt in TYPES:
+        w = synth.weights(qt, rows, k, seed=3).copy()
+        x = synth.activation(4, k).copy()
+        x[::7] = 0.0
+        x[1::11] = -0.0
+        x[2::13] = 3.0e38 if qt in (synth.F32,) else 6.0e4
+        x[3::17] = 1e-40
+        if qt in (synth.Q4_0, synth.Q8_0, synth.Q4_1):
+            bb = synth.BLOCK_BYTES[qt]
+            w[0::bb * 3] = 0x00  # some scales -> zero / subnormal f16
+            w[1::bb * 3] = 0x80  # negative zero
+        want = oracle.matvec(qt, w, k, rows, x, lanes=lanes)
+        got = oracle.fast_matvec(qt, w, k, rows, x, lanes=lanes)
+        np.testing.assert_array_equal(_bits(got), _bits(want), err_msg=str(qt))
+
+
+@pytest.mark.skipif(not FAST_LANES, reason="host has neither AVX2 nor AVX-512")
+@pytest.mark.parametrize("lanes", FAST_LANES)
+@pytest.mark.parametrize("qt", [synth.Q4_0, synth.Q8_0])
+def test_fast_int_sweep_is_the_oracle_bit_for_bit(qt, lanes):
+    rows, k = 71, 4096
+    w = synth.weights(qt, rows, k, seed=11 + qt)
+    x = synth.activation(12 + qt, k)
+    np.testing.assert_array_equal(_bits(oracle.fast_matvec_int(qt, w, k, rows, x, lanes=lanes)),
+                                  _bits(oracle.matvec_int(qt, w, k, rows, x, lanes=lanes)))
+
+
+@pytest.mark.skipif(not FAST_LANES, reason="host has neither AVX2 nor AVX-512")
+def test_pool_splits_rows_like_the_single_thread_sweep():
+    """The pinned pool (rangeOf parts, caller runs part 0) writes every row once,
+    with the single-thread result; the int path over several tokens too."""
+    rows, k = 1001, 1024
+    for qt in (synth.Q8_0, synth.Q4_K, synth.BF16):
+        w = synth.weights(qt, rows, k, seed=21)
+        x = synth.activation(22, k)
+        out = np.full(rows, np.nan, np.float32)
+        assert oracle.fast_time_matvec(qt, w, k, rows, x, threads=3, reps=2, out=out) > 0
+        np.testing.assert_array_equal(_bits(out), _bits(oracle.matvec(qt, w, k, rows, x,
+                                                                      lanes=oracle.fast_native_lanes())))
+    assert oracle.pool_threads() == min(3, max(1, len(oracle.physical_cores())))
+    m = 3
+    w = synth.weights(synth.Q4_0, rows, k, seed=23)
+    x = synth.activation(24, m * k)
+    out = np.full(m * rows, np.nan, np.float32)
+    assert oracle.fast_time_matmul_int(synth.Q4_0, w, k, rows, m, x, threads=2, reps=1, out=out) > 0
+    np.testing.assert_array_equal(_bits(out), _bits(oracle.matmul_int(synth.Q4_0, w, k, rows, m, x,
+                                                                       lanes=oracle.fast_native_lanes())))
+
+
+def test_physical_cores_are_distinct_and_allowed():
+    cores = oracle.physical_cores()
+    assert cores and len(set(cores)) == len(cores)
+    assert set(cores) <= os.sched_getaffinity(0)

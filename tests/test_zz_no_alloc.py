@@ -5,8 +5,9 @@ zlm_gpu_attention_decode_enqueue with the split partials in the library's
 fixed static scratch, so its outputs and cache appends must equal the
 allocating entry point's bit for bit: two calls in a row (the second on a
 smaller shape, so it reuses the array the first left behind), a HIP graph
-captured with no eager call before it and replayed with other work between
-the replays, and the size limit refused on the host.
+captured as the first op of a fresh device handle and replayed with other work
+between the replays (the library's own scratch stays at zero bytes through the
+capture and the replay), and the size limit refused on the host.
 """
 import math
 import sys
@@ -92,20 +93,31 @@ def test_noalloc_attention_matches_allocating_entry_point(dev):
             c.free()
 
 
-def test_noalloc_attention_in_a_graph_captured_before_any_eager_call(dev):
+def test_noalloc_attention_in_a_graph_captured_before_any_eager_call():
+    # a fresh device handle: the capture is its first op, so no library
+    # scratch was sized before it, and the no-alloc path must not size any
+    dev = zd.Device()
+    if not dev.available():
+        pytest.fail(f"HIP backend unavailable: {dev.last_error()}")
     nh, nkv, max_seq, pos = 16, 4, 1000, 777
     _say(f"no-alloc attention graph nh={nh} nkv={nkv} max_seq={max_seq} pos={pos}")
     c = _Case(dev, nh, nkv, max_seq, pos, seed=5)
     other = _Case(dev, 32, 8, 2048, 1500, seed=6)
     graph = None
     try:
+        assert dev.scratch_device_bytes() == 0
         assert dev.capture_begin(), dev.last_error()
         try:
             ok = c.enqueue(1, noalloc=True)
         finally:
             graph = dev.capture_end()
         assert ok and graph is not None, dev.last_error()
+        dev.graph_launch(graph, 1)
+        assert dev.scratch_device_bytes() == 0, "the no-alloc path allocated library scratch"
+        # the allocating entry point on the same handle sizes its own partials
+        # (this graph does not reference them, so that is allowed while it lives)
         assert c.enqueue(0, noalloc=False), dev.last_error()
+        assert dev.scratch_device_bytes() > 0
         want = c.host(0)
         for rep in range(3):
             # other work on the same array between the replays
@@ -118,6 +130,7 @@ def test_noalloc_attention_in_a_graph_captured_before_any_eager_call(dev):
             dev.graph_destroy(graph)
         c.free()
         other.free()
+        dev.deinit()
 
 
 def test_noalloc_attention_refuses_shapes_beyond_its_array(dev):

@@ -39,6 +39,9 @@ namespace {
 
 constexpr int kRing = ZLM_RING_SIZE;
 constexpr uint32_t kNoLayout = 0xffffffffu;
+// Library scratch kinds a captured graph can reference.
+constexpr uint32_t kUsesAttn = 1u;  // the attention partials
+constexpr uint32_t kUsesGemm = 2u;  // the GEMM's quantized activations and the residents' GEMM tiles
 constexpr uint32_t kQ4kRecords = 0xfffffffeu;
 constexpr uint32_t kQ6kRecords = 0xfffffffdu;
 
@@ -117,7 +120,6 @@ struct GemvKernel {
 
 struct Slot {
     hipEvent_t done = nullptr;
-    float* d_y = nullptr;
     float* h_y = nullptr;  // pinned; the result kernel writes it through h_y_dev
     float* h_y_dev = nullptr;
     size_t y_cap = 0;
@@ -193,6 +195,13 @@ struct zlm_device {
     float* attn_part = nullptr;
     size_t attn_part_cap = 0;
     bool capturing = false;
+    // Library scratch a capture recorded (kUses* bits, collected while the
+    // capture is open) and, per kind, the captured graphs not yet destroyed
+    // that reference it: a graph replays with the addresses it was captured
+    // with.
+    uint32_t capture_uses = 0;
+    int attn_graphs = 0;
+    int gemm_graphs = 0;
     // this device's address of the fixed static scratch (the no-alloc entry
     // point's partials); null if the lookup at init failed
     float* static_scratch = nullptr;
@@ -221,10 +230,8 @@ struct zlm_device {
     uint8_t* s_lay = nullptr;  // streamed-weight staging (device layout)
     uint64_t s_lay_cap = 0;
 
-    // the fused MLP's ffn_mid (device side; the host half is unused)
+    // the fused MLP's ffn_mid (device only)
     float* d_mid = nullptr;
-    float* h_mid = nullptr;
-    float* h_mid_dev = nullptr;
     size_t mid_cap = 0;
 
     // burst-shared activation
@@ -357,6 +364,64 @@ bool ensure_pair(zlm_device* d, float*& dev, float*& host, size_t& cap, size_t n
     return true;
 }
 
+// A device buffer of n floats (contents not kept when it grows).
+bool ensure_dev(zlm_device* d, float*& dev, size_t& cap, size_t n) {
+    if (cap >= n && dev) return true;
+    if (dev) {
+        hipStreamSynchronize(d->stream);
+        hipFree(dev);
+    }
+    dev = nullptr;
+    cap = 0;
+    if (!ok(d, hipMalloc(reinterpret_cast<void**>(&dev), n * sizeof(float)), "hipMalloc")) return false;
+    cap = n;
+    return true;
+}
+
+// A pinned host buffer of n floats and its device-side address (kernels write
+// it directly).
+bool ensure_host(zlm_device* d, float*& host, float*& host_dev, size_t& cap, size_t n) {
+    if (cap >= n && host && host_dev) return true;
+    if (host) hipHostFree(host);
+    host = nullptr;
+    host_dev = nullptr;
+    cap = 0;
+    if (!ok(d, hipHostMalloc(reinterpret_cast<void**>(&host), n * sizeof(float), hipHostMallocDefault),
+            "hipHostMalloc"))
+        return false;
+    void* p = nullptr;
+    if (!ok(d, hipHostGetDevicePointer(&p, host, 0), "host buffer device address")) {
+        hipHostFree(host);
+        host = nullptr;
+        return false;
+    }
+    host_dev = static_cast<float*>(p);
+    cap = n;
+    return true;
+}
+
+// Library scratch that a captured graph can reference -- the attention
+// partials (kUsesAttn), the GEMM's quantized activations and the residents'
+// GEMM tiles (kUsesGemm) -- is never freed or replaced while a capture is open
+// or a captured graph that used it exists.  Growth then fails with the
+// reason, and the caller falls back.
+bool may_replace_scratch(zlm_device* d, uint32_t kind, const char* what) {
+    if (d->capturing) return fail(d, "%s must be sized by an eager call before capture", what);
+    const int live = kind == kUsesAttn ? d->attn_graphs : d->gemm_graphs;
+    if (live > 0)
+        return fail(d, "%s cannot be replaced while %d captured graph(s) use it; destroy them first", what, live);
+    return true;
+}
+
+// The contract's host-buffer ops copy x and results through host memory on
+// the calling thread, so they cannot be recorded into a graph; under capture
+// they fail (the *_enqueue entry points are the capturable forms).
+bool contract_ready(zlm_device* d) {
+    if (!d || !d->avail) return false;
+    if (d->capturing) return fail(d, "host-buffer ops cannot run under graph capture; use the enqueue forms");
+    return true;
+}
+
 bool ensure_bytes(zlm_device* d, uint8_t*& p, uint64_t& cap, uint64_t n) {
     if (cap >= n && p) return true;
     if (p) {
@@ -405,6 +470,7 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
     if (r->layout == qi->type) return true;
     if (r->layout != kNoLayout) return fail(d, "resident already holds a type-%u layout", r->layout);
     if (!r->raw) return fail(d, "resident has no raw bytes");
+    if (d->capturing) return fail(d, "a resident's first op must run eagerly before capture (layout conversion)");
     const uint64_t nblk = r->bytes / qi->block_bytes;
     if (qi->scale_offset == kNoLayout) {  // f32 / f16 / bf16: the raw rows are the layout
         r->payload = r->raw;
@@ -878,7 +944,7 @@ bool submit_into_slot(zlm_device* d, int s, zlm_resident* r, uint32_t quant, siz
                       const float* x_dev) {
     Slot& sl = d->slots[s];
     size_t ycap = sl.y_cap;
-    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows, sl.h_y_dev)) return false;
+    if (!ensure_host(d, sl.h_y, sl.h_y_dev, ycap, rows)) return false;
     sl.y_cap = ycap;
     if (!sl.done && !ok(d, hipEventCreateWithFlags(&sl.done, hipEventDisableTiming), "event")) return false;
     // the GEMV writes the slot's pinned host buffer directly (no read-back copy)
@@ -936,6 +1002,8 @@ void free_gemm_tiles(zlm_resident* r) {
 
 bool ensure_gemm_tiles(zlm_device* d, zlm_resident* r, const QuantInfo* qi, uint64_t nb) {
     if (r->gemm_payload && r->gemm_nb == nb) return true;
+    if (d->capturing) return fail(d, "a resident's GEMM tiles must be built by an eager matMul before capture");
+    if (r->gemm_payload && !may_replace_scratch(d, kUsesGemm, "a resident's GEMM tiles")) return false;
     if (r->gemm_payload) hipStreamSynchronize(d->stream);
     free_gemm_tiles(r);
     const uint64_t wblocks = nb * 32 / qi->block_elems;  // layout blocks per row
@@ -1003,7 +1071,9 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     const uint64_t qbytes = mt * 32 * k;  // a multiple of 1024
     const uint64_t fbytes = mt * 32 * nb * 4;
     const uint64_t need = qbytes + fbytes * (with_min ? 2 : 1);
+    if (need > d->q_scratch_cap && !may_replace_scratch(d, kUsesGemm, "the GEMM activation scratch")) return false;
     if (!ensure_bytes(d, d->q_scratch, d->q_scratch_cap, need)) return false;
+    if (d->capturing) d->capture_uses |= kUsesGemm;
     int8_t* qx = reinterpret_cast<int8_t*>(d->q_scratch);
     float* dx = reinterpret_cast<float*>(d->q_scratch + qbytes);
     float* ds = with_min ? reinterpret_cast<float*>(d->q_scratch + qbytes + fbytes) : nullptr;
@@ -1099,7 +1169,6 @@ extern "C" void zlm_gpu_deinit(zlm_device* d) {
         hipStreamSynchronize(d->stream);
         for (Slot& s : d->slots) {
             if (s.done) hipEventDestroy(s.done);
-            if (s.d_y) hipFree(s.d_y);
             if (s.h_y) hipHostFree(s.h_y);
             if (s.d_x) hipFree(s.d_x);
             if (s.h_x) hipHostFree(s.h_x);
@@ -1110,7 +1179,6 @@ extern "C" void zlm_gpu_deinit(zlm_device* d) {
         if (d->h_y) hipHostFree(d->h_y);
         if (d->attn_part) hipFree(d->attn_part);
         if (d->d_mid) hipFree(d->d_mid);
-        if (d->h_mid) hipHostFree(d->h_mid);
         if (d->d_bx) hipFree(d->d_bx);
         if (d->h_bx) hipHostFree(d->h_bx);
         if (d->bx_copied) hipEventDestroy(d->bx_copied);
@@ -1132,7 +1200,7 @@ extern "C" const char* zlm_gpu_device_name(const zlm_device* d) { return (d && d
 extern "C" bool zlm_gpu_is_uma(const zlm_device*) { return false; }
 
 extern "C" zlm_resident* zlm_gpu_upload_resident(zlm_device* d, const void* bytes, size_t len) {
-    if (!d || !d->avail) return nullptr;
+    if (!contract_ready(d)) return nullptr;
     if (!bytes && len) return nullptr;
     return new_resident(d, bytes, len);
 }
@@ -1162,6 +1230,7 @@ extern "C" uint64_t zlm_gpu_layout_bytes(uint32_t quant, size_t rows, size_t k, 
 
 extern "C" bool zlm_gpu_release_gemm_tiles(zlm_device* d, zlm_resident* r) {
     if (!d || !d->avail || !r) return false;
+    if (r->gemm_payload && !may_replace_scratch(d, kUsesGemm, "a resident's GEMM tiles")) return false;
     if (r->gemm_payload) hipStreamSynchronize(d->stream);
     free_gemm_tiles(r);
     return true;
@@ -1169,7 +1238,7 @@ extern "C" bool zlm_gpu_release_gemm_tiles(zlm_device* d, zlm_resident* r) {
 
 extern "C" bool zlm_gpu_mat_vec_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
                                          const float* x, size_t x_len, float* out, size_t out_len) {
-    if (!d || !d->avail) return false;
+    if (!contract_ready(d)) return false;
     if (!x || !out || x_len != k || out_len < rows) return fail(d, "bad buffers");
     hipFunction_t f;
     unsigned g, b;
@@ -1182,7 +1251,7 @@ extern "C" bool zlm_gpu_mat_vec_resident(zlm_device* d, zlm_resident* r, uint32_
 
 extern "C" bool zlm_gpu_mat_vec(zlm_device* d, uint32_t quant, const void* w, size_t w_len, size_t rows, size_t k,
                                 const float* x, size_t x_len, float* out, size_t out_len) {
-    if (!d || !d->avail) return false;
+    if (!contract_ready(d)) return false;
     const QuantInfo* qi = quant_info(quant);
     if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
     if (!w || !x || !out || x_len != k || out_len < rows) return fail(d, "bad buffers");
@@ -1214,7 +1283,7 @@ extern "C" bool zlm_gpu_mat_vec(zlm_device* d, uint32_t quant, const void* w, si
 
 extern "C" int32_t zlm_gpu_mat_vec_resident_async(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows,
                                                   size_t k, const float* x, size_t x_len) {
-    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!contract_ready(d)) return ZLM_NULL_HANDLE;
     if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
     hipFunction_t f;
     unsigned g, b;
@@ -1265,7 +1334,7 @@ const float* stage_burst(zlm_device* d, const float* x, size_t x_len, bool first
 bool prepare_slot(zlm_device* d, int s, size_t rows) {
     Slot& sl = d->slots[s];
     size_t ycap = sl.y_cap;
-    if (!ensure_pair(d, sl.d_y, sl.h_y, ycap, rows, sl.h_y_dev)) return false;
+    if (!ensure_host(d, sl.h_y, sl.h_y_dev, ycap, rows)) return false;
     sl.y_cap = ycap;
     if (!sl.done && !ok(d, hipEventCreateWithFlags(&sl.done, hipEventDisableTiming), "event")) return false;
     return true;
@@ -1284,7 +1353,7 @@ bool finish_slot(zlm_device* d, int s, size_t rows) {
 // device-side ffn_mid, then the down GEMV into slot `s`.
 bool enqueue_mlp(zlm_device* d, int s, zlm_resident* rg, zlm_resident* ru, zlm_resident* rd, uint32_t gu_quant,
                  uint32_t down_quant, size_t rows, size_t k, size_t ffn, const float* x_dev, uint32_t act) {
-    if (!ensure_pair(d, d->d_mid, d->h_mid, d->mid_cap, ffn, d->h_mid_dev)) return false;
+    if (!ensure_dev(d, d->d_mid, d->mid_cap, ffn)) return false;
     zlm_gemv_op gu = {};
     gu.form = ZLM_FORM_PAIR;
     gu.quant = gu_quant;
@@ -1304,7 +1373,7 @@ bool enqueue_mlp(zlm_device* d, int s, zlm_resident* rg, zlm_resident* ru, zlm_r
 extern "C" int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device* d, zlm_resident* r, uint32_t quant,
                                                         size_t rows, size_t k, const float* x, size_t x_len,
                                                         bool first) {
-    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!contract_ready(d)) return ZLM_NULL_HANDLE;
     if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
     hipFunction_t f;
     unsigned g, b;
@@ -1318,7 +1387,7 @@ extern "C" int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device* d, zlm_resid
 }
 
 extern "C" bool zlm_gpu_wait_resident(zlm_device* d, int32_t h, float* out, size_t out_len, size_t rows) {
-    if (!d || !d->avail || h < 0) return false;
+    if (!contract_ready(d) || h < 0) return false;
     const int s = h & (kRing - 1);
     const uint32_t gen = static_cast<uint32_t>(h) >> 3;
     Slot& sl = d->slots[s];
@@ -1332,7 +1401,7 @@ extern "C" bool zlm_gpu_wait_resident(zlm_device* d, int32_t h, float* out, size
 
 extern "C" bool zlm_gpu_mat_vec_resident_batch(zlm_device* d, size_t k, const float* x, size_t x_len,
                                                const zlm_resident_op* ops, size_t n) {
-    if (!d || !d->avail) return false;
+    if (!contract_ready(d)) return false;
     if (!ops || n == 0 || n > kRing || !x || x_len != k) return fail(d, "bad batch");
     size_t total = 0;
     for (size_t i = 0; i < n; i++) {
@@ -1386,7 +1455,7 @@ extern "C" bool zlm_gpu_mat_vec_resident_batch(zlm_device* d, size_t k, const fl
 
 extern "C" bool zlm_gpu_mat_mul_resident(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k,
                                          size_t m, const float* x, size_t x_len, float* out, size_t out_len) {
-    if (!d || !d->avail) return false;
+    if (!contract_ready(d)) return false;
     if (!x || !out || m == 0 || x_len != m * k || out_len < m * rows) return fail(d, "bad buffers");
     if (!ensure_pair(d, d->d_x, d->h_x, d->x_cap, m * k, d->h_x_dev)) return false;
     if (!ensure_pair(d, d->d_y, d->h_y, d->y_cap, m * rows, d->h_y_dev)) return false;
@@ -1405,7 +1474,7 @@ extern "C" bool zlm_gpu_mat_mul_resident(zlm_device* d, zlm_resident* r, uint32_
 
 extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void* w, size_t w_len, size_t rows,
                                       size_t k, size_t m, const float* x, size_t x_len, float* out, size_t out_len) {
-    if (!d || !d->avail) return false;
+    if (!contract_ready(d)) return false;
     const QuantInfo* qi = quant_info(quant);
     if (!qi) return fail(d, "unsupported quant %u", quant & 0xffu);
     if (!gemm_supported(qi->type)) return fail(d, "no GEMM kernel for quant %u", qi->type);
@@ -1437,7 +1506,7 @@ extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, z
                                                                 const float* x, size_t x_len, uint32_t act,
                                                                 uint32_t variant, bool first) {
     (void)variant;
-    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!contract_ready(d)) return ZLM_NULL_HANDLE;
     if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
     if (act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", act), ZLM_NULL_HANDLE;
     const QuantInfo* qi = quant_info(quant);
@@ -1469,7 +1538,7 @@ extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, 
                                                                  size_t x_len, uint32_t act, uint32_t variant,
                                                                  bool first) {
     (void)variant;
-    if (!d || !d->avail) return ZLM_NULL_HANDLE;
+    if (!contract_ready(d)) return ZLM_NULL_HANDLE;
     if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
     if (act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", act), ZLM_NULL_HANDLE;
     const QuantInfo* gq = quant_info(gu_quant);
@@ -1658,7 +1727,7 @@ void probe_gate_up(zlm_device* d, uint32_t type, size_t rows, size_t k, const fl
 extern "C" void zlm_gpu_probe(zlm_device* d, size_t rows_in, size_t k_in, size_t m_in, zlm_probe* out) {
     if (!out) return;
     memset(out, 0, sizeof *out);
-    if (!d || !d->avail) return;
+    if (!contract_ready(d)) return;
     const size_t rows = std::min(rows_in, kProbeMaxRows);
     size_t k = std::min(k_in, kProbeMaxK);
     k -= k % 32;
@@ -1735,7 +1804,7 @@ extern "C" bool zlm_gpu_probe_rates(zlm_device* d, uint32_t ggml_type, bool gate
                                     double* rates) {
     if (!rates) return false;
     for (int v = 0; v < 8; v++) rates[v] = 0.0;
-    if (!d || !d->avail) return false;
+    if (!contract_ready(d)) return false;
     const QuantInfo* qi = quant_info(ggml_type);
     if (!qi || variant_of(ggml_type) != 0) return fail(d, "unsupported quant %u", ggml_type);
     const size_t rows = std::min(rows_in, kProbeMaxRows);
@@ -1838,7 +1907,7 @@ extern "C" bool zlm_gpu_mat_mul_enqueue(zlm_device* d, zlm_resident* r, uint32_t
 extern "C" bool zlm_gpu_time_mat_mul(zlm_device* d, zlm_resident* const* res, size_t n_res, uint32_t quant,
                                      size_t rows, size_t k, size_t m, const float* x_dev, float* out_dev, int iters,
                                      double* ms) {
-    if (!d || !d->avail || !res || n_res == 0 || iters < 1 || !ms) return false;
+    if (!contract_ready(d) || !res || n_res == 0 || iters < 1 || !ms) return false;
     for (size_t i = 0; i < n_res; i++)  // layouts and scratch outside the timed region
         if (!enqueue_gemm(d, res[i], quant, rows, k, m, x_dev, out_dev)) return false;
     hipEvent_t e0, e1;
@@ -1861,7 +1930,7 @@ extern "C" bool zlm_gpu_time_mat_mul(zlm_device* d, zlm_resident* const* res, si
 extern "C" bool zlm_gpu_time_mat_vec(zlm_device* d, zlm_resident* const* res, size_t n_res, uint32_t quant,
                                      size_t rows, size_t k, const float* x_dev, float* y_dev, int iters,
                                      double* ms) {
-    if (!d || !d->avail || !res || n_res == 0 || iters < 1 || !ms) return false;
+    if (!contract_ready(d) || !res || n_res == 0 || iters < 1 || !ms) return false;
     for (size_t i = 0; i < n_res; i++) {  // converts layouts outside the timed region
         hipFunction_t f;
         unsigned g, b;
@@ -1882,7 +1951,7 @@ extern "C" bool zlm_gpu_time_mat_vec(zlm_device* d, zlm_resident* const* res, si
 
 extern "C" bool zlm_gpu_time_gemv_sequence(zlm_device* d, const zlm_gemv_desc* descs, size_t n, int iters,
                                            double* ms) {
-    if (!d || !d->avail || !descs || n == 0 || iters < 1 || !ms) return false;
+    if (!contract_ready(d) || !descs || n == 0 || iters < 1 || !ms) return false;
     for (size_t i = 0; i < n; i++) {  // converts layouts outside the timed region
         hipFunction_t f;
         unsigned g, b;
@@ -1929,7 +1998,7 @@ extern "C" bool zlm_gpu_time_gemv_sequence(zlm_device* d, const zlm_gemv_desc* d
 
 extern "C" bool zlm_gpu_time_contract_gemv(zlm_device* d, zlm_resident* const* res, size_t n_res, uint32_t quant,
                                            size_t rows, size_t k, int iters, double* us) {
-    if (!d || !d->avail || !res || n_res == 0 || iters < 1 || !us) return false;
+    if (!contract_ready(d) || !res || n_res == 0 || iters < 1 || !us) return false;
     std::vector<float> x(k), y(rows);
     for (size_t i = 0; i < k; i++) x[i] = static_cast<float>(static_cast<int>((i * 7 + 3) % 17) - 8) * 0.125f;
     for (size_t i = 0; i < n_res; i++)  // layouts converted outside the timed region
@@ -1948,7 +2017,7 @@ extern "C" bool zlm_gpu_time_contract_decode(zlm_device* d, const zlm_contract_l
                                              uint32_t quant, size_t hidden, size_t q_rows, size_t kv_rows,
                                              size_t ffn, zlm_resident* lm_head, uint32_t lm_quant, size_t vocab,
                                              int iters, double* ms) {
-    if (!d || !d->avail || !layers || n_layers == 0 || !lm_head || iters < 1 || !ms) return false;
+    if (!contract_ready(d) || !layers || n_layers == 0 || !lm_head || iters < 1 || !ms) return false;
     std::vector<float> x(hidden), qo(q_rows), ko(kv_rows), vo(kv_rows), ho(hidden), mo(hidden), logits(vocab);
     for (size_t i = 0; i < hidden; i++) x[i] = static_cast<float>(static_cast<int>((i * 7 + 3) % 17) - 8) * 0.125f;
     for (size_t i = 0; i < q_rows; i++) qo[i] = x[i % hidden];
@@ -2016,7 +2085,7 @@ namespace {
 // a call under capture that would need it fails.
 bool ensure_attn_scratch(zlm_device* d, size_t need) {
     if (need > d->attn_part_cap) {
-        if (d->capturing) return fail(d, "attention scratch must be sized by an eager call before capture");
+        if (!may_replace_scratch(d, kUsesAttn, "the attention scratch")) return false;
         if (d->attn_part) {
             hipStreamSynchronize(d->stream);
             hipFree(d->attn_part);
@@ -2027,6 +2096,7 @@ bool ensure_attn_scratch(zlm_device* d, size_t need) {
             return false;
         d->attn_part_cap = need;
     }
+    if (d->capturing) d->capture_uses |= kUsesAttn;
     return true;
 }
 
@@ -2137,13 +2207,32 @@ extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const u
 struct zlm_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    zlm_device* owner = nullptr;
+    uint32_t uses = 0;  // kUses* bits: library scratch the graph references
 };
+
+// Whether a profiler library (rocprofiler-sdk, as rocprofv3 preloads it, or
+// the older librocprofiler64) is mapped into this process (maps_path: a
+// /proc/<pid>/maps-format file; null = this process's own).  The HIP runtime's
+// own librocprofiler-register and torch's roctracer/roctx are always mapped
+// and do not count.
+bool profiler_in_maps(const char* maps_path) {
+    FILE* f = fopen(maps_path ? maps_path : "/proc/self/maps", "r");
+    if (!f) return false;
+    char line[4096];
+    bool found = false;
+    while (!found && fgets(line, sizeof line, f))
+        found = strstr(line, "librocprofiler-sdk") != nullptr || strstr(line, "librocprofiler64") != nullptr;
+    fclose(f);
+    return found;
+}
 
 extern "C" bool zlm_gpu_capture_begin(zlm_device* d) {
     if (!d || !d->avail) return false;
     if (d->capturing) return fail(d, "already capturing");
     if (!ok(d, hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed), "begin capture")) return false;
     d->capturing = true;
+    d->capture_uses = 0;
     return true;
 }
 
@@ -2164,6 +2253,10 @@ extern "C" zlm_graph* zlm_gpu_capture_end(zlm_device* d) {
         delete g;
         return nullptr;
     }
+    g->owner = d;
+    g->uses = d->capture_uses;
+    if (g->uses & kUsesAttn) d->attn_graphs++;
+    if (g->uses & kUsesGemm) d->gemm_graphs++;
     return g;
 }
 
@@ -2173,8 +2266,27 @@ extern "C" zlm_graph* zlm_gpu_capture_end(zlm_device* d) {
 // (a decode step is ~220 kernels) in the stream's queue at once.
 constexpr int kGraphsInFlight = 4;
 
+extern "C" bool zlm_gpu_profiler_loaded(const char* maps_path) { return profiler_in_maps(maps_path); }
+
+extern "C" uint64_t zlm_gpu_scratch_device_bytes(const zlm_device* d) {
+    if (!d || !d->avail) return 0;
+    uint64_t b = (d->x_cap + d->y_cap + d->bx_cap + d->mid_cap + d->attn_part_cap) * sizeof(float) +
+                 d->q_scratch_cap + d->s_raw_cap + d->s_lay_cap;
+    for (const Slot& sl : d->slots) b += sl.x_cap * sizeof(float);
+    return b;
+}
+
 extern "C" bool zlm_gpu_graph_launch(zlm_device* d, zlm_graph* g, int iters, double* ms) {
     if (!d || !d->avail || !g || iters < 1) return false;
+    if (g->owner != d) return fail(d, "graph was captured on another device handle");
+    // Replays of a captured decode step aborted inside hipGraphLaunch ("invalid
+    // AQL packet") when the process ran under rocprofv3's kernel trace, while
+    // the same replays without the profiler run clean; the cause is not known,
+    // so replays are refused while a rocprofiler library is in the process
+    // (profile the same kernels from eager launches instead).
+    if (profiler_in_maps(nullptr))
+        return fail(d, "graph replay refused: a rocprofiler library is loaded in this process "
+                       "(replays under the kernel tracer aborted); trace eager launches instead");
     hipEvent_t e0 = nullptr, e1 = nullptr;
     hipEvent_t done[kGraphsInFlight] = {};
     bool good = true;
@@ -2206,6 +2318,10 @@ extern "C" bool zlm_gpu_graph_launch(zlm_device* d, zlm_graph* g, int iters, dou
 extern "C" void zlm_gpu_graph_destroy(zlm_device* d, zlm_graph* g) {
     if (!g) return;
     if (d && d->avail) hipStreamSynchronize(d->stream);
+    if (d && d == g->owner) {
+        if (g->uses & kUsesAttn) d->attn_graphs--;
+        if (g->uses & kUsesGemm) d->gemm_graphs--;
+    }
     if (g->exec) hipGraphExecDestroy(g->exec);
     if (g->graph) hipGraphDestroy(g->graph);
     delete g;

@@ -189,6 +189,8 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_capture_end": (P, [P]),
         "zlm_gpu_graph_launch": (B, [P, P, ctypes.c_int, P]),
         "zlm_gpu_graph_destroy": (None, [P, P]),
+        "zlm_gpu_profiler_loaded": (B, [ctypes.c_char_p]),
+        "zlm_gpu_scratch_device_bytes": (ctypes.c_uint64, [P]),
         "zlm_gpu_synth_resident": (P, [P, U, S, ctypes.c_uint64, ctypes.c_float]),
         "zlm_gpu_synth_f16": (B, [P, P, S, ctypes.c_uint64, ctypes.c_float]),
         "zlm_gpu_quantize_act_q8": (B, [P, P, S, P, P, P]),
@@ -559,6 +561,10 @@ class Device:
     def graph_destroy(self, graph: int) -> None:
         self._L.zlm_gpu_graph_destroy(self._h, graph)
 
+    def scratch_device_bytes(self) -> int:
+        """Device bytes the library holds for staging and scratch (not residents)."""
+        return int(self._L.zlm_gpu_scratch_device_bytes(self._h))
+
     def synth_resident(self, ggml_type: int, n_blocks: int, seed: int, scale: float) -> Optional[Resident]:
         p = self._L.zlm_gpu_synth_resident(self._h, ggml_type, n_blocks, seed & 0xFFFFFFFFFFFFFFFF, scale)
         return Resident(self, p) if p else None
@@ -582,3 +588,8 @@ class Device:
         if not self._L.zlm_gpu_quantize_act_q8(self._h, _p(x), n, _p(qx), _p(dx), _p(sums)):
             return None
         return qx, dx, sums
+
+
+def profiler_loaded(maps_path: Optional[str] = None) -> bool:
+    """Whether a rocprofiler library is mapped (this process, or a maps-format file)."""
+    return bool(lib().zlm_gpu_profiler_loaded(None if maps_path is None else maps_path.encode()))
