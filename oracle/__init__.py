@@ -94,6 +94,8 @@ def lib() -> ctypes.CDLL:
         L.orc_pool_threads.argtypes = []
         L.orc_fast_time_matvec.restype = ctypes.c_double
         L.orc_fast_time_matvec.argtypes = [U, P, S, S, S, P, P, I, I, I]
+        L.orc_fast_time_matvec_copies.restype = ctypes.c_double
+        L.orc_fast_time_matvec_copies.argtypes = [U, P, I, S, S, S, P, P, I, I, I]
         L.orc_fast_time_matmul_int.restype = ctypes.c_double
         L.orc_fast_time_matmul_int.argtypes = [U, P, S, S, S, S, P, P, I, I, I]
         _lib = L
@@ -289,6 +291,52 @@ def fast_time_matvec(t: int, w, k: int, rows: int, x, threads: int, reps: int, l
         out = np.zeros(rows, np.float32)
     assert out.dtype == np.float32 and out.size >= rows
     return lib().orc_fast_time_matvec(t, _ptr(wb), wb.size, k, rows, _ptr(xf), _ptr(out), threads, reps, lanes)
+
+
+def fast_time_matvec_copies(t: int, copies, k: int, rows: int, x, threads: int, reps: int, lanes: int = 0,
+                            out: np.ndarray | None = None) -> float:
+    """fast_time_matvec with call r reading copies[r % len(copies)] (distinct
+    buffers of the same weight, their total past the host's last level cache)."""
+    cb = [_u8(c) for c in copies]
+    n = min(c.size for c in cb)
+    ptrs = (ctypes.c_void_p * len(cb))(*[_ptr(c) for c in cb])
+    xf = _f32(x)
+    if out is None:
+        out = np.zeros(rows, np.float32)
+    assert out.dtype == np.float32 and out.size >= rows
+    return lib().orc_fast_time_matvec_copies(t, ctypes.addressof(ptrs), len(cb), n, k, rows, _ptr(xf), _ptr(out),
+                                             threads, reps, lanes)
+
+
+def last_level_cache_bytes() -> int:
+    """Total last-level cache of the CPUs this process may run on (distinct
+    cache instances summed), from sysfs; 0 if unknown."""
+    seen, total = set(), 0
+    for c in sorted(os.sched_getaffinity(0)):
+        base = f"/sys/devices/system/cpu/cpu{c}/cache"
+        try:
+            idx = sorted(d for d in os.listdir(base) if d.startswith("index"))
+        except OSError:
+            continue
+        best = None
+        for d in idx:
+            try:
+                with open(f"{base}/{d}/level") as f:
+                    level = int(f.read())
+                with open(f"{base}/{d}/size") as f:
+                    size = f.read().strip()
+                with open(f"{base}/{d}/shared_cpu_list") as f:
+                    shared = f.read().strip()
+            except (OSError, ValueError):
+                continue
+            mult = {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}.get(size[-1:], 1)
+            nbytes = int(size.rstrip("KMG")) * mult
+            if best is None or level > best[0]:
+                best = (level, nbytes, shared)
+        if best and best[2] not in seen:
+            seen.add(best[2])
+            total += best[1]
+    return total
 
 
 def fast_time_matmul_int(t: int, w, k: int, rows: int, m: int, x, threads: int, reps: int,

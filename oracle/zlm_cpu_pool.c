@@ -247,16 +247,21 @@ static double now_s(void) {
 }
 
 /* Min-of-`reps` wall seconds of one pooled call, the calling thread pinned to
- * the first physical core for the duration (its mask restored after). */
-static double time_pooled(const pool_job *job, int threads, int reps) {
+ * the first physical core for the duration (its mask restored after).  Call r
+ * reads weight copy r % n_copies: copies whose total exceeds the host's last
+ * level cache make every call stream its weights from DRAM, as a decode step
+ * streaming gigabytes of distinct weights does. */
+static double time_pooled(const pool_job *job, const uint8_t *const *copies, int n_copies, int threads, int reps) {
     orc_pool_start(threads);
     cpu_set_t saved;
     const int have_saved = sched_getaffinity(0, sizeof saved, &saved) == 0;
     if (P.cpus[0] >= 0) pin(P.cpus[0]);
     double best = 1e30;
+    pool_job j = *job;
     for (int r = 0; r < reps; r++) {
+        if (copies && n_copies > 0) j.w = copies[r % n_copies];
         const double t0 = now_s();
-        pool_run(job);
+        pool_run(&j);
         const double dt = now_s() - t0;
         if (dt < best) best = dt;
     }
@@ -264,12 +269,19 @@ static double time_pooled(const pool_job *job, int threads, int reps) {
     return best;
 }
 
-/* The production sweep of one GEMV split over the pool (zlm's matvec job). */
+/* The production sweep of one GEMV split over the pool (zlm's matvec job),
+ * rotating over n_copies weight copies of w_len bytes each. */
+double orc_fast_time_matvec_copies(uint32_t t, const uint8_t *const *ws, int n_copies, size_t w_len, size_t k,
+                                   size_t rows, const float *x, float *out, int threads, int reps, int lanes) {
+    if (!ws || n_copies < 1) return -1.0;
+    const pool_job job = {0, t, ws[0], w_len, k, rows, 1, x, out, pick_lanes(lanes)};
+    if (!job.lanes) return -1.0;
+    return time_pooled(&job, ws, n_copies, threads, reps);
+}
+
 double orc_fast_time_matvec(uint32_t t, const uint8_t *w, size_t w_len, size_t k, size_t rows, const float *x,
                             float *out, int threads, int reps, int lanes) {
-    const pool_job job = {0, t, w, w_len, k, rows, 1, x, out, pick_lanes(lanes)};
-    if (!job.lanes) return -1.0;
-    return time_pooled(&job, threads, reps);
+    return orc_fast_time_matvec_copies(t, &w, 1, w_len, k, rows, x, out, threads, reps, lanes);
 }
 
 /* The int path over m tokens (each worker its row range for every token). */
@@ -277,7 +289,7 @@ double orc_fast_time_matmul_int(uint32_t t, const uint8_t *w, size_t w_len, size
                                 const float *x, float *out, int threads, int reps, int lanes) {
     const pool_job job = {1, t, w, w_len, k, rows, m, x, out, pick_lanes(lanes)};
     if (!job.lanes || (t != ORC_Q4_0 && t != ORC_Q8_0)) return -1.0;
-    return time_pooled(&job, threads, reps);
+    return time_pooled(&job, NULL, 0, threads, reps);
 }
 
 /* The threads a started pool runs (0 before the first timed call). */

@@ -100,6 +100,11 @@ void orc_pool_stop(void);
 int orc_pool_threads(void);
 double orc_fast_time_matvec(uint32_t type, const uint8_t *w, size_t w_len, size_t k, size_t rows,
                             const float *x, float *out, int threads, int reps, int lanes);
+/* The same, call r reading weight copy r % n_copies (copies past the last
+ * level cache keep the weights streaming from DRAM). */
+double orc_fast_time_matvec_copies(uint32_t type, const uint8_t *const *ws, int n_copies, size_t w_len,
+                                   size_t k, size_t rows, const float *x, float *out, int threads, int reps,
+                                   int lanes);
 double orc_fast_time_matmul_int(uint32_t type, const uint8_t *w, size_t w_len, size_t k,
                                 size_t rows, size_t m, const float *x, float *out, int threads,
                                 int reps, int lanes);
