@@ -243,137 +243,13 @@ def cpu_decode_sample(cfg, budget_s: float):
                                       f"cache; attention and glue not timed"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--quick", action="store_true", help="headline workload only")
-    ap.add_argument("--cpu-seconds", type=float, default=16.0,
-                    help="CPU-baseline budget: half on the headline GEMV, a quarter each on configs[4] and [2]")
-    ap.add_argument("--decode-eager", type=int, default=0, metavar="N",
-                    help="run N eager decode steps instead of timing graph replays (for kernel-trace profiling)")
-    ap.add_argument("--decode-replays", type=int, default=30, metavar="N",
-                    help="graph replays per timed decode run (warm-up run + 3 timed runs of N)")
-    ap.add_argument("--no-long-context", action="store_true",
-                    help="skip the decode step at 8192 and 32768 cached positions")
-    ap.add_argument("--no-small-m", action="store_true",
-                    help="skip the small-token-count matMul sweep (its GEMVs share kernels with configs[0]/[3])")
-    ap.add_argument("--counters", action="store_true",
-                    help="short warm-ups and few launches per shape, for rocprofv3 --pmc passes (not a timing run)")
-    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
-                    help="also run the library copy kernel 5x over BYTES (for HBM traffic counter calibration)")
-    args = ap.parse_args()
-    if args.counters:
-        WARM["ms"], WARM["launch_scale"] = 0.0, 0.05
-    if args.gpus != 1:
-        print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
-        sys.exit(2)
-
-    dev = zd.Device()
-    if not dev.available():
-        raise SystemExit(f"HIP backend unavailable: {dev.last_error()}")
-    log(f"device: {dev.device_name()}, {dev.cu_count()} CUs")
-    if args.calibrate_copy:
-        nbytes = (args.calibrate_copy // 16) * 16
-        a, b = dev.dev_malloc(nbytes), dev.dev_malloc(nbytes)
-        for _ in range(5):
-            dev.dev_copy(b, a, nbytes)
-        dev.dev_free(a)
-        dev.dev_free(b)
-        log(f"copy calibration: 5 x {nbytes} bytes")
-
-    # ---- headline: configs[1], Q8_0 Qwen3-8B FFN GEMVs ------------------------------
-    step_w = 2 * synth.weight_bytes(synth.Q8_0, 12288, 4096) + synth.weight_bytes(synth.Q8_0, 4096, 12288)
-    copies = max(1, math.ceil(MALL_DEFEAT_BYTES / step_w))
-    log(f"C1: generating Q8_0 gate/up/down, {copies} resident copies each")
-    gate = Gemv(dev, "gate", synth.Q8_0, 12288, 4096, 0x5A4C4D01, copies)
-    up = Gemv(dev, "up", synth.Q8_0, 12288, 4096, 0x5A4C4D11, copies)
-    down = Gemv(dev, "down", synth.Q8_0, 4096, 12288, 0x5A4C4D21, copies)
-    step_descs = []
-    for c in range(copies):
-        step_descs += [gate.desc(c), up.desc(c), down.desc(c)]
-    step_bytes = gate.algo_bytes + up.algo_bytes + down.algo_bytes
-
-    def steps_of(n):  # n consecutive steps, step i on weight copy i % copies
-        out = []
-        for i in range(n):
-            out += [gate.desc(i), up.desc(i), down.desc(i)]
-        return out
-
-    # W warm-up steps, then untimed steps until >= 50 ms of GPU time have run
-    # since the host-side synthesis (the clocks ramp over the first
-    # milliseconds; a short warm-up alone reads several percent low), then
-    # exactly K timed steps.
-    steps = max(1, args.steps)
-    warmup = max(0, args.warmup)
-    clock_ms = dev.time_gemv_sequence(steps_of(warmup), 1) if warmup else 0.0
-    while clock_ms < WARM["ms"]:
-        clock_ms += dev.time_gemv_sequence(step_descs, max(1, 200 // copies))
-    ms_total = dev.time_gemv_sequence(steps_of(steps), 1)
-    ms_step = ms_total / steps
-    value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"C1 step: {ms_step * 1e3:.2f} us -> {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak) over "
-        f"{steps} steps after {warmup} warm-up steps ({clock_ms:.1f} ms of untimed GPU work)")
-
-    # dominant kernel: the k=4096 gate/up GEMV, alone, same rotation
-    gu_descs = []
-    for c in range(copies):
-        gu_descs += [gate.desc(c), up.desc(c)]
-    ms_gu = time_launches(dev, gu_descs, 4 * len(gu_descs) * 25) / len(gu_descs)
-    gu_gbps = gate.algo_bytes / (ms_gu * 1e-3) / 1e9
-    ms_dn = time_launches(dev, [down.desc(c) for c in range(copies)], 100 * copies) / copies
-    dn_gbps = down.algo_bytes / (ms_dn * 1e-3) / 1e9
-    log(f"gate/up GEMV {ms_gu * 1e3:.2f} us ({gu_gbps:.1f} GB/s); down GEMV {ms_dn * 1e3:.2f} us ({dn_gbps:.1f} GB/s)")
-
-    extra = {
-        "c1_gate_up_q8_0_12288x4096": {"us": round(ms_gu * 1e3, 3), "GBps": round(gu_gbps, 1)},
-        "c1_down_q8_0_4096x12288": {"us": round(ms_dn * 1e3, 3), "GBps": round(dn_gbps, 1)},
-    }
-    # gate and up over the same x as one matVecResidentBatch launch
-    pair = []
-    for c in range(copies):
-        pair += [gate.desc(c)[:4] + (gate.x_dev, gate.y_dev, 1), up.desc(c)[:4] + (gate.x_dev, up.y_dev, 0)]
-    ms_pair = time_launches(dev, pair, 4 * len(pair) * 25) / len(pair)
-    extra["c1_gate_up_batched"] = {
-        "us_per_gemv": round(ms_pair * 1e3, 3), "GBps": round(gate.algo_bytes / (ms_pair * 1e-3) / 1e9, 1),
-        "note": "gate and up over one x as one matVecResidentBatch launch (the batch kernel, both ops' rows)"}
-    log(f"gate + up as one batch launch: {ms_pair * 1e3:.2f} us per GEMV "
-        f"({extra['c1_gate_up_batched']['GBps']} GB/s)")
-
-    # the same GEMVs through the contract ops zlm's executor calls: a burst of
-    # one (host x staged) + waitResident (host y read back), host wall time
-    cit = max(20, int(400 * WARM["launch_scale"]))
-    for g_, key in ((gate, "c1_gate_up_q8_0_12288x4096"), (down, "c1_down_q8_0_4096x12288")):
-        dev.time_contract_gemv(g_.res, zd.quant(g_.qt), g_.rows, g_.k, cit)
-        us = sorted(dev.time_contract_gemv(g_.res, zd.quant(g_.qt), g_.rows, g_.k, cit) for _ in range(3))[1]
-        extra[key]["contract_us"] = round(us, 2)
-        extra[key]["contract_GBps"] = round(g_.algo_bytes / (us * 1e-6) / 1e9, 1)
-    log(f"contract path (burst + waitResident, host x/y): gate/up {extra['c1_gate_up_q8_0_12288x4096']['contract_us']}"
-        f" us, down {extra['c1_down_q8_0_4096x12288']['contract_us']} us")
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            t = json.load(f)
-        traffic = t.get(ROOFLINE_KERNEL, {}).get("bytes_per_launch")
-
-    cpu = None
-    if not args.no_cpu:
-        log(f"CPU baseline (~{0.5 * args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(gate, 0.5 * args.cpu_seconds)
-        log(f"CPU ({cpu['cpu']}, {cpu['lanes']} lanes): {cpu['value']} GB/s on {cpu['cores']} threads, "
-            f"{cpu['one_thread']['value']} GB/s on 1; [4096, 8192] on 1 thread: " +
-            ", ".join(f"{n} {v['GBps_1_thread']} GB/s (zlm {v['zlm_published_GBps_1_thread']})"
-                      for n, v in cpu["published_shapes_1_thread"].items()))
-    for g in (gate, up, down):
-        g.free()
-
+def sections(dev, args, want, extra):
+    """The reported sections after the headline: the other configs' GEMVs, the
+    configs[4] GEMM, the small-M sweep and the configs[2] decode step (each
+    runs when want(section) says so); results go into `extra`."""
+    only = args.only
     # ---- the other GEMV configs (reported, not the headline) --------------------
-    if not args.quick:
+    if want("gemvs"):
         others = [
             ("c0_q4_0_4096x4096", synth.Q4_0, 4096, 4096),
             ("c3_q4_k_15360x3840", synth.Q4_K, 15360, 3840),
@@ -406,7 +282,7 @@ def main():
             g.free()
 
     # ---- prefill GEMM, Q4_0 12288x4096 x 512 tokens, int8 MFMA ---------
-    if not args.quick:
+    if want("gemm"):
         rows, k, m = 12288, 4096, 512
         w = synth.weights(synth.Q4_0, rows, k, 0x5A4C4D04)
         ncopy = max(1, math.ceil(MALL_DEFEAT_BYTES / w.size))
@@ -438,7 +314,7 @@ def main():
         dev.dev_free(o_dev)
 
     # ---- small token counts (verify / microbatch), as reference gpu/root_test.zig:651-696 ----
-    if not args.quick and not args.no_small_m:
+    if only is None and not args.quick and not args.no_small_m:
         sweep = {}
         for sname, qt, rows, k in (("q4_0_4096x4096", synth.Q4_0, 4096, 4096),
                                    ("q4_k_4096x4096", synth.Q4_K, 4096, 4096),
@@ -475,7 +351,7 @@ def main():
 
     # ---- decode step of a Qwen3-8B-shaped Q4_0 model, batch 1 ----------
     cfg = None
-    if not args.quick:
+    if want("decode"):
         from zlm_amd import decode as zdec
 
         cfg = zdec.QWEN3_8B
@@ -497,7 +373,7 @@ def main():
             log(f"c2 decode: {args.decode_eager} eager steps (profiling run, not timed)")
             model.free()
             cfg = None
-    if not args.quick and cfg is not None:
+    if want("decode") and cfg is not None:
         if zd.profiler_loaded():
             # the library refuses graph replays under a profiler (replays of
             # this step under rocprofv3's kernel trace aborted the process)
@@ -574,6 +450,165 @@ def main():
             c2cpu = cpu_decode_sample(cfg, 0.25 * args.cpu_seconds)
             extra["c2_decode_qwen3_8b_q4_0"]["cpu_baseline"] = c2cpu
             log(f"c2 CPU: {c2cpu['tok_per_s']} tok/s (projection GEMVs) on {c2cpu['cores']} threads")
+
+    return extra
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline workload only")
+    ap.add_argument("--cpu-seconds", type=float, default=16.0,
+                    help="CPU-baseline budget: half on the headline GEMV, a quarter each on configs[4] and [2]")
+    ap.add_argument("--decode-eager", type=int, default=0, metavar="N",
+                    help="run N eager decode steps instead of timing graph replays (for kernel-trace profiling)")
+    ap.add_argument("--decode-replays", type=int, default=30, metavar="N",
+                    help="graph replays per timed decode run (warm-up run + 3 timed runs of N)")
+    ap.add_argument("--no-long-context", action="store_true",
+                    help="skip the decode step at 8192 and 32768 cached positions")
+    ap.add_argument("--no-small-m", action="store_true",
+                    help="skip the small-token-count matMul sweep (its GEMVs share kernels with configs[0]/[3])")
+    ap.add_argument("--counters", action="store_true",
+                    help="short warm-ups and few launches per shape, for rocprofv3 --pmc passes (not a timing run)")
+    ap.add_argument("--only", choices=("roofline", "gemvs", "gemm", "decode"), default=None,
+                    help="run one section for a profiler: the roofline kernel's timing (configs[1] gate/up), the "
+                         "other configs' GEMVs, the configs[4] GEMM or the decode step; no JSON line")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
+                    help="also run the library copy kernel 5x over BYTES (for HBM traffic counter calibration)")
+    args = ap.parse_args()
+    if args.counters:
+        WARM["ms"], WARM["launch_scale"] = 0.0, 0.05
+    if args.gpus != 1:
+        print(f"bench.py: this backend runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU sharding is a design note, not a measured path)", file=sys.stderr)
+        sys.exit(2)
+
+    dev = zd.Device()
+    if not dev.available():
+        raise SystemExit(f"HIP backend unavailable: {dev.last_error()}")
+    log(f"device: {dev.device_name()}, {dev.cu_count()} CUs")
+    if args.calibrate_copy:
+        nbytes = (args.calibrate_copy // 16) * 16
+        a, b = dev.dev_malloc(nbytes), dev.dev_malloc(nbytes)
+        for _ in range(5):
+            dev.dev_copy(b, a, nbytes)
+        dev.dev_free(a)
+        dev.dev_free(b)
+        log(f"copy calibration: 5 x {nbytes} bytes")
+
+    only = args.only
+
+    def want(section: str) -> bool:
+        return (only is None and not args.quick) or only == section
+
+    if only in ("gemvs", "gemm", "decode"):
+        return sections(dev, args, want, {})
+
+    # ---- headline: configs[1], Q8_0 Qwen3-8B FFN GEMVs ------------------------------
+    step_w = 2 * synth.weight_bytes(synth.Q8_0, 12288, 4096) + synth.weight_bytes(synth.Q8_0, 4096, 12288)
+    copies = max(1, math.ceil(MALL_DEFEAT_BYTES / step_w))
+    log(f"C1: generating Q8_0 gate/up/down, {copies} resident copies each")
+    gate = Gemv(dev, "gate", synth.Q8_0, 12288, 4096, 0x5A4C4D01, copies)
+    up = Gemv(dev, "up", synth.Q8_0, 12288, 4096, 0x5A4C4D11, copies)
+    down = Gemv(dev, "down", synth.Q8_0, 4096, 12288, 0x5A4C4D21, copies)
+    step_descs = []
+    for c in range(copies):
+        step_descs += [gate.desc(c), up.desc(c), down.desc(c)]
+    step_bytes = gate.algo_bytes + up.algo_bytes + down.algo_bytes
+
+    def steps_of(n):  # n consecutive steps, step i on weight copy i % copies
+        out = []
+        for i in range(n):
+            out += [gate.desc(i), up.desc(i), down.desc(i)]
+        return out
+
+    # W warm-up steps, then untimed steps until >= 50 ms of GPU time have run
+    # since the host-side synthesis (the clocks ramp over the first
+    # milliseconds; a short warm-up alone reads several percent low), then
+    # exactly K timed steps.
+    steps = max(1, args.steps)
+    warmup = max(0, args.warmup)
+    clock_ms = dev.time_gemv_sequence(steps_of(warmup), 1) if warmup else 0.0
+    while clock_ms < WARM["ms"]:
+        clock_ms += dev.time_gemv_sequence(step_descs, max(1, 200 // copies))
+    ms_total = dev.time_gemv_sequence(steps_of(steps), 1)
+    ms_step = ms_total / steps
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"C1 step: {ms_step * 1e3:.2f} us -> {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak) over "
+        f"{steps} steps after {warmup} warm-up steps ({clock_ms:.1f} ms of untimed GPU work)")
+
+    # dominant kernel: the k=4096 gate/up GEMV, alone, same rotation
+    gu_descs = []
+    for c in range(copies):
+        gu_descs += [gate.desc(c), up.desc(c)]
+    gu_target = 4 * len(gu_descs) * 25
+    ms_gu = time_launches(dev, gu_descs, gu_target) / len(gu_descs)
+    gu_gbps = gate.algo_bytes / (ms_gu * 1e-3) / 1e9
+    if only == "roofline":
+        # the timed launches are the last 3 x timed_launches dispatches of the kernel
+        timed = max(1, int(gu_target * WARM["launch_scale"]) // len(gu_descs)) * len(gu_descs)
+        log(f"roofline kernel {ROOFLINE_KERNEL}: {ms_gu * 1e3:.3f} us per launch (HIP events, median of 3 runs of "
+            f"{timed} launches: the last {3 * timed} dispatches of the kernel) -> {gu_gbps:.1f} GB/s; "
+            f"profiler loaded: {zd.profiler_loaded()}")
+        print(json.dumps({"roofline_only": {"kernel": ROOFLINE_KERNEL, "avg_launch_us": round(ms_gu * 1e3, 4),
+                                            "timed_dispatches": 3 * timed, "GBps": round(gu_gbps, 1),
+                                            "profiler_loaded": zd.profiler_loaded()}}), flush=True)
+        for g in (gate, up, down):
+            g.free()
+        dev.deinit()
+        return
+    ms_dn = time_launches(dev, [down.desc(c) for c in range(copies)], 100 * copies) / copies
+    dn_gbps = down.algo_bytes / (ms_dn * 1e-3) / 1e9
+    log(f"gate/up GEMV {ms_gu * 1e3:.2f} us ({gu_gbps:.1f} GB/s); down GEMV {ms_dn * 1e3:.2f} us ({dn_gbps:.1f} GB/s)")
+
+    extra = {
+        "c1_gate_up_q8_0_12288x4096": {"us": round(ms_gu * 1e3, 3), "GBps": round(gu_gbps, 1)},
+        "c1_down_q8_0_4096x12288": {"us": round(ms_dn * 1e3, 3), "GBps": round(dn_gbps, 1)},
+    }
+    # gate and up over the same x as one matVecResidentBatch launch
+    pair = []
+    for c in range(copies):
+        pair += [gate.desc(c)[:4] + (gate.x_dev, gate.y_dev, 1), up.desc(c)[:4] + (gate.x_dev, up.y_dev, 0)]
+    ms_pair = time_launches(dev, pair, 4 * len(pair) * 25) / len(pair)
+    extra["c1_gate_up_batched"] = {
+        "us_per_gemv": round(ms_pair * 1e3, 3), "GBps": round(gate.algo_bytes / (ms_pair * 1e-3) / 1e9, 1),
+        "note": "gate and up over one x as one matVecResidentBatch launch (the batch kernel, both ops' rows)"}
+    log(f"gate + up as one batch launch: {ms_pair * 1e3:.2f} us per GEMV "
+        f"({extra['c1_gate_up_batched']['GBps']} GB/s)")
+
+    # the same GEMVs through the contract ops zlm's executor calls: a burst of
+    # one (host x staged) + waitResident (host y read back), host wall time
+    cit = max(20, int(400 * WARM["launch_scale"]))
+    for g_, key in ((gate, "c1_gate_up_q8_0_12288x4096"), (down, "c1_down_q8_0_4096x12288")):
+        dev.time_contract_gemv(g_.res, zd.quant(g_.qt), g_.rows, g_.k, cit)
+        us = sorted(dev.time_contract_gemv(g_.res, zd.quant(g_.qt), g_.rows, g_.k, cit) for _ in range(3))[1]
+        extra[key]["contract_us"] = round(us, 2)
+        extra[key]["contract_GBps"] = round(g_.algo_bytes / (us * 1e-6) / 1e9, 1)
+    log(f"contract path (burst + waitResident, host x/y): gate/up {extra['c1_gate_up_q8_0_12288x4096']['contract_us']}"
+        f" us, down {extra['c1_down_q8_0_4096x12288']['contract_us']} us")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f)
+        traffic = t.get(ROOFLINE_KERNEL, {}).get("bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"CPU baseline (~{0.5 * args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(gate, 0.5 * args.cpu_seconds)
+        log(f"CPU ({cpu['cpu']}, {cpu['lanes']} lanes): {cpu['value']} GB/s on {cpu['cores']} threads, "
+            f"{cpu['one_thread']['value']} GB/s on 1; [4096, 8192] on 1 thread: " +
+            ", ".join(f"{n} {v['GBps_1_thread']} GB/s (zlm {v['zlm_published_GBps_1_thread']})"
+                      for n, v in cpu["published_shapes_1_thread"].items()))
+    for g in (gate, up, down):
+        g.free()
+
+    sections(dev, args, want, extra)
 
     line = {
         "metric": METRIC,
