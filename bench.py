@@ -596,6 +596,15 @@ def main():
         with open(tpath) as f:
             t = json.load(f)
         traffic = t.get(ROOFLINE_KERNEL, {}).get("bytes_per_launch")
+    # the same kernel's average duration in the committed kernel trace of its
+    # timed launches: algorithmic bytes / that duration / peak
+    frac_profile, trace_ns = None, None
+    rpath = os.path.join(ROOT, "profiles", "roofline_trace.json")
+    if os.path.exists(rpath):
+        with open(rpath) as f:
+            trace_ns = json.load(f).get(ROOFLINE_KERNEL, {}).get("trace_avg_ns")
+        if trace_ns:
+            frac_profile = round(gate.algo_bytes / (trace_ns * 1e-9) / 1e9 / PEAK_GBPS, 4)
 
     cpu = None
     if not args.no_cpu:
@@ -638,6 +647,8 @@ def main():
             "peak": PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gu_gbps / PEAK_GBPS, 4),
+            "frac_profile": frac_profile,
+            "profile_avg_ns": trace_ns,
             "traffic": traffic,
             "algorithmic_bytes_per_launch": gate.algo_bytes,
             "avg_launch_us": round(ms_gu * 1e3, 3),
