@@ -213,6 +213,58 @@ def cpu_prefill_sample(w: np.ndarray, rows: int, k: int, budget_s: float):
                                       f"rangeOf, min of {reps} reps"}
 
 
+def split_efficiency(dev, threads: int) -> dict:
+    """measureSplitEfficiency (reference tuner/calibrate.zig:778-834) on this
+    device: a 32768 x 4096 Q4_0 resident GEMV through matVecResident alone,
+    then split -- matVecResidentAsync over rows [0, m/2) while `threads` CPU
+    workers run zlm's production sweep over [m/2, m), then waitResident --
+    min of 5 each after 32 warm-up calls; the ratio split rate / GPU rate is
+    the tuner's split coefficient (< 1: a split loses to the whole-GPU op)."""
+    import oracle
+
+    n, m = 4096, 32768
+    q = zd.quant(zd.Q4_0)
+    w = synth.weights(synth.Q4_0, m, n, 0x5A4C4DB0)
+    x = np.array([((i * 7 + 3) % 17 - 8) * 0.125 for i in range(n)], np.float32)
+    res = dev.upload_resident(w)
+    if res is None:
+        raise RuntimeError(dev.last_error())
+    out = np.zeros(m, np.float32)
+    for _ in range(32):
+        dev.mat_vec_resident(res, q, m, n, x, out)
+    dev.sync()
+    g = m // 2
+    rb = synth.row_bytes(synth.Q4_0, n)
+    w_cpu = w[g * rb:]
+    gpu_best = split_best = float("inf")
+    split_out = np.zeros(m, np.float32)
+    for _ in range(5):
+        t0 = time.perf_counter()
+        dev.mat_vec_resident(res, q, m, n, x, out)
+        dev.sync()
+        gpu_best = min(gpu_best, time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        h = dev.mat_vec_resident_async(res, q, g, n, x)
+        if h is None:
+            raise RuntimeError(dev.last_error())
+        oracle.fast_time_matvec(synth.Q4_0, w_cpu, n, m - g, x, threads, 1, out=split_out[g:])
+        if not dev.wait_resident(h, split_out, g):
+            raise RuntimeError(dev.last_error())
+        split_best = min(split_best, time.perf_counter() - t0)
+    dev.free_resident(res)
+    # the split's rows agree with the whole-GPU op's (fp32 summation order aside)
+    err = float(np.linalg.norm(split_out.astype(np.float64) - out) / np.linalg.norm(out))
+    if not err <= 1e-3:
+        raise AssertionError(f"split GEMV rel-L2 {err:.2e} against the whole-GPU GEMV")
+    return {"ratio": round(gpu_best / split_best, 4), "gpu_us": round(gpu_best * 1e6, 1),
+            "split_us": round(split_best * 1e6, 1), "gpu_GBps": round(w.nbytes / gpu_best / 1e9, 1),
+            "split_GBps": round(w.nbytes / split_best / 1e9, 1), "cpu_threads": threads,
+            "rel_l2_split_vs_gpu": err,
+            "note": "measureSplitEfficiency: Q4_0 32768x4096 through matVecResident (host x and y) vs "
+                    "matVecResidentAsync rows [0, m/2) + CPU production sweep rows [m/2, m) + waitResident, "
+                    "min of 5 host wall times each"}
+
+
 def cpu_decode_sample(cfg, budget_s: float):
     """configs[2] on the CPU: one token's projection GEMVs (q;k;v, o, gate, up,
     down per layer, times the layer count, plus the Q8_0 lm_head) with zlm's
@@ -614,6 +666,10 @@ def main():
             f"{cpu['one_thread']['value']} GB/s on 1; [4096, 8192] on 1 thread: " +
             ", ".join(f"{n} {v['GBps_1_thread']} GB/s (zlm {v['zlm_published_GBps_1_thread']})"
                       for n, v in cpu["published_shapes_1_thread"].items()))
+        extra["split_efficiency"] = split_efficiency(dev, cpu["cores"])
+        log(f"split probe (GPU rows [0, m/2) + {cpu['cores']} CPU threads [m/2, m)): "
+            f"{extra['split_efficiency']['split_us']} us against {extra['split_efficiency']['gpu_us']} us "
+            f"whole-GPU, ratio {extra['split_efficiency']['ratio']}")
     for g in (gate, up, down):
         g.free()
 

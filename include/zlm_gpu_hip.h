@@ -149,7 +149,13 @@ int32_t zlm_gpu_mat_vec_resident_async(zlm_device *dev, zlm_resident *res, uint3
  * pointer and length, or they are refused. */
 int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows,
                                              size_t k, const float *x, size_t x_len, bool first);
-/* Device.matVecGateUpResidentBurstAsync (vulkan/root.zig:150-164). */
+/* Device.matVecGateUpResidentBurstAsync (vulkan/root.zig:150-164).  `variant`
+ * (a GpuVariant code; 0 keeps the quant code's own) selects the fused kernel's
+ * row tile as it does for the plain GEMV: u4/u8 four output rows per wave
+ * tile, un2/un4 two, the others one.  q4_0, q4_1 and q8_0 have the wider
+ * tiles (the quants the reference grid lists gate_up variants for); other
+ * quants run the one-row tile for every variant.  Both MLP ops apply
+ * `variant` to their gate_up part. */
 int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device *dev, zlm_resident *res_gate,
                                                      zlm_resident *res_up, uint32_t quant, size_t rows,
                                                      size_t k, const float *x, size_t x_len, uint32_t act,

@@ -61,6 +61,38 @@ def test_gate_up_matches_oracle(dev, qt, rows, k, act):
     dev.free_resident(ru)
 
 
+# GpuVariant codes select the fused kernel's row tile (u4/u8 four output rows
+# per wave tile, un2/un4 two, the others one) for the quants the reference
+# grid lists gate_up variants for; ragged row counts leave partial tiles.
+@pytest.mark.parametrize("qt", [synth.Q4_0, synth.Q4_1, synth.Q8_0], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("variant", [zd.PLAIN, zd.UN2, zd.U4, zd.SUB], ids=["plain", "un2", "u4", "sub"])
+@pytest.mark.parametrize("rows,k", [(333, 4096), (320, 1024), (41, 8192), (5, 256), (12288, 4096)])
+def test_gate_up_variants_match_oracle(dev, qt, variant, rows, k):
+    _say(f"gate_up variant {variant} {NAMES[qt]} rows={rows} k={k}")
+    wg = synth.weights(qt, rows, k, seed=3 * rows + k)
+    wu = synth.weights(qt, rows, k, seed=3 * rows + k + 1)
+    x = synth.activation(k + 9, k)
+    want = oracle.gate_up(qt, wg, wu, k, rows, x, zd.GELU)
+    rg, ru = dev.upload_resident(wg), dev.upload_resident(wu)
+    h = dev.mat_vec_gate_up_resident_burst_async(rg, ru, zd.quant(qt), rows, k, x, zd.GELU, variant, True)
+    assert h is not None, dev.last_error()
+    out = np.full(rows, np.nan, np.float32)
+    assert dev.wait_resident(h, out, rows), dev.last_error()
+    assert rel_l2(out, want) <= REL_L2
+    # the MLP op applies the variant to its gate_up: the down GEMV (64 rows,
+    # k = ffn = rows) over the gate_up result
+    if rows % 32 == 0 and rows <= 4096:
+        wd = synth.weights(qt, 64, rows, seed=7)
+        rd = dev.upload_resident(wd)
+        h = dev.mat_vec_mlp_resident_burst_async(rg, ru, rd, zd.quant(qt), 64, k, rows, x, zd.GELU, variant, True)
+        got = np.zeros(64, np.float32)
+        assert h is not None and dev.wait_resident(h, got, 64), dev.last_error()
+        assert rel_l2(got, oracle.matvec(qt, wd, rows, 64, want)) <= REL_L2
+        dev.free_resident(rd)
+    dev.free_resident(rg)
+    dev.free_resident(ru)
+
+
 def test_gate_up_reference_shape(dev):
     """The reference GPU test's gate_up case: 64 rows x k=256 q4_0, x[i] = (i%11)*0.1-0.5."""
     rows, k = 64, 256

@@ -145,7 +145,7 @@ def test_gemm_scratch_outlives_its_graph(fresh):
         eager = np.zeros(m_small * rows, np.float32)
         dev.dev_download(eager, d_os)
         want = oracle.matmul_int(synth.Q4_0, w, k, rows, m_small, x_small)
-        assert rel_l2(eager, want) <= 1e-5
+        assert rel_l2(eager.reshape(m_small, rows), want) <= 1e-5
         assert dev.capture_begin(), dev.last_error()
         try:
             ok = dev.mat_mul_enqueue(res, q, rows, k, m_small, d_xs, d_os)
@@ -169,7 +169,7 @@ def test_gemm_scratch_outlives_its_graph(fresh):
         assert dev.mat_mul_enqueue(res, q, rows, k, m_big, d_xb, d_ob), dev.last_error()
         got = np.zeros(m_big * rows, np.float32)
         dev.dev_download(got, d_ob)
-        assert rel_l2(got, oracle.matmul_int(synth.Q4_0, w, k, rows, m_big, x_big)) <= 1e-5
+        assert rel_l2(got.reshape(m_big, rows), oracle.matmul_int(synth.Q4_0, w, k, rows, m_big, x_big)) <= 1e-5
         assert dev.release_gemm_tiles(res), dev.last_error()
     finally:
         if graph is not None:

@@ -1684,6 +1684,25 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     ZLM_GEMVX(zlm_gemv_##QN##_normpair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_NORM, EPI_PAIR)        \
     ZLM_GEMVX(zlm_gemv_##QN##_resid_##SFX, QT, KCAP, 1, STEPS, EXACT, PRO_PLAIN, EPI_RESID)
 
+// The gate_up pair form with two and four output rows per wave tile
+// (zlm_gemv_<quant>_pair_<SFX>_r2 / _r4: RT 4 and 8, gate rows then up rows):
+// the row tiles the contract's GpuVariant codes select for the fused gate_up
+// (the reference's spec-constant gate_up variants, gpu/kernels/grid.zig:41-53).
+#define ZLM_GEMVX_PAIR_TILES(QN, QT, KCAP, STEPS, EXACT, SFX)                                        \
+    ZLM_GEMVX(zlm_gemv_##QN##_pair_##SFX##_r2, QT, KCAP, 4, STEPS, EXACT, PRO_PLAIN, EPI_PAIR)       \
+    ZLM_GEMVX(zlm_gemv_##QN##_pair_##SFX##_r4, QT, KCAP, 8, STEPS, EXACT, PRO_PLAIN, EPI_PAIR)
+#define ZLM_GEMVX_PAIR_TILES_Q4(QN, QT)                       \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 4096, 1, true, s1)           \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 4096, 2, true, s2)           \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 8192, 3, true, s3)           \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 8192, 4, true, s4)           \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 32768, 4, false, g)
+#define ZLM_GEMVX_PAIR_TILES_Q8(QN, QT)                       \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 4096, 2, true, s2)           \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 4096, 3, true, s3)           \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 4096, 4, true, s4)           \
+    ZLM_GEMVX_PAIR_TILES(QN, QT, 32768, 8, false, g)
+
 // q4_0 / q4_k / q6_k: KCAP = 2048 * STEPS rounded up to a tier.
 #define ZLM_GEMV_Q4(QN, QT)                                         \
     ZLM_GEMV_Q4_COMMON(QN, QT)                                      \

@@ -5,6 +5,7 @@
 
 ZLM_GEMV_Q4(q4_0, Q4_0)
 ZLM_GEMVX_Q4(q4_0, Q4_0)
+ZLM_GEMVX_PAIR_TILES_Q4(q4_0, Q4_0)
 ZLM_GEMVX_FORMS(q4_0, Q4_0, 16384, 6, true, s6)
 
 // The residual form with two-row tiles, taken for launches of at most 8192

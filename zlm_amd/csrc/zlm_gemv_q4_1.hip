@@ -5,5 +5,6 @@
 
 ZLM_GEMV_Q4_COMMON(q4_1, Q4_1)
 ZLM_GEMVX_Q4(q4_1, Q4_1)
+ZLM_GEMVX_PAIR_TILES_Q4(q4_1, Q4_1)
 
 ZLM_GEMV_MULTI_Q4(q4_1, Q4_1)

@@ -5,6 +5,7 @@
 
 ZLM_GEMV_Q8(q8_0, Q8_0)
 ZLM_GEMVX_Q8(q8_0, Q8_0)
+ZLM_GEMVX_PAIR_TILES_Q8(q8_0, Q8_0)
 
 // Split-K form of the FFN down projection (k = 12288): 12-wave workgroups,
 // one per CU, each wave one chunk step of two rows per tile.  Measured on

@@ -26,6 +26,7 @@
 #include <time.h>
 
 #include <algorithm>
+#include <cctype>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -84,6 +85,12 @@ const QuantInfo* quant_info(uint32_t quant) {
 
 uint32_t variant_of(uint32_t quant) { return (quant >> 8) & 0xffu; }
 
+// A fused op's quant code carrying the op's `variant` argument (a GpuVariant
+// code; 0 keeps whatever variant the quant code itself carries).
+uint32_t with_variant(uint32_t quant, uint32_t variant) {
+    return variant ? ((quant & 0xffu) | ((variant & 0xffu) << 8)) : quant;
+}
+
 // GEMV kernels: 4 waves (256 threads) per workgroup unless an instance's launch
 // bounds say otherwise; k up to 32768.
 constexpr size_t kMaxK = 32768;
@@ -114,6 +121,7 @@ struct GemvKernel {
     int threads = 256;     // the kernel's launch bounds
     int waves_per_cu = 0;  // grid target of a prefetching instance; 0 = gemv_grid's rule
     bool struct_args = false;  // takes one GemvArgs (fused forms, prefetching instances)
+    int role = 0;              // kernel_role(): the form it computes, or kRoleMulti
     bool split = false;        // split-K: the workgroup's waves share each tile of rt rows
     bool xq = false;           // sums in another order than the batch kernel (int8-plane x or split-K)
 };
@@ -500,6 +508,57 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
 
 // Look up (and cache) a GEMV entry point by name in its quant's code object;
 // the block size is the kernel's launch bound.
+// What a GEMV entry point computes and how it takes its arguments, read from
+// its name zlm_gemv_<quant>_<rest>: <rest> "multi_..." is the batch kernel,
+// "pair_" / "normpair_" / "norm_" / "resid_" a fused form (ZLM_FORM_*), anything
+// else the plain GEMV.  Only the plain exact-steps and generic instances
+// (r<RT>_s<STEPS>, r<RT>_g) take separate arguments; every other instance
+// takes one GemvArgs.  The host checks a cached kernel's role before each
+// launch, so a kernel picked for one form can never be launched as another.
+constexpr int kRoleMulti = 16;
+
+void kernel_role(const char* name, int slot, int* role, bool* struct_args) {
+    const char* rest = name + strlen("zlm_gemv_") + strlen(kQuantNames[slot]) + 1;
+    static const struct {
+        const char* prefix;
+        int role;
+    } kForms[] = {{"multi_", kRoleMulti},
+                  {"pair_", ZLM_FORM_PAIR},
+                  {"normpair_", ZLM_FORM_NORMPAIR},
+                  {"norm_", ZLM_FORM_NORM},
+                  {"resid_", ZLM_FORM_RESID}};
+    for (const auto& f : kForms) {
+        if (strncmp(rest, f.prefix, strlen(f.prefix)) == 0) {
+            *role = f.role;
+            *struct_args = true;
+            return;
+        }
+    }
+    *role = ZLM_FORM_PLAIN;
+    // r<digits>_s<digits> or r<digits>_g, nothing after
+    const char* p = rest;
+    bool separate = *p == 'r';
+    if (separate) {
+        p++;
+        separate = isdigit(static_cast<unsigned char>(*p));
+        while (isdigit(static_cast<unsigned char>(*p))) p++;
+        separate = separate && *p == '_';
+        if (separate) {
+            p++;
+            if (*p == 'g') {
+                p++;
+            } else if (*p == 's' && isdigit(static_cast<unsigned char>(p[1]))) {
+                p++;
+                while (isdigit(static_cast<unsigned char>(*p))) p++;
+            } else {
+                separate = false;
+            }
+            separate = separate && *p == '\0';
+        }
+    }
+    *struct_args = !separate;
+}
+
 const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, int steps, int waves_per_cu = 0,
                             bool struct_args = false, bool split = false, bool xq = false) {
     auto it = d->gemv.find(name);
@@ -509,7 +568,10 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
             g.rt = rt;
             g.steps = steps;
             g.waves_per_cu = waves_per_cu;
-            g.struct_args = struct_args;
+            bool by_name = false;
+            kernel_role(name, slot, &g.role, &by_name);
+            g.struct_args = by_name;
+            (void)struct_args;
             g.split = split;
             g.xq = xq || split;
             int mt = 0;
@@ -585,16 +647,20 @@ bool resid_two_rows(const QuantInfo* qi, int steps, size_t rows) {
 // tile or form, rows >= 65536, rows <= 8192); the device caches their result
 // per class so an op's host path is one hash lookup (the name lookups cost
 // ~1 us per launch, most of a small GEMV's enqueue).
-uint64_t pick_key(const QuantInfo* qi, size_t k, int rt_or_form, size_t rows) {
+// The kernel picked per shape class: (k, quant slot, what is picked, its
+// parameter, row-count class) in disjoint bit fields.
+enum PickKind : uint64_t { kPickPlain = 0, kPickForm = 1, kPickPairTile = 2 };
+
+uint64_t pick_key(const QuantInfo* qi, size_t k, PickKind kind, int param, size_t rows) {
     const uint64_t rows_class = rows >= 65536 ? 2 : rows <= 8192 ? 1 : 0;
-    return (static_cast<uint64_t>(k) << 16) | (static_cast<uint64_t>(qi->slot) << 8) |
-           (static_cast<uint64_t>(rt_or_form & 0x3f) << 2) | rows_class;
+    return (static_cast<uint64_t>(k) << 24) | (static_cast<uint64_t>(qi->slot) << 16) |
+           (static_cast<uint64_t>(kind) << 12) | (static_cast<uint64_t>(param & 0x3ff) << 2) | rows_class;
 }
 
 const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows);
 
 const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows) {
-    const uint64_t key = pick_key(qi, k, rt, rows);
+    const uint64_t key = pick_key(qi, k, kPickPlain, rt, rows);
     auto it = d->picks.find(key);
     if (it != d->picks.end()) return it->second;
     const GemvKernel* g = pick_gemv_named(d, qi, k, rt, rows);
@@ -703,6 +769,7 @@ bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     const GemvKernel* gk = nullptr;
     if (!prepare_gemv(d, r, quant, rows, k, &f, &grid, &block, &gk)) return false;
     const QuantInfo* qi = quant_info(quant);
+    if (gk->role != ZLM_FORM_PLAIN) return fail(d, "internal: picked kernel (role %d) is not a plain GEMV", gk->role);
     const uint8_t* w = r->payload;
     const uint16_t* s = r->scales;
     uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->kblock);
@@ -753,6 +820,7 @@ bool enqueue_multi(zlm_device* d, const QuantInfo* qi, size_t k, const float* x_
         gk = find_gemv(d, qi->slot, nm, 1, 0);
     }
     if (!gk) return fail(d, "no batch GEMV kernel for quant %u", qi->type);
+    if (gk->role != kRoleMulti) return fail(d, "internal: picked kernel (role %d) is not the batch GEMV", gk->role);
     GemvMultiArgsHost a = {};
     uint64_t total = 0;
     for (size_t i = 0; i < n; i++) {
@@ -785,7 +853,7 @@ bool batch_one_launch(zlm_device* d, const QuantInfo* qi, size_t k) {
 const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form, size_t rows);
 
 const GemvKernel* pick_gemvx(zlm_device* d, const QuantInfo* qi, size_t k, uint32_t form, size_t rows) {
-    const uint64_t key = pick_key(qi, k, 32 + static_cast<int>(form), rows);  // forms apart from row tiles
+    const uint64_t key = pick_key(qi, k, kPickForm, static_cast<int>(form), rows);
     auto it = d->picks.find(key);
     if (it != d->picks.end()) return it->second;
     const GemvKernel* g = pick_gemvx_named(d, qi, k, form, rows);
@@ -821,6 +889,29 @@ const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k,
 
 // Enqueue one GEMV op on device buffers: validate the residents, pick the
 // kernel of the op's form and launch it on the device stream.
+// The gate_up pair form with `rp` output rows per wave tile (2 or 4), the tile
+// a GpuVariant selects (rt_for_variant); built for q4_0, q4_1 and q8_0, the
+// quants the reference grid lists gate_up variants for
+// (gpu/kernels/grid.zig:150-254).  Null where no such instance exists: the
+// default tile runs.
+const GemvKernel* pick_pair_tile(zlm_device* d, const QuantInfo* qi, size_t k, int rp, size_t rows) {
+    const uint64_t key = pick_key(qi, k, kPickPairTile, rp, rows);
+    auto it = d->picks.find(key);
+    if (it != d->picks.end()) return it->second;
+    const size_t chunks = k / qi->chunk_elems;
+    const int steps = static_cast<int>((chunks + 63) / 64);
+    const char* qn = kQuantNames[qi->slot];
+    char nm[96];
+    snprintf(nm, sizeof nm, "zlm_gemv_%s_pair_s%d_r%d", qn, steps, rp);
+    const GemvKernel* g = find_gemv(d, qi->slot, nm, 2 * rp, steps);
+    if (!g) {
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_pair_g_r%d", qn, rp);
+        g = find_gemv(d, qi->slot, nm, 2 * rp, 0);
+    }
+    d->picks.emplace(key, g);
+    return g;
+}
+
 bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     if (!d || !d->avail) return fail(d, "device unavailable");
     if (op.form > ZLM_FORM_RESID) return fail(d, "unknown GEMV form %u", op.form);
@@ -836,8 +927,13 @@ bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     if (pair && op.act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", op.act);
     if (!check_resident(d, op.w, qi, op.rows, op.k)) return false;
     if (pair && !check_resident(d, op.w_up, qi, op.rows, op.k)) return false;
-    const GemvKernel* gk = pick_gemvx(d, qi, op.k, op.form, op.rows);
+    const int vrp = op.form == ZLM_FORM_PAIR ? rt_for_variant(variant_of(op.quant)) : 1;
+    const GemvKernel* gk = vrp > 1 ? pick_pair_tile(d, qi, op.k, vrp, op.rows) : nullptr;
+    if (!gk) gk = pick_gemvx(d, qi, op.k, op.form, op.rows);
     if (!gk) return fail(d, "no %s GEMV kernel for quant %u k=%zu", kFormNames[op.form], qi->type, op.k);
+    if (gk->role != static_cast<int>(op.form) || !gk->struct_args)
+        return fail(d, "internal: picked kernel (role %d) does not compute the %s form", gk->role,
+                    kFormNames[op.form]);
     GemvArgsHost a;
     a.w0 = op.w->payload;
     a.d0 = op.w->scales;
@@ -1505,7 +1601,6 @@ extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, z
                                                                 uint32_t quant, size_t rows, size_t k,
                                                                 const float* x, size_t x_len, uint32_t act,
                                                                 uint32_t variant, bool first) {
-    (void)variant;
     if (!contract_ready(d)) return ZLM_NULL_HANDLE;
     if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
     if (act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", act), ZLM_NULL_HANDLE;
@@ -1519,7 +1614,7 @@ extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, z
     if (!xd) return ZLM_NULL_HANDLE;
     zlm_gemv_op op = {};
     op.form = ZLM_FORM_PAIR;
-    op.quant = quant;
+    op.quant = with_variant(quant, variant);
     op.w = rg;
     op.w_up = ru;
     op.rows = rows;
@@ -1537,7 +1632,6 @@ extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, 
                                                                  size_t rows, size_t k, size_t ffn, const float* x,
                                                                  size_t x_len, uint32_t act, uint32_t variant,
                                                                  bool first) {
-    (void)variant;
     if (!contract_ready(d)) return ZLM_NULL_HANDLE;
     if (!x || x_len != k) return fail(d, "bad x"), ZLM_NULL_HANDLE;
     if (act > ZLM_ACT_GELU) return fail(d, "unknown activation %u", act), ZLM_NULL_HANDLE;
@@ -1552,7 +1646,8 @@ extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, 
     if (!prepare_slot(d, s, rows)) return ZLM_NULL_HANDLE;
     const float* xd = stage_burst(d, x, x_len, first);
     if (!xd) return ZLM_NULL_HANDLE;
-    if (!enqueue_mlp(d, s, rg, ru, rd, gu_quant, down_quant, rows, k, ffn, xd, act) || !finish_slot(d, s, rows))
+    if (!enqueue_mlp(d, s, rg, ru, rd, with_variant(gu_quant, variant), down_quant, rows, k, ffn, xd, act) ||
+        !finish_slot(d, s, rows))
         return ZLM_NULL_HANDLE;
     return make_handle(d, s);
 }
@@ -1579,8 +1674,8 @@ extern "C" void zlm_gpu_sync(zlm_device* d) {
 // every GpuVariant maps to one of this backend's row tiles (rt_for_variant).
 // Every quant the backend runs is probed (q4_0, q4_1, q8_0, q4_k, q6_k, f32,
 // f16, bf16) and the fused gate_up over q4_0, q8_0 and q4_1, as the
-// reference's probe does; the fused gate_up has one kernel per shape, so its
-// variants all measure that kernel.
+// reference's probe does; the gate_up variants map to the fused kernel's row
+// tiles the same way (one, two or four output rows per wave tile).
 
 namespace {
 
