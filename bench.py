@@ -641,6 +641,17 @@ def main():
         extra[key]["contract_GBps"] = round(g_.algo_bytes / (us * 1e-6) / 1e9, 1)
     log(f"contract path (burst + waitResident, host x/y): gate/up {extra['c1_gate_up_q8_0_12288x4096']['contract_us']}"
         f" us, down {extra['c1_down_q8_0_4096x12288']['contract_us']} us")
+    # where a contract GEMV's host wall time goes: the submit call, the
+    # waitResident call, and the GPU's time between events around the submission
+    split = [dev.time_contract_gemv_split(gate.res, zd.quant(gate.qt), gate.rows, gate.k, cit) for _ in range(3)]
+    split = sorted(split, key=lambda v: v["total_us"])[1]
+    extra["c1_gate_up_q8_0_12288x4096"]["contract_split_us"] = {
+        key: round(v, 2) for key, v in split.items()}
+    extra["c1_gate_up_q8_0_12288x4096"]["contract_split_us"]["note"] = (
+        "per op: total host wall time = submit (x into the slot's pinned buffer, copy kernel and GEMV enqueued) + "
+        "wait (waitResident: the rest of the GPU's run, wake-up, y copied out); gpu = HIP events around the "
+        "submission (copy kernel + GEMV); the two extra events add ~2-5 us to the total")
+    log(f"contract split (gate/up): {split}")
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")

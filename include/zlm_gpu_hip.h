@@ -280,6 +280,13 @@ bool zlm_gpu_time_gemv_sequence(zlm_device *dev, const zlm_gemv_desc *descs, siz
  * wall microseconds per op. */
 bool zlm_gpu_time_contract_gemv(zlm_device *dev, zlm_resident *const *res, size_t n_res, uint32_t quant, size_t rows,
                                 size_t k, int iters, double *us);
+/* The same op's host wall time split (per op, microseconds): out[0] total,
+ * out[1] the submit call (x copied into the slot's pinned buffer, the copy
+ * kernel and the GEMV enqueued), out[2] the waitResident call (the GPU's run
+ * as far as it is not yet done, the host's wake-up, y copied out), out[3] the
+ * GPU time between events around the submission (copy kernel + GEMV). */
+bool zlm_gpu_time_contract_gemv_split(zlm_device *dev, zlm_resident *const *res, size_t n_res, uint32_t quant,
+                                      size_t rows, size_t k, int iters, double *out);
 /* One layer's projections as separate residents (the GGUF tensors zlm uploads). */
 typedef struct {
     zlm_resident *q, *k, *v, *o, *gate, *up, *down;
@@ -400,6 +407,23 @@ bool zlm_gpu_profiler_loaded(const char *maps_path);
 /* Device bytes the library itself holds on `dev` (staging, attention and GEMM
  * scratch; not residents, not the fixed no-alloc array). */
 uint64_t zlm_gpu_scratch_device_bytes(const zlm_device *dev);
+
+/* ---- launch log (no reference counterpart; tests and diagnostics) ----
+ * Every launch is checked on the host against the kernel-dispatch limits
+ * (workgroup of 64..1024 work-items in whole waves; grid x workgroup below
+ * 2^32 work-items in x, at most 65536 workgroups in y and z; the kernel's
+ * static LDS at most 160 KiB) and fails with its parameters otherwise.  With
+ * the log on, each launch's parameters are recorded (at most 65536 records;
+ * enabling or disabling clears the log); zlm_gpu_launch_log_read copies up to
+ * `max` records and returns how many there are. */
+typedef struct {
+    const char *what;     /* the op's label (static string) */
+    uint32_t grid_x, grid_y, grid_z;  /* workgroups */
+    uint32_t block;       /* work-items per workgroup */
+    uint32_t lds_bytes;   /* the kernel's static LDS */
+} zlm_launch_record;
+bool zlm_gpu_launch_log(zlm_device *dev, bool enable);
+size_t zlm_gpu_launch_log_read(const zlm_device *dev, zlm_launch_record *out, size_t max);
 
 /* ---- synthetic data generated in HBM (benchmark, large-shape tests) ----
  * A resident of `n_blocks` raw GGUF blocks (q4_0: f16 d + 16 random bytes;

@@ -208,6 +208,10 @@ struct zlm_device {
     // that reference it: a graph replays with the addresses it was captured
     // with.
     uint32_t capture_uses = 0;
+    // static LDS bytes per kernel (launch checks) and the optional launch log
+    std::unordered_map<hipFunction_t, uint32_t> lds_bytes;
+    bool log_launches = false;
+    std::vector<zlm_launch_record> launch_log;
     int attn_graphs = 0;
     int gemm_graphs = 0;
     // this device's address of the fixed static scratch (the no-alloc entry
@@ -443,8 +447,44 @@ bool ensure_bytes(zlm_device* d, uint8_t*& p, uint64_t& cap, uint64_t n) {
     return true;
 }
 
+// Every kernel launch of the library: the dispatch checked on the host
+// against what an AQL kernel-dispatch packet can carry (workgroup of 1..1024
+// work-items, a whole number of 64-lane waves; each grid dimension's work-item
+// count, workgroups x workgroup size, below 2^32; the kernel's static LDS
+// within the CU's 160 KiB), so a launch outside them fails here with its
+// parameters instead of reaching the queue; then recorded in the launch log
+// when that is on.
+constexpr uint64_t kMaxLds = 160 * 1024;
+constexpr size_t kLaunchLogMax = 1 << 16;
+
+uint32_t static_lds(zlm_device* d, hipFunction_t f) {
+    auto it = d->lds_bytes.find(f);
+    if (it != d->lds_bytes.end()) return it->second;
+    int v = 0;
+    if (hipFuncGetAttribute(&v, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, f) != hipSuccess) {
+        hipGetLastError();
+        v = 0;
+    }
+    d->lds_bytes.emplace(f, static_cast<uint32_t>(v));
+    return static_cast<uint32_t>(v);
+}
+
+bool launch3(zlm_device* d, hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned block, void** args,
+             const char* what) {
+    if (!f) return fail(d, "%s: kernel not loaded", what);
+    const uint32_t lds = static_lds(d, f);
+    const bool dims_ok = gx > 0 && gy > 0 && gz > 0 && block >= 64 && block <= 1024 && block % 64 == 0;
+    const uint64_t wx = static_cast<uint64_t>(gx) * block;
+    if (!dims_ok || wx >= (1ull << 32) || gy > 65536 || gz > 65536 || lds > kMaxLds)
+        return fail(d, "%s: launch outside the dispatch limits (grid %u x %u x %u, block %u, LDS %u bytes)", what,
+                    gx, gy, gz, block, lds);
+    if (d->log_launches && d->launch_log.size() < kLaunchLogMax)
+        d->launch_log.push_back({what, gx, gy, gz, block, lds});
+    return ok(d, hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, 0, d->stream, args, nullptr), what);
+}
+
 bool launch(zlm_device* d, hipFunction_t f, unsigned grid, unsigned block, void** args, const char* what) {
-    return ok(d, hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, d->stream, args, nullptr), what);
+    return launch3(d, f, grid, 1, 1, block, args, what);
 }
 
 // Bytes of the device layout of `nblk` blocks: payload rounded to 256 B, then scales.
@@ -1191,19 +1231,17 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
                           : qi->type == ZLM_GGML_Q4_1 ? d->gemm_small_q4_1
                                                       : d->gemm_small_q4_k;
         const unsigned threads = with_min ? 8 * 64 : 16 * 64;
-        return ok(d, hipModuleLaunchKernel(f, static_cast<unsigned>((rows + 31) / 32), 1, 1, threads, 1, 1, 0,
-                                           d->stream, args, nullptr),
-                  "gemm small");
+        return launch3(d, f, static_cast<unsigned>((rows + 31) / 32), 1, 1, threads, args, "gemm small");
     }
     const unsigned gx = static_cast<unsigned>((rows + 63) / 64), gy = static_cast<unsigned>((m + 127) / 128);
     if (with_min) {
         void* args[] = {&wq, &ws, &qx, &dx, &ds, &out_dev, &rows32, &m32, &nb32, &mt32};
         hipFunction_t f = qi->type == ZLM_GGML_Q4_1 ? d->gemm_q4_1 : d->gemm_q4_k;
-        return ok(d, hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d->stream, args, nullptr), "gemm");
+        return launch3(d, f, gx, gy, 1, 256, args, "gemm");
     }
     void* args[] = {&wq, &ws, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
     hipFunction_t f = qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0 : d->gemm_q4_0;
-    return ok(d, hipModuleLaunchKernel(f, gx, gy, 1, 256, 1, 1, 0, d->stream, args, nullptr), "gemm");
+    return launch3(d, f, gx, gy, 1, 256, args, "gemm");
 }
 
 }  // namespace
@@ -2108,6 +2146,46 @@ extern "C" bool zlm_gpu_time_contract_gemv(zlm_device* d, zlm_resident* const* r
     return true;
 }
 
+extern "C" bool zlm_gpu_time_contract_gemv_split(zlm_device* d, zlm_resident* const* res, size_t n_res,
+                                                 uint32_t quant, size_t rows, size_t k, int iters, double* out) {
+    if (!contract_ready(d) || !res || n_res == 0 || iters < 1 || !out) return false;
+    std::vector<float> x(k), y(rows);
+    for (size_t i = 0; i < k; i++) x[i] = static_cast<float>(static_cast<int>((i * 7 + 3) % 17) - 8) * 0.125f;
+    for (size_t i = 0; i < n_res; i++)
+        if (!zlm_gpu_mat_vec_resident(d, res[i], quant, rows, k, x.data(), k, y.data(), rows)) return false;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (!ok(d, hipEventCreate(&e0), "event") || !ok(d, hipEventCreate(&e1), "event")) {
+        if (e0) hipEventDestroy(e0);
+        return false;
+    }
+    double total = 0, submit = 0, wait = 0, gpu = 0;
+    bool good = true;
+    for (int it = 0; it < iters && good; it++) {
+        const double t0 = now_ns();
+        good = ok(d, hipEventRecord(e0, d->stream), "record");
+        const int32_t h =
+            zlm_gpu_mat_vec_resident_burst_async(d, res[it % n_res], quant, rows, k, x.data(), k, true);
+        good = good && h != ZLM_NULL_HANDLE && ok(d, hipEventRecord(e1, d->stream), "record");
+        const double t1 = now_ns();
+        good = good && zlm_gpu_wait_resident(d, h, y.data(), rows, rows);
+        const double t2 = now_ns();
+        float ms = 0.0f;
+        good = good && ok(d, hipEventSynchronize(e1), "sync") && ok(d, hipEventElapsedTime(&ms, e0, e1), "elapsed");
+        total += t2 - t0;
+        submit += t1 - t0;
+        wait += t2 - t1;
+        gpu += ms * 1e6;
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (!good) return false;
+    out[0] = total / 1e3 / iters;
+    out[1] = submit / 1e3 / iters;
+    out[2] = wait / 1e3 / iters;
+    out[3] = gpu / 1e3 / iters;
+    return true;
+}
+
 extern "C" bool zlm_gpu_time_contract_decode(zlm_device* d, const zlm_contract_layer* layers, size_t n_layers,
                                              uint32_t quant, size_t hidden, size_t q_rows, size_t kv_rows,
                                              size_t ffn, zlm_resident* lm_head, uint32_t lm_quant, size_t vocab,
@@ -2206,9 +2284,7 @@ bool enqueue_attn_merge(zlm_device* d, float* part, uint32_t nsplit, uint32_t n_
     void* args[] = {&part, &nsplit, &out};
     if (nsplit > 64) {
         const unsigned waves = std::min<unsigned>(16u, (nsplit + 31) / 32);
-        return ok(d, hipModuleLaunchKernel(d->attn_combine_wide, n_heads, 2, 1, 64 * waves, 1, 1, 0, d->stream, args,
-                                           nullptr),
-                  "attention combine");
+        return launch3(d, d->attn_combine_wide, n_heads, 2, 1, 64 * waves, args, "attention combine wide");
     }
     return launch(d, d->attn_combine, n_heads, 256, args, "attention combine");
 }
@@ -2232,10 +2308,7 @@ bool enqueue_attn_decode(zlm_device* d, const float* qkv, const float* q_norm_w,
     {
         void* args[] = {&qkv, &q_norm_w, &k_norm_w, &n_heads, &n_kv_heads, &eps, &freq_base, &pos, &k_cache,
                         &v_cache, &max_seq, &scale, &part, &nsplit};
-        if (!ok(d, hipModuleLaunchKernel(d->attn_decode, n_kv_heads, nsplit, 1, 256, 1, 1, 0, d->stream, args,
-                                         nullptr),
-                "attention decode"))
-            return false;
+        if (!launch3(d, d->attn_decode, n_kv_heads, nsplit, 1, 256, args, "attention decode")) return false;
     }
     return enqueue_attn_merge(d, part, nsplit, n_heads, out);
 }
@@ -2291,10 +2364,7 @@ extern "C" bool zlm_gpu_attention_enqueue(zlm_device* d, const float* q, const u
     float* part = d->attn_part;
     {
         void* args[] = {&q, &k_cache, &v_cache, &n_heads, &n_kv_heads, &pos, &max_seq, &scale, &part, &nsplit};
-        if (!ok(d, hipModuleLaunchKernel(d->attn_partial, n_kv_heads, nsplit, 1, 256, 1, 1, 0, d->stream, args,
-                                         nullptr),
-                "attention"))
-            return false;
+        if (!launch3(d, d->attn_partial, n_kv_heads, nsplit, 1, 256, args, "attention")) return false;
     }
     return enqueue_attn_merge(d, part, nsplit, n_heads, out);
 }
@@ -2362,6 +2432,21 @@ extern "C" zlm_graph* zlm_gpu_capture_end(zlm_device* d) {
 constexpr int kGraphsInFlight = 4;
 
 extern "C" bool zlm_gpu_profiler_loaded(const char* maps_path) { return profiler_in_maps(maps_path); }
+
+extern "C" bool zlm_gpu_launch_log(zlm_device* d, bool enable) {
+    if (!d || !d->avail) return false;
+    d->log_launches = enable;
+    d->launch_log.clear();
+    return true;
+}
+
+extern "C" size_t zlm_gpu_launch_log_read(const zlm_device* d, zlm_launch_record* out, size_t max) {
+    if (!d || !d->avail) return 0;
+    const size_t n = std::min(max, d->launch_log.size());
+    if (out)
+        for (size_t i = 0; i < n; i++) out[i] = d->launch_log[i];
+    return d->launch_log.size();
+}
 
 extern "C" uint64_t zlm_gpu_scratch_device_bytes(const zlm_device* d) {
     if (!d || !d->avail) return 0;

@@ -91,6 +91,12 @@ class _GemvOp(ctypes.Structure):
     ]
 
 
+class LaunchRecord(ctypes.Structure):
+    """zlm_launch_record: one logged kernel launch."""
+    _fields_ = [("what", ctypes.c_char_p), ("grid_x", ctypes.c_uint32), ("grid_y", ctypes.c_uint32),
+                ("grid_z", ctypes.c_uint32), ("block", ctypes.c_uint32), ("lds_bytes", ctypes.c_uint32)]
+
+
 class _Probe(ctypes.Structure):
     _fields_ = [
         ("gemv_gbps", ctypes.c_double),
@@ -184,12 +190,15 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_release_gemm_tiles": (B, [P, P]),
         "zlm_gpu_probe_rates": (B, [P, U, ctypes.c_bool, S, S, P]),
         "zlm_gpu_time_contract_gemv": (B, [P, P, S, U, S, S, ctypes.c_int, P]),
+        "zlm_gpu_time_contract_gemv_split": (B, [P, P, S, U, S, S, ctypes.c_int, P]),
         "zlm_gpu_time_contract_decode": (B, [P, P, S, U, S, S, S, S, P, U, S, ctypes.c_int, P]),
         "zlm_gpu_capture_begin": (B, [P]),
         "zlm_gpu_capture_end": (P, [P]),
         "zlm_gpu_graph_launch": (B, [P, P, ctypes.c_int, P]),
         "zlm_gpu_graph_destroy": (None, [P, P]),
         "zlm_gpu_profiler_loaded": (B, [ctypes.c_char_p]),
+        "zlm_gpu_launch_log": (B, [P, B]),
+        "zlm_gpu_launch_log_read": (S, [P, P, S]),
         "zlm_gpu_scratch_device_bytes": (ctypes.c_uint64, [P]),
         "zlm_gpu_synth_resident": (P, [P, U, S, ctypes.c_uint64, ctypes.c_float]),
         "zlm_gpu_synth_f16": (B, [P, P, S, ctypes.c_uint64, ctypes.c_float]),
@@ -525,6 +534,16 @@ class Device:
             raise RuntimeError(self.last_error())
         return us.value
 
+    def time_contract_gemv_split(self, residents: Sequence[Resident], quant: int, rows: int, k: int,
+                                 iters: int) -> dict:
+        """Per-op host microseconds of a contract GEMV: total, submit, wait, and the GPU's own time."""
+        arr = (ctypes.c_void_p * len(residents))(*[r.ptr for r in residents])
+        out = (ctypes.c_double * 4)()
+        if not self._L.zlm_gpu_time_contract_gemv_split(self._h, arr, len(residents), quant, rows, k, iters,
+                                                        ctypes.addressof(out)):
+            raise RuntimeError(self.last_error())
+        return {"total_us": out[0], "submit_us": out[1], "wait_us": out[2], "gpu_us": out[3]}
+
     def time_contract_decode(self, layers: Sequence[Sequence[Resident]], quant: int, hidden: int, q_rows: int,
                              kv_rows: int, ffn: int, lm_head: Resident, lm_quant: int, vocab: int, iters: int) -> float:
         """Host-wall ms per token of the projections driven through the contract ops
@@ -560,6 +579,18 @@ class Device:
 
     def graph_destroy(self, graph: int) -> None:
         self._L.zlm_gpu_graph_destroy(self._h, graph)
+
+    def launch_log(self, enable: bool) -> bool:
+        """Turn the launch log on or off (either clears it)."""
+        return bool(self._L.zlm_gpu_launch_log(self._h, enable))
+
+    def launch_log_read(self) -> list:
+        """The logged launches as dicts (what, grid_x/y/z, block, lds_bytes)."""
+        n = int(self._L.zlm_gpu_launch_log_read(self._h, None, 0))
+        arr = (LaunchRecord * max(1, n))()
+        self._L.zlm_gpu_launch_log_read(self._h, ctypes.addressof(arr), n)
+        return [{"what": r.what.decode(), "grid_x": r.grid_x, "grid_y": r.grid_y, "grid_z": r.grid_z,
+                 "block": r.block, "lds_bytes": r.lds_bytes} for r in arr[:n]]
 
     def scratch_device_bytes(self) -> int:
         """Device bytes the library holds for staging and scratch (not residents)."""
