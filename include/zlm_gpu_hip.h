@@ -195,6 +195,11 @@ bool zlm_gpu_probe_rates(zlm_device *dev, uint32_t ggml_type, bool gate_up, size
 
 /* Resident.bytes (reference gpu/backend/root.zig:241-244): the raw GGUF bytes uploaded. */
 uint64_t zlm_gpu_resident_bytes(const zlm_resident *res);
+/* Copy a resident's raw GGUF bytes back to the host (no reference
+ * counterpart; tests and diagnostics, e.g. to check weights synthesised in
+ * HBM against the CPU kernels).  Only before its first op converts them to the
+ * device layout; `len` must equal the resident's byte count. */
+bool zlm_gpu_resident_read_raw(zlm_device *dev, const zlm_resident *res, void *dst, size_t len);
 
 /* ---- device-level entry points (no reference counterpart) ----
  * For callers that keep activations in HBM (the decode-step harness, the

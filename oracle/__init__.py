@@ -351,3 +351,14 @@ def fast_time_matmul_int(t: int, w, k: int, rows: int, m: int, x, threads: int, 
 
 def pool_threads() -> int:
     return int(lib().orc_pool_threads())
+
+
+def pooled_matvec(t: int, w, k: int, rows: int, x, lanes: int = DEFAULT_LANES, threads: int = 16) -> np.ndarray:
+    """matvec(t, w, k, rows, x, lanes) computed by the speed-faithful sweep over
+    the pinned pool (bit-identical to matvec at the same lanes); for checking
+    model-sized GEMVs in seconds."""
+    out = np.zeros(rows, np.float32)
+    cores = max(1, len(physical_cores()))
+    if fast_time_matvec(t, w, k, rows, x, min(threads, cores), 1, lanes=lanes, out=out) < 0:
+        raise OracleError(-4)
+    return out

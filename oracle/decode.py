@@ -84,11 +84,13 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     return (g / (1.0 + np.exp(-g))) * np.asarray(u, np.float64)
 
 
-def decode_step(cfg, layers, out_norm, lm_head, lm_type, proj_type, x_in, pos, k_caches, v_caches):
+def decode_step(cfg, layers, out_norm, lm_head, lm_type, proj_type, x_in, pos, k_caches, v_caches, matvec=matvec):
     """One token through the Qwen3 layer sequence (block.zig:20-41) and the
     tail (:43-46).  `layers[i]` holds raw GGUF bytes 'qkv' (q;k;v rows), 'o',
     'gate', 'up', 'down' and f32 'attn_norm', 'ffn_norm', 'q_norm', 'k_norm'.
-    Caches are updated in place.  Returns the logits (f32)."""
+    Caches are updated in place.  Returns the logits (f32).  `matvec` is the
+    production GEMV (the C oracle's, or its bit-identical pooled form for
+    model-sized weights)."""
     hd, nh, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     h = np.asarray(x_in, np.float32).copy()
     scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))

@@ -445,3 +445,14 @@ def test_physical_cores_are_distinct_and_allowed():
     cores = oracle.physical_cores()
     assert cores and len(set(cores)) == len(cores)
     assert set(cores) <= os.sched_getaffinity(0)
+
+
+@pytest.mark.skipif(not FAST_LANES, reason="host has neither AVX2 nor AVX-512")
+def test_pooled_matvec_is_the_oracle():
+    """The pooled GEMV the model-sized decode check uses: the oracle's result
+    bit for bit at the oracle's default lanes."""
+    for qt in (synth.Q4_0, synth.Q8_0):
+        w = synth.weights(qt, 777, 2048, seed=51)
+        x = synth.activation(52, 2048)
+        np.testing.assert_array_equal(_bits(oracle.pooled_matvec(qt, w, 2048, 777, x, threads=4)),
+                                      _bits(oracle.matvec(qt, w, 2048, 777, x)))

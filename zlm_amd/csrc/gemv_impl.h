@@ -1431,7 +1431,8 @@ __device__ __forceinline__ void sk_load(Frag<QT, RT> (&f)[SPL], const GemvArgs& 
 
 template <int RT>
 constexpr int sk_log() {
-    return (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
+    static_assert(RT == 1 || RT == 2 || RT == 4 || RT == 8 || RT == 16, "split-K row tiles: 1..16 rows, a power of two");
+    return (RT >= 16) ? 4 : (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
 }
 
 // The output row of this lane's fragment row after the butterfly (clamped).

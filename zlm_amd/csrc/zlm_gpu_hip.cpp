@@ -1348,6 +1348,13 @@ extern "C" void zlm_gpu_free_resident(zlm_device* d, zlm_resident* r) {
 
 extern "C" uint64_t zlm_gpu_resident_bytes(const zlm_resident* r) { return r ? r->bytes : 0; }
 
+extern "C" bool zlm_gpu_resident_read_raw(zlm_device* d, const zlm_resident* r, void* dst, size_t len) {
+    if (!contract_ready(d) || !r || !dst) return false;
+    if (!r->raw) return fail(d, "resident holds no raw bytes (its first op converted them)");
+    if (len != r->bytes) return fail(d, "resident holds %llu raw bytes, not %zu", (unsigned long long)r->bytes, len);
+    return ok(d, hipMemcpy(dst, r->raw, len, hipMemcpyDeviceToHost), "read raw bytes");
+}
+
 extern "C" uint64_t zlm_gpu_resident_device_bytes(const zlm_resident* r) {
     if (!r) return 0;
     return (r->raw ? r->bytes : 0) + r->layout_alloc + r->gemm_alloc;

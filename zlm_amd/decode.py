@@ -175,6 +175,36 @@ class DecodeModel:
         self.pos = buf(16)
         self.scale = 1.0 / math.sqrt(c.head_dim)
 
+    def host_copy(self) -> dict:
+        """The model's weights, norms and caches as host arrays, in the `host`
+        format the constructor takes (raw GGUF bytes, f32 norms, f16 caches
+        [n_kv_heads][max_seq][head_dim]); for checking a model synthesised in
+        HBM against the CPU kernels.  Only before the first step (a resident's
+        first op converts its raw bytes to the device layout)."""
+        d, c = self.dev, self.cfg
+
+        def f32(p: int, n: int) -> np.ndarray:
+            out = np.empty(n, np.float32)
+            d.dev_download(out, p)
+            return out
+
+        def f16(p: int) -> np.ndarray:
+            out = np.empty((c.n_kv_heads, c.max_seq, c.head_dim), np.float16)
+            d.dev_download(out, p)
+            return out
+
+        layers = []
+        for L in self.layers:
+            layers.append({
+                "qkv": d.resident_read_raw(L.qkv), "o": d.resident_read_raw(L.o),
+                "gate": d.resident_read_raw(L.gate), "up": d.resident_read_raw(L.up),
+                "down": d.resident_read_raw(L.down),
+                "attn_norm": f32(L.attn_norm, c.hidden), "ffn_norm": f32(L.ffn_norm, c.hidden),
+                "q_norm": f32(L.q_norm, c.head_dim), "k_norm": f32(L.k_norm, c.head_dim),
+                "k_cache": f16(L.k_cache), "v_cache": f16(L.v_cache)})
+        return {"layers": layers, "lm_head": d.resident_read_raw(self.lm_head),
+                "out_norm": f32(self.out_norm, c.hidden)}
+
     # -- one step --------------------------------------------------------------
     def enqueue_step(self) -> None:
         """Enqueue one token's step on the device stream (no waits)."""

@@ -161,6 +161,7 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_sync": (None, [P]),
         "zlm_gpu_probe": (None, [P, S, S, S, P]),
         "zlm_gpu_resident_bytes": (ctypes.c_uint64, [P]),
+        "zlm_gpu_resident_read_raw": (B, [P, P, P, S]),
         "zlm_gpu_last_error": (ctypes.c_char_p, [P]),
         "zlm_gpu_cu_count": (ctypes.c_int, [P]),
         "zlm_gpu_vram_info": (B, [P, P, P]),
@@ -555,6 +556,13 @@ class Device:
                                                     lm_head.ptr, lm_quant, vocab, iters, ctypes.addressof(ms)):
             raise RuntimeError(self.last_error())
         return ms.value
+
+    def resident_read_raw(self, res: Resident) -> np.ndarray:
+        """The resident's raw GGUF bytes (only before its first op)."""
+        out = np.empty(res.bytes, np.uint8)
+        if not self._L.zlm_gpu_resident_read_raw(self._h, res.ptr, _p(out), out.size):
+            raise RuntimeError(self.last_error())
+        return out
 
     def resident_device_bytes(self, res: Resident) -> int:
         """HBM the resident holds now (raw bytes, device layout, GEMM tiles)."""
