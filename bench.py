@@ -213,6 +213,32 @@ def cpu_prefill_sample(w: np.ndarray, rows: int, k: int, budget_s: float):
                                       f"rangeOf, min of {reps} reps"}
 
 
+def upload_rate(dev) -> dict:
+    """uploadResident's rate (reference runtime/session.zig:452-474 uploads
+    each planned tensor from the mmap'd image): a 256 MiB Q4_0 weight from
+    ordinary (pageable) host memory, as an mmap'd file page is, uploaded 8
+    times into fresh residents (2 GiB); host wall time per upload, median of
+    the 8, and the configs[2] model's 4.57 GB at that rate."""
+    from zlm_amd import decode as zdec
+
+    nb = (256 << 20) // 18
+    w = np.frombuffer(np.random.default_rng(7).bytes(nb * 18), np.uint8).copy()
+    times = []
+    for _ in range(8):
+        t0 = time.perf_counter()
+        r = dev.upload_resident(w)
+        times.append(time.perf_counter() - t0)
+        if r is None:
+            raise RuntimeError(dev.last_error())
+        dev.free_resident(r)
+    t = sorted(times)[len(times) // 2]
+    gbps = w.nbytes / t / 1e9
+    model = zdec.weight_bytes(zdec.QWEN3_8B)
+    return {"GBps": round(gbps, 2), "bytes_per_upload": int(w.nbytes), "ms_per_upload": round(t * 1e3, 2),
+            "configs2_model_bytes": model, "configs2_upload_s": round(model / gbps / 1e9, 3),
+            "note": "uploadResident from pageable host memory into a new resident (synchronous), median of 8"}
+
+
 def split_efficiency(dev, threads: int) -> dict:
     """measureSplitEfficiency (reference tuner/calibrate.zig:778-834) on this
     device: a 32768 x 4096 Q4_0 resident GEMV through matVecResident alone,
@@ -677,6 +703,9 @@ def main():
             f"{cpu['one_thread']['value']} GB/s on 1; [4096, 8192] on 1 thread: " +
             ", ".join(f"{n} {v['GBps_1_thread']} GB/s (zlm {v['zlm_published_GBps_1_thread']})"
                       for n, v in cpu["published_shapes_1_thread"].items()))
+        extra["upload_resident"] = upload_rate(dev)
+        log(f"uploadResident: {extra['upload_resident']['GBps']} GB/s from pageable host memory "
+            f"(configs[2] weights in {extra['upload_resident']['configs2_upload_s']} s)")
         extra["split_efficiency"] = split_efficiency(dev, cpu["cores"])
         log(f"split probe (GPU rows [0, m/2) + {cpu['cores']} CPU threads [m/2, m)): "
             f"{extra['split_efficiency']['split_us']} us against {extra['split_efficiency']['gpu_us']} us "
