@@ -423,8 +423,9 @@ def sections(dev, args, want, extra):
                 dev.free_resident(r)
             dev.dev_free(x_dev)
             dev.dev_free(o_dev)
-        sweep["note"] = ("device-level matMul at m tokens vs one GEMV (weights rotated over >= 512 MiB): m <= 2 one "
-                         "fp GEMV per token, 3..32 the split-K int8-MFMA GEMM (activation quantizer included)")
+        sweep["note"] = ("device-level matMul at m tokens vs one GEMV (weights rotated over >= 512 MiB): m = 1 the fp "
+                         "GEMV, m = 2 the two-token fp GEMV (one pass over the weights), 3..32 the split-K "
+                         "int8-MFMA GEMM (activation quantizer included)")
         extra["small_m_matmul"] = sweep
 
     # ---- decode step of a Qwen3-8B-shaped Q4_0 model, batch 1 ----------

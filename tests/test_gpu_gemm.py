@@ -7,8 +7,9 @@ activation quantizer of matvec/layout.zig:458-476) applied per token: relative
 L2 <= 1e-3 (the block dots are exact integers; only fp32 scaling and summation
 order differ).  Against the fp32 GEMM the reference's own int-vs-fp bound
 applies, |int - fp| <= 0.02 * sum|w*x| (kernels/quantized_test.zig:61).  One
-or two tokens run one fp GEMV per token, checked against the oracle's fp
-matMulRows (form/single.zig:213-292), relative L2 <= 1e-3.
+or two tokens run the fp GEMV (two tokens in one pass over the weights, more
+cases in test_gpu_two_token.py), checked against the oracle's fp matMulRows
+(form/single.zig:213-292), relative L2 <= 1e-3.
 """
 import sys
 
@@ -33,7 +34,7 @@ SHAPES = [(64, 256, 4), (100, 512, 37), (64, 1024, 64), (130, 4096, 70), (48, 16
 GEMM_QUANTS = [(synth.Q4_0, zd.Q4_0), (synth.Q8_0, zd.Q8_0), (synth.Q4_1, zd.Q4_1), (synth.Q4_K, zd.Q4_K)]
 
 
-# Token counts up to this run one fp GEMV per token (the host's kGemmGemvM).
+# Token counts up to this run the fp GEMV path (the host's kGemmGemvM).
 GEMV_M = 2
 
 

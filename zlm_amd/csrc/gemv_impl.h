@@ -156,7 +156,7 @@ __device__ __forceinline__ void xput(float4 v, int i, bool valid, float* xl) {
     }
 }
 
-template <int KCAP, int NX, bool XQ = false>
+template <int KCAP, int NX, bool XQ = false, bool SYNC = true>
 __device__ __forceinline__ void xstore(const XRegs<NX>& r, int k, float* xl, float* xs) {
     const int n4 = k >> 2;
 #pragma unroll
@@ -174,7 +174,7 @@ __device__ __forceinline__ void xstore(const XRegs<NX>& r, int k, float* xl, flo
         s += __shfl_xor(s, 2, kWave);
         xs[(valid && (i & 3) == 0) ? (i >> 2) : XTile<KCAP>::kRuns] = s;
     }
-    __syncthreads();
+    if constexpr (SYNC) __syncthreads();
 }
 
 // xstore with RMSNorm folded in (reference kernels/transformer/norm.zig:26-37:
@@ -805,12 +805,16 @@ __device__ __forceinline__ void compute_frag(const Frag<QT, RT>& f, const float*
 // Prologue / epilogue forms of the GEMV (template parameters PRO and EPI).
 //   PRO_PLAIN  x staged as is
 //   PRO_NORM   RMSNorm(x, xw, eps) folded in (xstore_norm)
+//   PRO_TOK2   two tokens: x holds two k-float rows, each staged in its own
+//              LDS tile; every weight fragment is loaded once and summed
+//              against both (with EPI_TOK2)
 //   EPI_PLAIN  y[r] = row sum
 //   EPI_RESID  y[r] = res[r] + row sum (res may alias y: one lane reads and
 //              writes each row)
 //   EPI_PAIR   fused gate_up: y[r] = act(gate row r . x, up row r . x)
-enum : int { PRO_PLAIN = 0, PRO_NORM = 1 };
-enum : int { EPI_PLAIN = 0, EPI_RESID = 1, EPI_PAIR = 2 };
+//   EPI_TOK2   two tokens: y[t * rows + r] = row r . x_t, t = 0, 1
+enum : int { PRO_PLAIN = 0, PRO_NORM = 1, PRO_TOK2 = 2 };
+enum : int { EPI_PLAIN = 0, EPI_RESID = 1, EPI_PAIR = 2, EPI_TOK2 = 3 };
 
 // Kernel arguments of every GEMV form, passed by value.
 struct GemvArgs {
@@ -882,6 +886,12 @@ __device__ __forceinline__ void reduce_store(float* v, const GemvArgs& a, uint32
         const float u = __shfl_xor(s, 32, kWave);
         const uint32_t row = t * (RT / 2) + fr;
         if (leader && fr < static_cast<uint32_t>(RT / 2) && row < a.rows) a.y[row] = gate_act(a.act, s, u);
+    } else if constexpr (EPI == EPI_TOK2) {
+        // RT values per lane: token 0's RT/2 rows, then token 1's
+        static_assert(RT >= 2, "a two-token tile holds a value per token");
+        constexpr uint32_t RH = RT / 2;
+        const uint32_t row = t * RH + fr % RH;
+        if (leader && row < a.rows) a.y[(fr / RH) * a.rows + row] = s;
     } else {
         const uint32_t row = t * RT + fr;
         if (leader && row < a.rows) {
@@ -986,6 +996,26 @@ __device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], co
     }
 }
 
+// compute_group over NTOK x tiles (XF floats and XR run sums apart), both
+// tokens' sums of a step before the next step, with a scheduling barrier
+// after each step (hoisting every step's LDS reads for two tokens would take
+// twice the registers of the one-token form).
+template <int QT, int RT, int STEPS, bool EXACT, int NTOK, int XF, int XR, int KCAP>
+__device__ __forceinline__ void compute_group_tok(const Frag<QT, RT> (&f)[STEPS], const float* xl, const float* xs,
+                                                  int C, int cb, int lane, float* acc) {
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+        const int c = cb + lane + s * kWave;
+        if (EXACT || cb + s * kWave < C) {
+#pragma unroll
+            for (int u = 0; u < NTOK; u++)
+                compute_frag<QT, RT, KCAP, false>(f[s], xl + u * XF, xs + u * XR, min(c, C - 1), c < C,
+                                                  acc + u * RT);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // One GEMV: y[r] = sum_k w[r,k] * x[k] for r < rows, k = nb * block_elems,
 // in the prologue/epilogue form PRO/EPI.  A wave owns row tiles
 // blockIdx*WAVES + wid + j*gridDim*WAVES.  For each tile it issues the loads
@@ -1005,8 +1035,12 @@ __device__ __forceinline__ void compute_group(const Frag<QT, RT> (&f)[STEPS], co
 template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT, int PRO, int EPI, bool PF = false,
           bool FENCE = false, bool XQ = false>
 __device__ __forceinline__ void gemv(const GemvArgs& a) {
-    __shared__ __attribute__((aligned(16))) float xl[XTile<KCAP>::kFloats];
-    __shared__ float xs[XTile<KCAP>::kRuns + 1];
+    static_assert((PRO == PRO_TOK2) == (EPI == EPI_TOK2), "the two-token prologue and epilogue go together");
+    static_assert(PRO != PRO_TOK2 || (!PF && !XQ), "two-token instances stage fp32 x and do not prefetch");
+    constexpr int NTOK = PRO == PRO_TOK2 ? 2 : 1;  // x rows staged, values per fragment row
+    constexpr int XF = XTile<KCAP>::kFloats, XR = XTile<KCAP>::kRuns + 1;
+    __shared__ __attribute__((aligned(16))) float xl[XF * NTOK];
+    __shared__ float xs[XR * NTOK];
     __shared__ float red[WAVES];
     constexpr bool PAIR = EPI == EPI_PAIR;
     constexpr int RP = PAIR ? RT / 2 : RT;  // output rows per tile
@@ -1023,14 +1057,21 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
     XRegs<NX> xr, gr;
     xload(a.x, k, xr);
     if constexpr (PRO == PRO_NORM) xload(a.xw, k, gr);
+    if constexpr (PRO == PRO_TOK2) xload(a.x + k, k, gr);  // the second token's row
     Frag<QT, RT> f[STEPS];
     TileRows<RT> tr = tile_rows<RT, PAIR>(a, min(tile, ntiles - 1));
     load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, 0, lane);
     float scale = 1.0f;
-    if constexpr (PRO == PRO_NORM) scale = xstore_norm<KCAP, NX, WAVES, XQ>(xr, gr, k, a.eps, xl, xs, red);
-    else xstore<KCAP, NX, XQ>(xr, k, xl, xs);
+    if constexpr (PRO == PRO_NORM) {
+        scale = xstore_norm<KCAP, NX, WAVES, XQ>(xr, gr, k, a.eps, xl, xs, red);
+    } else if constexpr (PRO == PRO_TOK2) {
+        xstore<KCAP, NX, false, false>(xr, k, xl, xs);
+        xstore<KCAP, NX>(gr, k, xl + XF, xs + XR);
+    } else {
+        xstore<KCAP, NX, XQ>(xr, k, xl, xs);
+    }
 
-    float acc[RT];
+    float acc[RT * NTOK];
     if constexpr (PF) {
         static_assert(EXACT, "the prefetching loop needs one step group per tile");
         Frag<QT, RT> g[STEPS];
@@ -1062,25 +1103,32 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
         }
         return;
     }
+    // the fragments' sums for every staged token
+    auto compute = [&](int cb) {
+        if constexpr (NTOK == 1)
+            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
+        else
+            compute_group_tok<QT, RT, STEPS, EXACT, NTOK, XF, XR, KCAP>(f, xl, xs, C, cb, lane, acc);
+    };
 #pragma unroll
-    for (int r = 0; r < RT; r++) acc[r] = 0.0f;
-    compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, 0, lane, acc);
+    for (int r = 0; r < RT * NTOK; r++) acc[r] = 0.0f;
+    compute(0);
     if constexpr (!EXACT) {
         for (int cb = GROUP; cb < C; cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
+            compute(cb);
         }
     }
-    if (tile < ntiles) reduce_store<RT, EPI>(acc, a, tile, scale, lane);
+    if (tile < ntiles) reduce_store<RT * NTOK, EPI>(acc, a, tile, scale, lane);
     for (tile += tstride; tile < ntiles; tile += tstride) {
         tr = tile_rows<RT, PAIR>(a, tile);
 #pragma unroll
-        for (int r = 0; r < RT; r++) acc[r] = 0.0f;
+        for (int r = 0; r < RT * NTOK; r++) acc[r] = 0.0f;
         for (int cb = 0; cb < (EXACT ? 1 : C); cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
+            compute(cb);
         }
-        reduce_store<RT, EPI>(acc, a, tile, scale, lane);
+        reduce_store<RT * NTOK, EPI>(acc, a, tile, scale, lane);
     }
 }
 // ---- several matrices over one x in one launch -------------------------------
@@ -1642,6 +1690,23 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
         GemvArgs a = {w, dsc, w, dsc, x, x, y, y, rows, nb, 0.0f, 0u};                                  \
         gemv<QT, KCAP, 4, RT, STEPS, EXACT, true, PRO_PLAIN, EPI_PLAIN>(a);                             \
     }
+
+// Two-token instances zlm_gemv_<quant>_tok2_g<T> (T = 4, 8, 16: k <= 1024*T):
+// matMul at m = 2, one pass over the weights for both tokens, one-row tiles,
+// fp32 x, the row walked in groups of STEPS chunk steps (the generic loop;
+// exact-step forms that issue a whole row's loads at once took 170-450 VGPRs
+// with two tokens).  Both x rows fill twice the single-token LDS tile (39 KB
+// at the 4096-float tier, 78 KB at 8192, 156 KB at 16384), so the workgroup
+// grows with the tier (4, 8, 16 waves) to keep 16 waves per CU.
+#define ZLM_GEMVT(NAME, QT, KCAP, WAVES, STEPS)                                   \
+    extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {   \
+        gemv<QT, KCAP, WAVES, 1, STEPS, false, true, PRO_TOK2, EPI_TOK2>(a);      \
+    }
+// STEPS: 2 for the 32-element chunks of q4_0 / q4_1 / q4_k, 4 for q8_0's 16
+#define ZLM_GEMV_TOK2(QN, QT, STEPS)                                    \
+    ZLM_GEMVT(zlm_gemv_##QN##_tok2_g4, QT, 4096, 4, STEPS)              \
+    ZLM_GEMVT(zlm_gemv_##QN##_tok2_g8, QT, 8192, 8, STEPS)              \
+    ZLM_GEMVT(zlm_gemv_##QN##_tok2_g16, QT, 16384, 16, STEPS)
 
 // The fused forms take one GemvArgs: zlm_gemv_<quant>_<form>_s<STEPS> (exact
 // steps) and zlm_gemv_<quant>_<form>_g<STEPS> (generic), form one of

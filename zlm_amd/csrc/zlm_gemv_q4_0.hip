@@ -35,3 +35,6 @@ ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s6_sk4x, Q4_0, 6, 4, 1, EPI_PLAIN, true, 2, true)
 ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s6_sk4x, Q4_0, 6, 4, 1, EPI_RESID, true, 2, true)
 
 ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)
+
+// matMul at m = 2 (both tokens in one pass over the weights)
+ZLM_GEMV_TOK2(q4_0, Q4_0, 2)

@@ -8,3 +8,6 @@ ZLM_GEMVX_Q4(q4_1, Q4_1)
 ZLM_GEMVX_PAIR_TILES_Q4(q4_1, Q4_1)
 
 ZLM_GEMV_MULTI_Q4(q4_1, Q4_1)
+
+// matMul at m = 2 (both tokens in one pass over the weights)
+ZLM_GEMV_TOK2(q4_1, Q4_1, 2)

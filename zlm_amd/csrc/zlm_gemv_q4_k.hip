@@ -25,3 +25,6 @@ ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s8_sk4, Q4_K, 8, 4, 1, EPI_PLAIN, true, 2, false, 
 ZLM_GEMVX_PFQ(zlm_gemv_q4_k_r1_s2_pfqw16, Q4_K, 4096, 16, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
 
 ZLM_GEMV_MULTI_Q4(q4_k, Q4_K)
+
+// matMul at m = 2 (both tokens in one pass over the weights)
+ZLM_GEMV_TOK2(q4_k, Q4_K, 2)

@@ -21,3 +21,6 @@ ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s4_tall, Q8_0, 4096, 8, 1, 4, PRO_PLAIN, EPI_PLAIN
 ZLM_GEMVX_PF(zlm_gemv_q8_0_norm_s4_tall, Q8_0, 4096, 8, 1, 4, PRO_NORM, EPI_PLAIN, false)
 
 ZLM_GEMV_MULTI_Q8(q8_0, Q8_0)
+
+// matMul at m = 2 (both tokens in one pass over the weights)
+ZLM_GEMV_TOK2(q8_0, Q8_0, 4)

@@ -550,12 +550,13 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
 // the block size is the kernel's launch bound.
 // What a GEMV entry point computes and how it takes its arguments, read from
 // its name zlm_gemv_<quant>_<rest>: <rest> "multi_..." is the batch kernel,
-// "pair_" / "normpair_" / "norm_" / "resid_" a fused form (ZLM_FORM_*), anything
-// else the plain GEMV.  Only the plain exact-steps and generic instances
+// "tok2_..." the two-token GEMV, "pair_" / "normpair_" / "norm_" / "resid_" a
+// fused form (ZLM_FORM_*), anything else the plain GEMV.  Only the plain exact-steps and generic instances
 // (r<RT>_s<STEPS>, r<RT>_g) take separate arguments; every other instance
 // takes one GemvArgs.  The host checks a cached kernel's role before each
 // launch, so a kernel picked for one form can never be launched as another.
 constexpr int kRoleMulti = 16;
+constexpr int kRoleTok2 = 17;
 
 void kernel_role(const char* name, int slot, int* role, bool* struct_args) {
     const char* rest = name + strlen("zlm_gemv_") + strlen(kQuantNames[slot]) + 1;
@@ -563,6 +564,7 @@ void kernel_role(const char* name, int slot, int* role, bool* struct_args) {
         const char* prefix;
         int role;
     } kForms[] = {{"multi_", kRoleMulti},
+                  {"tok2_", kRoleTok2},
                   {"pair_", ZLM_FORM_PAIR},
                   {"normpair_", ZLM_FORM_NORMPAIR},
                   {"norm_", ZLM_FORM_NORM},
@@ -689,7 +691,7 @@ bool resid_two_rows(const QuantInfo* qi, int steps, size_t rows) {
 // ~1 us per launch, most of a small GEMV's enqueue).
 // The kernel picked per shape class: (k, quant slot, what is picked, its
 // parameter, row-count class) in disjoint bit fields.
-enum PickKind : uint64_t { kPickPlain = 0, kPickForm = 1, kPickPairTile = 2 };
+enum PickKind : uint64_t { kPickPlain = 0, kPickForm = 1, kPickPairTile = 2, kPickTok2 = 3 };
 
 uint64_t pick_key(const QuantInfo* qi, size_t k, PickKind kind, int param, size_t rows) {
     const uint64_t rows_class = rows >= 65536 ? 2 : rows <= 8192 ? 1 : 0;
@@ -728,6 +730,27 @@ const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, 
     if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps)) return g;
     snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_g", qn);
     return find_gemv(d, qi->slot, nm, 1, 0);
+}
+
+// The two-token GEMV for matMul at m = 2: zlm_gemv_<quant>_tok2_g<T>, the
+// smallest tier T in {4, 8, 16} whose x tiles hold k <= 1024*T floats, or
+// null (the quant has none, or k > 16384), and the caller runs one GEMV per
+// token.
+constexpr size_t kTok2MaxK = 16384;
+
+const GemvKernel* pick_tok2(zlm_device* d, const QuantInfo* qi, size_t k) {
+    const uint64_t key = pick_key(qi, k, kPickTok2, 0, 0);
+    auto it = d->picks.find(key);
+    if (it != d->picks.end()) return it->second;
+    const GemvKernel* g = nullptr;
+    if (k <= kTok2MaxK) {
+        const int tier = k <= 4096 ? 4 : k <= 8192 ? 8 : 16;
+        char nm[96];
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_tok2_g%d", kQuantNames[qi->slot], tier);
+        g = find_gemv(d, qi->slot, nm, 1, 0);
+    }
+    d->picks.emplace(key, g);
+    return g;
 }
 
 // Validate resident `r` as a rows x k weight of quant `qi` and make sure its
@@ -820,6 +843,32 @@ bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     }
     void* args[] = {&w, &s, &x_dev, &y_dev, &rows32, &nb};
     return launch(d, f, grid, block, args, "gemv");
+}
+
+// Both tokens of an m = 2 product in one launch: y_dev[t * rows + r] = row r
+// . x_dev[t * k ..], t = 0, 1.  Returns false without an error when there is
+// no two-token instance for the shape (*ran = false); the caller then runs
+// one GEMV per token.  Workgroups per CU: 4, or as many as the two x tiles
+// leave room for in LDS.
+bool enqueue_gemv_tok2(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t rows, size_t k,
+                       const float* x_dev, float* y_dev, bool* ran) {
+    *ran = false;
+    const GemvKernel* gk = pick_tok2(d, qi, k);
+    if (!gk) return true;
+    if (gk->role != kRoleTok2 || !gk->struct_args)
+        return fail(d, "internal: picked kernel (role %d) is not the two-token GEMV", gk->role);
+    const uint32_t lds = static_lds(d, gk->fn);
+    const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, kMaxLds / std::max<uint32_t>(lds, 1)));
+    const uint64_t waves = static_cast<uint64_t>(gk->threads / 64);
+    const uint64_t wgs = (rows + waves - 1) / waves;
+    const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->cus) * per_cu));
+    const uint8_t* w = r->payload;
+    const uint16_t* s = r->scales;
+    GemvArgsHost a = {w, s, w, s, x_dev, x_dev, y_dev, y_dev, static_cast<uint32_t>(rows),
+                      static_cast<uint32_t>(k / qi->kblock), 0.0f, 0u};
+    void* args[] = {&a};
+    *ran = true;
+    return launch(d, gk->fn, grid, static_cast<unsigned>(gk->threads), args, "gemv two tokens");
 }
 
 // ---- fused GEMV forms (prologue/epilogue variants of the same kernel) ----
@@ -927,8 +976,6 @@ const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k,
     return find_gemv(d, qi->slot, nm, rt, 0);
 }
 
-// Enqueue one GEMV op on device buffers: validate the residents, pick the
-// kernel of the op's form and launch it on the device stream.
 // The gate_up pair form with `rp` output rows per wave tile (2 or 4), the tile
 // a GpuVariant selects (rt_for_variant); built for q4_0, q4_1 and q8_0, the
 // quants the reference grid lists gate_up variants for
@@ -952,6 +999,8 @@ const GemvKernel* pick_pair_tile(zlm_device* d, const QuantInfo* qi, size_t k, i
     return g;
 }
 
+// Enqueue one GEMV op on device buffers: validate the residents, pick the
+// kernel of the op's form and launch it on the device stream.
 bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     if (!d || !d->avail) return fail(d, "device unavailable");
     if (op.form > ZLM_FORM_RESID) return fail(d, "unknown GEMV form %u", op.form);
@@ -1097,10 +1146,12 @@ double now_ns() {
 }
 
 // The quants with a prefill GEMM and whether their tiles carry a min term.
-// Matrix products by token count m: up to kGemmGemvM tokens one fp GEMV per
-// token (the production GEMV's arithmetic, as zlm's CPU runs small batches
-// through its fp batched GEMV, reference form/single.zig:258-292; m GEMVs cost
-// less than the int path's quantizer + GEMM there); up to one 32-token tile
+// Matrix products by token count m: up to kGemmGemvM tokens the fp path (the
+// production GEMV's arithmetic, as zlm's CPU runs small batches through its fp
+// batched GEMV, reference form/single.zig:258-292; cheaper than the int path's
+// quantizer + GEMM there): one token the GEMV, two the two-token GEMV (one
+// pass over the weights, k <= 16384; beyond it one GEMV per token); up to one
+// 32-token tile
 // the split-K small-M int GEMM (zlm_gemm_small_*: 16 waves per workgroup for
 // q4_0 / q8_0, 8 for q4_1 / q4_k); beyond it the 128 x 64 tiled int GEMM.
 constexpr size_t kGemmGemvM = 2;
@@ -1195,7 +1246,13 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     if (r->bytes < rows * wblocks * qi->block_bytes) return fail(d, "resident too short");
     if (!ensure_layout(d, r, qi)) return false;
     if (r->blocks < rows * wblocks) return fail(d, "resident layout too short");
-    if (m <= kGemmGemvM) {  // one fp GEMV per token (no activation quantizer, no tiled weight copy)
+    if (m <= kGemmGemvM) {  // fp GEMVs (no activation quantizer, no tiled weight copy)
+        if (m == 2) {  // both tokens in one pass over the weights where an instance fits k
+            bool ran = false;
+            if (!check_resident(d, r, qi, rows, k)) return false;
+            if (!enqueue_gemv_tok2(d, r, qi, rows, k, x_dev, out_dev, &ran)) return false;
+            if (ran) return true;
+        }
         for (size_t t = 0; t < m; t++)
             if (!enqueue_gemv(d, r, quant, rows, k, x_dev + t * k, out_dev + t * rows)) return false;
         return true;
@@ -1640,8 +1697,9 @@ extern "C" bool zlm_gpu_mat_mul_batch(zlm_device* d, uint32_t quant, const void*
 }
 
 // The variant argument of the fused ops selects Vulkan shader variants in the
-// reference; here every variant runs the pair-tile kernel (results differ
-// only by fp32 summation order), so it is accepted and not used.
+// reference; here it selects the pair kernel's row tile (rt_for_variant: one,
+// two or four gate/up row pairs per wave tile, for q4_0, q4_1 and q8_0 where
+// those instances exist).  Results differ only by fp32 summation order.
 extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, zlm_resident* rg, zlm_resident* ru,
                                                                 uint32_t quant, size_t rows, size_t k,
                                                                 const float* x, size_t x_len, uint32_t act,
