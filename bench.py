@@ -424,8 +424,9 @@ def sections(dev, args, want, extra):
             dev.dev_free(x_dev)
             dev.dev_free(o_dev)
         sweep["note"] = ("device-level matMul at m tokens vs one GEMV (weights rotated over >= 512 MiB): m = 1 the fp "
-                         "GEMV, m = 2 the two-token fp GEMV (one pass over the weights), 3..32 the split-K "
-                         "int8-MFMA GEMM (activation quantizer included)")
+                         "GEMV, m = 2 the two-token fp GEMV (one pass over the weights), 3..4 the int-path token GEMV "
+                         "(activations quantized in its prologue), 5..32 the split-K int8-MFMA GEMM (activation "
+                         "quantizer included)")
         extra["small_m_matmul"] = sweep
 
     # ---- decode step of a Qwen3-8B-shaped Q4_0 model, batch 1 ----------

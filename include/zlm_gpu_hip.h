@@ -218,8 +218,9 @@ int zlm_gpu_cu_count(const zlm_device *dev);
  * both copies. */
 bool zlm_gpu_vram_info(zlm_device *dev, uint64_t *free_bytes, uint64_t *total_bytes);
 /* HBM a resident holds now: its raw bytes until the first op converts them,
- * then the device layout, plus the prefill GEMM's tiled copy once a GEMM of
- * 3 or more tokens has run on it. */
+ * then the device layout, plus the prefill GEMM's tiled copy once the tiled
+ * GEMM has run on it (more than 4 tokens, or 3-4 tokens at k > 8192; fewer
+ * tokens read the device layout). */
 uint64_t zlm_gpu_resident_device_bytes(const zlm_resident *res);
 /* HBM a rows x k weight of `quant` will hold once converted (its device
  * layout), plus its GEMM tiled copy when `with_gemm` (tensors the plan also
@@ -250,9 +251,13 @@ bool zlm_gpu_mat_vec_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant,
  * q4_0 fused forms), so every row always equals the single op's bit for bit. */
 bool zlm_gpu_mat_vec_batch_enqueue(zlm_device *dev, zlm_resident *const *res, uint32_t quant, const size_t *rows,
                                    size_t n, size_t k, const float *x_dev, float *const *y_dev);
-/* Enqueue the prefill GEMM out_dev[t*rows + r] (x_dev: m x k fp32, token-major):
- * the q8 activation quantizer, then the int8-MFMA GEMM.  Q4_0, Q8_0, Q4_1 and
- * Q4_K weights. */
+/* Enqueue the matrix product out_dev[t*rows + r] (x_dev: m x k fp32,
+ * token-major) over a Q4_0, Q8_0, Q4_1 or Q4_K resident, by token count:
+ * m = 1 the fp GEMV; m = 2 the two-token fp GEMV (k <= 16384, else a GEMV per
+ * token); m = 3, 4 at k <= 8192 the int-path token GEMV (q8 activations
+ * quantized in its prologue, the weights read once from the device layout);
+ * otherwise the q8 activation quantizer, then the int8-MFMA GEMM over the
+ * tiled copy (built on first use). */
 bool zlm_gpu_mat_mul_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k, size_t m,
                              const float *x_dev, float *out_dev);
 /* Enqueue `iters` prefill GEMMs (quantizer + GEMM each), rotating over `n_res`

@@ -1,6 +1,7 @@
 """GPU parity of the matrix products (matMulBatch / matMulResident) through the C ABI.
 
-From 3 tokens on the device runs zlm's int path (q8 activations, int8 MFMA);
+From 3 tokens on the device runs zlm's int path (q8 activations; the int8
+MFMA GEMM, or at 3-4 tokens the int-path token GEMV);
 its oracle is the int path of the reference (matvec/kernels/quantized.zig:49-55
 for Q4_0, :79-87 for Q4_1, :111-123 for Q4_K, :149-156 for Q8_0, over the
 activation quantizer of matvec/layout.zig:458-476) applied per token: relative
@@ -8,7 +9,7 @@ L2 <= 1e-3 (the block dots are exact integers; only fp32 scaling and summation
 order differ).  Against the fp32 GEMM the reference's own int-vs-fp bound
 applies, |int - fp| <= 0.02 * sum|w*x| (kernels/quantized_test.zig:61).  One
 or two tokens run the fp GEMV (two tokens in one pass over the weights, more
-cases in test_gpu_two_token.py), checked against the oracle's fp matMulRows
+cases in test_gpu_few_tokens.py), checked against the oracle's fp matMulRows
 (form/single.zig:213-292), relative L2 <= 1e-3.
 """
 import sys
@@ -162,10 +163,11 @@ def test_gemm_q4_k_c3_shape_rows_subset(dev):
 
 def test_resident_device_bytes_follow_the_conversions(dev):
     """The HBM a resident holds: its raw bytes after upload, the device layout
-    after the first op, plus the GEMM tiled copy after a GEMM of more than
-    two tokens (zlm_gpu_layout_bytes' estimate), and the layout again after
-    zlm_gpu_release_gemm_tiles (a later GEMM rebuilds the copy)."""
-    rows, k, m = 96, 4096, 8
+    after the first op (the token GEMVs of up to 4 tokens read it too), plus
+    the GEMM tiled copy after a tiled GEMM (zlm_gpu_layout_bytes' estimate),
+    and the layout again after zlm_gpu_release_gemm_tiles (a later GEMM
+    rebuilds the copy)."""
+    rows, k, m = 96, 4096, 9
     for qt, zq in GEMM_QUANTS:
         w = synth.weights(qt, rows, k, seed=77)
         x = synth.activation(78, m * k)
@@ -175,6 +177,10 @@ def test_resident_device_bytes_follow_the_conversions(dev):
         assert dev.mat_vec_resident(res, zd.quant(zq), rows, k, x[:k], out), dev.last_error()
         layout = zd.layout_bytes(zd.quant(zq), rows, k, False)
         assert dev.resident_device_bytes(res) == layout
+        for few in (2, 4):
+            outf = np.zeros(few * rows, np.float32)
+            assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, few, x[:few * k], outf), dev.last_error()
+            assert dev.resident_device_bytes(res) == layout
         outm = np.zeros(m * rows, np.float32)
         assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, outm), dev.last_error()
         assert dev.resident_device_bytes(res) == zd.layout_bytes(zd.quant(zq), rows, k, True) > layout

@@ -134,6 +134,39 @@ __device__ __forceinline__ void xq_planes(float4 v, float s, uint32_t& p0, uint3
     }
 }
 
+// The q8 activation quantizer (reference matvec/layout.zig:458-476) over a
+// 32-element block held as one float4 by each of 8 consecutive lanes: amax of
+// the block, d = amax/127, 1/d correctly rounded, q = round-half-away(v/d)
+// clamped to +-127.  Returns the lane's four q bytes (element order), the
+// block's d and the sum of the lane's four q.  Every lane of the 8 must call
+// it (the amax is shared with shuffles).
+__device__ __forceinline__ float max8(float v) {
+    v = fmaxf(v, __shfl_xor(v, 1, kWave));
+    v = fmaxf(v, __shfl_xor(v, 2, kWave));
+    return fmaxf(v, __shfl_xor(v, 4, kWave));
+}
+__device__ __forceinline__ int32_t sum8(int32_t v) {
+    v += __shfl_xor(v, 1, kWave);
+    v += __shfl_xor(v, 2, kWave);
+    return v + __shfl_xor(v, 4, kWave);
+}
+__device__ __forceinline__ uint32_t q8_quant4(float4 v, float& d, int32_t& s) {
+    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    d = __fdiv_rn(amax, 127.0f);
+    const float inv = (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    s = 0;
+    uint32_t wv = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        int32_t q = static_cast<int32_t>(roundf(e[j] * inv));
+        q = q > 127 ? 127 : (q < -127 ? -127 : q);
+        s += q;
+        wv |= (static_cast<uint32_t>(q) & 0xffu) << (8 * j);
+    }
+    return wv;
+}
+
 template <int KCAP, bool XQ>
 __device__ __forceinline__ void xput(float4 v, int i, bool valid, float* xl) {
     if constexpr (!XQ) {
@@ -807,14 +840,14 @@ __device__ __forceinline__ void compute_frag(const Frag<QT, RT>& f, const float*
 //   PRO_NORM   RMSNorm(x, xw, eps) folded in (xstore_norm)
 //   PRO_TOK2   two tokens: x holds two k-float rows, each staged in its own
 //              LDS tile; every weight fragment is loaded once and summed
-//              against both (with EPI_TOK2)
+//              against both (with EPI_TOK)
 //   EPI_PLAIN  y[r] = row sum
 //   EPI_RESID  y[r] = res[r] + row sum (res may alias y: one lane reads and
 //              writes each row)
 //   EPI_PAIR   fused gate_up: y[r] = act(gate row r . x, up row r . x)
-//   EPI_TOK2   two tokens: y[t * rows + r] = row r . x_t, t = 0, 1
+//   EPI_TOK    several tokens: y[t * rows + r] = row r . x_t for t < m
 enum : int { PRO_PLAIN = 0, PRO_NORM = 1, PRO_TOK2 = 2 };
-enum : int { EPI_PLAIN = 0, EPI_RESID = 1, EPI_PAIR = 2, EPI_TOK2 = 3 };
+enum : int { EPI_PLAIN = 0, EPI_RESID = 1, EPI_PAIR = 2, EPI_TOK = 3 };
 
 // Kernel arguments of every GEMV form, passed by value.
 struct GemvArgs {
@@ -830,6 +863,7 @@ struct GemvArgs {
     uint32_t nb;         // blocks per row
     float eps;           // PRO_NORM
     uint32_t act;        // EPI_PAIR: 0 silu, 1 gelu_tanh (reference GateUpAct)
+    uint32_t m;          // EPI_TOK: tokens (rows of x and of y)
 };
 
 // ActivationKind.apply (reference kernels/transformer/activation.zig:8-13).
@@ -855,26 +889,55 @@ __device__ __forceinline__ TileRows<RT> tile_rows(const GemvArgs& a, uint32_t t)
     return tr;
 }
 
+// `lower` in the lanes whose bit BIT (32, 16 or 8) is clear, `upper` where
+// it is set: a DPP move whose row mask (BIT 32, 16) or bank mask (BIT 8)
+// enables exactly those lanes.
+template <int BIT>
+__device__ __forceinline__ float lane_pick(float lower, float upper) {
+    static_assert(BIT == 32 || BIT == 16 || BIT == 8, "row or bank granularity");
+    constexpr int row = BIT == 32 ? 0xC : BIT == 16 ? 0xA : 0xF;
+    constexpr int bank = BIT == 8 ? 0xC : 0xF;
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, lower),
+                                                                 __builtin_bit_cast(int, upper), 0xE4, row, bank,
+                                                                 false));
+}
+
+// Stage ST of reduce_store's butterfly over RT values: exchange across lane
+// bit 5-ST and keep half of the live values.  From RT = 8 the lane choice is
+// lane_pick: as selects between array elements the compiler turned the
+// pair into one load at a lane-dependent index and kept the array in
+// scratch memory.
+template <int RT, int ST>
+__device__ __forceinline__ void butterfly_stage(float* v, int lane) {
+    constexpr int half = (RT >> ST) >> 1;
+    constexpr int bit = 32 >> ST;
+#pragma unroll
+    for (int i = 0; i < half; i++) {
+        float keep, send;
+        if constexpr (RT >= 8) {
+            keep = lane_pick<bit>(v[i], v[half + i]);
+            send = lane_pick<bit>(v[half + i], v[i]);
+        } else {
+            const bool upper = (lane & bit) != 0;
+            keep = upper ? v[half + i] : v[i];
+            send = upper ? v[i] : v[half + i];
+        }
+        v[i] = keep + __shfl_xor(send, bit, kWave);
+    }
+}
+
 // Reduce RT per-lane partials over the wavefront and store the tile's rows.
 // Stage s exchanges across lane bit (5-s) and keeps half of the live values,
 // so RT values cost RT-1 + (6-log2 RT) shuffles instead of 6*RT.  Afterwards
 // fragment row i's sum sits in lanes [i*64/RT, (i+1)*64/RT); for a pair tile
 // the up row of gate row i is row i + RT/2, i.e. 32 lanes up.
-template <int RT, int EPI>
+template <int RT, int EPI, int NTOK = 1>
 __device__ __forceinline__ void reduce_store(float* v, const GemvArgs& a, uint32_t t, float scale, int lane) {
     constexpr int LOG = (RT >= 8) ? 3 : (RT >= 4) ? 2 : (RT >= 2) ? 1 : 0;
-#pragma unroll
-    for (int st = 0; st < LOG; st++) {
-        const int half = (RT >> st) >> 1;
-        const int bit = 32 >> st;
-        const bool upper = (lane & bit) != 0;
-#pragma unroll
-        for (int i = 0; i < half; i++) {
-            const float keep = upper ? v[half + i] : v[i];
-            const float send = upper ? v[i] : v[half + i];
-            v[i] = keep + __shfl_xor(send, bit, kWave);
-        }
-    }
+    static_assert(RT <= 8, "at most 8 values per lane");
+    if constexpr (LOG >= 1) butterfly_stage<RT, 0>(v, lane);
+    if constexpr (LOG >= 2) butterfly_stage<RT, 1>(v, lane);
+    if constexpr (LOG >= 3) butterfly_stage<RT, 2>(v, lane);
     float s = v[0];
 #pragma unroll
     for (int off = 32 >> LOG; off >= 1; off >>= 1) s += __shfl_xor(s, off, kWave);
@@ -886,12 +949,12 @@ __device__ __forceinline__ void reduce_store(float* v, const GemvArgs& a, uint32
         const float u = __shfl_xor(s, 32, kWave);
         const uint32_t row = t * (RT / 2) + fr;
         if (leader && fr < static_cast<uint32_t>(RT / 2) && row < a.rows) a.y[row] = gate_act(a.act, s, u);
-    } else if constexpr (EPI == EPI_TOK2) {
-        // RT values per lane: token 0's RT/2 rows, then token 1's
-        static_assert(RT >= 2, "a two-token tile holds a value per token");
-        constexpr uint32_t RH = RT / 2;
-        const uint32_t row = t * RH + fr % RH;
-        if (leader && row < a.rows) a.y[(fr / RH) * a.rows + row] = s;
+    } else if constexpr (EPI == EPI_TOK) {
+        // RT values per lane: token 0's RT/NTOK rows, then token 1's, ...
+        static_assert(NTOK >= 2 && RT % NTOK == 0, "a token tile holds a value per token");
+        constexpr uint32_t RH = RT / NTOK;
+        const uint32_t row = t * RH + fr % RH, tok = fr / RH;
+        if (leader && row < a.rows && tok < a.m) a.y[tok * a.rows + row] = s;
     } else {
         const uint32_t row = t * RT + fr;
         if (leader && row < a.rows) {
@@ -1016,6 +1079,16 @@ __device__ __forceinline__ void compute_group_tok(const Frag<QT, RT> (&f)[STEPS]
     }
 }
 
+// The fragments' sums for every staged token (one: compute_group).
+template <int QT, int RT, int STEPS, bool EXACT, bool FENCE, int KCAP, bool XQ, int NTOK, int XF, int XR>
+__device__ __forceinline__ void compute_tokens(const Frag<QT, RT> (&f)[STEPS], const float* xl, const float* xs,
+                                               int C, int cb, int lane, float* acc) {
+    if constexpr (NTOK == 1)
+        compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
+    else
+        compute_group_tok<QT, RT, STEPS, EXACT, NTOK, XF, XR, KCAP>(f, xl, xs, C, cb, lane, acc);
+}
+
 // One GEMV: y[r] = sum_k w[r,k] * x[k] for r < rows, k = nb * block_elems,
 // in the prologue/epilogue form PRO/EPI.  A wave owns row tiles
 // blockIdx*WAVES + wid + j*gridDim*WAVES.  For each tile it issues the loads
@@ -1035,7 +1108,7 @@ __device__ __forceinline__ void compute_group_tok(const Frag<QT, RT> (&f)[STEPS]
 template <int QT, int KCAP, int WAVES, int RT, int STEPS, bool EXACT, bool NT, int PRO, int EPI, bool PF = false,
           bool FENCE = false, bool XQ = false>
 __device__ __forceinline__ void gemv(const GemvArgs& a) {
-    static_assert((PRO == PRO_TOK2) == (EPI == EPI_TOK2), "the two-token prologue and epilogue go together");
+    static_assert((PRO == PRO_TOK2) == (EPI == EPI_TOK), "the two-token prologue and epilogue go together");
     static_assert(PRO != PRO_TOK2 || (!PF && !XQ), "two-token instances stage fp32 x and do not prefetch");
     constexpr int NTOK = PRO == PRO_TOK2 ? 2 : 1;  // x rows staged, values per fragment row
     constexpr int XF = XTile<KCAP>::kFloats, XR = XTile<KCAP>::kRuns + 1;
@@ -1103,34 +1176,236 @@ __device__ __forceinline__ void gemv(const GemvArgs& a) {
         }
         return;
     }
-    // the fragments' sums for every staged token
-    auto compute = [&](int cb) {
-        if constexpr (NTOK == 1)
-            compute_group<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ>(f, xl, xs, C, cb, lane, acc);
-        else
-            compute_group_tok<QT, RT, STEPS, EXACT, NTOK, XF, XR, KCAP>(f, xl, xs, C, cb, lane, acc);
-    };
 #pragma unroll
     for (int r = 0; r < RT * NTOK; r++) acc[r] = 0.0f;
-    compute(0);
+    compute_tokens<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ, NTOK, XF, XR>(f, xl, xs, C, 0, lane, acc);
     if constexpr (!EXACT) {
         for (int cb = GROUP; cb < C; cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute(cb);
+            compute_tokens<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ, NTOK, XF, XR>(f, xl, xs, C, cb, lane, acc);
         }
     }
-    if (tile < ntiles) reduce_store<RT * NTOK, EPI>(acc, a, tile, scale, lane);
+    if (tile < ntiles) reduce_store<RT * NTOK, EPI, NTOK>(acc, a, tile, scale, lane);
     for (tile += tstride; tile < ntiles; tile += tstride) {
         tr = tile_rows<RT, PAIR>(a, tile);
 #pragma unroll
         for (int r = 0; r < RT * NTOK; r++) acc[r] = 0.0f;
         for (int cb = 0; cb < (EXACT ? 1 : C); cb += GROUP) {
             load_group<QT, RT, STEPS, EXACT, NT>(f, tr, a.nb, C, cb, lane);
-            compute(cb);
+            compute_tokens<QT, RT, STEPS, EXACT, FENCE, KCAP, XQ, NTOK, XF, XR>(f, xl, xs, C, cb, lane, acc);
         }
-        reduce_store<RT * NTOK, EPI>(acc, a, tile, scale, lane);
+        reduce_store<RT * NTOK, EPI, NTOK>(acc, a, tile, scale, lane);
     }
 }
+// ---- the int path for a few tokens -------------------------------------------
+// zlm's int prefill arithmetic (activations quantized to q8 blocks,
+// matvec/layout.zig:458-476; integer block dots scaled per block,
+// kernels/quantized.zig:49-55 q4_0, :79-87 q4_1, :111-123 q4_k, :149-156 q8_0)
+// for m <= NTOK tokens in one pass over the weights in the GEMV layout.  Each
+// workgroup quantizes the m activation rows into LDS itself (q8_quant4, the
+// quantizer kernel's arithmetic); each lane loads its weight chunk once and
+// forms the chunk's integer dot with every token (v_dot4_i32_i8; nibbles
+// 0..15 are valid int8), then scales it in fp32.
+
+// One token's q8 tile in LDS, in 4-byte words: the q bytes (KCAP/4 words, in
+// the order the quant's chunks read them, q8_pos), the 16-element run sums
+// (int32, natural order), the 32-element block scales dx (natural order) and
+// 4 dummy words that out-of-range threads store to.
+template <int KCAP>
+struct Q8Tile {
+    static constexpr int kRuns = KCAP / 4;
+    static constexpr int kDx = kRuns + KCAP / 16;
+    static constexpr int kDummy = kDx + KCAP / 32;
+    static constexpr int kWords = kDummy + 4;
+};
+
+// Byte offset in the q area of element e (e a multiple of 4 here): q8_0 in
+// order; q4_0 / q4_1 elements 0-15 of block b at 16b in the first half of
+// the area and elements 16-31 at 16b in the second; q4_k the elements of
+// sub-block 2g of super-block sb (nibble lows of the group's qs bytes) at
+// 128sb + 32g + r in the first half and those of sub-block 2g+1 in the
+// second.  Chunk c then reads its two 16-element runs at 16c in each half:
+// consecutive lanes read consecutive 16-byte words.
+template <int QT, int KCAP>
+__device__ __forceinline__ int q8_pos(int e) {
+    if constexpr (QT == Q8_0) {
+        return e;
+    } else if constexpr (QT == Q4_K) {
+        const int r = e & 63, base = 128 * (e >> 8) + 32 * ((e >> 6) & 3);
+        return r < 32 ? base + r : KCAP / 2 + base + r - 32;
+    } else {
+        const int j = e & 31, base = 16 * (e >> 5);
+        return j < 16 ? base + j : KCAP / 2 + base + j - 16;
+    }
+}
+
+// Quantize one token's x (NX float4 per thread, k elements) into its tile.
+// Thread i's float4 holds elements 4i..4i+3: lanes 8b..8b+7 of a wave share
+// block b (k is a multiple of 32, so a block's lanes are all in range or all
+// out), lanes 4r..4r+3 run r.
+template <int QT, int KCAP, int NX>
+__device__ __forceinline__ void q8_store(const XRegs<NX>& r, int k, uint32_t* t) {
+    using T = Q8Tile<KCAP>;
+    const int n4 = k >> 2;
+#pragma unroll
+    for (int j = 0; j < NX; j++) {
+        const int i = j * static_cast<int>(blockDim.x) + static_cast<int>(threadIdx.x);
+        const bool valid = i < n4;
+        const float4 v = valid ? r.v[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float d;
+        int32_t s;
+        const uint32_t wv = q8_quant4(v, d, s);
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        t[valid ? q8_pos<QT, KCAP>(4 * i) / 4 : T::kDummy] = wv;
+        t[(valid && (i & 3) == 0) ? T::kRuns + (i >> 2) : T::kDummy + 1] = static_cast<uint32_t>(s);
+        t[(valid && (i & 7) == 0) ? T::kDx + (i >> 3) : T::kDummy + 2] = __builtin_bit_cast(uint32_t, d);
+    }
+}
+
+__device__ __forceinline__ int dot16(const uint32_t (&w)[4], uint4 q, int acc) {
+    acc = __builtin_amdgcn_sdot4(static_cast<int>(w[0]), static_cast<int>(q.x), acc, false);
+    acc = __builtin_amdgcn_sdot4(static_cast<int>(w[1]), static_cast<int>(q.y), acc, false);
+    acc = __builtin_amdgcn_sdot4(static_cast<int>(w[2]), static_cast<int>(q.z), acc, false);
+    return __builtin_amdgcn_sdot4(static_cast<int>(w[3]), static_cast<int>(q.w), acc, false);
+}
+
+// Chunk c of one weight row against NTOK token tiles (tile t at tq + t *
+// kWords): acc[t] += the chunk's share of row . x_t in the int path's form:
+//   q4_0  (dw*dx) * (sum nib*q - 8 * sum q)             (block c)
+//   q4_1  (d*dx) * sum nib*q + (m*dx) * sum q          (block c)
+//   q8_0  (dw*dx) * sum w*q                            (half c&1 of block c>>1)
+//   q4_k  per sub-block half: (d*sc*dx) * sum nib*q - (dmin*mn*dx) * sum q
+//         (the lows of the chunk's 16 qs bytes: sub-block 2g, the highs 2g+1)
+// The integer parts are exact; valid = false zeroes the scales.
+template <int QT, int KCAP, int NTOK>
+__device__ __forceinline__ void compute_int(const Frag<QT, 1>& f, const uint32_t* tq, int c, bool valid,
+                                            float* acc) {
+    using T = Q8Tile<KCAP>;
+    const uint32_t w[4] = {f.q[0].x, f.q[0].y, f.q[0].z, f.q[0].w};
+    if constexpr (QT == Q8_0) {
+        const float dw = valid ? h2f(f.d[0]) : 0.0f;
+#pragma unroll
+        for (int t = 0; t < NTOK; t++) {
+            const uint32_t* tt = tq + t * T::kWords;
+            const int dot = dot16(w, *reinterpret_cast<const uint4*>(tt + 4 * c), 0);
+            const float dx = __builtin_bit_cast(float, tt[T::kDx + (c >> 1)]);
+            acc[t] = fmaf(dw * dx, static_cast<float>(dot), acc[t]);
+        }
+    } else {
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = w[i] & 0x0F0F0F0Fu;
+            hi[i] = (w[i] >> 4) & 0x0F0F0F0Fu;
+        }
+        if constexpr (QT == Q4_K) {
+            const uint32_t dd = valid ? f.dm[0] : 0u;
+            const float d = h2f(dd), dmin = h2f(dd >> 16);
+            const float sc1 = ub(f.sm[0], 0), sc2 = ub(f.sm[0], 1), mn1 = ub(f.sm[0], 2), mn2 = ub(f.sm[0], 3);
+            const int sb = c >> 3, p = c & 7, g = p >> 1;
+            const int run_lo = 16 * sb + 4 * g + (p & 1), blk_lo = 8 * sb + 2 * g;
+#pragma unroll
+            for (int t = 0; t < NTOK; t++) {
+                const uint32_t* tt = tq + t * T::kWords;
+                const int dlo = dot16(lo, *reinterpret_cast<const uint4*>(tt + 4 * c), 0);
+                const int dhi = dot16(hi, *reinterpret_cast<const uint4*>(tt + KCAP / 8 + 4 * c), 0);
+                const float slo = static_cast<float>(static_cast<int32_t>(tt[T::kRuns + run_lo]));
+                const float shi = static_cast<float>(static_cast<int32_t>(tt[T::kRuns + run_lo + 2]));
+                const float xlo = __builtin_bit_cast(float, tt[T::kDx + blk_lo]);
+                const float xhi = __builtin_bit_cast(float, tt[T::kDx + blk_lo + 1]);
+                float v = (d * sc1 * xlo) * static_cast<float>(dlo);
+                v = fmaf(d * sc2 * xhi, static_cast<float>(dhi), v);
+                v = fmaf(-(dmin * mn1 * xlo), slo, v);
+                v = fmaf(-(dmin * mn2 * xhi), shi, v);
+                acc[t] += v;
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NTOK; t++) {
+                const uint32_t* tt = tq + t * T::kWords;
+                int dot = dot16(lo, *reinterpret_cast<const uint4*>(tt + 4 * c), 0);
+                dot = dot16(hi, *reinterpret_cast<const uint4*>(tt + KCAP / 8 + 4 * c), dot);
+                const int sq = static_cast<int32_t>(tt[T::kRuns + 2 * c]) + static_cast<int32_t>(tt[T::kRuns + 2 * c + 1]);
+                const float dx = __builtin_bit_cast(float, tt[T::kDx + c]);
+                if constexpr (QT == Q4_0) {
+                    const float dw = valid ? h2f(f.d[0]) : 0.0f;
+                    acc[t] = fmaf(dw * dx, static_cast<float>(dot - 8 * sq), acc[t]);
+                } else {
+                    const uint32_t dm = valid ? f.dm[0] : 0u;
+                    acc[t] = fmaf(h2f(dm) * dx, static_cast<float>(dot), acc[t]);
+                    acc[t] = fmaf(h2f(dm >> 16) * dx, static_cast<float>(sq), acc[t]);
+                }
+            }
+        }
+    }
+}
+
+// compute_int over a group of STEPS chunk steps, a scheduling barrier after
+// each step.
+template <int QT, int KCAP, int NTOK, int STEPS>
+__device__ __forceinline__ void compute_group_int(const Frag<QT, 1> (&f)[STEPS], const uint32_t* tq, int C, int cb,
+                                                  int lane, float* acc) {
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+        const int c = cb + lane + s * kWave;
+        if (cb + s * kWave < C) compute_int<QT, KCAP, NTOK>(f[s], tq, min(c, C - 1), c < C, acc);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// y[t * rows + r] = row r . x_t (int path) for t < m <= NTOK: one-row wave
+// tiles (tile = blockIdx*WAVES + wid + j*gridDim*WAVES), each row walked in
+// groups of STEPS chunk steps (one memory round trip per group).  The first
+// tile's first group is loaded before the activations are quantized, so the
+// staging overlaps it.  Rows of x past m repeat row m-1 and are not stored.
+template <int QT, int NTOK, int KCAP, int WAVES, int STEPS>
+__device__ __forceinline__ void gemv_int(const GemvArgs& a) {
+    static_assert(QT == Q4_0 || QT == Q4_1 || QT == Q8_0 || QT == Q4_K, "int path quants");
+    static_assert(NTOK >= 2 && NTOK <= 8, "the row reduction holds at most 8 values per lane");
+    using T = Q8Tile<KCAP>;
+    __shared__ __attribute__((aligned(16))) uint32_t tq[T::kWords * NTOK];
+    constexpr int NX = (KCAP / 4 + WAVES * kWave - 1) / (WAVES * kWave);
+    constexpr int GROUP = STEPS * kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wid = threadIdx.x / kWave;
+    const int C = chunks_per_row<QT>(a.nb);
+    const uint32_t ntiles = a.rows;
+    const uint32_t tstride = gridDim.x * WAVES;
+    uint32_t tile = blockIdx.x * WAVES + wid;
+    const int k = static_cast<int>(a.nb) * elems_per_block<QT>();
+
+    XRegs<NX> xr[NTOK];
+#pragma unroll
+    for (int t = 0; t < NTOK; t++) xload(a.x + static_cast<size_t>(min(static_cast<uint32_t>(t), a.m - 1)) * k, k, xr[t]);
+    Frag<QT, 1> f[STEPS];
+    TileRows<1> tr = tile_rows<1, false>(a, min(tile, ntiles - 1));
+    load_group<QT, 1, STEPS, false, true>(f, tr, a.nb, C, 0, lane);
+#pragma unroll
+    for (int t = 0; t < NTOK; t++) q8_store<QT, KCAP, NX>(xr[t], k, tq + t * T::kWords);
+    __syncthreads();
+
+    float acc[NTOK];
+#pragma unroll
+    for (int t = 0; t < NTOK; t++) acc[t] = 0.0f;
+    compute_group_int<QT, KCAP, NTOK, STEPS>(f, tq, C, 0, lane, acc);
+    for (int cb = GROUP; cb < C; cb += GROUP) {
+        load_group<QT, 1, STEPS, false, true>(f, tr, a.nb, C, cb, lane);
+        compute_group_int<QT, KCAP, NTOK, STEPS>(f, tq, C, cb, lane, acc);
+    }
+    if (tile < ntiles) reduce_store<NTOK, EPI_TOK, NTOK>(acc, a, tile, 1.0f, lane);
+    for (tile += tstride; tile < ntiles; tile += tstride) {
+        tr = tile_rows<1, false>(a, tile);
+#pragma unroll
+        for (int t = 0; t < NTOK; t++) acc[t] = 0.0f;
+        for (int cb = 0; cb < C; cb += GROUP) {
+            load_group<QT, 1, STEPS, false, true>(f, tr, a.nb, C, cb, lane);
+            compute_group_int<QT, KCAP, NTOK, STEPS>(f, tq, C, cb, lane, acc);
+        }
+        reduce_store<NTOK, EPI_TOK, NTOK>(acc, a, tile, 1.0f, lane);
+    }
+}
+
 // ---- several matrices over one x in one launch -------------------------------
 // The contract's matVecResidentBatch (reference gpu/backend/root.zig:249-254,
 // vulkan/pipeline.zig:1770-1802) runs up to RingSize GEMVs that share k and x.
@@ -1700,13 +1975,27 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 // grows with the tier (4, 8, 16 waves) to keep 16 waves per CU.
 #define ZLM_GEMVT(NAME, QT, KCAP, WAVES, STEPS)                                   \
     extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {   \
-        gemv<QT, KCAP, WAVES, 1, STEPS, false, true, PRO_TOK2, EPI_TOK2>(a);      \
+        gemv<QT, KCAP, WAVES, 1, STEPS, false, true, PRO_TOK2, EPI_TOK>(a);       \
     }
 // STEPS: 2 for the 32-element chunks of q4_0 / q4_1 / q4_k, 4 for q8_0's 16
 #define ZLM_GEMV_TOK2(QN, QT, STEPS)                                    \
     ZLM_GEMVT(zlm_gemv_##QN##_tok2_g4, QT, 4096, 4, STEPS)              \
     ZLM_GEMVT(zlm_gemv_##QN##_tok2_g8, QT, 8192, 8, STEPS)              \
     ZLM_GEMVT(zlm_gemv_##QN##_tok2_g16, QT, 16384, 16, STEPS)
+
+// Int-path token instances zlm_gemv_<quant>_q8tok4_g<T> (T = 4, 8: k <=
+// 1024*T): matMul at m = 3, 4.  16-wave workgroups (one float4 of each
+// token's x per thread at the 4096-float tier); the tiles take 1.375 * T KiB
+// per token.  Eight token slots measured slower than the tiled GEMM on most
+// shapes (quantizing eight rows per workgroup and twice the LDS reads), so
+// from 5 tokens the GEMM runs.
+#define ZLM_GEMVQ(NAME, QT, NTOK, KCAP, STEPS)                                     \
+    extern "C" __global__ void __launch_bounds__(1024) NAME(GemvArgs a) {          \
+        gemv_int<QT, NTOK, KCAP, 16, STEPS>(a);                                    \
+    }
+#define ZLM_GEMV_Q8TOK(QN, QT, STEPS)                                   \
+    ZLM_GEMVQ(zlm_gemv_##QN##_q8tok4_g4, QT, 4, 4096, STEPS)            \
+    ZLM_GEMVQ(zlm_gemv_##QN##_q8tok4_g8, QT, 4, 8192, STEPS)
 
 // The fused forms take one GemvArgs: zlm_gemv_<quant>_<form>_s<STEPS> (exact
 // steps) and zlm_gemv_<quant>_<form>_g<STEPS> (generic), form one of

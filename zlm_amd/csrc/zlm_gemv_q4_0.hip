@@ -38,3 +38,6 @@ ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)
 
 // matMul at m = 2 (both tokens in one pass over the weights)
 ZLM_GEMV_TOK2(q4_0, Q4_0, 2)
+
+// matMul at m = 3, 4 (int path, the weights read once for all tokens)
+ZLM_GEMV_Q8TOK(q4_0, Q4_0, 2)

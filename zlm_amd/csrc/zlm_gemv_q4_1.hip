@@ -11,3 +11,6 @@ ZLM_GEMV_MULTI_Q4(q4_1, Q4_1)
 
 // matMul at m = 2 (both tokens in one pass over the weights)
 ZLM_GEMV_TOK2(q4_1, Q4_1, 2)
+
+// matMul at m = 3, 4 (int path, the weights read once for all tokens)
+ZLM_GEMV_Q8TOK(q4_1, Q4_1, 2)

@@ -550,13 +550,15 @@ bool ensure_layout(zlm_device* d, zlm_resident* r, const QuantInfo* qi) {
 // the block size is the kernel's launch bound.
 // What a GEMV entry point computes and how it takes its arguments, read from
 // its name zlm_gemv_<quant>_<rest>: <rest> "multi_..." is the batch kernel,
-// "tok2_..." the two-token GEMV, "pair_" / "normpair_" / "norm_" / "resid_" a
-// fused form (ZLM_FORM_*), anything else the plain GEMV.  Only the plain exact-steps and generic instances
-// (r<RT>_s<STEPS>, r<RT>_g) take separate arguments; every other instance
+// "tok2_..." the two-token GEMV, "q8tok..." the int-path token GEMV,
+// "pair_" / "normpair_" / "norm_" / "resid_" a fused form (ZLM_FORM_*),
+// anything else the plain GEMV.  Only the plain exact-steps and generic
+// instances (r<RT>_s<STEPS>, r<RT>_g) take separate arguments; every other instance
 // takes one GemvArgs.  The host checks a cached kernel's role before each
 // launch, so a kernel picked for one form can never be launched as another.
 constexpr int kRoleMulti = 16;
 constexpr int kRoleTok2 = 17;
+constexpr int kRoleQ8Tok = 18;
 
 void kernel_role(const char* name, int slot, int* role, bool* struct_args) {
     const char* rest = name + strlen("zlm_gemv_") + strlen(kQuantNames[slot]) + 1;
@@ -565,6 +567,7 @@ void kernel_role(const char* name, int slot, int* role, bool* struct_args) {
         int role;
     } kForms[] = {{"multi_", kRoleMulti},
                   {"tok2_", kRoleTok2},
+                  {"q8tok", kRoleQ8Tok},
                   {"pair_", ZLM_FORM_PAIR},
                   {"normpair_", ZLM_FORM_NORMPAIR},
                   {"norm_", ZLM_FORM_NORM},
@@ -691,7 +694,7 @@ bool resid_two_rows(const QuantInfo* qi, int steps, size_t rows) {
 // ~1 us per launch, most of a small GEMV's enqueue).
 // The kernel picked per shape class: (k, quant slot, what is picked, its
 // parameter, row-count class) in disjoint bit fields.
-enum PickKind : uint64_t { kPickPlain = 0, kPickForm = 1, kPickPairTile = 2, kPickTok2 = 3 };
+enum PickKind : uint64_t { kPickPlain = 0, kPickForm = 1, kPickPairTile = 2, kPickTok2 = 3, kPickQ8Tok = 4 };
 
 uint64_t pick_key(const QuantInfo* qi, size_t k, PickKind kind, int param, size_t rows) {
     const uint64_t rows_class = rows >= 65536 ? 2 : rows <= 8192 ? 1 : 0;
@@ -822,8 +825,9 @@ struct GemvArgsHost {
     uint32_t nb;
     float eps;
     uint32_t act;
+    uint32_t m;  // the token forms: rows of x and y
 };
-static_assert(sizeof(GemvArgsHost) == 80, "GemvArgs layout");
+static_assert(sizeof(GemvArgsHost) == 88, "GemvArgs layout");
 
 bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, size_t k, const float* x_dev,
                   float* y_dev) {
@@ -837,7 +841,7 @@ bool enqueue_gemv(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     const uint16_t* s = r->scales;
     uint32_t rows32 = static_cast<uint32_t>(rows), nb = static_cast<uint32_t>(k / qi->kblock);
     if (gk->struct_args) {
-        GemvArgsHost a = {w, s, w, s, x_dev, x_dev, y_dev, y_dev, rows32, nb, 0.0f, 0u};
+        GemvArgsHost a = {w, s, w, s, x_dev, x_dev, y_dev, y_dev, rows32, nb, 0.0f, 0u, 1u};
         void* args[] = {&a};
         return launch(d, f, grid, block, args, "gemv");
     }
@@ -865,10 +869,58 @@ bool enqueue_gemv_tok2(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size
     const uint8_t* w = r->payload;
     const uint16_t* s = r->scales;
     GemvArgsHost a = {w, s, w, s, x_dev, x_dev, y_dev, y_dev, static_cast<uint32_t>(rows),
-                      static_cast<uint32_t>(k / qi->kblock), 0.0f, 0u};
+                      static_cast<uint32_t>(k / qi->kblock), 0.0f, 0u, 2u};
     void* args[] = {&a};
     *ran = true;
     return launch(d, gk->fn, grid, static_cast<unsigned>(gk->threads), args, "gemv two tokens");
+}
+
+// The int path for 3 <= m <= kQ8TokM tokens and k <= kQ8TokMaxK in one pass
+// over the weights (zlm_gemv_<quant>_q8tok4_g<T>: T = 4 or 8 for k <= 4096
+// or 8192; every workgroup quantizes the m activation rows itself), or null:
+// the caller runs the small-M GEMM.  Measured on gfx950 (m = 3-4, against
+// the quantizer + small-M GEMM): 4096 x 4096 Q4_0 9.9 -> 7.4 us, Q4_K 13.2 ->
+// 7.7 us, 12288 x 4096 Q8_0 19.4 -> 14.7 us, the 262144 x 3840 Q4_K lm_head
+// 269 -> 194 us; eight token slots were slower than the GEMM on most shapes.
+constexpr size_t kQ8TokM = 4;
+constexpr size_t kQ8TokMaxK = 8192;
+
+const GemvKernel* pick_q8tok(zlm_device* d, const QuantInfo* qi, size_t k) {
+    const int ntok = static_cast<int>(kQ8TokM);
+    const uint64_t key = pick_key(qi, k, kPickQ8Tok, ntok, 0);
+    auto it = d->picks.find(key);
+    if (it != d->picks.end()) return it->second;
+    const GemvKernel* g = nullptr;
+    if (k <= kQ8TokMaxK) {
+        char nm[96];
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_q8tok%d_g%d", kQuantNames[qi->slot], ntok, k <= 4096 ? 4 : 8);
+        g = find_gemv(d, qi->slot, nm, 1, 0);
+    }
+    d->picks.emplace(key, g);
+    return g;
+}
+
+// Enqueue the int-path token GEMV (y_dev[t * rows + r], t < m) where an
+// instance covers (m, k); *ran = false otherwise.  One 16-wave workgroup per
+// CU, each looping over row tiles.
+bool enqueue_gemv_q8tok(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t rows, size_t k, size_t m,
+                        const float* x_dev, float* y_dev, bool* ran) {
+    *ran = false;
+    if (m < 3 || m > kQ8TokM) return true;
+    const GemvKernel* gk = pick_q8tok(d, qi, k);
+    if (!gk) return true;
+    if (gk->role != kRoleQ8Tok || !gk->struct_args)
+        return fail(d, "internal: picked kernel (role %d) is not the int token GEMV", gk->role);
+    const uint64_t waves = static_cast<uint64_t>(gk->threads / 64);
+    const uint64_t wgs = (rows + waves - 1) / waves;
+    const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->cus)));
+    const uint8_t* w = r->payload;
+    const uint16_t* s = r->scales;
+    GemvArgsHost a = {w, s, w, s, x_dev, x_dev, y_dev, y_dev, static_cast<uint32_t>(rows),
+                      static_cast<uint32_t>(k / qi->kblock), 0.0f, 0u, static_cast<uint32_t>(m)};
+    void* args[] = {&a};
+    *ran = true;
+    return launch(d, gk->fn, grid, static_cast<unsigned>(gk->threads), args, "gemv int tokens");
 }
 
 // ---- fused GEMV forms (prologue/epilogue variants of the same kernel) ----
@@ -1023,7 +1075,7 @@ bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     if (gk->role != static_cast<int>(op.form) || !gk->struct_args)
         return fail(d, "internal: picked kernel (role %d) does not compute the %s form", gk->role,
                     kFormNames[op.form]);
-    GemvArgsHost a;
+    GemvArgsHost a = {};
     a.w0 = op.w->payload;
     a.d0 = op.w->scales;
     a.w1 = pair ? op.w_up->payload : op.w->payload;
@@ -1036,6 +1088,7 @@ bool enqueue_op(zlm_device* d, const zlm_gemv_op& op) {
     a.nb = static_cast<uint32_t>(op.k / qi->kblock);
     a.eps = op.eps;
     a.act = op.act;
+    a.m = 1;
     void* args[] = {&a};
     const uint64_t per_tile = static_cast<uint64_t>(pair ? gk->rt / 2 : gk->rt);  // output rows per tile
     const uint64_t tiles = (op.rows + per_tile - 1) / per_tile;
@@ -1256,6 +1309,11 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
         for (size_t t = 0; t < m; t++)
             if (!enqueue_gemv(d, r, quant, rows, k, x_dev + t * k, out_dev + t * rows)) return false;
         return true;
+    }
+    {  // a few tokens: the int path in one pass over the GEMV layout, no tiled copy or quantizer launch
+        bool ran = false;
+        if (!enqueue_gemv_q8tok(d, r, qi, rows, k, m, x_dev, out_dev, &ran)) return false;
+        if (ran) return true;
     }
     if (!ensure_gemm_tiles(d, r, qi, nb)) return false;
     if (r->gemm_rt * 32 < rows) return fail(d, "GEMM tiles too short");

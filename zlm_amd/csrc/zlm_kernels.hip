@@ -274,16 +274,6 @@ extern "C" __global__ void __launch_bounds__(256)
 // the one-thread-per-block quantizer's.  At 512 x 4096: 6.3 -> 5.5 us (one
 // thread per slot before; numbering the threads in input order instead, so a
 // wave reads 1 KiB of one token's row, measured 5.9 us).
-__device__ __forceinline__ float max8(float v) {
-    v = fmaxf(v, __shfl_xor(v, 1, kWave));
-    v = fmaxf(v, __shfl_xor(v, 2, kWave));
-    return fmaxf(v, __shfl_xor(v, 4, kWave));
-}
-__device__ __forceinline__ int32_t sum8(int32_t v) {
-    v += __shfl_xor(v, 1, kWave);
-    v += __shfl_xor(v, 2, kWave);
-    return v + __shfl_xor(v, 4, kWave);
-}
 extern "C" __global__ void __launch_bounds__(256)
     zlm_quantize_q8_tiled(const float* __restrict__ x, int8_t* __restrict__ qx, float* __restrict__ dx,
                           uint32_t m, uint32_t nb, uint32_t mt, float* __restrict__ ds) {
@@ -296,19 +286,9 @@ extern "C" __global__ void __launch_bounds__(256)
     const uint32_t t = static_cast<uint32_t>(tb / nb) * 32 + static_cast<uint32_t>(slot % 32);
     float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     if (t < m) v = reinterpret_cast<const float4*>(x + (static_cast<uint64_t>(t) * nb + b) * 32)[part];
-    const float amax = max8(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    const float d = __fdiv_rn(amax, 127.0f);
-    const float inv = (d != 0.0f) ? __fdiv_rn(1.0f, d) : 0.0f;
-    const float e[4] = {v.x, v.y, v.z, v.w};
-    int32_t s = 0;
-    uint32_t wv = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        int32_t q = static_cast<int32_t>(roundf(e[j] * inv));
-        q = q > 127 ? 127 : (q < -127 ? -127 : q);
-        s += q;
-        wv |= (static_cast<uint32_t>(q) & 0xffu) << (8 * j);
-    }
+    float d;
+    int32_t s;
+    const uint32_t wv = q8_quant4(v, d, s);
     s = sum8(s);
     if (i / 8 >= nslot) return;
     reinterpret_cast<uint32_t*>(qx + slot * 32)[part] = wv;
