@@ -140,6 +140,11 @@ def test_int_tokens_match_oracle(dev, qt, zq, rows, k, m):
         again = np.full(m * rows, np.nan, np.float32)
         assert dev.mat_mul_resident(res, zd.quant(zq), rows, k, m, x, again), dev.last_error()
         np.testing.assert_array_equal(again.view(np.uint32), out.view(np.uint32))
+        # the reference's int-vs-fp bound (kernels/quantized_test.zig:61) against its fp matMulRows
+        fp = oracle.matmul_rows(qt, w, k, rows, m, x)
+        dq = np.abs(oracle.dequant(qt, w, rows * k).reshape(rows, k).astype(np.float64))
+        mag = np.abs(x.reshape(m, k).astype(np.float64)) @ dq.T
+        assert np.all(np.abs(out.reshape(m, rows) - fp) <= 0.02 * mag + 1e-6)
     finally:
         dev.free_resident(res)
 

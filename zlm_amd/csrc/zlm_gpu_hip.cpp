@@ -135,6 +135,9 @@ struct Slot {
     float* h_x = nullptr;
     float* h_x_dev = nullptr;
     size_t x_cap = 0;
+    float* h_bx = nullptr;  // pinned; a burst's activation when this slot is its first member
+    float* h_bx_dev = nullptr;
+    size_t bx_cap = 0;
     bool pending = false;
     uint32_t gen = 0;
     size_t rows = 0;
@@ -246,12 +249,9 @@ struct zlm_device {
     float* d_mid = nullptr;
     size_t mid_cap = 0;
 
-    // burst-shared activation
+    // burst-shared activation (device; staged through the first member's slot)
     float* d_bx = nullptr;
-    float* h_bx = nullptr;
-    float* h_bx_dev = nullptr;
     size_t bx_cap = 0;
-    hipEvent_t bx_copied = nullptr;
     const float* burst_src = nullptr;
     size_t burst_len = 0;
     bool burst_open = false;
@@ -1421,6 +1421,7 @@ extern "C" void zlm_gpu_deinit(zlm_device* d) {
             if (s.h_y) hipHostFree(s.h_y);
             if (s.d_x) hipFree(s.d_x);
             if (s.h_x) hipHostFree(s.h_x);
+            if (s.h_bx) hipHostFree(s.h_bx);
         }
         if (d->d_x) hipFree(d->d_x);
         if (d->h_x) hipHostFree(d->h_x);
@@ -1429,8 +1430,6 @@ extern "C" void zlm_gpu_deinit(zlm_device* d) {
         if (d->attn_part) hipFree(d->attn_part);
         if (d->d_mid) hipFree(d->d_mid);
         if (d->d_bx) hipFree(d->d_bx);
-        if (d->h_bx) hipHostFree(d->h_bx);
-        if (d->bx_copied) hipEventDestroy(d->bx_copied);
         if (d->s_raw) hipFree(d->s_raw);
         if (d->q_scratch) hipFree(d->q_scratch);
         if (d->s_lay) hipFree(d->s_lay);
@@ -1560,18 +1559,18 @@ namespace {
 
 // The burst-shared activation (reference pipeline.zig:1422-1484): `first`
 // stages x into the device-owned buffer, later members must pass the same x
-// pointer and length and reuse it.  Returns the device copy, or null.
-const float* stage_burst(zlm_device* d, const float* x, size_t x_len, bool first) {
+// pointer and length and reuse it.  Returns the device copy, or null.  x goes
+// through the pinned buffer of slot `s`, the burst's first member: that
+// slot's completion event follows the copy on the stream, and the slot is
+// only reused after a wait on it, so the pinned buffer is never overwritten
+// while the copy may still read it (no event of its own).
+const float* stage_burst(zlm_device* d, const float* x, size_t x_len, bool first, int s) {
     if (first) {
-        // The previous burst's host->device copy must have consumed the pinned
-        // buffer before it is overwritten.
-        if (d->bx_copied && !ok(d, hipEventSynchronize(d->bx_copied), "burst wait")) return nullptr;
-        if (!ensure_pair(d, d->d_bx, d->h_bx, d->bx_cap, x_len, d->h_bx_dev)) return nullptr;
-        if (!d->bx_copied && !ok(d, hipEventCreateWithFlags(&d->bx_copied, hipEventDisableTiming), "event"))
-            return nullptr;
-        memcpy(d->h_bx, x, x_len * sizeof(float));
-        if (!stage_in(d, d->d_bx, d->h_bx_dev, d->h_bx, x_len) ||
-            !ok(d, hipEventRecord(d->bx_copied, d->stream), "record")) {
+        Slot& sl = d->slots[s];
+        if (!ensure_host(d, sl.h_bx, sl.h_bx_dev, sl.bx_cap, x_len)) return nullptr;
+        if (!ensure_dev(d, d->d_bx, d->bx_cap, x_len)) return nullptr;
+        memcpy(sl.h_bx, x, x_len * sizeof(float));
+        if (!stage_in(d, d->d_bx, sl.h_bx_dev, sl.h_bx, x_len)) {
             d->burst_open = false;
             return nullptr;
         }
@@ -1636,7 +1635,7 @@ extern "C" int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device* d, zlm_resid
     if (!prepare_gemv(d, r, quant, rows, k, &f, &g, &b)) return ZLM_NULL_HANDLE;
     const int s = find_free_slot(d);
     if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
-    const float* xd = stage_burst(d, x, x_len, first);
+    const float* xd = stage_burst(d, x, x_len, first, s);
     if (!xd) return ZLM_NULL_HANDLE;
     if (!submit_into_slot(d, s, r, quant, rows, k, xd)) return ZLM_NULL_HANDLE;
     return make_handle(d, s);
@@ -1771,7 +1770,7 @@ extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, z
     const int s = find_free_slot(d);
     if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
     if (!prepare_slot(d, s, rows)) return ZLM_NULL_HANDLE;
-    const float* xd = stage_burst(d, x, x_len, first);
+    const float* xd = stage_burst(d, x, x_len, first, s);
     if (!xd) return ZLM_NULL_HANDLE;
     zlm_gemv_op op = {};
     op.form = ZLM_FORM_PAIR;
@@ -1805,7 +1804,7 @@ extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, 
     const int s = find_free_slot(d);
     if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
     if (!prepare_slot(d, s, rows)) return ZLM_NULL_HANDLE;
-    const float* xd = stage_burst(d, x, x_len, first);
+    const float* xd = stage_burst(d, x, x_len, first, s);
     if (!xd) return ZLM_NULL_HANDLE;
     if (!enqueue_mlp(d, s, rg, ru, rd, with_variant(gu_quant, variant), down_quant, rows, k, ffn, xd, act) ||
         !finish_slot(d, s, rows))
