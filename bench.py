@@ -392,7 +392,7 @@ def sections(dev, args, want, extra):
         dev.dev_free(o_dev)
 
     # ---- small token counts (verify / microbatch), as reference gpu/root_test.zig:651-696 ----
-    if only is None and not args.quick and not args.no_small_m:
+    if (only is None and not args.quick and not args.no_small_m) or only == "smallm":
         sweep = {}
         for sname, qt, rows, k in (("q4_0_4096x4096", synth.Q4_0, 4096, 4096),
                                    ("q4_k_4096x4096", synth.Q4_K, 4096, 4096),
@@ -553,9 +553,10 @@ def main():
                     help="skip the small-token-count matMul sweep (its GEMVs share kernels with configs[0]/[3])")
     ap.add_argument("--counters", action="store_true",
                     help="short warm-ups and few launches per shape, for rocprofv3 --pmc passes (not a timing run)")
-    ap.add_argument("--only", choices=("roofline", "gemvs", "gemm", "decode"), default=None,
+    ap.add_argument("--only", choices=("roofline", "gemvs", "gemm", "smallm", "decode"), default=None,
                     help="run one section for a profiler: the roofline kernel's timing (configs[1] gate/up), the "
-                         "other configs' GEMVs, the configs[4] GEMM or the decode step; no JSON line")
+                         "other configs' GEMVs, the configs[4] GEMM, the small-token-count matMul sweep or the "
+                         "decode step; no JSON line")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES",
                     help="also run the library copy kernel 5x over BYTES (for HBM traffic counter calibration)")
     args = ap.parse_args()
@@ -584,7 +585,7 @@ def main():
     def want(section: str) -> bool:
         return (only is None and not args.quick) or only == section
 
-    if only in ("gemvs", "gemm", "decode"):
+    if only in ("gemvs", "gemm", "smallm", "decode"):
         return sections(dev, args, want, {})
 
     # ---- headline: configs[1], Q8_0 Qwen3-8B FFN GEMVs ------------------------------
