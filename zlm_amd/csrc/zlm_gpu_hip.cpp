@@ -1584,6 +1584,16 @@ const float* stage_burst(zlm_device* d, const float* x, size_t x_len, bool first
     return d->d_bx;
 }
 
+// A burst op that fails after stage_burst: its slot stays free, so the copy
+// from that slot's pinned buffer must finish before the slot can be staged
+// into again, and the burst is closed (later members are refused).  Returns
+// the null handle.
+int32_t burst_failed(zlm_device* d, bool first) {
+    if (first) hipStreamSynchronize(d->stream);
+    d->burst_open = false;
+    return ZLM_NULL_HANDLE;
+}
+
 // Make slot `s` ready to receive `rows` floats (its result kernel writes the
 // pinned host buffer through sl.h_y_dev).
 bool prepare_slot(zlm_device* d, int s, size_t rows) {
@@ -1637,7 +1647,7 @@ extern "C" int32_t zlm_gpu_mat_vec_resident_burst_async(zlm_device* d, zlm_resid
     if (s < 0) return fail(d, "ring full: %d dispatches in flight", kRing), ZLM_NULL_HANDLE;
     const float* xd = stage_burst(d, x, x_len, first, s);
     if (!xd) return ZLM_NULL_HANDLE;
-    if (!submit_into_slot(d, s, r, quant, rows, k, xd)) return ZLM_NULL_HANDLE;
+    if (!submit_into_slot(d, s, r, quant, rows, k, xd)) return burst_failed(d, first);
     return make_handle(d, s);
 }
 
@@ -1782,7 +1792,7 @@ extern "C" int32_t zlm_gpu_mat_vec_gate_up_resident_burst_async(zlm_device* d, z
     op.x = xd;
     op.act = act;
     op.y = d->slots[s].h_y_dev;
-    if (!enqueue_op(d, op) || !finish_slot(d, s, rows)) return ZLM_NULL_HANDLE;
+    if (!enqueue_op(d, op) || !finish_slot(d, s, rows)) return burst_failed(d, first);
     return make_handle(d, s);
 }
 
@@ -1808,7 +1818,7 @@ extern "C" int32_t zlm_gpu_mat_vec_mlp_pair_resident_burst_async(zlm_device* d, 
     if (!xd) return ZLM_NULL_HANDLE;
     if (!enqueue_mlp(d, s, rg, ru, rd, with_variant(gu_quant, variant), down_quant, rows, k, ffn, xd, act) ||
         !finish_slot(d, s, rows))
-        return ZLM_NULL_HANDLE;
+        return burst_failed(d, first);
     return make_handle(d, s);
 }
 
