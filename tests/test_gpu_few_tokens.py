@@ -173,3 +173,43 @@ def test_int_token_route(dev, k, m, launches):
         dev.dev_free(x)
         dev.dev_free(out)
         dev.free_resident(res)
+
+
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_token_routes_replay_from_a_graph(dev, m):
+    """The token routes allocate nothing, so they capture into a HIP graph;
+    replays (with eager work between them) equal the eager result bit for
+    bit."""
+    rows, k = 300, 4096
+    w = synth.weights(synth.Q4_K, rows, k, seed=m)
+    res = dev.upload_resident(w)
+    x = dev.dev_malloc(m * k * 4)
+    out = dev.dev_malloc(m * rows * 4)
+    other = dev.dev_malloc(m * rows * 4)
+    graph = None
+    try:
+        dev.dev_upload(x, synth.activation(9 + m, m * k))
+        q = zd.quant(zd.Q4_K)
+        assert dev.mat_mul_enqueue(res, q, rows, k, m, x, out), dev.last_error()
+        eager = np.zeros(m * rows, np.float32)
+        dev.dev_download(eager, out)
+        assert dev.capture_begin(), dev.last_error()
+        try:
+            ok = dev.mat_mul_enqueue(res, q, rows, k, m, x, out)
+        finally:
+            graph = dev.capture_end()
+        assert ok and graph is not None, dev.last_error()
+        for rep in range(3):
+            dev.dev_upload(out, np.full(m * rows, np.nan, np.float32))
+            dev.graph_launch(graph, 1)
+            got = np.zeros(m * rows, np.float32)
+            dev.dev_download(got, out)
+            np.testing.assert_array_equal(got.view(np.uint32), eager.view(np.uint32), err_msg=f"replay {rep}")
+            assert dev.mat_mul_enqueue(res, q, rows, k, m, x, other), dev.last_error()  # eager work between
+            dev.sync()
+    finally:
+        if graph is not None:
+            dev.graph_destroy(graph)
+        for p in (x, out, other):
+            dev.dev_free(p)
+        dev.free_resident(res)

@@ -81,7 +81,7 @@ def test_gemm_and_long_attention_launches_within_dispatch_limits(dev):
     dev.dev_upload(x, synth.activation(4, 512 * k))
     try:
         assert dev.launch_log(True)
-        for m in (1, 2, 5, 32, 33, 512):
+        for m in (1, 2, 3, 5, 32, 33, 512):
             _say(f"launch limits: matMul m={m}")
             assert dev.mat_mul_enqueue(res, zd.quant(zd.Q4_0), rows, k, m, x, out), dev.last_error()
         dev.sync()

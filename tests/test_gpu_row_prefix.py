@@ -12,8 +12,9 @@ tokens), and leaves the output past r untouched:
 * matVecResidentBatch over prefixes of two residents;
 * the fused gate_up and the MLP ops (a prefix of the gate/up rows; a prefix
   of the down rows);
-* matMulResident for the four GEMM types at m = 1, 2 (fp GEMVs), 5 (the
-  small-M kernel) and 40 (the tiled GEMM).
+* matMulResident for the four GEMM types at m = 1, 2 (the fp GEMV and the
+  two-token GEMV), 3 (the int-path token GEMV), 5 (the small-M kernel) and
+  40 (the tiled GEMM).
 """
 import sys
 
@@ -123,7 +124,7 @@ GEMM_TYPES = [synth.Q4_0, synth.Q8_0, synth.Q4_1, synth.Q4_K]
 
 
 @pytest.mark.parametrize("qt", GEMM_TYPES, ids=lambda t: NAMES[t])
-@pytest.mark.parametrize("m", [1, 2, 5, 40])
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 40])
 def test_matmul_over_a_row_prefix(dev, qt, m):
     k = 1024
     w = synth.weights(qt, TOTAL, k, seed=41 + m)
