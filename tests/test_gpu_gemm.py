@@ -74,7 +74,8 @@ def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     dev.free_resident(res)
 
 
-# The small-M path (3 <= m <= 32: one 32-token tile; the workgroup's waves
+# The small-token paths (m = 3, 4 at k <= 8192: the int-path token GEMV;
+# otherwise up to 32: the small-M kernel, one 32-token tile; the workgroup's waves
 # split the row's blocks in pairs -- 16 waves and 32-block split steps for
 # q4_0 / q8_0, 8 waves and 16-block steps for q4_1 / q4_k): odd block counts
 # (a pair's second block past the end), block counts not a multiple of a split
