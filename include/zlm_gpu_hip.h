@@ -414,6 +414,13 @@ void zlm_gpu_graph_destroy(zlm_device *dev, zlm_graph *graph);
 /* Whether a rocprofiler library appears in a /proc/<pid>/maps-format file
  * (null: this process's own map): the check behind the replay refusal. */
 bool zlm_gpu_profiler_loaded(const char *maps_path);
+/* What the host reads from a GEMV entry point's name before launching it
+ * (no device needed): *role = the form it computes (ZLM_FORM_*), 16 the batch
+ * kernel, 17 the two-token GEMV, 18 the int-path token GEMV; *struct_args =
+ * it takes one GemvArgs block (else the plain GEMV's six arguments).  False
+ * for a name that is not zlm_gemv_<quant>_...  Lets a test check the parse
+ * against the code objects' kernel-argument metadata. */
+bool zlm_gpu_kernel_convention(const char *name, int32_t *role, bool *struct_args);
 /* Device bytes the library itself holds on `dev` (staging, attention and GEMM
  * scratch; not residents, not the fixed no-alloc array). */
 uint64_t zlm_gpu_scratch_device_bytes(const zlm_device *dev);

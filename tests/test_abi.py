@@ -149,3 +149,57 @@ def test_profiler_check_reads_the_process_map(tmp_path):
     assert not zd.profiler_loaded(str(tmp_path / "missing"))
     # this test process runs without a profiler
     assert not zd.profiler_loaded()
+
+
+def _kernel_args(path):
+    """{kernel name: [sizes of its explicit arguments]} from a code object's
+    metadata (the ROCm LLVM tools read the bundle and the ELF notes)."""
+    import subprocess
+    import tempfile
+    bundler = "/opt/rocm/llvm/bin/clang-offload-bundler"
+    readelf = "/opt/rocm/llvm/bin/llvm-readelf"
+    if not (os.path.exists(bundler) and os.path.exists(readelf)):
+        pytest.skip("ROCm LLVM tools not installed")
+    with tempfile.TemporaryDirectory() as tmp:
+        elf = os.path.join(tmp, "k.o")
+        subprocess.run([bundler, "--unbundle", "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                        f"--input={path}", f"--output={elf}"], check=True)
+        notes = subprocess.run([readelf, "--notes", elf], capture_output=True, text=True, check=True).stdout
+    out = {}
+    for entry in re.split(r"\n\s+- \.agpr_count:", notes[notes.find("amdhsa.kernels:"):])[1:]:
+        name = re.search(r"\n\s+\.name:\s+(\S+)", entry).group(1)
+        args = entry[entry.find(".args:"):entry.find(".group_segment_fixed_size")]
+        sizes = [int(x) for x in re.findall(r"\.size:\s+(\d+)", args)]
+        kinds = re.findall(r"\.value_kind:\s+(\S+)", args)
+        out[name] = [s for s, k in zip(sizes, kinds) if not k.startswith("hidden")]
+    return out
+
+
+def test_kernel_conventions_match_the_code_objects():
+    """The host launches a GEMV entry point with the argument convention and
+    checks the role it reads from the kernel's name (a kernel picked for one
+    form must never run as another).  For every entry point in the GEMV code
+    objects, that parse must agree with the compiled kernel: one 88-byte
+    GemvArgs block (the batch kernel: its own block), or the plain GEMV's six
+    arguments; and the name families map to their roles."""
+    gemv_args_bytes = 88  # sizeof(GemvArgsHost) in zlm_gpu_hip.cpp
+    families = {"multi_": 16, "tok2_": 17, "q8tok": 18, "pair_": 1, "norm_": 2, "normpair_": 3, "resid_": 4}
+    seen = 0
+    for q in ("q4_0", "q8_0", "q4_k", "q6_k", "q4_1", "f32", "f16", "bf16"):
+        path = os.path.join(zd.LIB_DIR, f"zlm_gemv_{q}_gfx950.hsaco")
+        for name, sizes in _kernel_args(path).items():
+            conv = zd.kernel_convention(name)
+            assert conv is not None, name
+            role, struct_args = conv
+            rest = name[len(f"zlm_gemv_{q}_"):]
+            want_role = next((r for p, r in families.items() if rest.startswith(p)), 0)
+            assert role == want_role, (name, role)
+            if struct_args:
+                assert len(sizes) == 1, (name, sizes)
+                if role != 16:
+                    assert sizes == [gemv_args_bytes], (name, sizes)
+            else:
+                assert sizes == [8, 8, 8, 8, 4, 4], (name, sizes)
+            seen += 1
+    assert seen > 300
+    assert zd.kernel_convention("zlm_attn_decode") is None

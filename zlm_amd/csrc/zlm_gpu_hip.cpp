@@ -2565,6 +2565,21 @@ constexpr int kGraphsInFlight = 4;
 
 extern "C" bool zlm_gpu_profiler_loaded(const char* maps_path) { return profiler_in_maps(maps_path); }
 
+extern "C" bool zlm_gpu_kernel_convention(const char* name, int32_t* role, bool* struct_args) {
+    if (!name || !role || !struct_args) return false;
+    for (int q = 0; q < kNumQuants; q++) {
+        const std::string prefix = std::string("zlm_gemv_") + kQuantNames[q] + "_";
+        if (strncmp(name, prefix.c_str(), prefix.size()) != 0) continue;
+        int r = 0;
+        bool st = false;
+        kernel_role(name, q, &r, &st);
+        *role = r;
+        *struct_args = st;
+        return true;
+    }
+    return false;
+}
+
 extern "C" bool zlm_gpu_launch_log(zlm_device* d, bool enable) {
     if (!d || !d->avail) return false;
     d->log_launches = enable;

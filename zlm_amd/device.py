@@ -198,6 +198,7 @@ def lib() -> ctypes.CDLL:
         "zlm_gpu_graph_launch": (B, [P, P, ctypes.c_int, P]),
         "zlm_gpu_graph_destroy": (None, [P, P]),
         "zlm_gpu_profiler_loaded": (B, [ctypes.c_char_p]),
+        "zlm_gpu_kernel_convention": (B, [ctypes.c_char_p, P, P]),
         "zlm_gpu_launch_log": (B, [P, B]),
         "zlm_gpu_launch_log_read": (S, [P, P, S]),
         "zlm_gpu_scratch_device_bytes": (ctypes.c_uint64, [P]),
@@ -632,3 +633,14 @@ class Device:
 def profiler_loaded(maps_path: Optional[str] = None) -> bool:
     """Whether a rocprofiler library is mapped (this process, or a maps-format file)."""
     return bool(lib().zlm_gpu_profiler_loaded(None if maps_path is None else maps_path.encode()))
+
+
+def kernel_convention(name: str) -> Optional[tuple]:
+    """(role, takes one GemvArgs block) as the host reads them from a GEMV
+    entry point's name, or None for a name outside zlm_gemv_<quant>_...; no
+    device needed."""
+    role = ctypes.c_int32(0)
+    st = ctypes.c_bool(False)
+    if not lib().zlm_gpu_kernel_convention(name.encode(), ctypes.addressof(role), ctypes.addressof(st)):
+        return None
+    return int(role.value), bool(st.value)
