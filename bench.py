@@ -494,6 +494,22 @@ def sections(dev, args, want, extra):
                                     "bytes_per_token": lbytes, "GBps": round(lbytes / (lms * 1e-3) / 1e9, 1)}
                 log(f"c2 decode at context {ctx}: {lms:.3f} ms/token = {1e3 / lms:.1f} tok/s, "
                     f"{longer[str(ctx)]['GBps']} GB/s")
+                if ctx == 32768:
+                    # a step early in that cache (position 511): the full-cache
+                    # graph reads every position's K/V, the graph captured for
+                    # the position's window bucket (512) only the first 512
+                    short = {}
+                    for name, window in (("full_cache_graph", None), ("window_graph", lmodel.window_for(511))):
+                        g_ = lmodel.capture(window)
+                        lmodel.set_input(x, 511)
+                        dev.graph_launch(g_, reps)
+                        short[name] = round(sorted(dev.graph_launch(g_, reps) / reps for _ in range(3))[1], 4)
+                        dev.graph_destroy(g_)
+                    short["note"] = ("ms/token at position 511 of a 32768-position cache: the full-cache graph "
+                                     "against the graph for the position's attention window (512)")
+                    longer[str(ctx)]["position_511"] = short
+                    log(f"c2 decode at position 511 of a 32768 cache: {short['full_cache_graph']:.3f} ms/token "
+                        f"(full-cache graph), {short['window_graph']:.3f} ms/token (window-512 graph)")
                 dev.graph_destroy(lgraph)
                 lmodel.free()
             extra["c2_decode_qwen3_8b_q4_0"]["longer_contexts"] = longer

@@ -365,6 +365,18 @@ bool zlm_gpu_attention_decode_enqueue(zlm_device *dev, const float *qkv, const f
                                       uint32_t head_dim, float eps, float freq_base, const int32_t *pos,
                                       uint16_t *k_cache, uint16_t *v_cache, uint32_t max_seq, float scale,
                                       float *out);
+/* zlm_gpu_attention_decode_enqueue over a window: positions [0, window) of
+ * the caches only (ceil(window / 64) splits; 1 <= window <= max_seq, the
+ * caches' stride stays max_seq).  No reference counterpart: the decode step
+ * at a position well below max_seq reads only the KV it needs (a serving loop
+ * captures one graph per window bucket and replays the smallest bucket above
+ * the position).  A position past the launched splits (64 * ceil(window /
+ * 64) positions) gives NaN heads, not a silently shortened attention. */
+bool zlm_gpu_attention_decode_window_enqueue(zlm_device *dev, const float *qkv, const float *q_norm_w,
+                                             const float *k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                             uint32_t head_dim, float eps, float freq_base, const int32_t *pos,
+                                             uint16_t *k_cache, uint16_t *v_cache, uint32_t max_seq,
+                                             uint32_t window, float scale, float *out);
 
 /* zlm_gpu_attention_decode_enqueue without any allocation: no counterpart in
  * the reference.  For callers that cannot allocate device memory at call time

@@ -245,3 +245,91 @@ def test_qwen3_8b_step_matches_oracle_and_graph_replays_match_eager(dev):
         if graph is not None:
             dev.graph_destroy(graph)
         model.free()
+
+
+# (nh, nkv, pos, max_seq, window): the attention over a window of the caches,
+# one split (64), the 128 bucket, a window of 1024 in a 32768 cache, and a
+# window past 64 splits (the wide merge) in a 40000 cache
+WINDOW_CASES = [(32, 8, 5, 2048, 64), (32, 8, 100, 2048, 128), (32, 8, 700, 32768, 1024),
+                (8, 2, 4100, 40000, 8192)]
+
+
+@pytest.mark.parametrize("nh,nkv,pos,max_seq,window", WINDOW_CASES)
+def test_windowed_attention_decode(dev, nh, nkv, pos, max_seq, window):
+    """The fused attention over positions [0, window) only: against the oracle,
+    and equal to the full-cache call bit for bit where both merges take the
+    same kernel (at most 64 splits); a position at or past the window gives
+    NaN heads instead of a shortened attention."""
+    hd, eps, base = 128, 1e-6, 1e6
+    _say(f"windowed attention nh={nh} nkv={nkv} pos={pos} max_seq={max_seq} window={window}")
+    rng = np.random.default_rng(pos + window)
+    qkv = (rng.standard_normal((nh + 2 * nkv) * hd) * 2).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kc0 = rng.standard_normal((nkv, max_seq, hd)).astype(np.float16)
+    vc0 = rng.standard_normal((nkv, max_seq, hd)).astype(np.float16)
+    scale = 1.0 / math.sqrt(hd)
+    q, k, v = od.qk_norm_rope(qkv, qn, kn, nh, nkv, hd, eps, base, pos)
+    kref, vref = kc0.copy(), vc0.copy()
+    od.write_kv(k, v, kref, vref, pos)
+    want = od.attend(q, kref, vref, nh, pos, scale)
+    bufs = [_vec(dev, a) for a in (qkv, qn, kn, kc0, vc0, np.array([pos, 0, 0, 0], np.int32))]
+    d_qkv, d_qn, d_kn, d_kc, d_vc, d_pos = bufs
+    d_out = dev.dev_malloc(nh * hd * 4)
+    try:
+        assert dev.attention_decode_window_enqueue(d_qkv, d_qn, d_kn, nh, nkv, hd, eps, base, d_pos, d_kc, d_vc,
+                                                   max_seq, window, scale, d_out), dev.last_error()
+        got = np.zeros(nh * hd, np.float32)
+        dev.dev_download(got, d_out)
+        assert rel_l2(got, want) <= 1e-4
+        assert dev.attention_decode_enqueue(d_qkv, d_qn, d_kn, nh, nkv, hd, eps, base, d_pos, d_kc, d_vc, max_seq,
+                                            scale, d_out), dev.last_error()
+        full = np.zeros(nh * hd, np.float32)
+        dev.dev_download(full, d_out)
+        if (max_seq + 63) // 64 <= 64:
+            np.testing.assert_array_equal(got.view(np.uint32), full.view(np.uint32))
+        else:
+            assert rel_l2(got, full) <= 1e-6
+        # the window must hold the position
+        dev.dev_upload(d_pos, np.array([window, 0, 0, 0], np.int32))
+        assert dev.attention_decode_window_enqueue(d_qkv, d_qn, d_kn, nh, nkv, hd, eps, base, d_pos, d_kc, d_vc,
+                                                   max_seq, window, scale, d_out), dev.last_error()
+        past = np.zeros(nh * hd, np.float32)
+        dev.dev_download(past, d_out)
+        assert np.all(np.isnan(past))
+        # windows outside 1..max_seq are refused
+        assert not dev.attention_decode_window_enqueue(d_qkv, d_qn, d_kn, nh, nkv, hd, eps, base, d_pos, d_kc,
+                                                       d_vc, max_seq, max_seq + 1, scale, d_out)
+        assert not dev.attention_decode_window_enqueue(d_qkv, d_qn, d_kn, nh, nkv, hd, eps, base, d_pos, d_kc,
+                                                       d_vc, max_seq, 0, scale, d_out)
+    finally:
+        for p in bufs + [d_out]:
+            dev.dev_free(p)
+
+
+def test_windowed_decode_step_graph_matches_the_full_step(dev):
+    """A two-layer model at Qwen3-8B dimensions with a 2048-position cache: the
+    step at position 100 through the graph captured for its window bucket
+    (128) equals the full-cache step bit for bit, replay after replay."""
+    import dataclasses
+    cfg = dataclasses.replace(zdec.QWEN3_8B, n_layers=2)
+    model = zdec.DecodeModel(dev, cfg)
+    graph = None
+    try:
+        x = synth.activation(0x5A4C4D03, cfg.hidden)
+        pos = 100
+        assert model.window_for(pos) == 128 and model.window_for(127) == 128 and model.window_for(128) == 256
+        assert model.window_for(cfg.max_seq - 1) == cfg.max_seq and model.window_for(0) == 128
+        full = model.step(x, pos)
+        assert np.all(np.isfinite(full))
+        windowed = model.step(x, pos, model.window_for(pos))
+        np.testing.assert_array_equal(windowed.view(np.uint32), full.view(np.uint32))
+        graph = model.capture(model.window_for(pos))
+        for _ in range(3):
+            model.set_input(x, pos)
+            dev.graph_launch(graph, 1)
+            np.testing.assert_array_equal(model.logits_host().view(np.uint32), full.view(np.uint32))
+    finally:
+        if graph is not None:
+            dev.graph_destroy(graph)
+        model.free()

@@ -2447,19 +2447,29 @@ bool enqueue_attn_decode(zlm_device* d, const float* qkv, const float* q_norm_w,
 
 }  // namespace
 
+extern "C" bool zlm_gpu_attention_decode_window_enqueue(zlm_device* d, const float* qkv, const float* q_norm_w,
+                                                        const float* k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
+                                                        uint32_t head_dim, float eps, float freq_base,
+                                                        const int32_t* pos, uint16_t* k_cache, uint16_t* v_cache,
+                                                        uint32_t max_seq, uint32_t window, float scale, float* out) {
+    if (!d || !d->avail) return false;
+    if (!check_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, head_dim, pos, k_cache, v_cache, max_seq,
+                           out))
+        return false;
+    if (window == 0 || window > max_seq) return fail(d, "attention window %u outside 1..max_seq %u", window, max_seq);
+    const uint32_t nsplit = static_cast<uint32_t>((static_cast<uint64_t>(window) + 63) / 64);
+    if (!ensure_attn_scratch(d, static_cast<size_t>(n_heads) * nsplit * 130)) return false;
+    return enqueue_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, eps, freq_base, pos, k_cache, v_cache,
+                               max_seq, scale, out, d->attn_part, nsplit);
+}
+
 extern "C" bool zlm_gpu_attention_decode_enqueue(zlm_device* d, const float* qkv, const float* q_norm_w,
                                                  const float* k_norm_w, uint32_t n_heads, uint32_t n_kv_heads,
                                                  uint32_t head_dim, float eps, float freq_base, const int32_t* pos,
                                                  uint16_t* k_cache, uint16_t* v_cache, uint32_t max_seq, float scale,
                                                  float* out) {
-    if (!d || !d->avail) return false;
-    if (!check_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, head_dim, pos, k_cache, v_cache, max_seq,
-                           out))
-        return false;
-    const uint32_t nsplit = static_cast<uint32_t>((static_cast<uint64_t>(max_seq) + 63) / 64);
-    if (!ensure_attn_scratch(d, static_cast<size_t>(n_heads) * nsplit * 130)) return false;
-    return enqueue_attn_decode(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, eps, freq_base, pos, k_cache, v_cache,
-                               max_seq, scale, out, d->attn_part, nsplit);
+    return zlm_gpu_attention_decode_window_enqueue(d, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads, head_dim, eps,
+                                                   freq_base, pos, k_cache, v_cache, max_seq, max_seq, scale, out);
 }
 
 extern "C" bool zlm_gpu_attention_decode_enqueue_noalloc(zlm_device* d, const float* qkv, const float* q_norm_w,

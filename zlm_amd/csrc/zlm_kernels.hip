@@ -1057,8 +1057,10 @@ __device__ __forceinline__ void attn_scores(const uint4 (&kraw)[4], uint32_t p, 
 }
 
 // Wave g's softmax over its head's 64 scores and the weighted V sum from LDS;
-// writes the split's partial (acc[128], m, l).
-__device__ __forceinline__ void attn_values(const AttnLds& sm, uint32_t g, uint32_t lane, float* __restrict__ out) {
+// writes the split's partial (acc[128], m, l).  `poison` makes l NaN, so the
+// merged head is NaN (a position past the launched splits: see zlm_attn_decode).
+__device__ __forceinline__ void attn_values(const AttnLds& sm, uint32_t g, uint32_t lane, float* __restrict__ out,
+                                            bool poison = false) {
     const float sv = sm.sc[g][lane];
     const float m = wave_max(sv);
     const float e = (sv == -INFINITY) ? 0.0f : expf(sv - m);
@@ -1080,7 +1082,7 @@ __device__ __forceinline__ void attn_values(const AttnLds& sm, uint32_t g, uint3
     *reinterpret_cast<float2*>(out + 2 * lane) = make_float2(a0, a1);
     if (lane == 0) {
         out[kAttnHd] = m;
-        out[kAttnHd + 1] = l;
+        out[kAttnHd + 1] = poison ? __builtin_nanf("") : l;
     }
 }
 
@@ -1253,7 +1255,12 @@ extern "C" __global__ void __launch_bounds__(1024)
 //     the V row goes straight into the LDS V tile, the K row replaces the
 //     loaded slice in the scores);
 //   * scores, softmax and values as zlm_attn_partial, into the same partials,
-//     which zlm_attn_combine merges.  (Merging in the last workgroup of each kv
+//     which zlm_attn_combine merges.
+// nsplit may cover fewer positions than the cache holds (a window: the host
+// launches ceil(window / 64) splits for steps whose position is below it).  A
+// position past the launched splits would leave positions out, so the first
+// split then writes a NaN denominator and the heads come out NaN instead of
+// silently wrong.  (Merging in the last workgroup of each kv
 //     head instead, behind a device-scope fence and counter, measured 3x
 //     slower on gfx950: every workgroup's release fence writes back its L2.)
 extern "C" __global__ void __launch_bounds__(256)
@@ -1333,7 +1340,10 @@ extern "C" __global__ void __launch_bounds__(256)
     __syncthreads();
     attn_scores<true>(kraw, p, qd, valid, prow, kn, sm);
     __syncthreads();
-    if (wid < G) attn_values(sm, wid, lane, part + (static_cast<size_t>(h * G + wid) * nsplit + s) * kAttnPart);
+    const bool past_window = L > nsplit * kAttnSplit;
+    if (wid < G)
+        attn_values(sm, wid, lane, part + (static_cast<size_t>(h * G + wid) * nsplit + s) * kAttnPart,
+                    past_window && s == 0);
 }
 
 // ---- synthetic data on the device (benchmark and large-shape tests) ---------

@@ -206,9 +206,20 @@ class DecodeModel:
                 "out_norm": f32(self.out_norm, c.hidden)}
 
     # -- one step --------------------------------------------------------------
-    def enqueue_step(self) -> None:
-        """Enqueue one token's step on the device stream (no waits)."""
+    def window_for(self, pos: int) -> int:
+        """The attention window a step at `pos` needs: the smallest power of
+        two >= pos + 1 (at least 128), capped at max_seq."""
+        w = 128
+        while w < pos + 1:
+            w *= 2
+        return min(w, self.cfg.max_seq)
+
+    def enqueue_step(self, window: Optional[int] = None) -> None:
+        """Enqueue one token's step on the device stream (no waits).  The
+        attention reads positions [0, window) of the caches (default: all of
+        them); the step's position must be below the window."""
         d, c = self.dev, self.cfg
+        window = c.max_seq if window is None else window
         q, lm = zd.quant(c.proj_type), zd.quant(c.lm_type)
 
         def ok(flag: bool, what: str) -> None:
@@ -219,9 +230,9 @@ class DecodeModel:
         for L in self.layers:
             ok(d.gemv_op_enqueue(zd.FORM_NORM, q, L.qkv, c.qkv_rows, c.hidden, self.h, self.qkv,
                                  norm_w=L.attn_norm, eps=c.eps), "qkv")
-            ok(d.attention_decode_enqueue(self.qkv, L.q_norm, L.k_norm, c.n_heads, c.n_kv_heads, c.head_dim, c.eps,
-                                          c.freq_base, self.pos, L.k_cache, L.v_cache, c.max_seq, self.scale,
-                                          self.attn), "attention")
+            ok(d.attention_decode_window_enqueue(self.qkv, L.q_norm, L.k_norm, c.n_heads, c.n_kv_heads,
+                                                 c.head_dim, c.eps, c.freq_base, self.pos, L.k_cache, L.v_cache,
+                                                 c.max_seq, window, self.scale, self.attn), "attention")
             ok(d.gemv_op_enqueue(zd.FORM_RESID, q, L.o, c.hidden, c.n_heads * c.head_dim, self.attn, self.h,
                                  res=self.h), "o")
             ok(d.gemv_op_enqueue(zd.FORM_NORMPAIR, q, L.gate, c.ffn, c.hidden, self.h, self.mid, w_up=L.up,
@@ -234,10 +245,11 @@ class DecodeModel:
         self.dev.dev_upload(self.x_in, np.ascontiguousarray(x_in, np.float32))
         self.dev.dev_upload(self.pos, np.array([pos, 0, 0, 0], np.int32))
 
-    def step(self, x_in: np.ndarray, pos: int) -> np.ndarray:
-        """One eager step for token row `x_in` at `pos`; returns the logits."""
+    def step(self, x_in: np.ndarray, pos: int, window: Optional[int] = None) -> np.ndarray:
+        """One eager step for token row `x_in` at `pos` (attention window:
+        default all of the caches); returns the logits."""
         self.set_input(x_in, pos)
-        self.enqueue_step()
+        self.enqueue_step(window)
         out = np.zeros(self.cfg.vocab, np.float32)
         self.dev.dev_download(out, self.logits)
         return out
@@ -247,13 +259,15 @@ class DecodeModel:
         self.dev.dev_download(out, self.logits)
         return out
 
-    def capture(self) -> int:
+    def capture(self, window: Optional[int] = None) -> int:
         """Record one step into a HIP graph (run a step eagerly first so every
-        layout and scratch buffer exists)."""
+        layout and scratch buffer exists).  A serving loop captures one graph
+        per window bucket (window_for) and replays the one for each position,
+        so a step reads only the KV it needs."""
         if not self.dev.capture_begin():
             raise RuntimeError(self.dev.last_error())
         try:
-            self.enqueue_step()
+            self.enqueue_step(window)
         finally:
             g = self.dev.capture_end()
         if g is None:

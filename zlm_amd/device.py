@@ -186,6 +186,8 @@ def lib() -> ctypes.CDLL:
                                                  ctypes.c_float, P]),
         "zlm_gpu_attention_decode_enqueue_noalloc": (B, [P, P, P, P, U, U, U, ctypes.c_float, ctypes.c_float, P, P,
                                                          P, U, ctypes.c_float, P]),
+        "zlm_gpu_attention_decode_window_enqueue": (B, [P, P, P, P, U, U, U, ctypes.c_float, ctypes.c_float, P, P,
+                                                        P, U, U, ctypes.c_float, P]),
         "zlm_gpu_resident_device_bytes": (ctypes.c_uint64, [P]),
         "zlm_gpu_layout_bytes": (ctypes.c_uint64, [U, S, S, ctypes.c_bool]),
         "zlm_gpu_release_gemm_tiles": (B, [P, P]),
@@ -510,6 +512,16 @@ class Device:
         return bool(self._L.zlm_gpu_attention_decode_enqueue(self._h, qkv, q_norm_w, k_norm_w, n_heads, n_kv_heads,
                                                              head_dim, eps, freq_base, pos, k_cache, v_cache,
                                                              max_seq, scale, out))
+
+    def attention_decode_window_enqueue(self, qkv: int, q_norm_w: int, k_norm_w: int, n_heads: int,
+                                        n_kv_heads: int, head_dim: int, eps: float, freq_base: float, pos: int,
+                                        k_cache: int, v_cache: int, max_seq: int, window: int, scale: float,
+                                        out: int) -> bool:
+        """attention_decode_enqueue over positions [0, window) only (a position
+        at or past the window gives NaN heads)."""
+        return bool(self._L.zlm_gpu_attention_decode_window_enqueue(self._h, qkv, q_norm_w, k_norm_w, n_heads,
+                                                                    n_kv_heads, head_dim, eps, freq_base, pos,
+                                                                    k_cache, v_cache, max_seq, window, scale, out))
 
     def attention_decode_enqueue_noalloc(self, qkv: int, q_norm_w: int, k_norm_w: int, n_heads: int,
                                          n_kv_heads: int, head_dim: int, eps: float, freq_base: float, pos: int,
