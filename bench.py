@@ -394,16 +394,17 @@ def sections(dev, args, want, extra):
     # ---- small token counts (verify / microbatch), as reference gpu/root_test.zig:651-696 ----
     if (only is None and not args.quick and not args.no_small_m) or only == "smallm":
         sweep = {}
-        for sname, qt, rows, k in (("q4_0_4096x4096", synth.Q4_0, 4096, 4096),
-                                   ("q4_k_4096x4096", synth.Q4_K, 4096, 4096),
-                                   ("q4_k_lm_head_262144x3840", synth.Q4_K, 262144, 3840)):
+        few = (1, 2, 3, 4, 5, 8, 9)
+        for sname, qt, rows, k, ms in (("q4_0_4096x4096", synth.Q4_0, 4096, 4096, few + (33, 64, 128, 256)),
+                                       ("q4_k_4096x4096", synth.Q4_K, 4096, 4096, few + (33, 64, 128, 256)),
+                                       ("q4_k_lm_head_262144x3840", synth.Q4_K, 262144, 3840, few)):
             w = synth.weights(qt, rows, k, 0x5A4C4D05)
             ncopy = max(1, math.ceil(MALL_DEFEAT_BYTES / w.size))
             ress = [dev.upload_resident(w) for _ in range(ncopy)]
-            xs = synth.activation(0x5A4C4D0E, 9 * k)
+            xs = synth.activation(0x5A4C4D0E, max(ms) * k)
             x_dev = dev.dev_malloc(xs.nbytes)
             dev.dev_upload(x_dev, xs)
-            o_dev = dev.dev_malloc(9 * rows * 4)
+            o_dev = dev.dev_malloc(max(ms) * rows * 4)
             it = max(2, int(4 * ncopy * WARM["launch_scale"]))
             spent = 0.0
             while spent < WARM["ms"]:
@@ -411,14 +412,14 @@ def sections(dev, args, want, extra):
             gemv_us = sorted(dev.time_mat_vec(ress, zd.quant(qt), rows, k, x_dev, o_dev, it) / it
                              for _ in range(3))[1] * 1e3
             row = {"gemv_us": round(gemv_us, 2)}
-            for m in (1, 2, 3, 4, 5, 8, 9):
+            for m in ms:
                 dev.time_mat_mul(ress, zd.quant(qt), rows, k, m, x_dev, o_dev, ncopy)
                 us = sorted(dev.time_mat_mul(ress, zd.quant(qt), rows, k, m, x_dev, o_dev, it) / it
                             for _ in range(3))[1] * 1e3
                 row[f"m{m}_us"] = round(us, 2)
             sweep[sname] = row
             log(f"small-m {sname}: GEMV {gemv_us:.1f} us; " +
-                ", ".join(f"M{m} {row[f'm{m}_us']:.1f}" for m in (1, 2, 3, 4, 5, 8, 9)))
+                ", ".join(f"M{m} {row[f'm{m}_us']:.1f}" for m in ms))
             for r in ress:
                 dev.free_resident(r)
             dev.dev_free(x_dev)
@@ -426,7 +427,8 @@ def sections(dev, args, want, extra):
         sweep["note"] = ("device-level matMul at m tokens vs one GEMV (weights rotated over >= 512 MiB): m = 1 the fp "
                          "GEMV, m = 2 the two-token fp GEMV (one pass over the weights), 3..4 the int-path token GEMV "
                          "(activations quantized in its prologue), 5..32 the split-K int8-MFMA GEMM (activation "
-                         "quantizer included)")
+                         "quantizer included), past 32 that kernel over several 32-token tiles or the tiled int8-MFMA "
+                         "GEMM, whichever the host's cost model predicts faster")
         extra["small_m_matmul"] = sweep
 
     # ---- decode step of a Qwen3-8B-shaped Q4_0 model, batch 1 ----------

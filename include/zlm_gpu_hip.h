@@ -256,8 +256,12 @@ bool zlm_gpu_mat_vec_batch_enqueue(zlm_device *dev, zlm_resident *const *res, ui
  * m = 1 the fp GEMV; m = 2 the two-token fp GEMV (k <= 16384, else a GEMV per
  * token); m = 3, 4 at k <= 8192 the int-path token GEMV (q8 activations
  * quantized in its prologue, the weights read once from the device layout);
- * otherwise the q8 activation quantizer, then the int8-MFMA GEMM over the
- * tiled copy (built on first use). */
+ * otherwise the q8 activation quantizer, then an int8-MFMA GEMM over the
+ * tiled copy (built on first use): up to 32 tokens the split-K small-M
+ * kernel, past that the small-M kernel over several 32-token tiles or the
+ * 128 x 64 tiled GEMM, whichever the library's cost model predicts faster
+ * for (rows, k, m).  A token's results do not depend on the other tokens of
+ * the call within one kernel. */
 bool zlm_gpu_mat_mul_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k, size_t m,
                              const float *x_dev, float *out_dev);
 /* Enqueue `iters` prefill GEMMs (quantizer + GEMM each), rotating over `n_res`

@@ -80,7 +80,7 @@ def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
 # q4_0 / q8_0, 8 waves and 16-block steps for q4_1 / q4_k): odd block counts
 # (a pair's second block past the end), block counts not a multiple of a split
 # step (k = 3840 and 288), ragged row tiles, one token, a full tile, and the
-# first m past it (the tiled kernel).  A k that is not whole super-blocks for
+# first m past it (a second, one-token tile).  A k that is not whole super-blocks for
 # q4_k is rounded up to the next one.
 SMALL_M = [(33, 4096, 2), (64, 4096, 9), (96, 3840, 32), (40, 12288, 31), (37, 288, 5), (64, 256, 33),
            (32, 512, 1), (4096 + 17, 4096, 8), (50, 4096, 3)]
@@ -110,6 +110,69 @@ def test_small_m_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
     mag = np.abs(x.reshape(m, k).astype(np.float64)) @ dq.T
     assert np.all(np.abs(out.reshape(m, rows) - fp) <= 0.02 * mag + 1e-6)
     dev.free_resident(res)
+
+
+def _route(dev, res, zq, rows, k, m, x_dev, out_dev):
+    """The launches of one matMul on device buffers (after a first call that
+    builds the layouts)."""
+    assert dev.mat_mul_enqueue(res, zd.quant(zq), rows, k, m, x_dev, out_dev), dev.last_error()
+    dev.sync()
+    assert dev.launch_log(True)
+    try:
+        assert dev.mat_mul_enqueue(res, zd.quant(zq), rows, k, m, x_dev, out_dev), dev.last_error()
+        dev.sync()
+        return dev.launch_log_read()
+    finally:
+        dev.launch_log(False)
+
+
+# Past one 32-token tile the host picks the small-M kernel (one workgroup per
+# 32-row x 32-token tile, grid.y = token tiles) or the tiled GEMM by a cost
+# model; these shapes sit well inside each side for all four quants: the
+# small-M kernel over four token tiles (the last one partial) and the tiled
+# GEMM over three 128-token tiles (the last partial) and a ragged row tile,
+# both over a row prefix of a resident holding 64 rows more.
+MULTI_TILE = [("small", 4096 + 17, 4096, 100), ("tiled", 12288 + 40, 4096, 300)]
+
+
+@pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0", "q4_1", "q4_k"])
+@pytest.mark.parametrize("route,rows,k,m", MULTI_TILE, ids=["small", "tiled"])
+def test_gemm_past_one_token_tile(dev, qt, zq, route, rows, k, m):
+    _say(f"gemm past one token tile type={qt} route={route} rows={rows} k={k} m={m}")
+    rb = synth.row_bytes(qt, k)
+    w = synth.weights(qt, rows + 64, k, seed=rows + m)
+    xs = synth.activation(m + 13, m * k)
+    res = dev.upload_resident(w)
+    x_dev = dev.dev_malloc(xs.nbytes)
+    out_dev = dev.dev_malloc(m * rows * 4)
+    try:
+        dev.dev_upload(x_dev, xs)
+        log = _route(dev, res, zq, rows, k, m, x_dev, out_dev)
+        gemm = [r for r in log if r["what"].startswith("gemm")]
+        assert len(gemm) == 1
+        if route == "small":
+            assert gemm[0]["what"] == "gemm small"
+            assert (gemm[0]["grid_x"], gemm[0]["grid_y"]) == ((rows + 31) // 32, (m + 31) // 32)
+        else:
+            assert gemm[0]["what"] == "gemm"
+            assert (gemm[0]["grid_x"], gemm[0]["grid_y"]) == ((rows + 63) // 64, (m + 127) // 128)
+        out = np.zeros(m * rows, np.float32)
+        dev.dev_download(out, out_dev)
+        got = out.reshape(m, rows)
+        for r0, r1 in ((0, 64), (rows // 2, rows // 2 + 32), (rows - 48, rows)):
+            want = oracle.matmul_int(qt, w[r0 * rb:r1 * rb], k, r1 - r0, m, xs)
+            assert rel_l2(got[:, r0:r1], want) <= 1e-5, (r0, r1)
+        if route == "small":
+            # each 32-token tile is its own workgroup column: the first tile's
+            # tokens come out bit for bit as in a one-tile call
+            assert dev.mat_mul_enqueue(res, zd.quant(zq), rows, k, 32, x_dev, out_dev), dev.last_error()
+            one = np.zeros(32 * rows, np.float32)
+            dev.dev_download(one, out_dev)
+            np.testing.assert_array_equal(one.view(np.uint32), out[:32 * rows].view(np.uint32))
+    finally:
+        dev.dev_free(x_dev)
+        dev.dev_free(out_dev)
+        dev.free_resident(res)
 
 
 def test_gemm_config4_rows_subset(dev):

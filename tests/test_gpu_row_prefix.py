@@ -13,8 +13,9 @@ tokens), and leaves the output past r untouched:
 * the fused gate_up and the MLP ops (a prefix of the gate/up rows; a prefix
   of the down rows);
 * matMulResident for the four GEMM types at m = 1, 2 (the fp GEMV and the
-  two-token GEMV), 3 (the int-path token GEMV), 5 (the small-M kernel) and
-  40 (the tiled GEMM).
+  two-token GEMV), 3 (the int-path token GEMV), 5 and 40 (the small-M kernel
+  over one and two token tiles; test_gpu_gemm.py runs the tiled GEMM over a
+  row prefix).
 """
 import sys
 

@@ -1203,17 +1203,42 @@ double now_ns() {
 // production GEMV's arithmetic, as zlm's CPU runs small batches through its fp
 // batched GEMV, reference form/single.zig:258-292; cheaper than the int path's
 // quantizer + GEMM there): one token the GEMV, two the two-token GEMV (one
-// pass over the weights, k <= 16384; beyond it one GEMV per token); up to one
-// 32-token tile
-// the split-K small-M int GEMM (zlm_gemm_small_*: 16 waves per workgroup for
-// q4_0 / q8_0, 8 for q4_1 / q4_k); beyond it the 128 x 64 tiled int GEMM.
+// pass over the weights, k <= 16384; beyond it one GEMV per token).  From 3
+// tokens the int path: 3-4 tokens the int-path token GEMV where it covers k;
+// up to one 32-token tile the split-K small-M int GEMM (zlm_gemm_small_*: 16
+// waves per workgroup for q4_0 / q8_0, 8 for q4_1 / q4_k; one workgroup per
+// 32-row x 32-token tile); beyond it whichever of that kernel and the
+// 128 x 64 tiled int GEMM the cost model below predicts faster.
 constexpr size_t kGemmGemvM = 2;
 constexpr size_t kGemmSmallM = 32;
+
+bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K; }
+
+// Predicted microseconds of the two int GEMM kernels for rows x k x m,
+// fitted to gfx950 measurements (256 CUs; 8 shapes, 4096-15360 rows, k
+// 3840-15360, m 33-512, weights rotated past the Infinity Cache).  The
+// small-M kernel costs a fixed part plus a rate per (32-row tile, 32-token
+// tile, 32-element block): 7 us + 0.15 ns (q4_0, q8_0), 6 us + 0.25 ns (the
+// min-carrying q4_1, q4_k: 8-wave workgroups).  The tiled kernel runs a whole
+// row's K loop per wave: at least 4.5 us + 0.35 us per block while its grid
+// fits one workgroup per CU (1.15x that beyond), and 0.95 ns per (64-row,
+// 128-token, block) tile-step at full occupancy.  The model picked the faster kernel on
+// 79 of 80 measured points (the miss: 2.4 us of 170).
+double gemm_small_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int cus) {
+    const double units = static_cast<double>((rows + 31) / 32) * static_cast<double>((m + 31) / 32) *
+                         static_cast<double>(nb) * 256.0 / cus;
+    return gemm_has_min(qi->type) ? 6.0 + 0.25e-3 * units : 7.0 + 0.15e-3 * units;
+}
+
+double gemm_tiled_us(size_t rows, size_t m, size_t nb, int cus) {
+    const double wgs = static_cast<double>((rows + 63) / 64) * static_cast<double>((m + 127) / 128);
+    const double latency = (4.5 + 0.35 * static_cast<double>(nb)) * (wgs <= cus ? 1.0 : 1.15);
+    return std::max(latency, 0.95e-3 * wgs * static_cast<double>(nb) * 256.0 / cus);
+}
 
 bool gemm_supported(uint32_t type) {
     return type == ZLM_GGML_Q4_0 || type == ZLM_GGML_Q8_0 || type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K;
 }
-bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K; }
 
 // Build (once per row length) the GEMM's tiled copy of a resident weight, over
 // all whole rows it holds, rows padded to 32; nb = 32-element blocks per row:
@@ -1338,7 +1363,8 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     }
     const uint8_t* wq = r->gemm_payload;
     const void* ws = r->gemm_scales;
-    if (m <= kGemmSmallM) {  // one token tile: the split-K kernel, a workgroup per 32-row tile
+    if (m <= kGemmSmallM || gemm_small_us(qi, rows, m, nb, d->cus) < gemm_tiled_us(rows, m, nb, d->cus)) {
+        // the split-K kernel, a workgroup per 32-row tile and 32-token tile
         const float* dsa = ds ? ds : dx;
         void* args[] = {&wq, &ws, &qx, &dx, &dsa, &out_dev, &rows32, &m32, &nb32};
         hipFunction_t f = qi->type == ZLM_GGML_Q4_0   ? d->gemm_small_q4_0
@@ -1346,7 +1372,7 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
                           : qi->type == ZLM_GGML_Q4_1 ? d->gemm_small_q4_1
                                                       : d->gemm_small_q4_k;
         const unsigned threads = with_min ? 8 * 64 : 16 * 64;
-        return launch3(d, f, static_cast<unsigned>((rows + 31) / 32), 1, 1, threads, args, "gemm small");
+        return launch3(d, f, static_cast<unsigned>((rows + 31) / 32), mt32, 1, threads, args, "gemm small");
     }
     const unsigned gx = static_cast<unsigned>((rows + 63) / 64), gy = static_cast<unsigned>((m + 127) / 128);
     if (with_min) {

@@ -673,8 +673,9 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 }
 
 
-// ---- small-M prefill GEMM (m <= 32: verify and microbatch batches) ----------
-// The same int path and tiled operands as gemm_tiles, for one 32-token tile.
+// ---- small-M prefill GEMM (verify and microbatch batches, short prompts) -----
+// The same int path and tiled operands as gemm_tiles, one 32-token tile per
+// workgroup (grid.y: the token tiles).
 // A 32-row tile is too little work for one wave over the whole row (the
 // 128-token GEMM would leave most CUs idle and run a 4096-long K loop per
 // wave), so the kGemmSmallWaves waves of a workgroup split the row's blocks:
@@ -705,9 +706,14 @@ __device__ __forceinline__ void gemm_small(const uint8_t* __restrict__ wq, const
     const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int half = lane >> 5;
     const int l32 = lane & 31;
-    const uint32_t rt = blockIdx.x;  // the grid is exactly the row tiles
+    const uint32_t rt = blockIdx.x;  // the grid is exactly the row tiles x the token tiles
+    const uint32_t tt = blockIdx.y;
     constexpr uint32_t kWStride = QT == Q8_0 ? 1024 : 512;
     constexpr uint32_t kScBytes = MIN ? 8 : 2;
+    // token tile tt of the quantizer's layout: q bytes at tt * nb * 1024, scales at tt * nb * 32
+    qx += static_cast<size_t>(tt) * nb * 1024;
+    dx += static_cast<size_t>(tt) * nb * 32;
+    if constexpr (MIN) ds += static_cast<size_t>(tt) * nb * 32;
     GemmPtrs ptr;
     ptr.a = gemm_rsrc(qx, nb * 1024);
     ptr.a1 = 0;
@@ -812,7 +818,7 @@ __device__ __forceinline__ void gemm_small(const uint8_t* __restrict__ wq, const
             v += red[w][i][lane];
             if constexpr (MIN) vm += red[w][16 + i][lane];
         }
-        const uint32_t t = 8 * (i / 4) + 4 * half + (i % 4);
+        const uint32_t t = tt * 32 + 8 * (i / 4) + 4 * half + (i % 4);
         if (r < rows && t < m) out[static_cast<size_t>(t) * rows + r] = v * kOut + vm;
     }
 }
