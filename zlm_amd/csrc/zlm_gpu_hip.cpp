@@ -188,12 +188,15 @@ struct zlm_device {
     hipFunction_t gemm_q4_1 = nullptr;
     hipFunction_t gemm_q4_k = nullptr;
     hipFunction_t copy16 = nullptr;
-    hipFunction_t gemm_q4_0 = nullptr;
     hipFunction_t gemm_small_q4_0 = nullptr;  // m <= kGemmSmallM: split-K, one 32-token tile
     hipFunction_t gemm_small_q8_0 = nullptr;
     hipFunction_t gemm_small_q4_1 = nullptr;
     hipFunction_t gemm_small_q4_k = nullptr;
-    hipFunction_t gemm_q8_0 = nullptr;
+    // the tiled GEMMs with each tile's blocks split over two wave groups
+    hipFunction_t gemm_q4_0_k2 = nullptr;
+    hipFunction_t gemm_q8_0_k2 = nullptr;
+    hipFunction_t gemm_q4_1_k2 = nullptr;
+    hipFunction_t gemm_q4_k_k2 = nullptr;
     hipFunction_t qk_norm_rope_kv = nullptr;
     hipFunction_t attn_partial = nullptr;
     hipFunction_t attn_combine = nullptr;
@@ -318,9 +321,7 @@ bool load_kernels(zlm_device* d) {
         return false;
     if (!ok(d, hipModuleGetFunction(&d->tile_q4_0, d->mod, "zlm_tile_q4_0"), "zlm_tile_q4_0")) return false;
     if (!ok(d, hipModuleGetFunction(&d->copy16, d->mod, "zlm_copy16"), "zlm_copy16")) return false;
-    if (!ok(d, hipModuleGetFunction(&d->gemm_q4_0, d->mod, "zlm_gemm_q4_0_q8"), "zlm_gemm_q4_0_q8")) return false;
     if (!ok(d, hipModuleGetFunction(&d->tile_q8_0, d->mod, "zlm_tile_q8_0"), "zlm_tile_q8_0")) return false;
-    if (!ok(d, hipModuleGetFunction(&d->gemm_q8_0, d->mod, "zlm_gemm_q8_0_q8"), "zlm_gemm_q8_0_q8")) return false;
     if (!ok(d, hipModuleGetFunction(&d->tile_q4_1, d->mod, "zlm_tile_q4_1"), "zlm_tile_q4_1")) return false;
     if (!ok(d, hipModuleGetFunction(&d->tile_q4_k, d->mod, "zlm_tile_q4_k"), "zlm_tile_q4_k")) return false;
     if (!ok(d, hipModuleGetFunction(&d->gemm_q4_1, d->mod, "zlm_gemm_q4_1_q8"), "zlm_gemm_q4_1_q8")) return false;
@@ -328,7 +329,11 @@ bool load_kernels(zlm_device* d) {
     const struct {
         hipFunction_t* f;
         const char* name;
-    } more[] = {{&d->gemm_small_q4_0, "zlm_gemm_small_q4_0_q8"},
+    } more[] = {{&d->gemm_q4_0_k2, "zlm_gemm_q4_0_q8_k2"},
+                {&d->gemm_q8_0_k2, "zlm_gemm_q8_0_q8_k2"},
+                {&d->gemm_q4_1_k2, "zlm_gemm_q4_1_q8_k2"},
+                {&d->gemm_q4_k_k2, "zlm_gemm_q4_k_q8_k2"},
+                {&d->gemm_small_q4_0, "zlm_gemm_small_q4_0_q8"},
                 {&d->gemm_small_q8_0, "zlm_gemm_small_q8_0_q8"},
                 {&d->gemm_small_q4_1, "zlm_gemm_small_q4_1_q8"},
                 {&d->gemm_small_q4_k, "zlm_gemm_small_q4_k_q8"},
@@ -1208,32 +1213,50 @@ double now_ns() {
 // up to one 32-token tile the split-K small-M int GEMM (zlm_gemm_small_*: 16
 // waves per workgroup for q4_0 / q8_0, 8 for q4_1 / q4_k; one workgroup per
 // 32-row x 32-token tile); beyond it whichever of that kernel and the
-// 128 x 64 tiled int GEMM the cost model below predicts faster.
+// 128 x 64 tiled int GEMM (its blocks split over two wave groups, or not) the
+// cost model below predicts faster.
 constexpr size_t kGemmGemvM = 2;
 constexpr size_t kGemmSmallM = 32;
 
 bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K; }
 
-// Predicted microseconds of the two int GEMM kernels for rows x k x m,
-// fitted to gfx950 measurements (256 CUs; 8 shapes, 4096-15360 rows, k
-// 3840-15360, m 33-512, weights rotated past the Infinity Cache).  The
-// small-M kernel costs a fixed part plus a rate per (32-row tile, 32-token
-// tile, 32-element block): 7 us + 0.15 ns (q4_0, q8_0), 6 us + 0.25 ns (the
-// min-carrying q4_1, q4_k: 8-wave workgroups).  The tiled kernel runs a whole
-// row's K loop per wave: at least 4.5 us + 0.35 us per block while its grid
-// fits one workgroup per CU (1.15x that beyond), and 0.95 ns per (64-row,
-// 128-token, block) tile-step at full occupancy.  The model picked the faster kernel on
-// 79 of 80 measured points (the miss: 2.4 us of 170).
+// Predicted microseconds of the int GEMM kernels for rows x k x m, fitted to
+// gfx950 measurements (256 CUs; 8 shapes, 4096-15360 rows, k 3840-15360,
+// m 33-512, weights rotated past the Infinity Cache; on those 80 points the
+// picks below lose 1.0 us in all against the fastest kernel).
+// - The small-M kernel: a fixed part plus a rate per (32-row tile, 32-token
+//   tile, 32-element block): 7 us + 0.15 ns (q4_0, q8_0), 6 us + 0.25 ns (the
+//   min-carrying q4_1, q4_k: 8-wave workgroups).
+// - The tiled kernel: each wave walks a tile's whole block range, so its time
+//   is a per-block cost set by n = its workgroups per CU (rounded up): 3 us +
+//   c(n) us per block.  Split over two wave groups (`*k2 = true`, 8-wave
+//   workgroups, half the blocks per wave): c = 0.215 / 0.345 / 0.18n for
+//   n = 1 / 2 / >= 3 (q4_0, q8_0: at every n at or below the unsplit
+//   kernel, configs[4] included), 0.26 at n = 1 for q4_1 / q4_k (one resident
+//   workgroup per CU, 159 VGPRs and 64 KB of LDS); unsplit q4_1 / q4_k past
+//   that: 0.475 / 0.67 / 0.22n for n = 2 / 3 / >= 4.
 double gemm_small_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int cus) {
     const double units = static_cast<double>((rows + 31) / 32) * static_cast<double>((m + 31) / 32) *
                          static_cast<double>(nb) * 256.0 / cus;
     return gemm_has_min(qi->type) ? 6.0 + 0.25e-3 * units : 7.0 + 0.15e-3 * units;
 }
 
-double gemm_tiled_us(size_t rows, size_t m, size_t nb, int cus) {
-    const double wgs = static_cast<double>((rows + 63) / 64) * static_cast<double>((m + 127) / 128);
-    const double latency = (4.5 + 0.35 * static_cast<double>(nb)) * (wgs <= cus ? 1.0 : 1.15);
-    return std::max(latency, 0.95e-3 * wgs * static_cast<double>(nb) * 256.0 / cus);
+double gemm_tiled_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int cus, bool* k2) {
+    const uint64_t wgs = static_cast<uint64_t>((rows + 63) / 64) * static_cast<uint64_t>((m + 127) / 128);
+    const uint64_t n = std::max<uint64_t>(1, (wgs + static_cast<uint64_t>(cus) - 1) / static_cast<uint64_t>(cus));
+    const double dn = static_cast<double>(n);
+    double c;
+    if (!gemm_has_min(qi->type)) {
+        *k2 = true;
+        c = n == 1 ? 0.215 : n == 2 ? 0.345 : 0.18 * dn;
+    } else if (n == 1) {
+        *k2 = true;
+        c = 0.26;
+    } else {
+        *k2 = false;
+        c = n == 2 ? 0.475 : n == 3 ? 0.67 : 0.22 * dn;
+    }
+    return 3.0 + c * static_cast<double>(nb);
 }
 
 bool gemm_supported(uint32_t type) {
@@ -1363,7 +1386,9 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     }
     const uint8_t* wq = r->gemm_payload;
     const void* ws = r->gemm_scales;
-    if (m <= kGemmSmallM || gemm_small_us(qi, rows, m, nb, d->cus) < gemm_tiled_us(rows, m, nb, d->cus)) {
+    bool use_k2 = false;
+    const double tiled_us = gemm_tiled_us(qi, rows, m, nb, d->cus, &use_k2);
+    if (m <= kGemmSmallM || gemm_small_us(qi, rows, m, nb, d->cus) < tiled_us) {
         // the split-K kernel, a workgroup per 32-row tile and 32-token tile
         const float* dsa = ds ? ds : dx;
         void* args[] = {&wq, &ws, &qx, &dx, &dsa, &out_dev, &rows32, &m32, &nb32};
@@ -1375,14 +1400,17 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
         return launch3(d, f, static_cast<unsigned>((rows + 31) / 32), mt32, 1, threads, args, "gemm small");
     }
     const unsigned gx = static_cast<unsigned>((rows + 63) / 64), gy = static_cast<unsigned>((m + 127) / 128);
+    const char* what = use_k2 ? "gemm k2" : "gemm";
+    const unsigned threads = use_k2 ? 512 : 256;
     if (with_min) {
         void* args[] = {&wq, &ws, &qx, &dx, &ds, &out_dev, &rows32, &m32, &nb32, &mt32};
-        hipFunction_t f = qi->type == ZLM_GGML_Q4_1 ? d->gemm_q4_1 : d->gemm_q4_k;
-        return launch3(d, f, gx, gy, 1, 256, args, "gemm");
+        hipFunction_t f = qi->type == ZLM_GGML_Q4_1 ? (use_k2 ? d->gemm_q4_1_k2 : d->gemm_q4_1)
+                                                    : (use_k2 ? d->gemm_q4_k_k2 : d->gemm_q4_k);
+        return launch3(d, f, gx, gy, 1, threads, args, what);
     }
     void* args[] = {&wq, &ws, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
-    hipFunction_t f = qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0 : d->gemm_q4_0;
-    return launch3(d, f, gx, gy, 1, 256, args, "gemm");
+    hipFunction_t f = qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0_k2 : d->gemm_q4_0_k2;
+    return launch3(d, f, gx, gy, 1, threads, args, what);
 }
 
 }  // namespace

@@ -453,8 +453,9 @@ struct GemmPtrs {
     uint32_t oa, ow, osc, ox;               // lane byte offsets
 };
 
-// 119 VGPRs (q4_0), so the 3 waves per SIMD that the 12288 x 512 launch
-// places are all resident at once.
+// At most 168 VGPRs per wave (3 waves per SIMD): the split q4_0 GEMM takes
+// 120 (two of its 8-wave workgroups resident per CU), the min-carrying
+// quants' kernels 156-159.
 #ifndef ZLM_GEMM_WAVES_PER_EU
 #define ZLM_GEMM_WAVES_PER_EU 3
 #endif
@@ -566,13 +567,22 @@ __device__ __forceinline__ void gemm_acc(const v32f& c, const GemmI& I, v16f& ac
 // scales per 32-row tile.
 // q4_1 / q4_k take the (scale, min) tiles (zlm_tile_q4_1 / zlm_tile_q4_k) and
 // the quantizer's dx*sum(q): out = sum_b scale*dx*dot(nib, q) + min*dx*sum(q).
-template <int QT>
+//
+// SPLIT = 2 (8-wave workgroups): waves 0-3 and 4-7 take the same four output
+// tiles over the first and the second half of the row's blocks, and the
+// second group's sums reach the first through LDS (added in a fixed order),
+// for grids of about one workgroup per CU, where a lone wave per SIMD runs its
+// block chain latency-bound.
+template <int QT, int SPLIT = 1>
 __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const void* __restrict__ wsc,
                                            const int8_t* __restrict__ qx, const float* __restrict__ dx,
                                            const float* __restrict__ ds, float* __restrict__ out, uint32_t rows,
                                            uint32_t m, uint32_t nb, uint32_t mt) {
+    static_assert(SPLIT == 1 || SPLIT == 2, "one or two block ranges");
     const int lane = threadIdx.x & 63;
-    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const uint32_t wall = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+    const uint32_t wid = SPLIT == 1 ? wall : wall & 3;  // output tile
+    const uint32_t kh = SPLIT == 1 ? 0u : wall >> 2;    // block range
     const uint32_t tok0 = blockIdx.y * 128 + 64 * (wid & 1);  // multiple of 32
     const uint32_t row0 = blockIdx.x * 64 + 32 * (wid >> 1);  // multiple of 32
     const int half = lane >> 5;
@@ -608,23 +618,53 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
     // (Issuing block b+1's MFMAs ahead of block b's epilogue -- a software
     // pipeline at 164 VGPRs -- measured the same; VALU and MFMA of different
     // waves co-issue only in part on gfx950, so the kernel stays VALU-bound.)
+    // this wave's blocks [b0, b1): all of them, or one of two even-length halves
+    const uint32_t nbh = SPLIT == 1 ? nb : (nb + 3) / 4 * 2;
+    const uint32_t b0 = min(kh * nbh, nb), b1 = min(b0 + nbh, nb);
     GemmBlk A, B;
-    gemm_load<QT>(A, ptr, 0);
-    for (uint32_t b = 0; b < nb; b += 2) {
+    gemm_load<QT>(A, ptr, min(b0, nb - 1));
+    for (uint32_t b = b0; b < b1; b += 2) {
         gemm_load<QT>(B, ptr, min(b + 1, nb - 1));
         __builtin_amdgcn_sched_barrier(0);
         {
             const GemmI I = gemm_int<QT>(A, lo_half, sh);
-            gemm_acc(gemm_scale<QT>(A, b < nb, accm), I, acc0, acc1);
+            gemm_acc(gemm_scale<QT>(A, b < b1, accm), I, acc0, acc1);
         }
         __builtin_amdgcn_sched_barrier(0);
         gemm_load<QT>(A, ptr, min(b + 2, nb - 1));
         __builtin_amdgcn_sched_barrier(0);
         {
             const GemmI I = gemm_int<QT>(B, lo_half, sh);
-            gemm_acc(gemm_scale<QT>(B, b + 1 < nb, accm), I, acc0, acc1);
+            gemm_acc(gemm_scale<QT>(B, b + 1 < b1, accm), I, acc0, acc1);
         }
         __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (SPLIT == 2) {
+        // the second half's sums (and min terms) to the first half's waves
+        constexpr int NV = gemm_has_min(QT) ? 64 : 32;
+        __shared__ float red[4][NV][kWave];
+        if (kh == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                red[wid][i][lane] = acc0[i];
+                red[wid][16 + i][lane] = acc1[i];
+            }
+            if constexpr (gemm_has_min(QT)) {
+#pragma unroll
+                for (int i = 0; i < 32; i++) red[wid][32 + i][lane] = accm[i];
+            }
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            acc0[i] += red[wid][i][lane];
+            acc1[i] += red[wid][16 + i][lane];
+        }
+        if constexpr (gemm_has_min(QT)) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) accm[i] += red[wid][32 + i][lane];
+        }
     }
     constexpr float kOut = QT == Q4_0 ? 0.0625f : 1.0f;
     const uint32_t r = row0 + l32;
@@ -643,21 +683,10 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
     }
 }
 
-extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
-    zlm_gemm_q4_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
-                     const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
-                     uint32_t mt) {
-    gemm_tiles<Q4_0>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
-}
-
-extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
-    zlm_gemm_q8_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
-                     const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
-                     uint32_t mt) {
-    gemm_tiles<Q8_0>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
-}
-
-// q4_1 / q4_k: nb is the row's 32-element block count (k/32 for both).
+// The unsplit tiled GEMMs of the min-carrying quants (q4_1 / q4_k: nb is the
+// row's 32-element block count, k/32 for both), for grids of more than one
+// workgroup per CU; q4_0 / q8_0 run only the split form below, which measured
+// at or below the unsplit one at every occupancy.
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
     zlm_gemm_q4_1_q8(const uint8_t* __restrict__ wq, const float2* __restrict__ wsm, const int8_t* __restrict__ qx,
                      const float* __restrict__ dx, const float* __restrict__ ds, float* __restrict__ out,
@@ -670,6 +699,37 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
                      const float* __restrict__ dx, const float* __restrict__ ds, float* __restrict__ out,
                      uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
     gemm_tiles<Q4_K>(wq, wsm, qx, dx, ds, out, rows, m, nb, mt);
+}
+
+// The tiled GEMMs with each tile's blocks split over two 4-wave groups
+// (gemm_tiles SPLIT = 2): all of q4_0 / q8_0 past the small-M kernel, and
+// q4_1 / q4_k at up to one workgroup per CU.
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q4_0_q8_k2(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                        const int8_t* __restrict__ qx, const float* __restrict__ dx, float* __restrict__ out,
+                        uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q4_0, 2>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
+}
+
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q8_0_q8_k2(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                        const int8_t* __restrict__ qx, const float* __restrict__ dx, float* __restrict__ out,
+                        uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q8_0, 2>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
+}
+
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q4_1_q8_k2(const uint8_t* __restrict__ wq, const float2* __restrict__ wsm,
+                        const int8_t* __restrict__ qx, const float* __restrict__ dx, const float* __restrict__ ds,
+                        float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q4_1, 2>(wq, wsm, qx, dx, ds, out, rows, m, nb, mt);
+}
+
+extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q4_k_q8_k2(const uint8_t* __restrict__ wq, const float2* __restrict__ wsm,
+                        const int8_t* __restrict__ qx, const float* __restrict__ dx, const float* __restrict__ ds,
+                        float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q4_K, 2>(wq, wsm, qx, dx, ds, out, rows, m, nb, mt);
 }
 
 
