@@ -129,18 +129,20 @@ def _route(dev, res, zq, rows, k, m, x_dev, out_dev):
 # Past one 32-token tile the host picks, by a cost model, the small-M kernel
 # (one workgroup per 32-row x 32-token tile, grid.y = token tiles) or the
 # 128 x 64 tiled GEMM, whose tiles' blocks are split over two 4-wave groups
-# (8-wave workgroups: q4_0 / q8_0 always, q4_1 / q4_k at up to one workgroup
-# per CU) or not (q4_1 / q4_k on larger grids).  These shapes sit well inside
+# (8-wave workgroups; grids of up to two workgroups per CU for q4_0 / q8_0,
+# one for q4_1 / q4_k) or not (larger grids).  These shapes sit well inside
 # each choice: the small-M kernel over four token tiles (the last partial);
-# the split tiled GEMM over three 128-token tiles; and a larger grid with three
-# 128-token tiles (the last partial) and a ragged row tile, split for q4_0 /
-# q8_0 and unsplit for q4_1 / q4_k.  All over a row prefix of a resident
-# holding 64 rows more.
-MULTI_TILE = [("small", 4096 + 17, 4096, 100), ("split", 4096 + 17, 4096, 384), ("large", 12288 + 40, 4096, 300)]
+# the split tiled GEMM at 0.76 workgroups per CU (three 128-token tiles);
+# 1.5 workgroups per CU (two 128-token tiles and a ragged row tile), split for
+# q4_0 / q8_0 and unsplit for q4_1 / q4_k; and 2.3 workgroups per CU (three
+# 128-token tiles, the last partial), unsplit.  All over a row prefix of a
+# resident holding 64 rows more.
+MULTI_TILE = [("small", 4096 + 17, 4096, 100), ("split", 4096 + 17, 4096, 384), ("two", 12288 + 40, 4096, 256),
+              ("large", 12288 + 40, 4096, 300)]
 
 
 @pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0", "q4_1", "q4_k"])
-@pytest.mark.parametrize("route,rows,k,m", MULTI_TILE, ids=["small", "split", "large"])
+@pytest.mark.parametrize("route,rows,k,m", MULTI_TILE, ids=["small", "split", "two", "large"])
 def test_gemm_past_one_token_tile(dev, qt, zq, route, rows, k, m):
     _say(f"gemm past one token tile type={qt} route={route} rows={rows} k={k} m={m}")
     rb = synth.row_bytes(qt, k)
@@ -158,7 +160,7 @@ def test_gemm_past_one_token_tile(dev, qt, zq, route, rows, k, m):
             assert gemm[0]["what"] == "gemm small"
             assert (gemm[0]["grid_x"], gemm[0]["grid_y"]) == ((rows + 31) // 32, (m + 31) // 32)
         else:
-            split = route == "split" or zq in (zd.Q4_0, zd.Q8_0)
+            split = route == "split" or (route == "two" and zq in (zd.Q4_0, zd.Q8_0))
             assert (gemm[0]["what"], gemm[0]["block"]) == (("gemm k2", 512) if split else ("gemm", 256))
             assert (gemm[0]["grid_x"], gemm[0]["grid_y"]) == ((rows + 63) // 64, (m + 127) // 128)
         out = np.zeros(m * rows, np.float32)

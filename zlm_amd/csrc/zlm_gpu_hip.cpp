@@ -195,6 +195,8 @@ struct zlm_device {
     // the tiled GEMMs with each tile's blocks split over two wave groups
     hipFunction_t gemm_q4_0_k2 = nullptr;
     hipFunction_t gemm_q8_0_k2 = nullptr;
+    hipFunction_t gemm_q4_0 = nullptr;  // unsplit
+    hipFunction_t gemm_q8_0 = nullptr;
     hipFunction_t gemm_q4_1_k2 = nullptr;
     hipFunction_t gemm_q4_k_k2 = nullptr;
     hipFunction_t qk_norm_rope_kv = nullptr;
@@ -329,7 +331,9 @@ bool load_kernels(zlm_device* d) {
     const struct {
         hipFunction_t* f;
         const char* name;
-    } more[] = {{&d->gemm_q4_0_k2, "zlm_gemm_q4_0_q8_k2"},
+    } more[] = {{&d->gemm_q4_0, "zlm_gemm_q4_0_q8"},
+                {&d->gemm_q8_0, "zlm_gemm_q8_0_q8"},
+                {&d->gemm_q4_0_k2, "zlm_gemm_q4_0_q8_k2"},
                 {&d->gemm_q8_0_k2, "zlm_gemm_q8_0_q8_k2"},
                 {&d->gemm_q4_1_k2, "zlm_gemm_q4_1_q8_k2"},
                 {&d->gemm_q4_k_k2, "zlm_gemm_q4_k_q8_k2"},
@@ -1230,11 +1234,12 @@ bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_G
 // - The tiled kernel: each wave walks a tile's whole block range, so its time
 //   is a per-block cost set by n = its workgroups per CU (rounded up): 3 us +
 //   c(n) us per block.  Split over two wave groups (`*k2 = true`, 8-wave
-//   workgroups, half the blocks per wave): c = 0.215 / 0.345 / 0.18n for
-//   n = 1 / 2 / >= 3 (q4_0, q8_0: at every n at or below the unsplit
-//   kernel, configs[4] included), 0.26 at n = 1 for q4_1 / q4_k (one resident
-//   workgroup per CU, 159 VGPRs and 64 KB of LDS); unsplit q4_1 / q4_k past
-//   that: 0.475 / 0.67 / 0.22n for n = 2 / 3 / >= 4.
+//   workgroups, half the blocks per wave): c = 0.215 / 0.345 for n = 1 / 2
+//   (q4_0, q8_0), 0.26 at n = 1 for q4_1 / q4_k (one resident workgroup per
+//   CU: 159 VGPRs and 64 KB of LDS).  Unsplit past that: 0.19n for q4_0 /
+//   q8_0 at n >= 3 (configs[4]: the split form measured 2-3% faster there but
+//   re-read 1.3x the HBM bytes), 0.475 / 0.67 / 0.22n for q4_1 / q4_k at
+//   n = 2 / 3 / >= 4.
 double gemm_small_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int cus) {
     const double units = static_cast<double>((rows + 31) / 32) * static_cast<double>((m + 31) / 32) *
                          static_cast<double>(nb) * 256.0 / cus;
@@ -1247,8 +1252,8 @@ double gemm_tiled_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int 
     const double dn = static_cast<double>(n);
     double c;
     if (!gemm_has_min(qi->type)) {
-        *k2 = true;
-        c = n == 1 ? 0.215 : n == 2 ? 0.345 : 0.18 * dn;
+        *k2 = n <= 2;
+        c = n == 1 ? 0.215 : n == 2 ? 0.345 : 0.19 * dn;
     } else if (n == 1) {
         *k2 = true;
         c = 0.26;
@@ -1409,7 +1414,8 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
         return launch3(d, f, gx, gy, 1, threads, args, what);
     }
     void* args[] = {&wq, &ws, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
-    hipFunction_t f = qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0_k2 : d->gemm_q4_0_k2;
+    hipFunction_t f = qi->type == ZLM_GGML_Q8_0 ? (use_k2 ? d->gemm_q8_0_k2 : d->gemm_q8_0)
+                                                : (use_k2 ? d->gemm_q4_0_k2 : d->gemm_q4_0);
     return launch3(d, f, gx, gy, 1, threads, args, what);
 }
 

@@ -453,9 +453,10 @@ struct GemmPtrs {
     uint32_t oa, ow, osc, ox;               // lane byte offsets
 };
 
-// At most 168 VGPRs per wave (3 waves per SIMD): the split q4_0 GEMM takes
-// 120 (two of its 8-wave workgroups resident per CU), the min-carrying
-// quants' kernels 156-159.
+// At most 168 VGPRs per wave (3 waves per SIMD): the q4_0 GEMM takes 119, so
+// the 3 waves per SIMD that the 12288 x 512 launch places are all resident
+// at once (the split form 120: two of its 8-wave workgroups per CU); the
+// min-carrying quants' kernels 156-159.
 #ifndef ZLM_GEMM_WAVES_PER_EU
 #define ZLM_GEMM_WAVES_PER_EU 3
 #endif
@@ -683,10 +684,25 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
     }
 }
 
-// The unsplit tiled GEMMs of the min-carrying quants (q4_1 / q4_k: nb is the
-// row's 32-element block count, k/32 for both), for grids of more than one
-// workgroup per CU; q4_0 / q8_0 run only the split form below, which measured
-// at or below the unsplit one at every occupancy.
+// The unsplit tiled GEMMs, for grids of three or more workgroups per CU
+// (q4_0 / q8_0; configs[4] is one) or more than one (q4_1 / q4_k: nb is the
+// row's 32-element block count, k/32 for both).  There the split form below
+// is no faster: its 8-wave workgroups run two per CU and re-read more of the
+// weight panels through L2.
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q4_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
+                     const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
+                     uint32_t mt) {
+    gemm_tiles<Q4_0>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
+}
+
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
+    zlm_gemm_q8_0_q8(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd, const int8_t* __restrict__ qx,
+                     const float* __restrict__ dx, float* __restrict__ out, uint32_t rows, uint32_t m, uint32_t nb,
+                     uint32_t mt) {
+    gemm_tiles<Q8_0>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
+}
+
 extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
     zlm_gemm_q4_1_q8(const uint8_t* __restrict__ wq, const float2* __restrict__ wsm, const int8_t* __restrict__ qx,
                      const float* __restrict__ dx, const float* __restrict__ ds, float* __restrict__ out,
@@ -702,8 +718,8 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 }
 
 // The tiled GEMMs with each tile's blocks split over two 4-wave groups
-// (gemm_tiles SPLIT = 2): all of q4_0 / q8_0 past the small-M kernel, and
-// q4_1 / q4_k at up to one workgroup per CU.
+// (gemm_tiles SPLIT = 2), for grids of up to two workgroups per CU (q4_0 /
+// q8_0) or one (q4_1 / q4_k).
 extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
     zlm_gemm_q4_0_q8_k2(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                         const int8_t* __restrict__ qx, const float* __restrict__ dx, float* __restrict__ out,
