@@ -128,15 +128,16 @@ def _route(dev, res, zq, rows, k, m, x_dev, out_dev):
 
 # Past one 32-token tile the host picks, by a cost model, the small-M kernel
 # (one workgroup per 32-row x 32-token tile, grid.y = token tiles) or the
-# 128 x 64 tiled GEMM, whose tiles' blocks are split over two 4-wave groups
-# (8-wave workgroups; grids of up to two workgroups per CU for q4_0 / q8_0,
-# one for q4_1 / q4_k) or not (larger grids).  These shapes sit well inside
-# each choice: the small-M kernel over four token tiles (the last partial);
-# the split tiled GEMM at 0.76 workgroups per CU (three 128-token tiles);
-# 1.5 workgroups per CU (two 128-token tiles and a ragged row tile), split for
-# q4_0 / q8_0 and unsplit for q4_1 / q4_k; and 2.3 workgroups per CU (three
-# 128-token tiles, the last partial), unsplit.  All over a row prefix of a
-# resident holding 64 rows more.
+# 128 x 64 tiled GEMM, whose tiles' blocks are split over four 4-wave groups
+# (q4_0 / q8_0 at up to one workgroup per CU), two (q4_0 / q8_0 at two per
+# CU, q4_1 / q4_k at one) or none (larger grids).  These shapes sit well
+# inside each choice: the small-M kernel over four token tiles (the last
+# partial); 0.76 workgroups per CU (three 128-token tiles): four groups for
+# q4_0 / q8_0, two for q4_1 / q4_k; 1.5 workgroups per CU (two 128-token
+# tiles and a ragged row tile): two groups for q4_0 / q8_0, unsplit for
+# q4_1 / q4_k; and 2.3 workgroups per CU (three 128-token tiles, the last
+# partial): unsplit.  All over a row prefix of a resident holding 64 rows
+# more.
 MULTI_TILE = [("small", 4096 + 17, 4096, 100), ("split", 4096 + 17, 4096, 384), ("two", 12288 + 40, 4096, 256),
               ("large", 12288 + 40, 4096, 300)]
 
@@ -160,8 +161,10 @@ def test_gemm_past_one_token_tile(dev, qt, zq, route, rows, k, m):
             assert gemm[0]["what"] == "gemm small"
             assert (gemm[0]["grid_x"], gemm[0]["grid_y"]) == ((rows + 31) // 32, (m + 31) // 32)
         else:
-            split = route == "split" or (route == "two" and zq in (zd.Q4_0, zd.Q8_0))
-            assert (gemm[0]["what"], gemm[0]["block"]) == (("gemm k2", 512) if split else ("gemm", 256))
+            plain = zq in (zd.Q4_0, zd.Q8_0)
+            groups = {"split": 4 if plain else 2, "two": 2 if plain else 1, "large": 1}[route]
+            what = {4: "gemm k4", 2: "gemm k2", 1: "gemm"}[groups]
+            assert (gemm[0]["what"], gemm[0]["block"]) == (what, 256 * groups)
             assert (gemm[0]["grid_x"], gemm[0]["grid_y"]) == ((rows + 63) // 64, (m + 127) // 128)
         out = np.zeros(m * rows, np.float32)
         dev.dev_download(out, out_dev)

@@ -195,6 +195,8 @@ struct zlm_device {
     // the tiled GEMMs with each tile's blocks split over two wave groups
     hipFunction_t gemm_q4_0_k2 = nullptr;
     hipFunction_t gemm_q8_0_k2 = nullptr;
+    hipFunction_t gemm_q4_0_k4 = nullptr;
+    hipFunction_t gemm_q8_0_k4 = nullptr;
     hipFunction_t gemm_q4_0 = nullptr;  // unsplit
     hipFunction_t gemm_q8_0 = nullptr;
     hipFunction_t gemm_q4_1_k2 = nullptr;
@@ -334,6 +336,8 @@ bool load_kernels(zlm_device* d) {
     } more[] = {{&d->gemm_q4_0, "zlm_gemm_q4_0_q8"},
                 {&d->gemm_q8_0, "zlm_gemm_q8_0_q8"},
                 {&d->gemm_q4_0_k2, "zlm_gemm_q4_0_q8_k2"},
+                {&d->gemm_q4_0_k4, "zlm_gemm_q4_0_q8_k4"},
+                {&d->gemm_q8_0_k4, "zlm_gemm_q8_0_q8_k4"},
                 {&d->gemm_q8_0_k2, "zlm_gemm_q8_0_q8_k2"},
                 {&d->gemm_q4_1_k2, "zlm_gemm_q4_1_q8_k2"},
                 {&d->gemm_q4_k_k2, "zlm_gemm_q4_k_q8_k2"},
@@ -1217,48 +1221,50 @@ double now_ns() {
 // up to one 32-token tile the split-K small-M int GEMM (zlm_gemm_small_*: 16
 // waves per workgroup for q4_0 / q8_0, 8 for q4_1 / q4_k; one workgroup per
 // 32-row x 32-token tile); beyond it whichever of that kernel and the
-// 128 x 64 tiled int GEMM (its blocks split over two wave groups, or not) the
-// cost model below predicts faster.
+// 128 x 64 tiled int GEMM (each tile's blocks split over four or two wave
+// groups, or not) the cost model below predicts faster.
 constexpr size_t kGemmGemvM = 2;
 constexpr size_t kGemmSmallM = 32;
 
 bool gemm_has_min(uint32_t type) { return type == ZLM_GGML_Q4_1 || type == ZLM_GGML_Q4_K; }
 
 // Predicted microseconds of the int GEMM kernels for rows x k x m, fitted to
-// gfx950 measurements (256 CUs; 8 shapes, 4096-15360 rows, k 3840-15360,
-// m 33-512, weights rotated past the Infinity Cache; on those 80 points the
-// picks below lose 1.0 us in all against the fastest kernel).
+// gfx950 measurements (256 CUs; 10 shapes, 3840-15360 rows, k 3840-15360,
+// m 33-512, weights rotated past the Infinity Cache).  On those 100 points
+// the picks below lose 3.7 us in all against the fastest kernel, 3.0 of it
+// at configs[4]'s shape (below).
 // - The small-M kernel: a fixed part plus a rate per (32-row tile, 32-token
 //   tile, 32-element block): 7 us + 0.15 ns (q4_0, q8_0), 6 us + 0.25 ns (the
 //   min-carrying q4_1, q4_k: 8-wave workgroups).
 // - The tiled kernel: each wave walks a tile's whole block range, so its time
 //   is a per-block cost set by n = its workgroups per CU (rounded up): 3 us +
-//   c(n) us per block.  Split over two wave groups (`*k2 = true`, 8-wave
-//   workgroups, half the blocks per wave): c = 0.215 / 0.345 for n = 1 / 2
-//   (q4_0, q8_0), 0.26 at n = 1 for q4_1 / q4_k (one resident workgroup per
-//   CU: 159 VGPRs and 64 KB of LDS).  Unsplit past that: 0.19n for q4_0 /
-//   q8_0 at n >= 3 (configs[4]: the split form measured 2-3% faster there but
-//   re-read 1.3x the HBM bytes), 0.475 / 0.67 / 0.22n for q4_1 / q4_k at
-//   n = 2 / 3 / >= 4.
+//   c(n) us per block.  q4_0 / q8_0: split over four wave groups (*split =
+//   4, 16-wave workgroups, a quarter of the blocks per wave) at n = 1,
+//   c = 0.195; over two (*split = 2, 8-wave workgroups) at n = 2, c = 0.345;
+//   unsplit from n = 3, c = 0.19n (configs[4]: the two-way split measured
+//   2-3% faster there but re-read 1.3x the HBM bytes).  q4_1 / q4_k: split
+//   over two at n = 1, c = 0.26 (one resident workgroup per CU: 159 VGPRs and
+//   64 KB of LDS; four groups do not fit); unsplit past that, c = 0.475 /
+//   0.67 / 0.22n at n = 2 / 3 / >= 4.
 double gemm_small_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int cus) {
     const double units = static_cast<double>((rows + 31) / 32) * static_cast<double>((m + 31) / 32) *
                          static_cast<double>(nb) * 256.0 / cus;
     return gemm_has_min(qi->type) ? 6.0 + 0.25e-3 * units : 7.0 + 0.15e-3 * units;
 }
 
-double gemm_tiled_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int cus, bool* k2) {
+double gemm_tiled_us(const QuantInfo* qi, size_t rows, size_t m, size_t nb, int cus, int* split) {
     const uint64_t wgs = static_cast<uint64_t>((rows + 63) / 64) * static_cast<uint64_t>((m + 127) / 128);
     const uint64_t n = std::max<uint64_t>(1, (wgs + static_cast<uint64_t>(cus) - 1) / static_cast<uint64_t>(cus));
     const double dn = static_cast<double>(n);
     double c;
     if (!gemm_has_min(qi->type)) {
-        *k2 = n <= 2;
-        c = n == 1 ? 0.215 : n == 2 ? 0.345 : 0.19 * dn;
+        *split = n == 1 ? 4 : n == 2 ? 2 : 1;
+        c = n == 1 ? 0.195 : n == 2 ? 0.345 : 0.19 * dn;
     } else if (n == 1) {
-        *k2 = true;
+        *split = 2;
         c = 0.26;
     } else {
-        *k2 = false;
+        *split = 1;
         c = n == 2 ? 0.475 : n == 3 ? 0.67 : 0.22 * dn;
     }
     return 3.0 + c * static_cast<double>(nb);
@@ -1391,8 +1397,8 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
     }
     const uint8_t* wq = r->gemm_payload;
     const void* ws = r->gemm_scales;
-    bool use_k2 = false;
-    const double tiled_us = gemm_tiled_us(qi, rows, m, nb, d->cus, &use_k2);
+    int split = 1;
+    const double tiled_us = gemm_tiled_us(qi, rows, m, nb, d->cus, &split);
     if (m <= kGemmSmallM || gemm_small_us(qi, rows, m, nb, d->cus) < tiled_us) {
         // the split-K kernel, a workgroup per 32-row tile and 32-token tile
         const float* dsa = ds ? ds : dx;
@@ -1405,8 +1411,9 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
         return launch3(d, f, static_cast<unsigned>((rows + 31) / 32), mt32, 1, threads, args, "gemm small");
     }
     const unsigned gx = static_cast<unsigned>((rows + 63) / 64), gy = static_cast<unsigned>((m + 127) / 128);
-    const char* what = use_k2 ? "gemm k2" : "gemm";
-    const unsigned threads = use_k2 ? 512 : 256;
+    const bool use_k2 = split == 2;
+    const char* what = split == 4 ? "gemm k4" : use_k2 ? "gemm k2" : "gemm";
+    const unsigned threads = 256u * static_cast<unsigned>(split);
     if (with_min) {
         void* args[] = {&wq, &ws, &qx, &dx, &ds, &out_dev, &rows32, &m32, &nb32, &mt32};
         hipFunction_t f = qi->type == ZLM_GGML_Q4_1 ? (use_k2 ? d->gemm_q4_1_k2 : d->gemm_q4_1)
@@ -1414,6 +1421,8 @@ bool enqueue_gemm(zlm_device* d, zlm_resident* r, uint32_t quant, size_t rows, s
         return launch3(d, f, gx, gy, 1, threads, args, what);
     }
     void* args[] = {&wq, &ws, &qx, &dx, &out_dev, &rows32, &m32, &nb32, &mt32};
+    if (split == 4)
+        return launch3(d, qi->type == ZLM_GGML_Q8_0 ? d->gemm_q8_0_k4 : d->gemm_q4_0_k4, gx, gy, 1, threads, args, what);
     hipFunction_t f = qi->type == ZLM_GGML_Q8_0 ? (use_k2 ? d->gemm_q8_0_k2 : d->gemm_q8_0)
                                                 : (use_k2 ? d->gemm_q4_0_k2 : d->gemm_q4_0);
     return launch3(d, f, gx, gy, 1, threads, args, what);

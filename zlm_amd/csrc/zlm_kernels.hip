@@ -569,17 +569,16 @@ __device__ __forceinline__ void gemm_acc(const v32f& c, const GemmI& I, v16f& ac
 // q4_1 / q4_k take the (scale, min) tiles (zlm_tile_q4_1 / zlm_tile_q4_k) and
 // the quantizer's dx*sum(q): out = sum_b scale*dx*dot(nib, q) + min*dx*sum(q).
 //
-// SPLIT = 2 (8-wave workgroups): waves 0-3 and 4-7 take the same four output
-// tiles over the first and the second half of the row's blocks, and the
-// second group's sums reach the first through LDS (added in a fixed order),
-// for grids of about one workgroup per CU, where a lone wave per SIMD runs its
-// block chain latency-bound.
+// SPLIT = 2 or 4 (8- or 16-wave workgroups): each group of 4 waves takes the
+// same four output tiles over its part of the row's blocks, and the other
+// groups' sums reach group 0 through LDS (added in a fixed order), for small
+// grids, where a lone wave per SIMD would run its block chain latency-bound.
 template <int QT, int SPLIT = 1>
 __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const void* __restrict__ wsc,
                                            const int8_t* __restrict__ qx, const float* __restrict__ dx,
                                            const float* __restrict__ ds, float* __restrict__ out, uint32_t rows,
                                            uint32_t m, uint32_t nb, uint32_t mt) {
-    static_assert(SPLIT == 1 || SPLIT == 2, "one or two block ranges");
+    static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "one, two or four block ranges");
     const int lane = threadIdx.x & 63;
     const uint32_t wall = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const uint32_t wid = SPLIT == 1 ? wall : wall & 3;  // output tile
@@ -619,8 +618,8 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
     // (Issuing block b+1's MFMAs ahead of block b's epilogue -- a software
     // pipeline at 164 VGPRs -- measured the same; VALU and MFMA of different
     // waves co-issue only in part on gfx950, so the kernel stays VALU-bound.)
-    // this wave's blocks [b0, b1): all of them, or one of two even-length halves
-    const uint32_t nbh = SPLIT == 1 ? nb : (nb + 3) / 4 * 2;
+    // this wave's blocks [b0, b1): all of them, or one of SPLIT even-length parts
+    const uint32_t nbh = SPLIT == 1 ? nb : (nb + 2 * SPLIT - 1) / (2 * SPLIT) * 2;
     const uint32_t b0 = min(kh * nbh, nb), b1 = min(b0 + nbh, nb);
     GemmBlk A, B;
     gemm_load<QT>(A, ptr, min(b0, nb - 1));
@@ -665,6 +664,42 @@ __device__ __forceinline__ void gemm_tiles(const uint8_t* __restrict__ wq, const
         if constexpr (gemm_has_min(QT)) {
 #pragma unroll
             for (int i = 0; i < 32; i++) accm[i] += red[wid][32 + i][lane];
+        }
+    }
+    if constexpr (SPLIT == 4) {
+        // groups 2 and 3 add into 0 and 1, then group 1 into 0: the order is
+        // fixed, (g0 + g2) + (g1 + g3)
+        static_assert(!gemm_has_min(QT), "four block ranges: q4_0 / q8_0");
+        __shared__ float red[2][4][32][kWave];
+        if (kh >= 2) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                red[kh - 2][wid][i][lane] = acc0[i];
+                red[kh - 2][wid][16 + i][lane] = acc1[i];
+            }
+        }
+        __syncthreads();
+        if (kh < 2) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                acc0[i] += red[kh][wid][i][lane];
+                acc1[i] += red[kh][wid][16 + i][lane];
+            }
+        }
+        __syncthreads();
+        if (kh == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                red[0][wid][i][lane] = acc0[i];
+                red[0][wid][16 + i][lane] = acc1[i];
+            }
+        }
+        __syncthreads();
+        if (kh != 0) return;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            acc0[i] += red[0][wid][i][lane];
+            acc1[i] += red[0][wid][16 + i][lane];
         }
     }
     constexpr float kOut = QT == Q4_0 ? 0.0625f : 1.0f;
@@ -718,8 +753,8 @@ extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_pe
 }
 
 // The tiled GEMMs with each tile's blocks split over two 4-wave groups
-// (gemm_tiles SPLIT = 2), for grids of up to two workgroups per CU (q4_0 /
-// q8_0) or one (q4_1 / q4_k).
+// (gemm_tiles SPLIT = 2), for grids of two workgroups per CU (q4_0 / q8_0)
+// or one (q4_1 / q4_k).
 extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
     zlm_gemm_q4_0_q8_k2(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
                         const int8_t* __restrict__ qx, const float* __restrict__ dx, float* __restrict__ out,
@@ -732,6 +767,23 @@ extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_pe
                         const int8_t* __restrict__ qx, const float* __restrict__ dx, float* __restrict__ out,
                         uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
     gemm_tiles<Q8_0, 2>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
+}
+
+// Four block ranges (16-wave workgroups, 4 waves per SIMD), for grids of up
+// to one workgroup per CU: q4_0 / q8_0 only, whose 121 VGPRs fit; the
+// min-carrying kernels' 159 do not.
+extern "C" __global__ void __launch_bounds__(1024)
+    zlm_gemm_q4_0_q8_k4(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                        const int8_t* __restrict__ qx, const float* __restrict__ dx, float* __restrict__ out,
+                        uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q4_0, 4>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
+}
+
+extern "C" __global__ void __launch_bounds__(1024)
+    zlm_gemm_q8_0_q8_k4(const uint8_t* __restrict__ wq, const uint16_t* __restrict__ wd,
+                        const int8_t* __restrict__ qx, const float* __restrict__ dx, float* __restrict__ out,
+                        uint32_t rows, uint32_t m, uint32_t nb, uint32_t mt) {
+    gemm_tiles<Q8_0, 4>(wq, wd, qx, dx, nullptr, out, rows, m, nb, mt);
 }
 
 extern "C" __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(ZLM_GEMM_WAVES_PER_EU)))
