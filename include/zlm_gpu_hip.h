@@ -259,8 +259,8 @@ bool zlm_gpu_mat_vec_batch_enqueue(zlm_device *dev, zlm_resident *const *res, ui
  * otherwise the q8 activation quantizer, then an int8-MFMA GEMM over the
  * tiled copy (built on first use): up to 32 tokens the split-K small-M
  * kernel, past that the small-M kernel over several 32-token tiles or the
- * 128 x 64 tiled GEMM (each tile's blocks split over two wave groups on
- * small grids), whichever the library's cost model predicts faster for
+ * 128 x 64 tiled GEMM (each tile's blocks split over four or two wave
+ * groups on small grids), whichever the library's cost model predicts faster for
  * (rows, k, m).  A token's results do not depend on the other tokens of the
  * call within one kernel. */
 bool zlm_gpu_mat_mul_enqueue(zlm_device *dev, zlm_resident *res, uint32_t quant, size_t rows, size_t k, size_t m,
