@@ -80,10 +80,13 @@ def test_gemm_matches_int_oracle(dev, qt, zq, rows, k, m):
 # q4_0 / q8_0, 8 waves and 16-block steps for q4_1 / q4_k): odd block counts
 # (a pair's second block past the end), block counts not a multiple of a split
 # step (k = 3840 and 288), ragged row tiles, one token, a full tile, and the
-# first m past it (a second, one-token tile).  A k that is not whole super-blocks for
-# q4_k is rounded up to the next one.
+# first m past it (a second, one-token tile).  Two more shapes past one token
+# tile reach the tiled GEMM split over wave groups (four for q4_0 / q8_0, two
+# for q4_1 / q4_k) with an odd block count (k = 288: 9 blocks) and with fewer
+# blocks than groups have pairs (k = 96: 3 blocks; the last groups get none).
+# A k that is not whole super-blocks for q4_k is rounded up to the next one.
 SMALL_M = [(33, 4096, 2), (64, 4096, 9), (96, 3840, 32), (40, 12288, 31), (37, 288, 5), (64, 256, 33),
-           (32, 512, 1), (4096 + 17, 4096, 8), (50, 4096, 3)]
+           (32, 512, 1), (4096 + 17, 4096, 8), (50, 4096, 3), (37, 288, 64), (40, 96, 40)]
 
 
 @pytest.mark.parametrize("qt,zq", GEMM_QUANTS, ids=["q4_0", "q8_0", "q4_1", "q4_k"])
