@@ -44,7 +44,12 @@ def test_dequant_bit_exact(dev, qt):
     dev.free_resident(res)
 
 
-SHAPES = [(64, 256), (37, 512), (333, 4096), (129, 3840), (64, 8192), (257, 12288), (40, 15360), (16, 32768)]
+# Row lengths of the configs, every x tier, and the long rows of other models'
+# FFN down projections and hidden sizes (5120, 7168, 10240, 11008, 14336,
+# 17408, 18944: the split-K instances of 5-10 chunk steps for the 32-element
+# chunk quants and 9-19 for q8_0, plus its exact 5- and 7-step instances).
+SHAPES = [(64, 256), (37, 512), (333, 4096), (129, 3840), (64, 8192), (257, 12288), (40, 15360), (16, 32768),
+          (70, 5120), (41, 7168), (33, 10240), (67, 11008), (130, 14336), (29, 17408), (65, 18944)]
 
 
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])

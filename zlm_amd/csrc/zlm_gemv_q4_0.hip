@@ -34,6 +34,22 @@ ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s2_pfqw16, Q4_0, 4096, 8, 1, 2, PRO_NORM, EPI_P
 ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s6_sk4x, Q4_0, 6, 4, 1, EPI_PLAIN, true, 2, true)
 ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s6_sk4x, Q4_0, 6, 4, 1, EPI_RESID, true, 2, true)
 
+// The same split-K forms for the other long rows (k 8193-20480: the FFN down
+// projections of other models, e.g. k = 11008, 14336, 17408), any row of
+// ceil(chunks / 64) == STEPS, one wave per chunk step.
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s5_sk4, Q4_0, 5, 4, 1, EPI_PLAIN, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s6_sk4, Q4_0, 6, 4, 1, EPI_PLAIN, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s7_sk4, Q4_0, 7, 4, 1, EPI_PLAIN, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s8_sk4, Q4_0, 8, 4, 1, EPI_PLAIN, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s9_sk4, Q4_0, 9, 4, 1, EPI_PLAIN, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s10_sk4, Q4_0, 10, 4, 1, EPI_PLAIN, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s5_sk4, Q4_0, 5, 4, 1, EPI_RESID, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s6_sk4, Q4_0, 6, 4, 1, EPI_RESID, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s7_sk4, Q4_0, 7, 4, 1, EPI_RESID, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s8_sk4, Q4_0, 8, 4, 1, EPI_RESID, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s9_sk4, Q4_0, 9, 4, 1, EPI_RESID, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s10_sk4, Q4_0, 10, 4, 1, EPI_RESID, true, 2, false)
+
 ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)
 
 // matMul at m = 2 (both tokens in one pass over the weights)

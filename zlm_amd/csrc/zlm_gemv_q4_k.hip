@@ -17,6 +17,12 @@ ZLM_GEMVX_PF(zlm_gemv_q4_k_r1_s8_pf, Q4_K, 16384, 8, 1, 8, PRO_PLAIN, EPI_PLAIN,
 // qs + record layout, 10.4 us with the parked reduction (one barrier per 16
 // tiles instead of one per tile).
 ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s8_sk4, Q4_K, 8, 4, 1, EPI_PLAIN, true, 2, false, 16)
+// The same for the other long rows (k 8193-20480, e.g. 11008, 14336, 17408).
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s5_sk4, Q4_K, 5, 4, 1, EPI_PLAIN, true, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s6_sk4, Q4_K, 6, 4, 1, EPI_PLAIN, true, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s7_sk4, Q4_K, 7, 4, 1, EPI_PLAIN, true, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s9_sk4, Q4_K, 9, 4, 1, EPI_PLAIN, true, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s10_sk4, Q4_K, 10, 4, 1, EPI_PLAIN, true, 2, false, 16)
 
 // k <= 4096 (the C3 gate/up 15360 x 3840): x as int8 planes, prefetching
 // 16-wave workgroups, one per CU (the x planes are built once per 16 waves);

@@ -26,5 +26,11 @@ ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r2_s2_tallq, Q6_K, 4096, 8, 2, 2, PRO_PLAIN, EPI_PLA
 // q8_0 / q4_0 split-K downs measured slower parked (10.6 -> 11.4, 9.1 -> 9.5
 // us) and keep one barrier per tile.
 ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s8_sk2, Q6_K, 8, 2, 1, EPI_PLAIN, false, 2, false, 16)
+// The same for the other long rows (k 8193-20480, e.g. 11008, 14336, 17408).
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s5_sk2, Q6_K, 5, 2, 1, EPI_PLAIN, false, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s6_sk2, Q6_K, 6, 2, 1, EPI_PLAIN, false, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s7_sk2, Q6_K, 7, 2, 1, EPI_PLAIN, false, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s9_sk2, Q6_K, 9, 2, 1, EPI_PLAIN, false, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s10_sk2, Q6_K, 10, 2, 1, EPI_PLAIN, false, 2, false, 16)
 
 ZLM_GEMV_MULTI_Q4(q6_k, Q6_K)

@@ -13,6 +13,26 @@ ZLM_GEMVX_PAIR_TILES_Q8(q8_0, Q8_0)
 // ~320 registers per wave and runs one wave per SIMD).
 ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s12_sk2x, Q8_0, 12, 2, 1, EPI_PLAIN, false, 2, true)
 
+// The same for the other long rows (k 8193-20480, e.g. 11008, 14336, 17408),
+// any row of ceil(chunks / 64) == STEPS: one wave per chunk step up to 16
+// steps, two steps per wave beyond (17 steps take the 18-step workgroup).
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s9_sk2, Q8_0, 9, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s10_sk2, Q8_0, 10, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s11_sk2, Q8_0, 11, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s12_sk2, Q8_0, 12, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s13_sk2, Q8_0, 13, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s14_sk2, Q8_0, 14, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s15_sk2, Q8_0, 15, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s16_sk2, Q8_0, 16, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s17_sk2, Q8_0, 9, 2, 2, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s18_sk2, Q8_0, 9, 2, 2, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s19_sk2, Q8_0, 10, 2, 2, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s20_sk2, Q8_0, 10, 2, 2, EPI_PLAIN, false, 2, false)
+
+// Exact-steps instances for k = 5120 and 7168 (hidden sizes of other models).
+ZLM_GEMV(zlm_gemv_q8_0_r1_s5, Q8_0, 8192, 1, 5, true)
+ZLM_GEMV(zlm_gemv_q8_0_r1_s7, Q8_0, 8192, 1, 7, true)
+
 // The lm_heads (from 65536 rows, k = 4096): prefetching 8-wave workgroups at
 // 16 waves per CU, plain and RMSNorm-fused; measured on gfx950 at 151936 x
 // 4096: 98.6 -> 94.8 us against the 4-wave exact-steps instance at 8
