@@ -49,6 +49,8 @@ ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s7_sk4, Q4_0, 7, 4, 1, EPI_RESID, true, 2, false
 ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s8_sk4, Q4_0, 8, 4, 1, EPI_RESID, true, 2, false)
 ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s9_sk4, Q4_0, 9, 4, 1, EPI_RESID, true, 2, false)
 ZLM_GEMV_SK(zlm_gemv_q4_0_resid_s10_sk4, Q4_0, 10, 4, 1, EPI_RESID, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s3_sk4, Q4_0, 3, 4, 1, EPI_PLAIN, true, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q4_0_r1_s4_sk4, Q4_0, 4, 4, 1, EPI_PLAIN, true, 2, false)
 
 ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)
 

@@ -23,6 +23,8 @@ ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s6_sk4, Q4_K, 6, 4, 1, EPI_PLAIN, true, 2, false, 
 ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s7_sk4, Q4_K, 7, 4, 1, EPI_PLAIN, true, 2, false, 16)
 ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s9_sk4, Q4_K, 9, 4, 1, EPI_PLAIN, true, 2, false, 16)
 ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s10_sk4, Q4_K, 10, 4, 1, EPI_PLAIN, true, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s3_sk4, Q4_K, 3, 4, 1, EPI_PLAIN, true, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q4_k_r1_s4_sk4, Q4_K, 4, 4, 1, EPI_PLAIN, true, 2, false, 16)
 
 // k <= 4096 (the C3 gate/up 15360 x 3840): x as int8 planes, prefetching
 // 16-wave workgroups, one per CU (the x planes are built once per 16 waves);

@@ -32,5 +32,7 @@ ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s6_sk2, Q6_K, 6, 2, 1, EPI_PLAIN, false, 2, false,
 ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s7_sk2, Q6_K, 7, 2, 1, EPI_PLAIN, false, 2, false, 16)
 ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s9_sk2, Q6_K, 9, 2, 1, EPI_PLAIN, false, 2, false, 16)
 ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s10_sk2, Q6_K, 10, 2, 1, EPI_PLAIN, false, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s3_sk2, Q6_K, 3, 2, 1, EPI_PLAIN, false, 2, false, 16)
+ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s4_sk2, Q6_K, 4, 2, 1, EPI_PLAIN, false, 2, false, 16)
 
 ZLM_GEMV_MULTI_Q4(q6_k, Q6_K)

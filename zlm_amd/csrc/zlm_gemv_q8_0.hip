@@ -28,6 +28,10 @@ ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s17_sk2, Q8_0, 9, 2, 2, EPI_PLAIN, false, 2, false)
 ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s18_sk2, Q8_0, 9, 2, 2, EPI_PLAIN, false, 2, false)
 ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s19_sk2, Q8_0, 10, 2, 2, EPI_PLAIN, false, 2, false)
 ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s20_sk2, Q8_0, 10, 2, 2, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s5_sk2, Q8_0, 5, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s6_sk2, Q8_0, 6, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s7_sk2, Q8_0, 7, 2, 1, EPI_PLAIN, false, 2, false)
+ZLM_GEMV_SK(zlm_gemv_q8_0_r1_s8_sk2, Q8_0, 8, 2, 1, EPI_PLAIN, false, 2, false)
 
 // Exact-steps instances for k = 5120 and 7168 (hidden sizes of other models).
 ZLM_GEMV(zlm_gemv_q8_0_r1_s5, Q8_0, 8192, 1, 5, true)

@@ -666,10 +666,24 @@ constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true, 2}, {"_tall", 16
 // 64 * steps); one workgroup per CU.
 constexpr int kSkRows[] = {2, 4};
 
-const GemvKernel* find_split(zlm_device* d, const QuantInfo* qi, size_t k, const char* form) {
+// Whether a launch of `rows` rows at a row length of 4097-8192 elements takes
+// the split-K instance (rows of 3-4 chunk steps; q8_0 5-8).  Measured on
+// gfx950 (alternating runs, rows 1024-28672 x k 5120-8192, weights rotated
+// past the Infinity Cache): q4_0 and q4_k gain at every row count (4096 x
+// 8192 Q4_0 9.2 -> 7.4 us, 14336 x 8192 21.6 -> 16.6 us), q8_0 and q6_k up
+// to 8192 rows (4096 x 8192 Q6_K 10.9 -> 9.1 us) but lose 2-10% from 14336
+// rows; 65536 rows and more keep the one-wave-per-row instances.
+bool split_mid_rows(const QuantInfo* qi, size_t rows) {
+    if (rows <= 8192) return true;
+    return rows < 65536 && (qi->type == ZLM_GGML_Q4_0 || qi->type == ZLM_GGML_Q4_K);
+}
+
+const GemvKernel* find_split(zlm_device* d, const QuantInfo* qi, size_t k, const char* form, size_t rows) {
     const size_t chunks = k / qi->chunk_elems;
     const int steps = static_cast<int>((chunks + 63) / 64);
     const bool exact = chunks % 64 == 0;
+    const bool mid = qi->type == ZLM_GGML_Q8_0 ? (steps >= 5 && steps <= 8) : (steps >= 3 && steps <= 4);
+    if (mid && !split_mid_rows(qi, rows)) return nullptr;
     char nm[96];
     for (int rt : kSkRows) {
         if (exact) {
@@ -732,7 +746,7 @@ const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, 
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
     if (rt == 1) {
-        if (const GemvKernel* g = find_split(d, qi, k, "r1")) return g;
+        if (const GemvKernel* g = find_split(d, qi, k, "r1", rows)) return g;
         for (const PfSuffix& v : kPfSuffixes) {
             if (rows < v.min_rows) continue;
             snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d%s", qn, v.rt, steps, v.suffix);
@@ -1022,7 +1036,7 @@ const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k,
     const char* qn = kQuantNames[qi->slot];
     char nm[96];
     if (form == ZLM_FORM_RESID) {
-        if (const GemvKernel* g = find_split(d, qi, k, kFormNames[form])) return g;
+        if (const GemvKernel* g = find_split(d, qi, k, kFormNames[form], rows)) return g;
         if (resid_two_rows(qi, steps, rows)) {
             snprintf(nm, sizeof nm, "zlm_gemv_%s_resid_s%d_r2", qn, steps);
             if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 2, steps)) return g;
