@@ -41,7 +41,7 @@ def _rmsnorm(x, w, eps):
 
 
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
-@pytest.mark.parametrize("rows,k", [(64, 256), (333, 4096), (130, 3840), (96, 8192), (40, 12288)])
+@pytest.mark.parametrize("rows,k", [(64, 256), (333, 4096), (130, 3840), (70, 5120), (96, 8192), (40, 12288)])
 @pytest.mark.parametrize("act", [zd.SILU, zd.GELU], ids=["silu", "gelu"])
 def test_gate_up_matches_oracle(dev, qt, rows, k, act):
     if k % synth.BLOCK_ELEMS[qt]:
@@ -196,7 +196,8 @@ def _dev_vec(dev, a):
 
 
 @pytest.mark.parametrize("qt", TYPES, ids=lambda t: NAMES[t])
-@pytest.mark.parametrize("rows,k", [(256, 4096), (100, 3840), (64, 2048), (5000, 4096), (4133, 12288), (77, 11264)])
+@pytest.mark.parametrize("rows,k", [(256, 4096), (100, 3840), (64, 2048), (5000, 4096), (4133, 12288), (77, 11264),
+                                    (72, 5120), (40, 8192)])
 def test_device_forms_match_oracle(dev, qt, rows, k):
     """norm / resid / normpair forms on device buffers (the decode step's ops);
     the larger shapes give the prefetching instances several row tiles per

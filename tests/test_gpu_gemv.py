@@ -134,8 +134,10 @@ def test_async_burst_batch_agree(dev):
 
 
 @pytest.mark.parametrize("qt,k", [(synth.Q8_0, 4096), (synth.Q4_K, 3840), (synth.F16, 1024), (synth.Q4_1, 12288),
-                                  (synth.Q8_0, 12288), (synth.Q4_0, 12288)],
-                         ids=["q8_0", "q4_k", "f16", "q4_1", "q8_0_split", "q4_0_split"])
+                                  (synth.Q8_0, 12288), (synth.Q4_0, 12288), (synth.Q4_1, 5120), (synth.Q6_K, 5120),
+                                  (synth.Q4_0, 8192), (synth.Q8_0, 14336)],
+                         ids=["q8_0", "q4_k", "f16", "q4_1", "q8_0_split", "q4_0_split", "q4_1_g8k", "q6_k_g8k",
+                              "q4_0_split_mid", "q8_0_split_long"])
 def test_batch_one_launch_matches_single_ops(dev, qt, k):
     """A same-quant batch runs as one launch of the batch kernel (op by op
     where the single op sums in another order: split-K at k = 12288 for

@@ -2039,6 +2039,19 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     ZLM_GEMVX(zlm_gemv_##QN##_normpair_##SFX, QT, KCAP, 2, STEPS, EXACT, PRO_NORM, EPI_PAIR)        \
     ZLM_GEMVX(zlm_gemv_##QN##_resid_##SFX, QT, KCAP, 1, STEPS, EXACT, PRO_PLAIN, EPI_RESID)
 
+// Rows of 3-4 chunk steps (4097-8192 elements) for the 32-element-chunk
+// quants: the generic loop (two chunk steps per group) over an 8192-element x
+// tile, zlm_gemv_<quant>_{r1,pair,norm,normpair,resid}_g8k.  The exact-steps
+// instances there hold every step's loads at once (159-264 VGPRs, one to
+// three waves per SIMD); these take 62-118.  The host takes them where they
+// measured faster.
+#define ZLM_GEMV_G8K(QN, QT)                                                                  \
+    ZLM_GEMVX(zlm_gemv_##QN##_r1_g8k, QT, 8192, 1, 2, false, PRO_PLAIN, EPI_PLAIN)            \
+    ZLM_GEMVX(zlm_gemv_##QN##_pair_g8k, QT, 8192, 2, 2, false, PRO_PLAIN, EPI_PAIR)           \
+    ZLM_GEMVX(zlm_gemv_##QN##_norm_g8k, QT, 8192, 1, 2, false, PRO_NORM, EPI_PLAIN)           \
+    ZLM_GEMVX(zlm_gemv_##QN##_normpair_g8k, QT, 8192, 2, 2, false, PRO_NORM, EPI_PAIR)        \
+    ZLM_GEMVX(zlm_gemv_##QN##_resid_g8k, QT, 8192, 1, 2, false, PRO_PLAIN, EPI_RESID)
+
 // The gate_up pair form with two and four output rows per wave tile
 // (zlm_gemv_<quant>_pair_<SFX>_r2 / _r4: RT 4 and 8, gate rows then up rows):
 // the row tiles the contract's GpuVariant codes select for the fused gate_up

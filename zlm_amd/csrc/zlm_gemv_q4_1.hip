@@ -14,3 +14,7 @@ ZLM_GEMV_TOK2(q4_1, Q4_1, 2)
 
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q4_1, Q4_1, 2)
+
+// Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
+// x tile, where the host takes it (measured faster than the exact-steps forms)
+ZLM_GEMV_G8K(q4_1, Q4_1)

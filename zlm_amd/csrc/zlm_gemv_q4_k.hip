@@ -39,3 +39,7 @@ ZLM_GEMV_TOK2(q4_k, Q4_K, 2)
 
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q4_k, Q4_K, 2)
+
+// Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
+// x tile, where the host takes it (measured faster than the exact-steps forms)
+ZLM_GEMV_G8K(q4_k, Q4_K)

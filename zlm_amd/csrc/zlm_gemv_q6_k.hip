@@ -36,3 +36,7 @@ ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s3_sk2, Q6_K, 3, 2, 1, EPI_PLAIN, false, 2, false,
 ZLM_GEMV_SKP(zlm_gemv_q6_k_r1_s4_sk2, Q6_K, 4, 2, 1, EPI_PLAIN, false, 2, false, 16)
 
 ZLM_GEMV_MULTI_Q4(q6_k, Q6_K)
+
+// Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
+// x tile, where the host takes it (measured faster than the exact-steps forms)
+ZLM_GEMV_G8K(q6_k, Q6_K)

@@ -731,6 +731,33 @@ uint64_t pick_key(const QuantInfo* qi, size_t k, PickKind kind, int param, size_
 
 const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows);
 
+// Whether a launch of `form` over rows of 3-4 chunk steps (4097-8192
+// elements, the 32-element-chunk quants) takes the generic two-step
+// instance over an 8192-element x tile (zlm_gemv_<quant>_<form>_g8k) instead
+// of the exact-steps one.  Measured on gfx950 (alternating runs, graph
+// replays, k 5120-8192, weights rotated past the Infinity Cache):
+// - norm and resid: faster for q4_0 / q4_1 / q4_k / q6_k (e.g. q4_k resid
+//   8192 x 8192 18.2 -> 15.5 us);
+// - pair and normpair: q4_1 and q6_k (q6_k 32768 x 8192 gate_up 117 -> 88
+//   us), q4_0 at 3 steps only (20480 x 5120 59 -> 35 us; 1-4% slower at 4),
+//   not q4_k (equal at 3 steps, 2% slower at 4);
+// - plain (rows the split-K instances do not take): q4_1, and q6_k at 3
+//   steps (q4_1 14336 x 8192 21.8 -> 18.0 us, q6_k 152064 x 5120 190 -> 161
+//   us); q6_k at 4 steps was faster at 14336 rows but slower from 28672, and
+//   q4_0 / q4_k from 65536 rows slower.
+// Launches of 65536 rows and more keep the exact-steps instances for the
+// fused forms (not measured there).
+bool use_g8k(const QuantInfo* qi, uint32_t form, int steps, size_t rows) {
+    if (steps != 3 && steps != 4) return false;
+    const uint32_t t = qi->type;
+    if (t != ZLM_GGML_Q4_0 && t != ZLM_GGML_Q4_1 && t != ZLM_GGML_Q4_K && t != ZLM_GGML_Q6_K) return false;
+    if (form == ZLM_FORM_PLAIN)
+        return (t == ZLM_GGML_Q4_1 && rows < 65536) || (t == ZLM_GGML_Q6_K && steps == 3);
+    if (rows >= 65536) return false;
+    if (form == ZLM_FORM_NORM || form == ZLM_FORM_RESID) return true;
+    return t == ZLM_GGML_Q4_1 || t == ZLM_GGML_Q6_K || (t == ZLM_GGML_Q4_0 && steps == 3);
+}
+
 const GemvKernel* pick_gemv(zlm_device* d, const QuantInfo* qi, size_t k, int rt, size_t rows) {
     const uint64_t key = pick_key(qi, k, kPickPlain, rt, rows);
     auto it = d->picks.find(key);
@@ -747,6 +774,10 @@ const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, 
     char nm[96];
     if (rt == 1) {
         if (const GemvKernel* g = find_split(d, qi, k, "r1", rows)) return g;
+        if (use_g8k(qi, ZLM_FORM_PLAIN, steps, rows)) {
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_r1_g8k", qn);
+            if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 1, steps, 0, true)) return g;
+        }
         for (const PfSuffix& v : kPfSuffixes) {
             if (rows < v.min_rows) continue;
             snprintf(nm, sizeof nm, "zlm_gemv_%s_r%d_s%d%s", qn, v.rt, steps, v.suffix);
@@ -1041,6 +1072,10 @@ const GemvKernel* pick_gemvx_named(zlm_device* d, const QuantInfo* qi, size_t k,
             snprintf(nm, sizeof nm, "zlm_gemv_%s_resid_s%d_r2", qn, steps);
             if (const GemvKernel* g = find_gemv(d, qi->slot, nm, 2, steps)) return g;
         }
+    }
+    if (use_g8k(qi, form, steps, rows)) {
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_%s_g8k", qn, kFormNames[form]);
+        if (const GemvKernel* g = find_gemv(d, qi->slot, nm, rt, steps, 0, true)) return g;
     }
     for (const PfSuffix& v : kPfSuffixes) {
         if (rows < v.min_rows) continue;
