@@ -255,6 +255,7 @@ def test_quantizer_bit_exact(dev):
 CONFIG_SHAPES = [
     ("c0_q4_0", synth.Q4_0, 4096, 4096),
     ("tall_q6_k", synth.Q6_K, 65536 + 37, 3840),  # the lm_head kernels (from 65536 rows)
+    ("tall_q6_k_5120", synth.Q6_K, 65536 + 37, 5120),  # the two-row 3-step lm_head instance
     ("tall_q8_0", synth.Q8_0, 65536 + 37, 4096),
     ("c1_gate_q8_0", synth.Q8_0, 12288, 4096),
     ("c1_down_q8_0", synth.Q8_0, 4096, 12288),
@@ -277,3 +278,32 @@ def test_benchmark_shapes_match_oracle(dev, name, qt, rows, k):
     assert dev.mat_vec_resident(res, zd.quant(qt), rows, k, x, out), dev.last_error()
     assert rel_l2(out, want) <= REL_L2
     dev.free_resident(res)
+
+
+@pytest.mark.parametrize("rows,k,block", [(65536 + 37, 3840, 512), (65536 + 37, 5120, 512), (65535, 5120, 256)])
+def test_tall_q6_k_route(dev, rows, k, block):
+    """Q6_K GEMVs of 65536 rows and more at 2-3 chunk steps take the two-row
+    prefetching lm_head instances (8-wave workgroups); one row fewer keeps the
+    4-wave generic instance."""
+    _say(f"tall q6_k route {rows}x{k}")
+    w = synth.weights(synth.Q6_K, rows, k, seed=0x5A4C4D50 + k)
+    res = dev.upload_resident(w)
+    xs = synth.activation(0x5A4C4D51, k)
+    x = dev.dev_malloc(xs.nbytes)
+    y = dev.dev_malloc(rows * 4)
+    try:
+        dev.dev_upload(x, xs)
+        assert dev.mat_vec_enqueue(res, zd.quant(synth.Q6_K), rows, k, x, y), dev.last_error()
+        dev.sync()
+        assert dev.launch_log(True)
+        try:
+            assert dev.mat_vec_enqueue(res, zd.quant(synth.Q6_K), rows, k, x, y), dev.last_error()
+            dev.sync()
+            log = dev.launch_log_read()
+        finally:
+            dev.launch_log(False)
+        assert [(r["what"], r["block"]) for r in log] == [("gemv", block)]
+    finally:
+        dev.dev_free(x)
+        dev.dev_free(y)
+        dev.free_resident(res)

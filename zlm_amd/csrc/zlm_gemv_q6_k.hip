@@ -17,7 +17,13 @@ ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r1_s2_pfqw16, Q6_K, 4096, 16, 1, 2, PRO_PLAIN, EPI_P
 // 8-wave workgroups at 16 waves per CU, two rows per wave tile; measured on
 // gfx950 at 262144 x 3840: 190.7 -> 156.5 us against the 4-wave exact-steps
 // instance, 147.7 us on the ql + record layout, 140.8 us with two-row tiles.
+// The same at 3 steps (k 4097-6144; 235 VGPRs, two waves per SIMD, so one
+// resident 8-wave workgroup per CU): 152064 x 5120 161 -> 134 us against the
+// generic two-step instance, 65536 x 5120 81 -> 71 us; at 4 steps the
+// one-row form measured slower than the exact-steps instance (190 against
+// 183 us at 152064 x 8192) and is not built.
 ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r2_s2_tallq, Q6_K, 4096, 8, 2, 2, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q6_k_r2_s3_tallq, Q6_K, 8192, 8, 2, 3, PRO_PLAIN, EPI_PLAIN, false)
 
 // Split-K form for 7 < chunks/64 <= 8 (the C3 down projection 3840 x 15360):
 // 8-wave workgroups, one per CU, two rows per tile; measured on gfx950 19.5 ->

@@ -741,19 +741,19 @@ const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, 
 // - pair and normpair: q4_1 and q6_k (q6_k 32768 x 8192 gate_up 117 -> 88
 //   us), q4_0 at 3 steps only (20480 x 5120 59 -> 35 us; 1-4% slower at 4),
 //   not q4_k (equal at 3 steps, 2% slower at 4);
-// - plain (rows the split-K instances do not take): q4_1, and q6_k at 3
-//   steps (q4_1 14336 x 8192 21.8 -> 18.0 us, q6_k 152064 x 5120 190 -> 161
-//   us); q6_k at 4 steps was faster at 14336 rows but slower from 28672, and
-//   q4_0 / q4_k from 65536 rows slower.
-// Launches of 65536 rows and more keep the exact-steps instances for the
-// fused forms (not measured there).
+// - plain (rows the split-K instances do not take), below 65536 rows: q4_1,
+//   and q6_k at 3 steps (q4_1 14336 x 8192 21.8 -> 18.0 us); q6_k at 4 steps
+//   was faster at 14336 rows but slower from 28672.
+// Launches of 65536 rows and more keep the other instances: q6_k's two-row
+// prefetching lm_head instance at 3 steps (152064 x 5120 190 us exact-steps,
+// 161 us g8k, 134 us _r2_s3_tallq), the exact-steps ones otherwise (q4_0 /
+// q4_k plain slower with g8k there; the fused forms not measured).
 bool use_g8k(const QuantInfo* qi, uint32_t form, int steps, size_t rows) {
     if (steps != 3 && steps != 4) return false;
     const uint32_t t = qi->type;
     if (t != ZLM_GGML_Q4_0 && t != ZLM_GGML_Q4_1 && t != ZLM_GGML_Q4_K && t != ZLM_GGML_Q6_K) return false;
-    if (form == ZLM_FORM_PLAIN)
-        return (t == ZLM_GGML_Q4_1 && rows < 65536) || (t == ZLM_GGML_Q6_K && steps == 3);
     if (rows >= 65536) return false;
+    if (form == ZLM_FORM_PLAIN) return t == ZLM_GGML_Q4_1 || (t == ZLM_GGML_Q6_K && steps == 3);
     if (form == ZLM_FORM_NORM || form == ZLM_FORM_RESID) return true;
     return t == ZLM_GGML_Q4_1 || t == ZLM_GGML_Q6_K || (t == ZLM_GGML_Q4_0 && steps == 3);
 }
