@@ -188,6 +188,52 @@ def test_gemm_past_one_token_tile(dev, qt, zq, route, rows, k, m):
         dev.free_resident(res)
 
 
+# The split tiled GEMMs' block ranges on rows of few or odd 32-element block
+# counts (a group's range is an even number of blocks, the last one short or
+# empty): nb = 7 over four groups is 2 + 2 + 2 + 1, nb = 3 is 2 + 1 + 0 + 0,
+# nb = 9 over two groups (two workgroups per CU) 6 + 3; q4_k rows are whole
+# 256-element super-blocks, so it runs nb = 8 only (4 + 4 over two groups).
+# (case, rows, k, m, what the host picks for q4_0 / q8_0 and for q4_1 /
+# q4_k.)
+SPLIT_RANGES = [("nb7", 4096 + 17, 224, 384, "gemm k4", "gemm k2"),
+                ("nb3", 4096 + 17, 96, 384, "gemm k4", "gemm k2"),
+                ("nb9", 12288 + 40, 288, 256, "gemm k2", "gemm"),
+                ("nb8", 4096 + 17, 256, 384, "gemm k4", "gemm k2")]
+
+
+SPLIT_RANGE_CASES = [(qt, zq) + c for c in SPLIT_RANGES for qt, zq in GEMM_QUANTS
+                     if c[2] % synth.BLOCK_ELEMS[qt] == 0]
+GEMM_QUANT_IDS = {synth.Q4_0: "q4_0", synth.Q8_0: "q8_0", synth.Q4_1: "q4_1", synth.Q4_K: "q4_k"}
+
+
+@pytest.mark.parametrize("qt,zq,case,rows,k,m,plain_what,min_what", SPLIT_RANGE_CASES,
+                         ids=[f"{c[2]}-{GEMM_QUANT_IDS[c[0]]}" for c in SPLIT_RANGE_CASES])
+def test_gemm_split_block_ranges(dev, qt, zq, case, rows, k, m, plain_what, min_what):
+    _say(f"gemm split block ranges type={qt} case={case} rows={rows} k={k} m={m}")
+    rb = synth.row_bytes(qt, k)
+    w = synth.weights(qt, rows, k, seed=rows + k + m)
+    xs = synth.activation(k + m, m * k)
+    res = dev.upload_resident(w)
+    x_dev = dev.dev_malloc(xs.nbytes)
+    out_dev = dev.dev_malloc(m * rows * 4)
+    try:
+        dev.dev_upload(x_dev, xs)
+        log = _route(dev, res, zq, rows, k, m, x_dev, out_dev)
+        gemm = [r for r in log if r["what"].startswith("gemm")]
+        want_what = plain_what if zq in (zd.Q4_0, zd.Q8_0) else min_what
+        assert [r["what"] for r in gemm] == [want_what]
+        out = np.zeros(m * rows, np.float32)
+        dev.dev_download(out, out_dev)
+        got = out.reshape(m, rows)
+        for r0, r1 in ((0, 64), (rows // 2, rows // 2 + 32), (rows - 48, rows)):
+            want = oracle.matmul_int(qt, w[r0 * rb:r1 * rb], k, r1 - r0, m, xs)
+            assert rel_l2(got[:, r0:r1], want) <= 1e-5, (r0, r1)
+    finally:
+        dev.dev_free(x_dev)
+        dev.dev_free(out_dev)
+        dev.free_resident(res)
+
+
 def test_gemm_config4_rows_subset(dev):
     """configs[4] at full size (12288 x 4096 Q4_0 x 512 tokens); rows checked
     against the oracle on a slice of the weight (a GEMM row depends only on its
