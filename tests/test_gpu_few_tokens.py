@@ -4,13 +4,15 @@ m = 2 (the fp path):
 
 Two tokens run zlm's fp path (the oracle's matMulRows, form/single.zig:213-292:
 the batched q4_0 / q8_0 forms, per-token production GEMVs for q4_1 / q4_k),
-relative L2 <= 1e-3.  The device's two-token GEMV (zlm_gemv_<quant>_tok2_g<T>)
-loads every weight fragment once and sums it against both tokens' x tiles;
-k beyond its 16384-float tier runs one GEMV per token.  Checked here:
+relative L2 <= 1e-3.  The device's two-token GEMV (zlm_gemv_<quant>_tok2_g<T>,
+two-row wave tiles at the 4096- and 8192-float tiers, four rows for q4_k at
+4096) loads every weight fragment once and sums it against both tokens' x
+tiles; k beyond its 16384-float tier runs one GEMV per token.  Checked here:
 
 * every tier (k <= 4096, 8192, 16384), a k that ends inside a step group
-  (k = 256 and the q4_k k = 3840), ragged row counts, and k = 20480 past the
-  last tier, for the four matMul quants, resident and streamed;
+  (k = 256 and the q4_k k = 3840), row counts that end inside a wave tile
+  (odd, and 65573 rows: many tiles per wave), and k = 20480 past the last
+  tier, for the four matMul quants, resident and streamed;
 * the route: the launch log shows one two-token launch up to k = 16384 and two
   GEMV launches past it;
 * each token's row equals the one-token product to fp32 rounding (the same
@@ -19,7 +21,8 @@ k beyond its 16384-float tier runs one GEMV per token.  Checked here:
 m = 3, 4 (zlm's int path: q8 activations, exact integer block dots,
 kernels/quantized.zig:49-55, :79-87, :111-123, :149-156 over the quantizer of
 matvec/layout.zig:458-476): the int-path token GEMV (zlm_gemv_<quant>_q8tok4_
-g<T>) quantizes the activations in its own prologue.  Against the oracle's int
+g<T>, two-row tiles for the nibble quants from 32768 rows) quantizes the
+activations in its own prologue.  Against the oracle's int
 path (orc_matmul_int) at relative L2 <= 1e-5, which one activation off by one
 quantization unit would exceed, with activations that stress the quantizer
 (a zero block, a block with one nonzero, values near rounding ties and a
@@ -42,7 +45,8 @@ pytestmark = pytest.mark.gpu
 
 QUANTS = [(synth.Q4_0, zd.Q4_0), (synth.Q8_0, zd.Q8_0), (synth.Q4_1, zd.Q4_1), (synth.Q4_K, zd.Q4_K)]
 IDS = ["q4_0", "q8_0", "q4_1", "q4_k"]
-SHAPES = [(1, 256), (67, 3840), (4097, 4096), (300, 8192), (129, 12288), (64, 16384), (33, 20480)]
+SHAPES = [(1, 256), (67, 3840), (4097, 4096), (301, 6144), (300, 8192), (129, 12288), (64, 16384), (33, 20480),
+          (65536 + 37, 3840)]
 
 
 def _say(msg):
@@ -105,7 +109,9 @@ def test_two_token_route(dev, k, launches):
         dev.free_resident(res)
 
 
-INT_SHAPES = [(1, 256), (67, 3840), (4097, 4096), (300, 8192), (129, 12288)]
+# (32768 + 37, 1024) and (32768 + 1, 5120): the two-row tiles of the nibble
+# quants (from 32768 rows), ending inside a tile, at both x tiers
+INT_SHAPES = [(1, 256), (67, 3840), (4097, 4096), (300, 8192), (129, 12288), (32768 + 37, 1024), (32768 + 1, 5120)]
 
 
 def _stress_x(m, k, seed):

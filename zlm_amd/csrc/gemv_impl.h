@@ -1270,71 +1270,108 @@ __device__ __forceinline__ int dot16(const uint32_t (&w)[4], uint4 q, int acc) {
     return __builtin_amdgcn_sdot4(static_cast<int>(w[3]), static_cast<int>(q.w), acc, false);
 }
 
-// Chunk c of one weight row against NTOK token tiles (tile t at tq + t *
-// kWords): acc[t] += the chunk's share of row . x_t in the int path's form:
+// Chunk c of RT weight rows against NTOK token tiles (tile t at tq + t *
+// kWords): acc[t * RT + r] += the chunk's share of row r . x_t in the int
+// path's form:
 //   q4_0  (dw*dx) * (sum nib*q - 8 * sum q)             (block c)
 //   q4_1  (d*dx) * sum nib*q + (m*dx) * sum q          (block c)
 //   q8_0  (dw*dx) * sum w*q                            (half c&1 of block c>>1)
 //   q4_k  per sub-block half: (d*sc*dx) * sum nib*q - (dmin*mn*dx) * sum q
 //         (the lows of the chunk's 16 qs bytes: sub-block 2g, the highs 2g+1)
-// The integer parts are exact; valid = false zeroes the scales.
-template <int QT, int KCAP, int NTOK>
-__device__ __forceinline__ void compute_int(const Frag<QT, 1>& f, const uint32_t* tq, int c, bool valid,
+// A token's LDS words are read once for all RT rows.  The integer parts are
+// exact; valid = false zeroes the scales.
+template <int QT, int KCAP, int NTOK, int RT>
+__device__ __forceinline__ void compute_int(const Frag<QT, RT>& f, const uint32_t* tq, int c, bool valid,
                                             float* acc) {
     using T = Q8Tile<KCAP>;
-    const uint32_t w[4] = {f.q[0].x, f.q[0].y, f.q[0].z, f.q[0].w};
+    uint32_t w[RT][4];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        w[r][0] = f.q[r].x;
+        w[r][1] = f.q[r].y;
+        w[r][2] = f.q[r].z;
+        w[r][3] = f.q[r].w;
+    }
     if constexpr (QT == Q8_0) {
-        const float dw = valid ? h2f(f.d[0]) : 0.0f;
+        float dw[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++) dw[r] = valid ? h2f(f.d[r]) : 0.0f;
 #pragma unroll
         for (int t = 0; t < NTOK; t++) {
             const uint32_t* tt = tq + t * T::kWords;
-            const int dot = dot16(w, *reinterpret_cast<const uint4*>(tt + 4 * c), 0);
+            const uint4 q = *reinterpret_cast<const uint4*>(tt + 4 * c);
             const float dx = __builtin_bit_cast(float, tt[T::kDx + (c >> 1)]);
-            acc[t] = fmaf(dw * dx, static_cast<float>(dot), acc[t]);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const int dot = dot16(w[r], q, 0);
+                acc[t * RT + r] = fmaf(dw[r] * dx, static_cast<float>(dot), acc[t * RT + r]);
+            }
         }
     } else {
-        uint32_t lo[4], hi[4];
+        uint32_t lo[RT][4], hi[RT][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            lo[i] = w[i] & 0x0F0F0F0Fu;
-            hi[i] = (w[i] >> 4) & 0x0F0F0F0Fu;
+        for (int r = 0; r < RT; r++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                lo[r][i] = w[r][i] & 0x0F0F0F0Fu;
+                hi[r][i] = (w[r][i] >> 4) & 0x0F0F0F0Fu;
+            }
         }
         if constexpr (QT == Q4_K) {
-            const uint32_t dd = valid ? f.dm[0] : 0u;
-            const float d = h2f(dd), dmin = h2f(dd >> 16);
-            const float sc1 = ub(f.sm[0], 0), sc2 = ub(f.sm[0], 1), mn1 = ub(f.sm[0], 2), mn2 = ub(f.sm[0], 3);
+            float d[RT], dmin[RT], sc1[RT], sc2[RT], mn1[RT], mn2[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const uint32_t dd = valid ? f.dm[r] : 0u;
+                d[r] = h2f(dd);
+                dmin[r] = h2f(dd >> 16);
+                sc1[r] = ub(f.sm[r], 0);
+                sc2[r] = ub(f.sm[r], 1);
+                mn1[r] = ub(f.sm[r], 2);
+                mn2[r] = ub(f.sm[r], 3);
+            }
             const int sb = c >> 3, p = c & 7, g = p >> 1;
             const int run_lo = 16 * sb + 4 * g + (p & 1), blk_lo = 8 * sb + 2 * g;
 #pragma unroll
             for (int t = 0; t < NTOK; t++) {
                 const uint32_t* tt = tq + t * T::kWords;
-                const int dlo = dot16(lo, *reinterpret_cast<const uint4*>(tt + 4 * c), 0);
-                const int dhi = dot16(hi, *reinterpret_cast<const uint4*>(tt + KCAP / 8 + 4 * c), 0);
+                const uint4 qlo = *reinterpret_cast<const uint4*>(tt + 4 * c);
+                const uint4 qhi = *reinterpret_cast<const uint4*>(tt + KCAP / 8 + 4 * c);
                 const float slo = static_cast<float>(static_cast<int32_t>(tt[T::kRuns + run_lo]));
                 const float shi = static_cast<float>(static_cast<int32_t>(tt[T::kRuns + run_lo + 2]));
                 const float xlo = __builtin_bit_cast(float, tt[T::kDx + blk_lo]);
                 const float xhi = __builtin_bit_cast(float, tt[T::kDx + blk_lo + 1]);
-                float v = (d * sc1 * xlo) * static_cast<float>(dlo);
-                v = fmaf(d * sc2 * xhi, static_cast<float>(dhi), v);
-                v = fmaf(-(dmin * mn1 * xlo), slo, v);
-                v = fmaf(-(dmin * mn2 * xhi), shi, v);
-                acc[t] += v;
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    const int dlo = dot16(lo[r], qlo, 0);
+                    const int dhi = dot16(hi[r], qhi, 0);
+                    float v = (d[r] * sc1[r] * xlo) * static_cast<float>(dlo);
+                    v = fmaf(d[r] * sc2[r] * xhi, static_cast<float>(dhi), v);
+                    v = fmaf(-(dmin[r] * mn1[r] * xlo), slo, v);
+                    v = fmaf(-(dmin[r] * mn2[r] * xhi), shi, v);
+                    acc[t * RT + r] += v;
+                }
             }
         } else {
 #pragma unroll
             for (int t = 0; t < NTOK; t++) {
                 const uint32_t* tt = tq + t * T::kWords;
-                int dot = dot16(lo, *reinterpret_cast<const uint4*>(tt + 4 * c), 0);
-                dot = dot16(hi, *reinterpret_cast<const uint4*>(tt + KCAP / 8 + 4 * c), dot);
+                const uint4 qlo = *reinterpret_cast<const uint4*>(tt + 4 * c);
+                const uint4 qhi = *reinterpret_cast<const uint4*>(tt + KCAP / 8 + 4 * c);
                 const int sq = static_cast<int32_t>(tt[T::kRuns + 2 * c]) + static_cast<int32_t>(tt[T::kRuns + 2 * c + 1]);
                 const float dx = __builtin_bit_cast(float, tt[T::kDx + c]);
-                if constexpr (QT == Q4_0) {
-                    const float dw = valid ? h2f(f.d[0]) : 0.0f;
-                    acc[t] = fmaf(dw * dx, static_cast<float>(dot - 8 * sq), acc[t]);
-                } else {
-                    const uint32_t dm = valid ? f.dm[0] : 0u;
-                    acc[t] = fmaf(h2f(dm) * dx, static_cast<float>(dot), acc[t]);
-                    acc[t] = fmaf(h2f(dm >> 16) * dx, static_cast<float>(sq), acc[t]);
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    int dot = dot16(lo[r], qlo, 0);
+                    dot = dot16(hi[r], qhi, dot);
+                    float& a = acc[t * RT + r];
+                    if constexpr (QT == Q4_0) {
+                        const float dw = valid ? h2f(f.d[r]) : 0.0f;
+                        a = fmaf(dw * dx, static_cast<float>(dot - 8 * sq), a);
+                    } else {
+                        const uint32_t dm = valid ? f.dm[r] : 0u;
+                        a = fmaf(h2f(dm) * dx, static_cast<float>(dot), a);
+                        a = fmaf(h2f(dm >> 16) * dx, static_cast<float>(sq), a);
+                    }
                 }
             }
         }
@@ -1343,34 +1380,36 @@ __device__ __forceinline__ void compute_int(const Frag<QT, 1>& f, const uint32_t
 
 // compute_int over a group of STEPS chunk steps, a scheduling barrier after
 // each step.
-template <int QT, int KCAP, int NTOK, int STEPS>
-__device__ __forceinline__ void compute_group_int(const Frag<QT, 1> (&f)[STEPS], const uint32_t* tq, int C, int cb,
+template <int QT, int KCAP, int NTOK, int RT, int STEPS>
+__device__ __forceinline__ void compute_group_int(const Frag<QT, RT> (&f)[STEPS], const uint32_t* tq, int C, int cb,
                                                   int lane, float* acc) {
 #pragma unroll
     for (int s = 0; s < STEPS; s++) {
         const int c = cb + lane + s * kWave;
-        if (cb + s * kWave < C) compute_int<QT, KCAP, NTOK>(f[s], tq, min(c, C - 1), c < C, acc);
+        if (cb + s * kWave < C) compute_int<QT, KCAP, NTOK, RT>(f[s], tq, min(c, C - 1), c < C, acc);
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-// y[t * rows + r] = row r . x_t (int path) for t < m <= NTOK: one-row wave
+// y[t * rows + r] = row r . x_t (int path) for t < m <= NTOK: RT-row wave
 // tiles (tile = blockIdx*WAVES + wid + j*gridDim*WAVES), each row walked in
 // groups of STEPS chunk steps (one memory round trip per group).  The first
 // tile's first group is loaded before the activations are quantized, so the
 // staging overlaps it.  Rows of x past m repeat row m-1 and are not stored.
-template <int QT, int NTOK, int KCAP, int WAVES, int STEPS>
+// Each row's sums and their reduction are the same for any RT.
+template <int QT, int NTOK, int KCAP, int WAVES, int STEPS, int RT = 1>
 __device__ __forceinline__ void gemv_int(const GemvArgs& a) {
     static_assert(QT == Q4_0 || QT == Q4_1 || QT == Q8_0 || QT == Q4_K, "int path quants");
-    static_assert(NTOK >= 2 && NTOK <= 8, "the row reduction holds at most 8 values per lane");
+    static_assert(NTOK >= 2 && NTOK * RT <= 8, "the row reduction holds at most 8 values per lane");
     using T = Q8Tile<KCAP>;
     __shared__ __attribute__((aligned(16))) uint32_t tq[T::kWords * NTOK];
     constexpr int NX = (KCAP / 4 + WAVES * kWave - 1) / (WAVES * kWave);
     constexpr int GROUP = STEPS * kWave;
+    constexpr int NV = NTOK * RT;
     const int lane = threadIdx.x & (kWave - 1);
     const uint32_t wid = threadIdx.x / kWave;
     const int C = chunks_per_row<QT>(a.nb);
-    const uint32_t ntiles = a.rows;
+    const uint32_t ntiles = (a.rows + RT - 1) / RT;
     const uint32_t tstride = gridDim.x * WAVES;
     uint32_t tile = blockIdx.x * WAVES + wid;
     const int k = static_cast<int>(a.nb) * elems_per_block<QT>();
@@ -1378,31 +1417,31 @@ __device__ __forceinline__ void gemv_int(const GemvArgs& a) {
     XRegs<NX> xr[NTOK];
 #pragma unroll
     for (int t = 0; t < NTOK; t++) xload(a.x + static_cast<size_t>(min(static_cast<uint32_t>(t), a.m - 1)) * k, k, xr[t]);
-    Frag<QT, 1> f[STEPS];
-    TileRows<1> tr = tile_rows<1, false>(a, min(tile, ntiles - 1));
-    load_group<QT, 1, STEPS, false, true>(f, tr, a.nb, C, 0, lane);
+    Frag<QT, RT> f[STEPS];
+    TileRows<RT> tr = tile_rows<RT, false>(a, min(tile, ntiles - 1));
+    load_group<QT, RT, STEPS, false, true>(f, tr, a.nb, C, 0, lane);
 #pragma unroll
     for (int t = 0; t < NTOK; t++) q8_store<QT, KCAP, NX>(xr[t], k, tq + t * T::kWords);
     __syncthreads();
 
-    float acc[NTOK];
+    float acc[NV];
 #pragma unroll
-    for (int t = 0; t < NTOK; t++) acc[t] = 0.0f;
-    compute_group_int<QT, KCAP, NTOK, STEPS>(f, tq, C, 0, lane, acc);
+    for (int i = 0; i < NV; i++) acc[i] = 0.0f;
+    compute_group_int<QT, KCAP, NTOK, RT, STEPS>(f, tq, C, 0, lane, acc);
     for (int cb = GROUP; cb < C; cb += GROUP) {
-        load_group<QT, 1, STEPS, false, true>(f, tr, a.nb, C, cb, lane);
-        compute_group_int<QT, KCAP, NTOK, STEPS>(f, tq, C, cb, lane, acc);
+        load_group<QT, RT, STEPS, false, true>(f, tr, a.nb, C, cb, lane);
+        compute_group_int<QT, KCAP, NTOK, RT, STEPS>(f, tq, C, cb, lane, acc);
     }
-    if (tile < ntiles) reduce_store<NTOK, EPI_TOK, NTOK>(acc, a, tile, 1.0f, lane);
+    if (tile < ntiles) reduce_store<NV, EPI_TOK, NTOK>(acc, a, tile, 1.0f, lane);
     for (tile += tstride; tile < ntiles; tile += tstride) {
-        tr = tile_rows<1, false>(a, tile);
+        tr = tile_rows<RT, false>(a, tile);
 #pragma unroll
-        for (int t = 0; t < NTOK; t++) acc[t] = 0.0f;
+        for (int i = 0; i < NV; i++) acc[i] = 0.0f;
         for (int cb = 0; cb < C; cb += GROUP) {
-            load_group<QT, 1, STEPS, false, true>(f, tr, a.nb, C, cb, lane);
-            compute_group_int<QT, KCAP, NTOK, STEPS>(f, tq, C, cb, lane, acc);
+            load_group<QT, RT, STEPS, false, true>(f, tr, a.nb, C, cb, lane);
+            compute_group_int<QT, KCAP, NTOK, RT, STEPS>(f, tq, C, cb, lane, acc);
         }
-        reduce_store<NTOK, EPI_TOK, NTOK>(acc, a, tile, 1.0f, lane);
+        reduce_store<NV, EPI_TOK, NTOK>(acc, a, tile, 1.0f, lane);
     }
 }
 
@@ -1967,15 +2006,18 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
     }
 
 // Two-token instances zlm_gemv_<quant>_tok2_g<T> (T = 4, 8, 16: k <= 1024*T):
-// matMul at m = 2, one pass over the weights for both tokens, one-row tiles,
+// matMul at m = 2, one pass over the weights for both tokens, one-row tiles
+// (ZLM_GEMVTR, zlm_gemv_<quant>_tok2_g<T>_r<RT>: RT-row tiles, whose lanes
+// read each x value once for RT rows),
 // fp32 x, the row walked in groups of STEPS chunk steps (the generic loop;
 // exact-step forms that issue a whole row's loads at once took 170-450 VGPRs
 // with two tokens).  Both x rows fill twice the single-token LDS tile (39 KB
 // at the 4096-float tier, 78 KB at 8192, 156 KB at 16384), so the workgroup
 // grows with the tier (4, 8, 16 waves) to keep 16 waves per CU.
-#define ZLM_GEMVT(NAME, QT, KCAP, WAVES, STEPS)                                   \
+#define ZLM_GEMVT(NAME, QT, KCAP, WAVES, STEPS) ZLM_GEMVTR(NAME, QT, KCAP, WAVES, 1, STEPS)
+#define ZLM_GEMVTR(NAME, QT, KCAP, WAVES, RT, STEPS)                              \
     extern "C" __global__ void __launch_bounds__(WAVES * 64) NAME(GemvArgs a) {   \
-        gemv<QT, KCAP, WAVES, 1, STEPS, false, true, PRO_TOK2, EPI_TOK>(a);       \
+        gemv<QT, KCAP, WAVES, RT, STEPS, false, true, PRO_TOK2, EPI_TOK>(a);      \
     }
 // STEPS: 2 for the 32-element chunks of q4_0 / q4_1 / q4_k, 4 for q8_0's 16
 #define ZLM_GEMV_TOK2(QN, QT, STEPS)                                    \
@@ -1989,13 +2031,20 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 // per token.  Eight token slots measured slower than the tiled GEMM on most
 // shapes (quantizing eight rows per workgroup and twice the LDS reads), so
 // from 5 tokens the GEMM runs.
-#define ZLM_GEMVQ(NAME, QT, NTOK, KCAP, STEPS)                                     \
+#define ZLM_GEMVQ(NAME, QT, NTOK, KCAP, STEPS) ZLM_GEMVQR(NAME, QT, NTOK, KCAP, STEPS, 1)
+#define ZLM_GEMVQR(NAME, QT, NTOK, KCAP, STEPS, RT)                                \
     extern "C" __global__ void __launch_bounds__(1024) NAME(GemvArgs a) {          \
-        gemv_int<QT, NTOK, KCAP, 16, STEPS>(a);                                    \
+        gemv_int<QT, NTOK, KCAP, 16, STEPS, RT>(a);                                \
     }
 #define ZLM_GEMV_Q8TOK(QN, QT, STEPS)                                   \
     ZLM_GEMVQ(zlm_gemv_##QN##_q8tok4_g4, QT, 4, 4096, STEPS)            \
     ZLM_GEMVQ(zlm_gemv_##QN##_q8tok4_g8, QT, 4, 8192, STEPS)
+// Two-row tiles (_r2) for launches of 32768 rows and more: each lane reads a
+// token's LDS words once for both rows (the nibble quants; q8_0's two LDS
+// reads per token gain nothing).
+#define ZLM_GEMV_Q8TOK_R2(QN, QT, STEPS)                                \
+    ZLM_GEMVQR(zlm_gemv_##QN##_q8tok4_g4_r2, QT, 4, 4096, STEPS, 2)     \
+    ZLM_GEMVQR(zlm_gemv_##QN##_q8tok4_g8_r2, QT, 4, 8192, STEPS, 2)
 
 // The fused forms take one GemvArgs: zlm_gemv_<quant>_<form>_s<STEPS> (exact
 // steps) and zlm_gemv_<quant>_<form>_g<STEPS> (generic), form one of

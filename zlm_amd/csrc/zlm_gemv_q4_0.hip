@@ -56,9 +56,12 @@ ZLM_GEMV_MULTI_Q4(q4_0, Q4_0)
 
 // matMul at m = 2 (both tokens in one pass over the weights)
 ZLM_GEMV_TOK2(q4_0, Q4_0, 2)
+ZLM_GEMVTR(zlm_gemv_q4_0_tok2_g4_r2, Q4_0, 4096, 4, 2, 2)
+ZLM_GEMVTR(zlm_gemv_q4_0_tok2_g8_r2, Q4_0, 8192, 8, 2, 2)
 
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q4_0, Q4_0, 2)
+ZLM_GEMV_Q8TOK_R2(q4_0, Q4_0, 2)
 
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
 // x tile, where the host takes it (measured faster than the exact-steps forms)

@@ -36,9 +36,13 @@ ZLM_GEMV_MULTI_Q4(q4_k, Q4_K)
 
 // matMul at m = 2 (both tokens in one pass over the weights)
 ZLM_GEMV_TOK2(q4_k, Q4_K, 2)
+ZLM_GEMVTR(zlm_gemv_q4_k_tok2_g4_r2, Q4_K, 4096, 4, 2, 2)
+ZLM_GEMVTR(zlm_gemv_q4_k_tok2_g4_r4, Q4_K, 4096, 4, 4, 2)
+ZLM_GEMVTR(zlm_gemv_q4_k_tok2_g8_r2, Q4_K, 8192, 8, 2, 2)
 
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q4_k, Q4_K, 2)
+ZLM_GEMV_Q8TOK_R2(q4_k, Q4_K, 2)
 
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
 // x tile, where the host takes it (measured faster than the exact-steps forms)

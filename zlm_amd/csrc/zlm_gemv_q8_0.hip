@@ -48,6 +48,8 @@ ZLM_GEMV_MULTI_Q8(q8_0, Q8_0)
 
 // matMul at m = 2 (both tokens in one pass over the weights)
 ZLM_GEMV_TOK2(q8_0, Q8_0, 4)
+ZLM_GEMVTR(zlm_gemv_q8_0_tok2_g4_r2, Q8_0, 4096, 4, 2, 4)
+ZLM_GEMVTR(zlm_gemv_q8_0_tok2_g8_r2, Q8_0, 8192, 8, 2, 4)
 
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q8_0, Q8_0, 4)

@@ -716,15 +716,15 @@ bool resid_two_rows(const QuantInfo* qi, int steps, size_t rows) {
 }
 
 // The pick functions below depend on the shape only through (quant, k, row
-// tile or form, rows >= 65536, rows <= 8192); the device caches their result
-// per class so an op's host path is one hash lookup (the name lookups cost
-// ~1 us per launch, most of a small GEMV's enqueue).
+// tile or form, rows >= 65536, rows >= 32768, rows <= 8192); the device
+// caches their result per class so an op's host path is one hash lookup (the
+// name lookups cost ~1 us per launch, most of a small GEMV's enqueue).
 // The kernel picked per shape class: (k, quant slot, what is picked, its
 // parameter, row-count class) in disjoint bit fields.
 enum PickKind : uint64_t { kPickPlain = 0, kPickForm = 1, kPickPairTile = 2, kPickTok2 = 3, kPickQ8Tok = 4 };
 
 uint64_t pick_key(const QuantInfo* qi, size_t k, PickKind kind, int param, size_t rows) {
-    const uint64_t rows_class = rows >= 65536 ? 2 : rows <= 8192 ? 1 : 0;
+    const uint64_t rows_class = rows >= 65536 ? 2 : rows >= 32768 ? 3 : rows <= 8192 ? 1 : 0;
     return (static_cast<uint64_t>(k) << 24) | (static_cast<uint64_t>(qi->slot) << 16) |
            (static_cast<uint64_t>(kind) << 12) | (static_cast<uint64_t>(param & 0x3ff) << 2) | rows_class;
 }
@@ -796,7 +796,17 @@ const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, 
 // The two-token GEMV for matMul at m = 2: zlm_gemv_<quant>_tok2_g<T>, the
 // smallest tier T in {4, 8, 16} whose x tiles hold k <= 1024*T floats, or
 // null (the quant has none, or k > 16384), and the caller runs one GEMV per
-// token.
+// token.  At the 4096- and 8192-float tiers the wave tile holds two rows
+// (_r2; q4_k at 4096 four, _r4), which halves the x reads from LDS per row;
+// the results are bit for bit those of one-row tiles (the same per-lane sums
+// and reduction tree).  Measured on gfx950 (alternating runs, weights rotated
+// past the Infinity Cache): Q4_K 262144 x 3840 192 -> 163 us (170 with two
+// rows), Q8_0 151936 x 4096 122 -> 109 us, Q4_1 151936 x 4096 106 -> 101 us,
+// Q8_0 12288 x 4096 15.5 -> 13.4 us, Q4_0 4096 x 4096 7.4 -> 6.6 us, Q4_K
+// 4096 x 8192 11.5 -> 10.5 us.  Four rows measured slower at q4_0 / q8_0
+// (Q4_0 4096 x 8192 12.8 against 10.1 us); the 16-wave tier's two-row form
+// (capped at 128 VGPRs) was slower too (Q8_0 4096 x 12288 19.5 against 15.5
+// us), so it keeps one row.
 constexpr size_t kTok2MaxK = 16384;
 
 const GemvKernel* pick_tok2(zlm_device* d, const QuantInfo* qi, size_t k) {
@@ -807,8 +817,15 @@ const GemvKernel* pick_tok2(zlm_device* d, const QuantInfo* qi, size_t k) {
     if (k <= kTok2MaxK) {
         const int tier = k <= 4096 ? 4 : k <= 8192 ? 8 : 16;
         char nm[96];
-        snprintf(nm, sizeof nm, "zlm_gemv_%s_tok2_g%d", kQuantNames[qi->slot], tier);
-        g = find_gemv(d, qi->slot, nm, 1, 0);
+        const int rt = tier == 16 ? 1 : (qi->type == ZLM_GGML_Q4_K && tier == 4) ? 4 : 2;
+        if (rt > 1) {
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_tok2_g%d_r%d", kQuantNames[qi->slot], tier, rt);
+            g = find_gemv(d, qi->slot, nm, rt, 0);
+        }
+        if (!g) {
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_tok2_g%d", kQuantNames[qi->slot], tier);
+            g = find_gemv(d, qi->slot, nm, 1, 0);
+        }
     }
     d->picks.emplace(key, g);
     return g;
@@ -922,7 +939,8 @@ bool enqueue_gemv_tok2(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size
     const uint32_t lds = static_lds(d, gk->fn);
     const uint64_t per_cu = std::max<uint64_t>(1, std::min<uint64_t>(4, kMaxLds / std::max<uint32_t>(lds, 1)));
     const uint64_t waves = static_cast<uint64_t>(gk->threads / 64);
-    const uint64_t wgs = (rows + waves - 1) / waves;
+    const uint64_t tiles = (rows + gk->rt - 1) / gk->rt;
+    const uint64_t wgs = (tiles + waves - 1) / waves;
     const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->cus) * per_cu));
     const uint8_t* w = r->payload;
     const uint16_t* s = r->scales;
@@ -940,19 +958,30 @@ bool enqueue_gemv_tok2(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size
 // the quantizer + small-M GEMM): 4096 x 4096 Q4_0 9.9 -> 7.4 us, Q4_K 13.2 ->
 // 7.7 us, 12288 x 4096 Q8_0 19.4 -> 14.7 us, the 262144 x 3840 Q4_K lm_head
 // 269 -> 194 us; eight token slots were slower than the GEMM on most shapes.
+// From 32768 rows the nibble quants take two-row tiles (_r2; bit for bit the
+// one-row results): Q4_K 262144 x 3840 175 -> 155 us, Q4_0 151936 x 4096 91
+// -> 80 us, Q4_1 the same shape 95 -> 85 us, Q4_0 32768 x 4096 26.7 -> 25.1
+// us.  Below that they idle waves: the grid holds one 16-wave workgroup per
+// CU, so 4096 rows are 2048 two-row tiles for 4096 waves (7.3 -> 8.8 us).
 constexpr size_t kQ8TokM = 4;
 constexpr size_t kQ8TokMaxK = 8192;
 
-const GemvKernel* pick_q8tok(zlm_device* d, const QuantInfo* qi, size_t k) {
+const GemvKernel* pick_q8tok(zlm_device* d, const QuantInfo* qi, size_t k, size_t rows) {
     const int ntok = static_cast<int>(kQ8TokM);
-    const uint64_t key = pick_key(qi, k, kPickQ8Tok, ntok, 0);
+    const uint64_t key = pick_key(qi, k, kPickQ8Tok, ntok, rows);
     auto it = d->picks.find(key);
     if (it != d->picks.end()) return it->second;
     const GemvKernel* g = nullptr;
     if (k <= kQ8TokMaxK) {
         char nm[96];
-        snprintf(nm, sizeof nm, "zlm_gemv_%s_q8tok%d_g%d", kQuantNames[qi->slot], ntok, k <= 4096 ? 4 : 8);
-        g = find_gemv(d, qi->slot, nm, 1, 0);
+        if (rows >= 32768 && qi->type != ZLM_GGML_Q8_0) {
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_q8tok%d_g%d_r2", kQuantNames[qi->slot], ntok, k <= 4096 ? 4 : 8);
+            g = find_gemv(d, qi->slot, nm, 2, 0);
+        }
+        if (!g) {
+            snprintf(nm, sizeof nm, "zlm_gemv_%s_q8tok%d_g%d", kQuantNames[qi->slot], ntok, k <= 4096 ? 4 : 8);
+            g = find_gemv(d, qi->slot, nm, 1, 0);
+        }
     }
     d->picks.emplace(key, g);
     return g;
@@ -965,12 +994,13 @@ bool enqueue_gemv_q8tok(zlm_device* d, zlm_resident* r, const QuantInfo* qi, siz
                         const float* x_dev, float* y_dev, bool* ran) {
     *ran = false;
     if (m < 3 || m > kQ8TokM) return true;
-    const GemvKernel* gk = pick_q8tok(d, qi, k);
+    const GemvKernel* gk = pick_q8tok(d, qi, k, rows);
     if (!gk) return true;
     if (gk->role != kRoleQ8Tok || !gk->struct_args)
         return fail(d, "internal: picked kernel (role %d) is not the int token GEMV", gk->role);
     const uint64_t waves = static_cast<uint64_t>(gk->threads / 64);
-    const uint64_t wgs = (rows + waves - 1) / waves;
+    const uint64_t tiles = (rows + gk->rt - 1) / gk->rt;
+    const uint64_t wgs = (tiles + waves - 1) / waves;
     const unsigned grid = static_cast<unsigned>(std::min<uint64_t>(wgs, static_cast<uint64_t>(d->cus)));
     const uint8_t* w = r->payload;
     const uint16_t* s = r->scales;
