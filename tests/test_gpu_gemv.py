@@ -256,6 +256,20 @@ CONFIG_SHAPES = [
     ("c0_q4_0", synth.Q4_0, 4096, 4096),
     ("tall_q6_k", synth.Q6_K, 65536 + 37, 3840),  # the lm_head kernels (from 65536 rows)
     ("tall_q6_k_5120", synth.Q6_K, 65536 + 37, 5120),  # the two-row 3-step lm_head instance
+    # the other lm_head instances (prefetching 8-wave workgroups from 65536 rows)
+    ("tall_q4_0_4096", synth.Q4_0, 65536 + 37, 4096),
+    ("tall_q4_0_5120", synth.Q4_0, 65536 + 37, 5120),
+    ("tall_q4_0_8192", synth.Q4_0, 65536 + 37, 8192),
+    ("tall_q4_k_4096", synth.Q4_K, 65536 + 37, 4096),
+    ("tall_q4_k_5120", synth.Q4_K, 65536 + 37, 5120),
+    ("tall_q4_k_8192", synth.Q4_K, 65536 + 37, 8192),
+    ("tall_q4_1_4096", synth.Q4_1, 65536 + 37, 4096),
+    ("tall_q4_1_6144", synth.Q4_1, 65536 + 37, 6144),
+    ("tall_q4_1_8192", synth.Q4_1, 65536 + 37, 8192),
+    ("tall_q8_0_5120", synth.Q8_0, 65536 + 37, 5120),
+    ("tall_q8_0_6144", synth.Q8_0, 65536 + 37, 6144),
+    ("tall_q8_0_7168", synth.Q8_0, 65536 + 37, 7168),
+    ("tall_q8_0_8192", synth.Q8_0, 65536 + 37, 8192),
     ("tall_q8_0", synth.Q8_0, 65536 + 37, 4096),
     ("c1_gate_q8_0", synth.Q8_0, 12288, 4096),
     ("c1_down_q8_0", synth.Q8_0, 4096, 12288),
@@ -280,29 +294,37 @@ def test_benchmark_shapes_match_oracle(dev, name, qt, rows, k):
     dev.free_resident(res)
 
 
-@pytest.mark.parametrize("rows,k,block", [(65536 + 37, 3840, 512), (65536 + 37, 5120, 512), (65535, 5120, 256)])
-def test_tall_q6_k_route(dev, rows, k, block):
-    """Q6_K GEMVs of 65536 rows and more at 2-3 chunk steps take the two-row
-    prefetching lm_head instances (8-wave workgroups); one row fewer keeps the
-    4-wave generic instance."""
-    _say(f"tall q6_k route {rows}x{k}")
-    w = synth.weights(synth.Q6_K, rows, k, seed=0x5A4C4D50 + k)
+TALL_ROUTES = [(synth.Q6_K, 3840), (synth.Q6_K, 5120), (synth.Q8_0, 4096), (synth.Q8_0, 5120), (synth.Q8_0, 8192),
+               (synth.Q4_0, 4096), (synth.Q4_0, 5120), (synth.Q4_0, 8192), (synth.Q4_K, 5120), (synth.Q4_K, 8192),
+               (synth.Q4_1, 4096), (synth.Q4_1, 8192)]
+
+
+@pytest.mark.parametrize("qt,k", TALL_ROUTES, ids=[f"{synth.TYPE_NAMES[q]}_{k}" for q, k in TALL_ROUTES])
+@pytest.mark.parametrize("rows", [65536 + 37, 65535])
+def test_tall_route(dev, qt, k, rows):
+    """GEMVs of 65536 rows and more take the prefetching lm_head instances
+    (8-wave workgroups) where the quant has one for the row length (q4_k's
+    k <= 4096 keeps its 16-wave instance); one row fewer keeps the 4- or
+    16-wave (or split-K) instances."""
+    _say(f"tall route quant={qt} {rows}x{k}")
+    w = synth.weights(qt, rows, k, seed=0x5A4C4D50 + k)
     res = dev.upload_resident(w)
     xs = synth.activation(0x5A4C4D51, k)
     x = dev.dev_malloc(xs.nbytes)
     y = dev.dev_malloc(rows * 4)
     try:
         dev.dev_upload(x, xs)
-        assert dev.mat_vec_enqueue(res, zd.quant(synth.Q6_K), rows, k, x, y), dev.last_error()
+        assert dev.mat_vec_enqueue(res, zd.quant(qt), rows, k, x, y), dev.last_error()
         dev.sync()
         assert dev.launch_log(True)
         try:
-            assert dev.mat_vec_enqueue(res, zd.quant(synth.Q6_K), rows, k, x, y), dev.last_error()
+            assert dev.mat_vec_enqueue(res, zd.quant(qt), rows, k, x, y), dev.last_error()
             dev.sync()
             log = dev.launch_log_read()
         finally:
             dev.launch_log(False)
-        assert [(r["what"], r["block"]) for r in log] == [("gemv", block)]
+        assert [r["what"] for r in log] == ["gemv"]
+        assert (log[0]["block"] == 512) == (rows >= 65536), log[0]
     finally:
         dev.dev_free(x)
         dev.dev_free(y)

@@ -66,3 +66,12 @@ ZLM_GEMV_Q8TOK_R2(q4_0, Q4_0, 2)
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
 // x tile, where the host takes it (measured faster than the exact-steps forms)
 ZLM_GEMV_G8K(q4_0, Q4_0)
+// The lm_heads (from 65536 rows): prefetching 8-wave workgroups at 16 waves
+// per CU with x as int8 planes, two-row wave tiles at 2-3 chunk steps (k <=
+// 6144), one row at 4 (two hold too many registers).  Measured on gfx950
+// against the 4-wave exact-steps instances (alternating runs, weights rotated
+// past the Infinity Cache): 151936 x 4096 84 -> 62 us, 152064 x 5120 116 ->
+// 88 us, 128256 x 8192 129 -> 102 us.
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_r2_s2_tallq, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_r2_s3_tallq, Q4_0, 8192, 8, 2, 3, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_r1_s4_tallq1, Q4_0, 8192, 8, 1, 4, PRO_PLAIN, EPI_PLAIN, false)

@@ -21,3 +21,10 @@ ZLM_GEMV_Q8TOK_R2(q4_1, Q4_1, 2)
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
 // x tile, where the host takes it (measured faster than the exact-steps forms)
 ZLM_GEMV_G8K(q4_1, Q4_1)
+// The lm_heads (from 65536 rows): prefetching 8-wave workgroups at 16 waves
+// per CU (fp32 x).  Measured on gfx950 against the exact-steps instances
+// (alternating runs, weights rotated past the Infinity Cache): 151936 x 4096
+// 87 -> 84 us, 152064 x 5120 117 -> 110 us, 128256 x 8192 134 -> 128 us.
+ZLM_GEMVX_PF(zlm_gemv_q4_1_r1_s2_tall, Q4_1, 4096, 8, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q4_1_r1_s3_tall, Q4_1, 8192, 8, 1, 3, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q4_1_r1_s4_tall, Q4_1, 8192, 8, 1, 4, PRO_PLAIN, EPI_PLAIN, false)

@@ -47,3 +47,11 @@ ZLM_GEMV_Q8TOK_R2(q4_k, Q4_K, 2)
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
 // x tile, where the host takes it (measured faster than the exact-steps forms)
 ZLM_GEMV_G8K(q4_k, Q4_K)
+// The lm_heads at 3-4 chunk steps (k 4097-8192, from 65536 rows): prefetching
+// 8-wave workgroups at 16 waves per CU with x as int8 planes, two-row wave
+// tiles at 3 steps.  Measured on gfx950 against the exact-steps instances
+// (alternating runs, weights rotated past the Infinity Cache): 152064 x 5120
+// 123 -> 106 us, 128256 x 8192 141 -> 124 us.  At 2 steps the one-row form
+// matched the 16-wave pfqw16 instance (151936 x 4096: 81 us either way).
+ZLM_GEMVX_PFQ(zlm_gemv_q4_k_r2_s3_tallq, Q4_K, 8192, 8, 2, 3, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_k_r1_s4_tallq1, Q4_K, 8192, 8, 1, 4, PRO_PLAIN, EPI_PLAIN, false)

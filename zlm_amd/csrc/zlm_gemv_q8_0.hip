@@ -53,3 +53,14 @@ ZLM_GEMVTR(zlm_gemv_q8_0_tok2_g8_r2, Q8_0, 8192, 8, 2, 4)
 
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q8_0, Q8_0, 4)
+// The lm_heads at 5-8 chunk steps (k 4097-8192, from 65536 rows): the
+// prefetching 8-wave instance of the 4-step lm_head; at 7-8 steps with
+// scheduling fences (without them the 8-step form spills).  Measured on
+// gfx950 against the exact-steps and generic instances (alternating runs,
+// weights rotated past the Infinity Cache): 152064 x 5120 179 -> 129 us,
+// 65536 x 5120 81 -> 59 us, 151936 x 6144 232 -> 155 us, 151936 x 7168 200 ->
+// 181 us, 128256 x 8192 184 -> 172 us.
+ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s5_tall, Q8_0, 8192, 8, 1, 5, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s6_tall, Q8_0, 8192, 8, 1, 6, PRO_PLAIN, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s7_tall, Q8_0, 8192, 8, 1, 7, PRO_PLAIN, EPI_PLAIN, true)
+ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s8_tall, Q8_0, 8192, 8, 1, 8, PRO_PLAIN, EPI_PLAIN, true)

@@ -647,9 +647,9 @@ const GemvKernel* find_gemv(zlm_device* d, int slot, const char* name, int rt, i
 }
 
 // The prefetching instances' name suffixes, the grid's waves per CU, the
-// fewest rows a suffix is taken for (_tallq / _tall: the lm_heads, with and
-// without int8-plane x) and whether x is staged as int8 planes (a summation
-// the batch kernel does not share).
+// fewest rows a suffix is taken for (_tallq / _tallq1 / _tall: the lm_heads,
+// with int8-plane x in two- or one-row tiles, or with fp32 x) and whether x
+// is staged as int8 planes (a summation the batch kernel does not share).
 struct PfSuffix {
     const char* suffix;
     int waves_per_cu;
@@ -657,7 +657,8 @@ struct PfSuffix {
     bool xq;
     int rt;  // rows per wave tile of the plain (r<rt>) instance
 };
-constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true, 2}, {"_tall", 16, 65536, false, 1},
+constexpr PfSuffix kPfSuffixes[] = {{"_tallq", 16, 65536, true, 2},     {"_tallq1", 16, 65536, true, 1},
+                                    {"_tall", 16, 65536, false, 1},
                                     {"_pf", 8, 0, false, 1},         {"_pfw16", 16, 0, false, 1},
                                     {"_pfq", 8, 0, true, 1},         {"_pfqw16", 16, 0, true, 1}};
 
