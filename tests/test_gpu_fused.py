@@ -350,6 +350,48 @@ BOUNDARY_SHAPES = [
 ]
 
 
+# The lm_head instances from 65536 rows at row lengths past 4096 (prefetching
+# 8-wave workgroups, plain and RMSNorm-fused), at 65573 rows (a ragged last
+# tile): each form against the oracle and the route in the launch log.
+TALL_FORM_SHAPES = [(synth.Q6_K, 5120), (synth.Q8_0, 5120), (synth.Q8_0, 6144), (synth.Q8_0, 7168), (synth.Q8_0, 8192),
+                    (synth.Q4_0, 5120), (synth.Q4_0, 8192), (synth.Q4_K, 5120), (synth.Q4_K, 8192), (synth.Q4_1, 5120),
+                    (synth.Q4_1, 8192)]
+
+
+@pytest.mark.parametrize("qt,k", TALL_FORM_SHAPES, ids=[f"{NAMES[q]}-{k}" for q, k in TALL_FORM_SHAPES])
+def test_tall_forms_match_oracle(dev, qt, k):
+    rows = 65536 + 37
+    _say(f"tall forms {NAMES[qt]} rows={rows} k={k}")
+    eps = 1e-6
+    w = synth.weights(qt, rows, k, seed=rows + 5 * k + qt)
+    x = synth.activation(k + 2, k) * np.float32(2.0)
+    nw = (1.0 + 0.1 * synth.activation(k + 8, k)).astype(np.float32)
+    rw = dev.upload_resident(w)
+    assert rw is not None, dev.last_error()
+    xd, nwd, yd = _dev_vec(dev, x), _dev_vec(dev, nw), dev.dev_malloc(rows * 4)
+    try:
+        cases = [(zd.FORM_PLAIN, dict(), oracle.matvec(qt, w, k, rows, x)),
+                 (zd.FORM_NORM, dict(norm_w=nwd, eps=eps), oracle.matvec(qt, w, k, rows, _rmsnorm(x, nw, eps)))]
+        for form, kw, want in cases:
+            assert dev.gemv_op_enqueue(form, zd.quant(qt), rw, rows, k, xd, yd, **kw), dev.last_error()
+            dev.sync()
+            assert dev.launch_log(True)
+            try:
+                assert dev.gemv_op_enqueue(form, zd.quant(qt), rw, rows, k, xd, yd, **kw), dev.last_error()
+                dev.sync()
+                log = dev.launch_log_read()
+            finally:
+                dev.launch_log(False)
+            assert [r["block"] for r in log] == [512], (form, log)
+            got = np.zeros(rows, np.float32)
+            dev.dev_download(got, yd)
+            assert np.isfinite(got).all() and rel_l2(got, want) <= REL_L2, form
+    finally:
+        for p in (xd, nwd, yd):
+            dev.dev_free(p)
+        dev.free_resident(rw)
+
+
 @pytest.mark.parametrize("qt,rows,k", BOUNDARY_SHAPES,
                          ids=[f"{NAMES[q]}-{r}x{k}" for q, r, k in BOUNDARY_SHAPES])
 def test_picker_boundary_shapes_match_oracle(dev, qt, rows, k):

@@ -75,3 +75,8 @@ ZLM_GEMV_G8K(q4_0, Q4_0)
 ZLM_GEMVX_PFQ(zlm_gemv_q4_0_r2_s2_tallq, Q4_0, 4096, 8, 2, 2, PRO_PLAIN, EPI_PLAIN, false)
 ZLM_GEMVX_PFQ(zlm_gemv_q4_0_r2_s3_tallq, Q4_0, 8192, 8, 2, 3, PRO_PLAIN, EPI_PLAIN, false)
 ZLM_GEMVX_PFQ(zlm_gemv_q4_0_r1_s4_tallq1, Q4_0, 8192, 8, 1, 4, PRO_PLAIN, EPI_PLAIN, false)
+// The RMSNorm-fused lm_heads at 3-4 chunk steps (from 65536 rows).  Measured
+// on gfx950 (graph replays, weights rotated past the Infinity Cache): 152064
+// x 5120 110 -> 79 us, 128256 x 8192 121 -> 91.5 us.
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s3_tallq, Q4_0, 8192, 8, 2, 3, PRO_NORM, EPI_PLAIN, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_0_norm_s4_tallq1, Q4_0, 8192, 8, 1, 4, PRO_NORM, EPI_PLAIN, false)

@@ -28,3 +28,8 @@ ZLM_GEMV_G8K(q4_1, Q4_1)
 ZLM_GEMVX_PF(zlm_gemv_q4_1_r1_s2_tall, Q4_1, 4096, 8, 1, 2, PRO_PLAIN, EPI_PLAIN, false)
 ZLM_GEMVX_PF(zlm_gemv_q4_1_r1_s3_tall, Q4_1, 8192, 8, 1, 3, PRO_PLAIN, EPI_PLAIN, false)
 ZLM_GEMVX_PF(zlm_gemv_q4_1_r1_s4_tall, Q4_1, 8192, 8, 1, 4, PRO_PLAIN, EPI_PLAIN, false)
+// The RMSNorm-fused lm_heads at 3-4 chunk steps (from 65536 rows).  Measured
+// on gfx950 (graph replays, weights rotated past the Infinity Cache): 152064
+// x 5120 112 -> 101 us, 128256 x 8192 125 -> 117 us.
+ZLM_GEMVX_PF(zlm_gemv_q4_1_norm_s3_tall, Q4_1, 8192, 8, 1, 3, PRO_NORM, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q4_1_norm_s4_tall, Q4_1, 8192, 8, 1, 4, PRO_NORM, EPI_PLAIN, false)

@@ -55,3 +55,8 @@ ZLM_GEMV_G8K(q4_k, Q4_K)
 // matched the 16-wave pfqw16 instance (151936 x 4096: 81 us either way).
 ZLM_GEMVX_PFQ(zlm_gemv_q4_k_r2_s3_tallq, Q4_K, 8192, 8, 2, 3, PRO_PLAIN, EPI_PLAIN, false)
 ZLM_GEMVX_PFQ(zlm_gemv_q4_k_r1_s4_tallq1, Q4_K, 8192, 8, 1, 4, PRO_PLAIN, EPI_PLAIN, false)
+// The RMSNorm-fused lm_heads at 3-4 chunk steps (from 65536 rows).  Measured
+// on gfx950 (graph replays, weights rotated past the Infinity Cache): 152064
+// x 5120 119 -> 98 us, 128256 x 8192 133 -> 114 us.
+ZLM_GEMVX_PFQ(zlm_gemv_q4_k_norm_s3_tallq, Q4_K, 8192, 8, 2, 3, PRO_NORM, EPI_PLAIN, false)
+ZLM_GEMVX_PFQ(zlm_gemv_q4_k_norm_s4_tallq1, Q4_K, 8192, 8, 1, 4, PRO_NORM, EPI_PLAIN, false)

@@ -46,3 +46,10 @@ ZLM_GEMV_MULTI_Q4(q6_k, Q6_K)
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element
 // x tile, where the host takes it (measured faster than the exact-steps forms)
 ZLM_GEMV_G8K(q6_k, Q6_K)
+// The RMSNorm-fused lm_head at 3 chunk steps (from 65536 rows; the decode
+// step's last op): the plain instance above with the norm prologue.  Measured
+// on gfx950 (graph replays, weights rotated past the Infinity Cache): 152064 x
+// 5120 191 -> 126 us against the 4-wave exact-steps instance.  At 2 steps the
+// 4-wave normed instance already matches the plain lm_head instance (151936
+// x 4096: 88.9 us both).
+ZLM_GEMVX_PFQ(zlm_gemv_q6_k_norm_s3_tallq, Q6_K, 8192, 8, 2, 3, PRO_NORM, EPI_PLAIN, false)

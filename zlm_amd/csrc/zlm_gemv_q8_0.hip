@@ -64,3 +64,11 @@ ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s5_tall, Q8_0, 8192, 8, 1, 5, PRO_PLAIN, EPI_PLAIN
 ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s6_tall, Q8_0, 8192, 8, 1, 6, PRO_PLAIN, EPI_PLAIN, false)
 ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s7_tall, Q8_0, 8192, 8, 1, 7, PRO_PLAIN, EPI_PLAIN, true)
 ZLM_GEMVX_PF(zlm_gemv_q8_0_r1_s8_tall, Q8_0, 8192, 8, 1, 8, PRO_PLAIN, EPI_PLAIN, true)
+// The RMSNorm-fused lm_heads at 5-8 chunk steps (from 65536 rows): the
+// instances above with the norm prologue.  Measured on gfx950 (graph
+// replays, weights rotated past the Infinity Cache): 152064 x 5120 240 -> 123
+// us (the generic instance before), 128256 x 8192 177 -> 169 us.
+ZLM_GEMVX_PF(zlm_gemv_q8_0_norm_s5_tall, Q8_0, 8192, 8, 1, 5, PRO_NORM, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q8_0_norm_s6_tall, Q8_0, 8192, 8, 1, 6, PRO_NORM, EPI_PLAIN, false)
+ZLM_GEMVX_PF(zlm_gemv_q8_0_norm_s7_tall, Q8_0, 8192, 8, 1, 7, PRO_NORM, EPI_PLAIN, true)
+ZLM_GEMVX_PF(zlm_gemv_q8_0_norm_s8_tall, Q8_0, 8192, 8, 1, 8, PRO_NORM, EPI_PLAIN, true)
