@@ -745,10 +745,12 @@ const GemvKernel* pick_gemv_named(zlm_device* d, const QuantInfo* qi, size_t k, 
 // - plain (rows the split-K instances do not take), below 65536 rows: q4_1,
 //   and q6_k at 3 steps (q4_1 14336 x 8192 21.8 -> 18.0 us); q6_k at 4 steps
 //   was faster at 14336 rows but slower from 28672.
-// Launches of 65536 rows and more keep the other instances: q6_k's two-row
-// prefetching lm_head instance at 3 steps (152064 x 5120 190 us exact-steps,
-// 161 us g8k, 134 us _r2_s3_tallq), the exact-steps ones otherwise (q4_0 /
-// q4_k plain slower with g8k there; the fused forms not measured).
+// Launches of 65536 rows and more take the lm_head instances instead (the
+// prefetching _tallq / _tallq1 / _tall suffixes, plain and RMSNorm-fused)
+// where the quant has one for the step count, else the exact-steps instances
+// (e.g. q6_k 152064 x 5120: 190 us exact-steps, 161 us g8k, 134 us
+// _r2_s3_tallq; q4_0 / q4_k plain were slower with g8k there; the pair and
+// residual forms were not measured at that size).
 bool use_g8k(const QuantInfo* qi, uint32_t form, int steps, size_t rows) {
     if (steps != 3 && steps != 4) return false;
     const uint32_t t = qi->type;
