@@ -358,6 +358,21 @@ def sections(dev, args, want, extra):
                 log(f"{name} batched: " + ", ".join(f"{key} {v['us_per_gemv']} us/GEMV ({v['GBps']} GB/s)"
                                                     for key, v in batched.items()))
             g.free()
+        # lm_heads of other models (hidden 4096-8192, vocab 128256-152064): the
+        # prefetching lm_head instances beyond the configs' row lengths
+        lm = {}
+        for name, qt, rows, k in (("q4_0_151936x4096", synth.Q4_0, 151936, 4096),
+                                  ("q8_0_152064x5120", synth.Q8_0, 152064, 5120),
+                                  ("q6_k_152064x5120", synth.Q6_K, 152064, 5120),
+                                  ("q4_k_128256x8192", synth.Q4_K, 128256, 8192)):
+            g = Gemv(dev, name, qt, rows, k, 0x5A4C4D60 + rows)
+            descs = [g.desc(c) for c in range(g.copies)]
+            ms = time_launches(dev, descs, max(len(descs), min(400, int(2e9 / g.wbytes)))) / len(descs)
+            gbps = g.algo_bytes / (ms * 1e-3) / 1e9
+            lm[name] = {"us": round(ms * 1e3, 3), "GBps": round(gbps, 1), "pct_peak": round(100 * gbps / PEAK_GBPS, 1)}
+            log(f"lm_head {name}: {ms * 1e3:.2f} us, {gbps:.1f} GB/s ({100 * gbps / PEAK_GBPS:.1f}%)")
+            g.free()
+        extra["other_models_lm_heads"] = lm
 
     # ---- prefill GEMM, Q4_0 12288x4096 x 512 tokens, int8 MFMA ---------
     if want("gemm"):
