@@ -22,7 +22,9 @@ m = 3, 4 (zlm's int path: q8 activations, exact integer block dots,
 kernels/quantized.zig:49-55, :79-87, :111-123, :149-156 over the quantizer of
 matvec/layout.zig:458-476): the int-path token GEMV (zlm_gemv_<quant>_q8tok4_
 g<T>, two-row tiles for the nibble quants from 32768 rows) quantizes the
-activations in its own prologue.  Against the oracle's int
+activations in its own prologue; m = 5..8 its eight-slot form for q4_1 at k
+<= 4096 and q4_k there up to 8192 rows, the small-M GEMM otherwise (both
+checked here at m = 5 and 8).  Against the oracle's int
 path (orc_matmul_int) at relative L2 <= 1e-5, which one activation off by one
 quantization unit would exceed, with activations that stress the quantizer
 (a zero block, a block with one nonzero, values near rounding ties and a
@@ -129,7 +131,7 @@ def _stress_x(m, k, seed):
 
 @pytest.mark.parametrize("qt,zq", QUANTS, ids=IDS)
 @pytest.mark.parametrize("rows,k", INT_SHAPES)
-@pytest.mark.parametrize("m", [3, 4])
+@pytest.mark.parametrize("m", [3, 4, 5, 8])
 def test_int_tokens_match_oracle(dev, qt, zq, rows, k, m):
     be = synth.BLOCK_ELEMS[qt]
     k = (k + be - 1) // be * be
@@ -219,3 +221,32 @@ def test_token_routes_replay_from_a_graph(dev, m):
         for p in (x, out, other):
             dev.dev_free(p)
         dev.free_resident(res)
+
+
+@pytest.mark.parametrize("qt,rows,k,m,launches", [
+    (zd.Q4_K, 96, 4096, 5, ["gemv int tokens"]), (zd.Q4_K, 96, 4096, 8, ["gemv int tokens"]),
+    (zd.Q4_1, 12288, 4096, 8, ["gemv int tokens"]), (zd.Q4_K, 12288, 4096, 8, ["quantize tiled", "gemm small"]),
+    (zd.Q4_K, 96, 8192, 5, ["quantize tiled", "gemm small"]), (zd.Q4_1, 96, 4096, 9, ["quantize tiled", "gemm small"]),
+    (zd.Q4_0, 96, 4096, 8, ["quantize tiled", "gemm small"])], ids=lambda v: str(v) if not isinstance(v, list) else "")
+def test_eight_token_route(dev, qt, rows, k, m, launches):
+    """m = 5..8: the eight-slot int-path GEMV for q4_1 at k <= 4096 and q4_k
+    there up to 8192 rows; everything else past 4 tokens the small-M GEMM."""
+    sq = {zd.Q4_K: synth.Q4_K, zd.Q4_1: synth.Q4_1, zd.Q4_0: synth.Q4_0}[qt]
+    w = synth.weights(sq, rows, k, seed=k + m + rows)
+    res = dev.upload_resident(w)
+    x = dev.dev_malloc(m * k * 4)
+    out = dev.dev_malloc(m * rows * 4)
+    try:
+        dev.dev_upload(x, synth.activation(9, m * k))
+        assert dev.mat_mul_enqueue(res, zd.quant(qt), rows, k, m, x, out), dev.last_error()  # layouts
+        dev.sync()
+        assert dev.launch_log(True)
+        assert dev.mat_mul_enqueue(res, zd.quant(qt), rows, k, m, x, out), dev.last_error()
+        dev.sync()
+        assert [r["what"] for r in dev.launch_log_read()] == launches
+    finally:
+        dev.launch_log(False)
+        dev.dev_free(x)
+        dev.dev_free(out)
+        dev.free_resident(res)
+

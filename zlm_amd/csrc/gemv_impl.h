@@ -2042,6 +2042,10 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 // Two-row tiles (_r2) for launches of 32768 rows and more: each lane reads a
 // token's LDS words once for both rows (the nibble quants; q8_0's two LDS
 // reads per token gain nothing).
+// Eight token slots at the 4096-float tier (m = 5..8), for the quants whose
+// small-M GEMM carries the min term (q4_1, q4_k): there the GEMM's extra
+// outer products cost more than the doubled LDS reads of eight slots.
+#define ZLM_GEMV_Q8TOK8(QN, QT, STEPS) ZLM_GEMVQ(zlm_gemv_##QN##_q8tok8_g4, QT, 8, 4096, STEPS)
 #define ZLM_GEMV_Q8TOK_R2(QN, QT, STEPS)                                \
     ZLM_GEMVQR(zlm_gemv_##QN##_q8tok4_g4_r2, QT, 4, 4096, STEPS, 2)     \
     ZLM_GEMVQR(zlm_gemv_##QN##_q8tok4_g8_r2, QT, 4, 8192, STEPS, 2)

@@ -954,7 +954,8 @@ bool enqueue_gemv_tok2(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size
     return launch(d, gk->fn, grid, static_cast<unsigned>(gk->threads), args, "gemv two tokens");
 }
 
-// The int path for 3 <= m <= kQ8TokM tokens and k <= kQ8TokMaxK in one pass
+// The int path for 3 <= m <= kQ8TokM tokens and k <= kQ8TokMaxK (and for
+// 5 <= m <= 8 where pick_q8tok8 below has an instance) in one pass
 // over the weights (zlm_gemv_<quant>_q8tok4_g<T>: T = 4 or 8 for k <= 4096
 // or 8192; every workgroup quantizes the m activation rows itself), or null:
 // the caller runs the small-M GEMM.  Measured on gfx950 (m = 3-4, against
@@ -968,6 +969,30 @@ bool enqueue_gemv_tok2(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size
 // CU, so 4096 rows are 2048 two-row tiles for 4096 waves (7.3 -> 8.8 us).
 constexpr size_t kQ8TokM = 4;
 constexpr size_t kQ8TokMaxK = 8192;
+
+// m = 5..8: the eight-slot instance (zlm_gemv_<quant>_q8tok8_g4) for q4_1 at
+// k <= 4096, and for q4_k there up to 8192 rows, or null (the small-M GEMM
+// runs).  Measured on gfx950 against the quantizer + small-M GEMM (m = 5 and
+// 8, alternating runs): Q4_K 4096 x 4096 13.3 -> 11.9 us, 1024 x 4096 13.0
+// -> 11.1 us; Q4_1 4096 x 4096 13.3 -> 11.7 us, 12288 x 4096 22.4 -> 20.4
+// us, 151936 x 4096 173 -> 143 us.  Slower: Q4_K 15360 x 3840 (21.9 ->
+// 26.3 us) and 4096 x 8192 (21.1 -> 23.4), Q4_0 and Q8_0 (4096 x 4096 Q4_0
+// 9.9 -> 11.2 us), whose GEMMs carry no min term.
+constexpr size_t kQ8Tok8M = 8;
+
+const GemvKernel* pick_q8tok8(zlm_device* d, const QuantInfo* qi, size_t k, size_t rows) {
+    const uint64_t key = pick_key(qi, k, kPickQ8Tok, static_cast<int>(kQ8Tok8M), rows);
+    auto it = d->picks.find(key);
+    if (it != d->picks.end()) return it->second;
+    const GemvKernel* g = nullptr;
+    if (k <= 4096 && (qi->type == ZLM_GGML_Q4_1 || (qi->type == ZLM_GGML_Q4_K && rows <= 8192))) {
+        char nm[96];
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_q8tok8_g4", kQuantNames[qi->slot]);
+        g = find_gemv(d, qi->slot, nm, 1, 0);
+    }
+    d->picks.emplace(key, g);
+    return g;
+}
 
 const GemvKernel* pick_q8tok(zlm_device* d, const QuantInfo* qi, size_t k, size_t rows) {
     const int ntok = static_cast<int>(kQ8TokM);
@@ -996,8 +1021,8 @@ const GemvKernel* pick_q8tok(zlm_device* d, const QuantInfo* qi, size_t k, size_
 bool enqueue_gemv_q8tok(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size_t rows, size_t k, size_t m,
                         const float* x_dev, float* y_dev, bool* ran) {
     *ran = false;
-    if (m < 3 || m > kQ8TokM) return true;
-    const GemvKernel* gk = pick_q8tok(d, qi, k, rows);
+    if (m < 3 || m > kQ8Tok8M) return true;
+    const GemvKernel* gk = m <= kQ8TokM ? pick_q8tok(d, qi, k, rows) : pick_q8tok8(d, qi, k, rows);
     if (!gk) return true;
     if (gk->role != kRoleQ8Tok || !gk->struct_args)
         return fail(d, "internal: picked kernel (role %d) is not the int token GEMV", gk->role);
