@@ -219,9 +219,9 @@ int zlm_gpu_cu_count(const zlm_device *dev);
 bool zlm_gpu_vram_info(zlm_device *dev, uint64_t *free_bytes, uint64_t *total_bytes);
 /* HBM a resident holds now: its raw bytes until the first op converts them,
  * then the device layout, plus the prefill GEMM's tiled copy once the tiled
- * GEMM has run on it (more than 4 tokens, or 3-4 tokens at k > 8192; fewer
- * tokens, and 5-8 tokens where the eight-slot int-path GEMV runs, read the
- * device layout). */
+ * GEMM has run on it (more than 4 tokens, or 3-4 tokens at k > 8192, k >
+ * 16384 for Q4_1 / Q4_K; fewer tokens, and 5-8 tokens where the eight-slot
+ * int-path GEMV runs, read the device layout). */
 uint64_t zlm_gpu_resident_device_bytes(const zlm_resident *res);
 /* HBM a rows x k weight of `quant` will hold once converted (its device
  * layout), plus its GEMM tiled copy when `with_gemm` (tensors the plan also
@@ -255,7 +255,7 @@ bool zlm_gpu_mat_vec_batch_enqueue(zlm_device *dev, zlm_resident *const *res, ui
 /* Enqueue the matrix product out_dev[t*rows + r] (x_dev: m x k fp32,
  * token-major) over a Q4_0, Q8_0, Q4_1 or Q4_K resident, by token count:
  * m = 1 the fp GEMV; m = 2 the two-token fp GEMV (k <= 16384, else a GEMV per
- * token); m = 3, 4 at k <= 8192 the int-path token GEMV (q8 activations
+ * token); m = 3, 4 at k <= 8192 (16384 for Q4_1 / Q4_K) the int-path token GEMV (q8 activations
  * quantized in its prologue, the weights read once from the device layout),
  * and its eight-slot form at m = 5..8 for Q4_1 at k <= 4096 and Q4_K there up
  * to 8192 rows; otherwise the q8 activation quantizer, then an int8-MFMA GEMM over the

@@ -112,8 +112,11 @@ def test_two_token_route(dev, k, launches):
 
 
 # (32768 + 37, 1024) and (32768 + 1, 5120): the two-row tiles of the nibble
-# quants (from 32768 rows), ending inside a tile, at both x tiers
-INT_SHAPES = [(1, 256), (67, 3840), (4097, 4096), (300, 8192), (129, 12288), (32768 + 37, 1024), (32768 + 1, 5120)]
+# quants (from 32768 rows), ending inside a tile, at both x tiers; (129,
+# 12288) and (65, 15360): the 16384-float tier of q4_1 / q4_k (the GEMM for
+# the others)
+INT_SHAPES = [(1, 256), (67, 3840), (4097, 4096), (300, 8192), (129, 12288), (65, 15360), (32768 + 37, 1024),
+              (32768 + 1, 5120)]
 
 
 def _stress_x(m, k, seed):
@@ -227,10 +230,16 @@ def test_token_routes_replay_from_a_graph(dev, m):
     (zd.Q4_K, 96, 4096, 5, ["gemv int tokens"]), (zd.Q4_K, 96, 4096, 8, ["gemv int tokens"]),
     (zd.Q4_1, 12288, 4096, 8, ["gemv int tokens"]), (zd.Q4_K, 12288, 4096, 8, ["quantize tiled", "gemm small"]),
     (zd.Q4_K, 96, 8192, 5, ["quantize tiled", "gemm small"]), (zd.Q4_1, 96, 4096, 9, ["quantize tiled", "gemm small"]),
-    (zd.Q4_0, 96, 4096, 8, ["quantize tiled", "gemm small"])], ids=lambda v: str(v) if not isinstance(v, list) else "")
-def test_eight_token_route(dev, qt, rows, k, m, launches):
-    """m = 5..8: the eight-slot int-path GEMV for q4_1 at k <= 4096 and q4_k
-    there up to 8192 rows; everything else past 4 tokens the small-M GEMM."""
+    (zd.Q4_0, 96, 4096, 8, ["quantize tiled", "gemm small"]),
+    (zd.Q4_K, 96, 15360, 3, ["gemv int tokens"]), (zd.Q4_1, 96, 16384, 4, ["gemv int tokens"]),
+    (zd.Q4_K, 96, 20480, 3, ["quantize tiled", "gemm small"]), (zd.Q4_0, 96, 12288, 4, ["quantize tiled", "gemm small"])],
+    ids=lambda v: str(v) if not isinstance(v, list) else "")
+def test_min_quant_token_routes(dev, qt, rows, k, m, launches):
+    """The int-path token GEMV's extra routes for the quants whose small-M
+    GEMM carries a min term: m = 5..8 the eight-slot form for q4_1 at k <=
+    4096 and q4_k there up to 8192 rows; m = 3, 4 the 16384-float tier for
+    both at k 8193-16384.  Everything else past 4 tokens, or past k = 8192
+    for q4_0 / q8_0, runs the small-M GEMM."""
     sq = {zd.Q4_K: synth.Q4_K, zd.Q4_1: synth.Q4_1, zd.Q4_0: synth.Q4_0}[qt]
     w = synth.weights(sq, rows, k, seed=k + m + rows)
     res = dev.upload_resident(w)

@@ -2042,6 +2042,9 @@ __device__ __forceinline__ void gemv_sk(const GemvArgs& a) {
 // Two-row tiles (_r2) for launches of 32768 rows and more: each lane reads a
 // token's LDS words once for both rows (the nibble quants; q8_0's two LDS
 // reads per token gain nothing).
+// The 16384-float tier (m = 3, 4, k 8193-16384) for the quants whose
+// small-M GEMM carries the min term (q4_1, q4_k).
+#define ZLM_GEMV_Q8TOK16(QN, QT, STEPS) ZLM_GEMVQ(zlm_gemv_##QN##_q8tok4_g16, QT, 4, 16384, STEPS)
 // Eight token slots at the 4096-float tier (m = 5..8), for the quants whose
 // small-M GEMM carries the min term (q4_1, q4_k): there the GEMM's extra
 // outer products cost more than the doubled LDS reads of eight slots.

@@ -17,6 +17,7 @@ ZLM_GEMVTR(zlm_gemv_q4_1_tok2_g8_r2, Q4_1, 8192, 8, 2, 2)
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q4_1, Q4_1, 2)
 ZLM_GEMV_Q8TOK8(q4_1, Q4_1, 2)
+ZLM_GEMV_Q8TOK16(q4_1, Q4_1, 2)
 ZLM_GEMV_Q8TOK_R2(q4_1, Q4_1, 2)
 
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element

@@ -43,6 +43,7 @@ ZLM_GEMVTR(zlm_gemv_q4_k_tok2_g8_r2, Q4_K, 8192, 8, 2, 2)
 // matMul at m = 3, 4 (int path, the weights read once for all tokens)
 ZLM_GEMV_Q8TOK(q4_k, Q4_K, 2)
 ZLM_GEMV_Q8TOK8(q4_k, Q4_K, 2)
+ZLM_GEMV_Q8TOK16(q4_k, Q4_K, 2)
 ZLM_GEMV_Q8TOK_R2(q4_k, Q4_K, 2)
 
 // Rows of 4097-8192 elements: the generic two-step loop over an 8192-element

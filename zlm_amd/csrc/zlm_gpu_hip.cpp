@@ -967,6 +967,11 @@ bool enqueue_gemv_tok2(zlm_device* d, zlm_resident* r, const QuantInfo* qi, size
 // -> 80 us, Q4_1 the same shape 95 -> 85 us, Q4_0 32768 x 4096 26.7 -> 25.1
 // us.  Below that they idle waves: the grid holds one 16-wave workgroup per
 // CU, so 4096 rows are 2048 two-row tiles for 4096 waves (7.3 -> 8.8 us).
+// q4_1 and q4_k also run k 8193-16384 here (zlm_gemv_<quant>_q8tok4_g16,
+// one-row tiles), where their min-carrying GEMM is slower: Q4_K 3840 x 15360
+// 34.4 -> 25.7 us, Q4_1 4096 x 12288 28.8 -> 20.5 us (m = 3, 4; alternating
+// runs).  For q4_0 the tier measured slower than the GEMM (4096 x 12288:
+// 19.3 -> 20.4 us) and q8_0 about even (23.8 -> 23.1 us).
 constexpr size_t kQ8TokM = 4;
 constexpr size_t kQ8TokMaxK = 8192;
 
@@ -1010,6 +1015,12 @@ const GemvKernel* pick_q8tok(zlm_device* d, const QuantInfo* qi, size_t k, size_
             snprintf(nm, sizeof nm, "zlm_gemv_%s_q8tok%d_g%d", kQuantNames[qi->slot], ntok, k <= 4096 ? 4 : 8);
             g = find_gemv(d, qi->slot, nm, 1, 0);
         }
+    } else if (k <= 2 * kQ8TokMaxK && (qi->type == ZLM_GGML_Q4_1 || qi->type == ZLM_GGML_Q4_K)) {
+        // q4_1 / q4_k, k 8193-16384: the 16384-float tier (the min-carrying
+        // GEMM is the slower route there)
+        char nm[96];
+        snprintf(nm, sizeof nm, "zlm_gemv_%s_q8tok%d_g16", kQuantNames[qi->slot], ntok);
+        g = find_gemv(d, qi->slot, nm, 1, 0);
     }
     d->picks.emplace(key, g);
     return g;
